@@ -1,0 +1,446 @@
+"""Pins the CPU oracle (oracle/smq_oracle.c) before anything is checked
+against it: known answers from the reference's own tests and goldens, library
+routines (numpy's IEEE half conversion), closed forms, exact-integer brute
+force, and the reference's kernels compiled from its sources (oracle/_ref)."""
+import hashlib
+import json
+import os
+import struct
+
+import numpy as np
+import pytest
+
+from patterns import LcgUniform, bf16_patterns, bf16_to_f32
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+Q8B, Q5B = 36, 22
+
+
+def f32_bits(x):
+    return np.asarray(x, np.float32).view(np.uint32)
+
+
+# ---------------------------------------------------------------- binary16
+
+def test_f16_to_f32_matches_numpy_all_halves(orc):
+    h = np.arange(65536, dtype=np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    got = np.array([orc.f16_to_f32(int(v)) for v in h], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(f32_bits(got[~nan]), f32_bits(want[~nan]))
+
+
+def test_f16_round_trip_and_constants(orc):
+    # tests/test_kernels.c:51-61 and tests/convert-quant.test.ts:117-132
+    for h in range(0, 65536, 7):
+        f = orc.f16_to_f32(h)
+        if f != f:
+            continue
+        assert orc.f32_to_f16(f) == h
+    cases = [(1.0, 0x3C00), (-2.0, 0xC000), (65504.0, 0x7BFF), (65520.0, 0x7C00), (1e-8, 0x0000),
+             (5.960464477539063e-8, 0x0001), (1 + 2 ** -11, 0x3C00), (1 + 3 * 2 ** -11, 0x3C02),
+             (float("inf"), 0x7C00), (-0.0, 0x8000)]
+    for x, h in cases:
+        assert orc.f32_to_f16(x) == h, (x, hex(h))
+
+
+def test_f32_to_f16_matches_numpy_random(orc):
+    rng = np.random.default_rng(5)
+    bits = rng.integers(0, 2 ** 32, 20000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[np.isfinite(x)]
+    # concentrate on the half range, subnormals and rounding ties too
+    extra = (rng.standard_normal(20000) * np.exp2(rng.integers(-26, 17, 20000))).astype(np.float32)
+    ties = (np.arange(-3000, 3000) * 2.0 ** -11 + 2.0 ** -12).astype(np.float32)
+    for arr in (x, extra, ties):
+        want = arr.astype(np.float16).view(np.uint16)
+        got = np.array([orc.f32_to_f16(float(v)) for v in arr], np.uint16)
+        assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------- quantize_q8
+
+def numpy_quantize_q8(x):
+    """Vectorised restatement used only to cross-check the C oracle."""
+    n = x.shape[0]
+    nb = (n + 31) // 32
+    pad = np.zeros(nb * 32, np.float32)
+    pad[:n] = x
+    blocks = pad.reshape(nb, 32)
+    amax = np.abs(blocks).max(axis=1)
+    scale = (amax / np.float32(127.0)).astype(np.float32)
+    inv = np.where(scale >= np.finfo(np.float32).tiny, np.float32(1.0) / np.where(scale > 0, scale, 1),
+                   0).astype(np.float32)
+    q = np.rint((blocks * inv[:, None]).astype(np.float32))
+    q = np.clip(q, -127, 127).astype(np.int8).reshape(-1)
+    q[n:] = 0
+    return scale, q
+
+
+def test_quantize_properties(orc):
+    # tests/test_kernels.c:89-107
+    g = LcgUniform()
+    x = g.uniform(-3.0, 3.0, 100)
+    s, d, q = orc.quantize_q8(x)
+    d, q = d[0], q[0]
+    assert s == 0
+    back = d[np.arange(100) // 32] * q[:100].astype(np.float32)
+    assert np.all(np.abs(back - x) <= d[np.arange(100) // 32] * 0.5 + 1e-6)
+    assert np.all(np.abs(q) <= 127)
+    assert np.all(q[100:] == 0)
+    s, d, q = orc.quantize_q8(np.zeros(32, np.float32))
+    assert s == 0 and d[0, 0] == 0 and np.all(q == 0)
+    for bad in (np.inf, -np.inf, np.nan):
+        z = np.zeros(32, np.float32)
+        z[3] = bad
+        assert orc.quantize_q8(z)[0] == -1
+
+
+@pytest.mark.parametrize("spread", [50.0, 1e-30, 1e30, 1e-37, 1e-39, 3.0])
+def test_quantize_matches_numpy(orc, spread):
+    g = LcgUniform(77)
+    for n in (1, 31, 32, 33, 100, 896, 4864 + 7):
+        x = g.uniform(-spread, spread, n)
+        x[::33] = 0.0
+        s, d, q = orc.quantize_q8(x)
+        wd, wq = numpy_quantize_q8(x)
+        assert s == 0
+        assert np.array_equal(f32_bits(d[0]), f32_bits(wd))
+        assert np.array_equal(q[0], wq)
+
+
+def test_quantize_matches_reference(orc, ref):
+    g = LcgUniform(9)
+    for trial in range(200):
+        n = 1 + int(g.next(1)[0] % (64 * 32 + 7))
+        spread = [1e-30, 1e30, 1e-37, 1e-39, 50.0, 7.0][trial % 6]
+        x = g.uniform(-spread, spread, n)
+        s, d, q = orc.quantize_q8(x)
+        for avx2 in (False, True):
+            rs, rd, rq = ref.quantize_q8(x, avx2=avx2)
+            assert rs == s
+            assert np.array_equal(f32_bits(d[0]), f32_bits(rd)) and np.array_equal(q[0], rq)
+    for at in (0, 7, 31, 40, 66):  # tests/test_kernels.c:400-410
+        x = np.ones(67, np.float32)
+        x[at] = np.nan if at % 2 else np.inf
+        assert orc.quantize_q8(x)[0] == -1 and ref.quantize_q8(x)[0] == -1
+
+
+# ---------------------------------------------------------------- dot contract
+
+def random_q8_weights(g, nb, extremes=False):
+    """tests/test_kernels.c:37-49: scales U(0, 0.05), q uniform in [-127, 127]
+    (plus -128/127 at every 7th lane when extremes)."""
+    w = np.zeros((nb, Q8B), np.uint8)
+    scales = g.uniform(0.0, 0.05, nb)
+    q = (g.next(nb * 32) % np.uint64(255)).astype(np.int64) - 127
+    q = q.reshape(nb, 32)
+    if extremes:
+        j = np.arange(32)
+        q[:, j % 7 == 0] = np.where(j[j % 7 == 0] % 2 == 1, -128, 127)
+    w[:, :4] = scales.view(np.uint8).reshape(nb, 4)
+    w[:, 4:] = q.astype(np.int8).view(np.uint8)
+    return w.reshape(-1)
+
+
+def exact_dot(w, xd, xq, nb, q5, orc):
+    """float64 value of sum_b wscale*xscale*sum_j wq*xq, and the exact integer lanes."""
+    tot = 0.0
+    lanes = []
+    for b in range(nb):
+        if q5:
+            blk = w[b * Q5B:(b + 1) * Q5B]
+            ws = np.frombuffer(blk[:2].tobytes(), np.float16)[0].astype(np.float64)
+            wq = unpack_q5_numpy(blk)
+        else:
+            blk = w[b * Q8B:(b + 1) * Q8B]
+            ws = float(np.frombuffer(blk[:4].tobytes(), np.float32)[0])
+            wq = blk[4:].view(np.int8).astype(np.int64)
+        prods = wq * xq[b * 32:(b + 1) * 32].astype(np.int64)
+        lanes.append(prods.reshape(8, 4).sum(axis=1))
+        tot += ws * float(xd[b]) * float(prods.sum())
+    return tot, np.array(lanes)
+
+
+def unpack_q5_numpy(blk):
+    high = int.from_bytes(blk[2:6].tobytes(), "little")
+    nib = blk[6:22]
+    lo = np.concatenate([nib & 15, nib >> 4]).astype(np.int64)
+    hi = np.array([(high >> j) & 1 for j in range(32)], np.int64)
+    return (lo | (hi << 4)) - 16
+
+
+def test_dot_closed_form(orc):
+    # tests/test_kernels.c:109-127
+    g = LcgUniform(12345)
+    for nb in range(1, 65):
+        w = random_q8_weights(g, nb)
+        x = g.uniform(-2.0, 2.0, nb * 32)
+        _, xd, xq = orc.quantize_q8(x)
+        exact, _ = exact_dot(w, xd[0], xq[0], nb, False, orc)
+        got = orc.dot(w, xd[0], xq[0], nb)
+        assert abs(got - exact) <= 1e-4 * (1 + abs(exact)), nb
+
+
+def test_dot_lane_order_by_hand(orc):
+    """Builds the dot from exact integer lanes with numpy float32 scalars in
+    the contract's order; a dropped lane, a swapped reduction pair or a fused
+    multiply-add fails this on random data."""
+    g = LcgUniform(3)
+    for nb in (1, 2, 5, 28):
+        w = random_q8_weights(g, nb, extremes=True)
+        x = g.uniform(-20, 20, nb * 32)
+        _, xd, xq = orc.quantize_q8(x)
+        _, lanes = exact_dot(w, xd[0], xq[0], nb, False, orc)
+        acc = [np.float32(0)] * 8
+        for b in range(nb):
+            ws = np.frombuffer(w[b * Q8B:b * Q8B + 4].tobytes(), np.float32)[0]
+            d = np.float32(ws * xd[0][b])
+            for l in range(8):
+                acc[l] = np.float32(acc[l] + np.float32(d * np.float32(lanes[b][l])))
+        want = np.float32(np.float32(np.float32(acc[0] + acc[4]) + np.float32(acc[2] + acc[6])) +
+                          np.float32(np.float32(acc[1] + acc[5]) + np.float32(acc[3] + acc[7])))
+        assert f32_bits(orc.dot(w, xd[0], xq[0], nb)) == f32_bits(want)
+
+
+def fma_probe_inputs():
+    # tests/test_kernels.c:223-249, 531-550
+    w = np.zeros(2 * Q8B, np.uint8)
+    w[0:4] = np.array([1.0], np.float32).view(np.uint8)
+    w[Q8B:Q8B + 4] = np.array([1.0 + 1.0 / 4096], np.float32).view(np.uint8)
+    w[4], w[5] = 127, 17
+    w[Q8B + 4], w[Q8B + 5] = 127, 1
+    xq = np.zeros(64, np.int8)
+    xq[0], xq[1], xq[32], xq[33] = -32, -2, 32, 33
+    xd = np.ones(2, np.float32)
+    return w, xd, xq
+
+
+def test_fma_probe(orc):
+    w, xd, xq = fma_probe_inputs()
+    assert orc.dot(w, xd, xq, 2) == 0.0
+    assert orc.dot(w, xd, xq, 2, fast=True) == 2.0 ** -12
+
+
+def test_backend_edges(orc):
+    """tests/test_kernels.c:251-278: Q5 high planes all / none / alternating,
+    Q8 weights -128/127 against activations of -127 — checked against exact
+    integer lanes in float64."""
+    high = [0xFFFFFFFF, 0, 0xAAAAAAAA]
+    low = [0xF0, 0xFF, 0x5A]
+    w5 = np.zeros(3 * Q5B, np.uint8)
+    w8 = np.zeros(3 * Q8B, np.uint8)
+    xq = np.zeros(96, np.int8)
+    for b in range(3):
+        blk = w5[b * Q5B:(b + 1) * Q5B]
+        blk[0], blk[1] = 0x00, 0x3C
+        blk[2:6] = np.frombuffer(struct.pack("<I", high[b]), np.uint8)
+        blk[6:] = low[b]
+        w8[b * Q8B:b * Q8B + 4] = np.array([1.0], np.float32).view(np.uint8)
+        j = np.arange(32)
+        w8[b * Q8B + 4:(b + 1) * Q8B] = np.where(j % 2 == 1, -128, 127).astype(np.int8).view(np.uint8)
+        xq[b * 32:(b + 1) * 32] = np.where(b == 2, np.where(j % 3 != 0, 127, -127), -127)
+    xd = np.array([1.0, 0.5, 2.0], np.float32)
+    for q5, w in ((True, w5), (False, w8)):
+        exact, _ = exact_dot(w, xd, xq, 3, q5, orc)
+        got = orc.dot(w, xd, xq, 3, q5=q5)
+        # all partial sums here are integers times powers of two below 2^24: exact
+        assert got == exact
+
+
+def random_q5_weights(orc, g, nb, spread):
+    x = g.uniform(-spread, spread, nb * 32)
+    return orc.quantize_q5_rows(x.reshape(1, -1))
+
+
+def test_dots_match_reference(orc, ref):
+    g = LcgUniform(11)
+    for trial in range(120):
+        nb = 1 + int(g.next(1)[0] % 64)
+        q5 = trial % 2 == 1
+        ntok = 1 + int(g.next(1)[0] % 9)
+        nrows = 1 + int(g.next(1)[0] % 7)
+        if q5:
+            w = random_q5_weights(orc, g, nb * nrows, 0.5 + trial % 7)
+        else:
+            w = random_q8_weights(g, nb * nrows, extremes=trial % 3 == 0)
+        x = g.uniform(-50, 50, ntok * nb * 32).reshape(ntok, nb * 32)
+        _, xd, xq = orc.quantize_q8(x)
+        rb = nb * (Q5B if q5 else Q8B)
+        for fast in (False, True):
+            got = orc.gemm(w, rb, xd, xq, nrows, ntok, nb, q5=q5, fast=fast)
+            want = ref.gemm(w, rb, xd, xq, nrows, ntok, nb, q5=q5, variant="scalar_fast" if fast else "scalar")
+            assert np.array_equal(f32_bits(got), f32_bits(want)), (trial, fast)
+        want = ref.gemm(w, rb, xd, xq, nrows, ntok, nb, q5=q5, variant="avx2")
+        assert np.array_equal(f32_bits(orc.gemm(w, rb, xd, xq, nrows, ntok, nb, q5=q5)), f32_bits(want))
+
+
+def test_gemm_wide_repack_matches_reference(orc, ref):
+    # tests/test_kernels.c:632-670: rows over 16 KiB take the repack in the AVX2 kernel
+    g = LcgUniform(21)
+    nb, nrows, ntok = 480, 3, 9
+    for q5 in (False, True):
+        if q5:
+            w = np.concatenate([random_q5_weights(orc, g, nb, 1.0) for _ in range(nrows)])
+        else:
+            w = random_q8_weights(g, nb * nrows, extremes=True)
+        _, xd, xq = orc.quantize_q8(g.uniform(-2, 2, ntok * nb * 32).reshape(ntok, -1))
+        rb = nb * (Q5B if q5 else Q8B)
+        got = orc.gemm(w, rb, xd, xq, nrows, ntok, nb, stride=5, q5=q5)
+        want = ref.gemm(w, rb, xd, xq, nrows, ntok, nb, stride=5, q5=q5, variant="avx2")
+        assert np.array_equal(f32_bits(got), f32_bits(want))
+
+
+def test_block_sums_brute_force(orc):
+    g = LcgUniform(4)
+    for q5 in (False, True):
+        nb, nrows, ntok = 5, 3, 2
+        w = random_q5_weights(orc, g, nb * nrows, 2.0) if q5 else random_q8_weights(g, nb * nrows, True)
+        _, xd, xq = orc.quantize_q8(g.uniform(-9, 9, ntok * nb * 32).reshape(ntok, -1))
+        bb = Q5B if q5 else Q8B
+        sums = orc.block_sums(w, nb * bb, xq, nrows, ntok, nb, q5=q5)
+        for t in range(ntok):
+            for r in range(nrows):
+                for b in range(nb):
+                    blk = w[(r * nb + b) * bb:(r * nb + b + 1) * bb]
+                    wq = unpack_q5_numpy(blk) if q5 else blk[4:].view(np.int8).astype(np.int64)
+                    assert sums[t, r, b] == int((wq * xq[t, b * 32:(b + 1) * 32].astype(np.int64)).sum())
+
+
+# ---------------------------------------------------------------- offline weight rules
+
+def test_q8_weight_rule_goldens(orc):
+    """tests/goldens/convert-q8.json: SHA-256 of q8pack.c's output on the
+    bf16 pattern generator — a known-answer test of the weight rule."""
+    with open(os.path.join(GOLDEN, "convert-q8.json")) as f:
+        cases = json.load(f)["cases"]
+    for c in cases:
+        x = bf16_to_f32(bf16_patterns(c["rows"], c["cols"], c["seed"]))
+        out = orc.q8_weight_rows(x)
+        assert out.nbytes == c["bytes"]
+        if "firstRowHex" in c:
+            nb = (c["cols"] + 31) // 32
+            assert out[:nb * Q8B].tobytes().hex() == c["firstRowHex"]
+        assert hashlib.sha256(out.tobytes()).hexdigest() == c["sha256"], c
+
+
+def test_q8_weight_rule_small_cases(orc):
+    # tests/convert-quant.test.ts:75-103
+    out = orc.q8_weight_rows(np.array([[1, -2, 0.5, 4, -4]], np.float32))
+    assert np.frombuffer(out[:4].tobytes(), np.float32)[0] == np.float32(4) / np.float32(127)
+    assert list(out[4:9].view(np.int8)) == [32, -64, 16, 127, -127]
+    assert np.all(out[9:] == 0)
+    out = orc.q8_weight_rows(np.array([[-0.0, -0.0, -0.0]], np.float32))
+    assert out[:4].view(np.uint32)[0] == 0
+    assert np.all(orc.q8_weight_rows(np.zeros((1, 896), np.float32)) == 0)
+
+
+def q5_errors_float64(x, d):
+    inv = np.float32(1.0) / np.float32(d)
+    lv = np.clip(np.rint((x * inv).astype(np.float32)), -16, 15)
+    return float(((x.astype(np.float64) - lv.astype(np.float64) * float(d)) ** 2).sum())
+
+
+def test_q5_rule_is_first_minimum_of_candidates(orc):
+    """The chosen scale must be the first of the 21 f16-rounded candidates
+    with the least squared error, recomputed here in numpy."""
+    g = LcgUniform(8)
+    for trial in range(40):
+        cols = 1 + int(g.next(1)[0] % 100)
+        x = g.uniform(-3, 3, cols)
+        if trial % 5 == 0:
+            x[int(g.next(1)[0] % cols)] = -7.5
+        out = orc.quantize_q5_rows(x.reshape(1, -1))
+        for b in range((cols + 31) // 32):
+            xb = x[b * 32:(b + 1) * 32]
+            ext = xb[np.argmax(np.abs(xb))]
+            best, best_h = None, 0
+            for k in range(21):
+                div = -(np.float32(14.5) + np.float32(0.1) * np.float32(k))
+                h = np.float32(ext / div).astype(np.float16)
+                d = h.astype(np.float32)
+                if d == 0 or not np.isfinite(d):
+                    continue
+                e = q5_errors_float64(xb, d)
+                if best is None or e < best:
+                    best, best_h = e, int(h.view(np.uint16))
+            blk = out[b * Q5B:(b + 1) * Q5B]
+            assert int(blk[0]) | (int(blk[1]) << 8) == best_h
+            back = orc.dequantize_row(blk, len(xb), q5=True)
+            d = np.uint16(best_h).view(np.float16).astype(np.float32)
+            inv = np.float32(1) / d
+            lv = np.clip(np.rint((xb * inv).astype(np.float32)), -16, 15).astype(np.float32)
+            assert np.array_equal(back, (d * lv).astype(np.float32))
+
+
+def test_q5_round_trip_bound(orc):
+    # tests/test_kernels.c:71-87
+    g = LcgUniform(12345)
+    x = g.uniform(-1, 1, 100)
+    x[7] = 3.0
+    out = orc.quantize_q5_rows(x.reshape(1, -1))
+    back = orc.dequantize_row(out, 100, q5=True)
+    amax = np.where(np.arange(100) < 32, 3.0, 1.0)
+    assert np.all(np.abs(back - x) <= amax / 15.0)
+    z = orc.quantize_q5_rows(np.zeros((1, 32), np.float32))
+    assert np.all(orc.dequantize_row(z, 32, q5=True) == 0)
+
+
+def test_q5_rule_and_dequant_match_reference(orc, ref):
+    g = LcgUniform(31)
+    for trial in range(60):
+        cols = 1 + int(g.next(1)[0] % 300)
+        x = g.uniform(-(0.1 + trial), 0.1 + trial, cols)
+        mine = orc.quantize_q5_rows(x.reshape(1, -1))
+        theirs = ref.quantize_q5_row(x)
+        assert np.array_equal(mine, theirs), trial
+        assert np.array_equal(f32_bits(orc.dequantize_row(mine, cols, q5=True)),
+                              f32_bits(ref.dequantize_row(theirs, cols, q5=True)))
+        w8 = orc.q8_weight_rows(x.reshape(1, -1))
+        assert np.array_equal(f32_bits(orc.dequantize_row(w8, cols)), f32_bits(ref.dequantize_row(w8, cols)))
+
+
+# ---------------------------------------------------------------- caller glue
+
+def test_split_range_coverage(orc):
+    # tests/test_kernels.c:514-529
+    for total in range(50):
+        for count in range(1, 9):
+            prev = 0
+            covered = 0
+            for i in range(count):
+                b, e = orc.split_range(total, i, count)
+                assert b == prev and b <= e
+                covered += e - b
+                prev = e
+            assert covered == total
+
+
+def test_mat_item_bias_and_finiteness(orc):
+    g = LcgUniform(6)
+    nb, rows, ntok = 4, 5, 3
+    w = random_q8_weights(g, nb * rows)
+    _, xd, xq = orc.quantize_q8(g.uniform(-4, 4, ntok * nb * 32).reshape(ntok, -1))
+    bias = g.uniform(-1, 1, rows)
+    ok, y = orc.mat_item(w, nb * Q8B, rows, bias, xd, xq, ntok, nb)
+    base = orc.gemm(w, nb * Q8B, xd, xq, rows, ntok, nb)
+    assert ok
+    assert np.array_equal(f32_bits(y), f32_bits((base.reshape(ntok, rows) + bias).astype(np.float32).reshape(-1)))
+    w2 = w.copy()
+    w2[0:4] = np.array([np.inf], np.float32).view(np.uint8)
+    ok, _ = orc.mat_item(w2, nb * Q8B, rows, None, xd, xq, ntok, nb)
+    assert not ok
+
+
+def test_rmsnorm_sequential(orc):
+    g = LcgUniform(2)
+    x = g.uniform(-3, 3, 896)
+    w = g.uniform(0.5, 1.5, 896)
+    s, y = orc.rmsnorm(x, w, 1e-6)
+    sq = np.float32(0)
+    for v in x:
+        sq = np.float32(sq + np.float32(v * v))
+    inv = np.float32(1) / np.sqrt(np.float32(sq / np.float32(896) + np.float32(1e-6)))
+    assert s == 0
+    assert np.array_equal(f32_bits(y), f32_bits(((x * inv).astype(np.float32) * w).astype(np.float32)))

@@ -1,0 +1,159 @@
+/* smq.h - C ABI of the MI355X (gfx950) quantized matrix-product path.
+ *
+ * A drop-in for the reference's kernel seam (src/kernels.h in
+ * ktfth/smolmoe-c99): activation quantization to Q8, Q8 and Q5 weight rows
+ * against Q8 activations (dot, 4-token, 4-row and gemm variants), the fused
+ * matmul of up to four matrices sharing one input with bias and a finiteness
+ * check (src/model.c:236-310), and row dequantization for embeddings.
+ *
+ * Conventions
+ *  - Every array argument is a DEVICE pointer (hipMalloc'd or from smq_malloc)
+ *    unless its comment says "host".
+ *  - Work is enqueued on the library stream (smq_stream / smq_set_stream) and
+ *    is ordered like any other work on that stream. Functions that return a
+ *    computed value (smq_quantize_q8, smq_dot_q8, smq_dot_q5) synchronize.
+ *  - Block layouts are the reference's on-disk layouts (docs/FORMAT.md:124-150):
+ *    Q8 block = f32 LE scale + int8[32] (36 B); Q5 block = f16 LE scale + u32 LE
+ *    high-bit plane + 16 nibble bytes (22 B); value = scale * (q - 16).
+ *  - Results follow the reference's arithmetic contract (docs/FORMAT.md:152-171):
+ *    exact int32 lane sums of 4 products, per lane acc = acc + (ws*xs)*lane in
+ *    increasing block order (a single fmaf per lane in fast mode), then
+ *    ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)). Every smq_gemm_* output is bit
+ *    identical to the reference's scalar kernel, except smq_gemm_*_mfma, whose
+ *    per-block int32 sums are exact but whose f32 block order differs.
+ *  - Errors: functions return or record an smq_status (the reference's
+ *    sm_status values, src/util.h:28-37); smq_last_status / smq_last_error give
+ *    the calling thread's latest failure (src/util.h:44-47).
+ */
+#ifndef SMQ_H
+#define SMQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SMQ_QK 32u
+#define SMQ_Q8_BLOCK_BYTES 36u /* kernels.h:46 */
+#define SMQ_Q5_BLOCK_BYTES 22u /* kernels.h:47 */
+
+/* src/util.h:28-37 */
+typedef enum smq_status {
+    SMQ_OK = 0,
+    SMQ_ERR = 1,
+    SMQ_ERR_IO = 2,
+    SMQ_ERR_FORMAT = 3,
+    SMQ_ERR_RANGE = 4,
+    SMQ_ERR_NUMERIC = 5,
+    SMQ_ERR_NOMEM = 6,
+    SMQ_ERR_STATE = 7
+} smq_status;
+
+/* The calling thread's latest status and message (src/util.h:44-47). */
+smq_status smq_last_status(void);
+const char *smq_last_error(void);
+void smq_clear_error(void);
+
+/* ---- context ------------------------------------------------------------
+ * One device per process (the reference's kernel table is process-global,
+ * src/kernels.c:20-27). smq_init selects the device, checks it is gfx950 and
+ * creates the library stream. */
+smq_status smq_init(int device);
+void smq_shutdown(void);
+void *smq_stream(void);                      /* hipStream_t */
+smq_status smq_set_stream(void *hip_stream); /* NULL restores the library stream */
+smq_status smq_synchronize(void);
+/* Device name of the selected GPU, e.g. "gfx950". */
+const char *smq_device_arch(void);
+
+/* ---- backend selection (src/kernels.h:72-87) -----------------------------
+ * smq_kernels_select installs the GPU kernels behind the smq_* entry points
+ * and returns the backend name: "gfx950" (exact mul+add contract) or
+ * "gfx950-fast" (lane-wise FMA, kernels.h:9-11). force_exact ignores fast. */
+const char *smq_kernels_select(int force_exact);
+void smq_kernels_set_fast(int fast); /* kernels.h:77 */
+int smq_kernels_fast(void);          /* kernels.h:78 */
+/* kernels.h:72-73. The GPU kernels need no caller scratch: returns 0, and
+ * every smq_gemm_* accepts scratch == NULL (a non-NULL scratch is ignored). */
+size_t smq_gemm_scratch_bytes(uint32_t nb);
+/* Host-side bounds checks of every operand range against its device
+ * allocation before a launch (no reference counterpart). On by default, or
+ * off when the environment sets SMQ_CHECKS=0. */
+void smq_set_checks(int on);
+
+/* ---- activation quantizer (src/kernels.h:183-187, kernels.c:912-935) ---- */
+/* QuantizeQ8: n floats -> ceil(n/32) f32 scales d and 32*ceil(n/32) int8 q,
+ * padding zero. Synchronous. Returns 0, or -1 if any input is inf or NaN (then
+ * d and q are unspecified, as the reference's caller never reads them). */
+int smq_quantize_q8(const float *x, uint32_t n, float *d, int8_t *q);
+/* The caller's per-token loop (model.c:354-370): `rows` rows of n floats,
+ * row r at x + r*n, into d + r*nb and q + r*nb*32. Asynchronous: a non-finite
+ * input raises the sticky numeric flag read by smq_numeric_check. */
+smq_status smq_quantize_q8_rows(const float *x, uint32_t rows, uint32_t n, float *d, int8_t *q);
+
+/* ---- dot products and gemm (src/kernels.h:49-70) -------------------------
+ * Parameter lists are those of DotQ8, DotQ8x4, DotQ8R4 and GemmQ8. out is a
+ * device array; smq_dot_q8/q5 return the value (synchronous). */
+float smq_dot_q8(const unsigned char *w, const float *xd, const int8_t *xq, uint32_t nb);
+float smq_dot_q5(const unsigned char *w, const float *xd, const int8_t *xq, uint32_t nb);
+void smq_dot_q8_x4(const unsigned char *w, const float *xd, const int8_t *xq, uint32_t nb, uint32_t stride,
+                   float *out);
+void smq_dot_q5_x4(const unsigned char *w, const float *xd, const int8_t *xq, uint32_t nb, uint32_t stride,
+                   float *out);
+void smq_dot_q8_r4(const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq, uint32_t nb,
+                   float *out);
+void smq_dot_q5_r4(const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq, uint32_t nb,
+                   float *out);
+/* GemmQ8: out[t*stride + r] = dot(row r, activation t); activation t at
+ * xd + t*nb, xq + t*nb*32. Decode (ntok == 1) runs the bandwidth GEMV;
+ * ntok > 1 runs the exact LDS-tiled GEMM. Asynchronous. */
+void smq_gemm_q8(const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq, uint32_t nrows,
+                 uint32_t ntok, uint32_t nb, float *out, size_t stride, unsigned char *scratch);
+void smq_gemm_q5(const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq, uint32_t nrows,
+                 uint32_t ntok, uint32_t nb, float *out, size_t stride, unsigned char *scratch);
+/* ---- fused matmul with bias and finiteness (src/model.c:236-310) -------- */
+/* QMat (model.h:15-19): a weight matrix in device memory. dtype 1 = Q8, 2 = Q5
+ * (docs/FORMAT.md:101). */
+typedef struct smq_qmat {
+    const unsigned char *data;
+    uint32_t rows, cols, nb, dtype;
+    size_t row_bytes;
+} smq_qmat;
+/* MatItem (model.c:236-240): y[token*w->rows + row] = dot + bias[row]. */
+typedef struct smq_mat_item {
+    const smq_qmat *w; /* host pointer to the descriptor */
+    const float *bias; /* device, may be NULL */
+    float *y;          /* device */
+} smq_mat_item;
+#define SMQ_MAX_ITEMS 4
+/* Up to SMQ_MAX_ITEMS matrices with the same nb sharing one quantized input,
+ * in one launch. A non-finite output raises the sticky numeric flag.
+ * Asynchronous; SMQ_ERR_STATE if the items differ in width (model.c:298). */
+smq_status smq_matmul(const smq_mat_item *items, uint32_t n, const float *xd, const int8_t *xq, uint32_t ntok);
+/* Synchronizes, then returns SMQ_ERR_NUMERIC (and clears the flag) if any
+ * quantize or matmul since the last check saw a non-finite value. */
+smq_status smq_numeric_check(void);
+
+/* ---- dequantization (src/kernels.h:193-196, kernels.c:1044-1062) -------- */
+void smq_dequantize_q8_row(const unsigned char *w, uint32_t cols, float *out);
+void smq_dequantize_q5_row(const unsigned char *w, uint32_t cols, float *out);
+
+/* ---- device memory and timing helpers (plumbing for C hosts and tests) -- */
+void *smq_malloc(size_t bytes);
+void smq_free(void *p);
+smq_status smq_memcpy_htod(void *dst, const void *host_src, size_t bytes);
+smq_status smq_memcpy_dtoh(void *host_dst, const void *src, size_t bytes);
+smq_status smq_memcpy_dtod(void *dst, const void *src, size_t bytes);
+smq_status smq_memset(void *dst, int value, size_t bytes);
+/* Records a start event on the library stream. */
+smq_status smq_timer_start(void);
+/* Records a stop event, waits for it, returns milliseconds since start (<0 on error). */
+double smq_timer_stop(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -37,7 +37,7 @@ def build():
     targets = ["all"]
     if os.path.isdir("/root/reference/src"):
         targets.append("ref")
-    subprocess.run(["make", "-s", "-C", HERE] + targets, check=True)
+    subprocess.run(["make", "-s", "-B", "-C", HERE] + targets, check=True)
 
 
 class Oracle:

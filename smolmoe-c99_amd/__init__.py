@@ -1,0 +1,324 @@
+"""Python host mirror of the gfx950 quantized matrix-product path.
+
+Binds include/smq.h (libsmq_gfx950.so, built in this directory by build.py)
+with ctypes and mirrors the reference's kernel seam by name and meaning
+(src/kernels.h:49-87, 183-196 and the matmul glue of src/model.c:236-310):
+``kernels_select``, ``kernels_set_fast``, ``quantize_q8``, ``dot_q8``,
+``dot_q8_x4``, ``dot_q8_r4``, ``gemm_q8``, ``gemm_q5``, ``matmul``, ...
+
+Array arguments are ``DeviceBuffer`` objects (device memory owned by the
+library). There is no CPU fallback: importing works anywhere, but every call
+needs the compiled library and a gfx950 GPU and raises ``SmqError``
+otherwise.
+
+The directory name is not a Python identifier; import it with
+``importlib.import_module("smolmoe-c99_amd")``.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsmq_gfx950.so")
+QK = 32
+Q8_BLOCK_BYTES = 36
+Q5_BLOCK_BYTES = 22
+DTYPE_Q8, DTYPE_Q5 = 1, 2
+
+# src/util.h:28-37
+STATUS = {0: "SM_OK", 1: "SM_ERR", 2: "SM_ERR_IO", 3: "SM_ERR_FORMAT", 4: "SM_ERR_RANGE", 5: "SM_ERR_NUMERIC",
+          6: "SM_ERR_NOMEM", 7: "SM_ERR_STATE"}
+SM_ERR_NUMERIC = 5
+
+
+class SmqError(RuntimeError):
+    def __init__(self, status, message):
+        super().__init__(f"{STATUS.get(status, status)}: {message}")
+        self.status = status
+
+
+_vp = ctypes.c_void_p
+_u32 = ctypes.c_uint32
+_sz = ctypes.c_size_t
+
+
+class _QMat(ctypes.Structure):
+    _fields_ = [("data", _vp), ("rows", _u32), ("cols", _u32), ("nb", _u32), ("dtype", _u32), ("row_bytes", _sz)]
+
+
+class _MatItem(ctypes.Structure):
+    _fields_ = [("w", ctypes.POINTER(_QMat)), ("bias", _vp), ("y", _vp)]
+
+
+_SIGS = {
+    "smq_last_status": (ctypes.c_int, []),
+    "smq_last_error": (ctypes.c_char_p, []),
+    "smq_clear_error": (None, []),
+    "smq_init": (ctypes.c_int, [ctypes.c_int]),
+    "smq_shutdown": (None, []),
+    "smq_stream": (_vp, []),
+    "smq_set_stream": (ctypes.c_int, [_vp]),
+    "smq_synchronize": (ctypes.c_int, []),
+    "smq_device_arch": (ctypes.c_char_p, []),
+    "smq_kernels_select": (ctypes.c_char_p, [ctypes.c_int]),
+    "smq_kernels_set_fast": (None, [ctypes.c_int]),
+    "smq_kernels_fast": (ctypes.c_int, []),
+    "smq_gemm_scratch_bytes": (_sz, [_u32]),
+    "smq_set_checks": (None, [ctypes.c_int]),
+    "smq_quantize_q8": (ctypes.c_int, [_vp, _u32, _vp, _vp]),
+    "smq_quantize_q8_rows": (ctypes.c_int, [_vp, _u32, _u32, _vp, _vp]),
+    "smq_dot_q8": (ctypes.c_float, [_vp, _vp, _vp, _u32]),
+    "smq_dot_q5": (ctypes.c_float, [_vp, _vp, _vp, _u32]),
+    "smq_dot_q8_x4": (None, [_vp, _vp, _vp, _u32, _u32, _vp]),
+    "smq_dot_q5_x4": (None, [_vp, _vp, _vp, _u32, _u32, _vp]),
+    "smq_dot_q8_r4": (None, [_vp, _sz, _vp, _vp, _u32, _vp]),
+    "smq_dot_q5_r4": (None, [_vp, _sz, _vp, _vp, _u32, _vp]),
+    "smq_gemm_q8": (None, [_vp, _sz, _vp, _vp, _u32, _u32, _u32, _vp, _sz, _vp]),
+    "smq_gemm_q5": (None, [_vp, _sz, _vp, _vp, _u32, _u32, _u32, _vp, _sz, _vp]),
+    "smq_matmul": (ctypes.c_int, [ctypes.POINTER(_MatItem), _u32, _vp, _vp, _u32]),
+    "smq_numeric_check": (ctypes.c_int, []),
+    "smq_dequantize_q8_row": (None, [_vp, _u32, _vp]),
+    "smq_dequantize_q5_row": (None, [_vp, _u32, _vp]),
+    "smq_malloc": (_vp, [_sz]),
+    "smq_free": (None, [_vp]),
+    "smq_memcpy_htod": (ctypes.c_int, [_vp, _vp, _sz]),
+    "smq_memcpy_dtoh": (ctypes.c_int, [_vp, _vp, _sz]),
+    "smq_memcpy_dtod": (ctypes.c_int, [_vp, _vp, _sz]),
+    "smq_memset": (ctypes.c_int, [_vp, ctypes.c_int, _sz]),
+    "smq_timer_start": (ctypes.c_int, []),
+    "smq_timer_stop": (ctypes.c_double, []),
+}
+
+_lib = None
+
+
+def load():
+    """Loads libsmq_gfx950.so; raises if it was not built (no fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise SmqError(7, f"{LIB_PATH} is missing: run __graft_entry__.build() (hipcc, gfx950)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def exported_symbols():
+    return sorted(_SIGS)
+
+
+def _check(status=None):
+    lib = load()
+    st = lib.smq_last_status() if status is None else status
+    if st != 0:
+        msg = lib.smq_last_error().decode()
+        lib.smq_clear_error()
+        raise SmqError(st, msg)
+
+
+def init(device=0):
+    lib = load()
+    _check(lib.smq_init(device))
+    return lib.smq_device_arch().decode()
+
+
+def shutdown():
+    load().smq_shutdown()
+
+
+def synchronize():
+    _check(load().smq_synchronize())
+
+
+def set_checks(on):
+    load().smq_set_checks(int(bool(on)))
+
+
+class DeviceBuffer:
+    """Device memory from smq_malloc, with numpy upload/download."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        self.ptr = load().smq_malloc(max(1, self.nbytes))
+        if not self.ptr:
+            _check()
+            raise SmqError(6, "smq_malloc returned NULL")
+
+    @classmethod
+    def from_array(cls, arr):
+        arr = np.ascontiguousarray(arr)
+        buf = cls(arr.nbytes)
+        buf.upload(arr)
+        return buf
+
+    def upload(self, arr, offset=0):
+        arr = np.ascontiguousarray(arr)
+        if offset + arr.nbytes > self.nbytes:
+            raise ValueError("upload exceeds buffer")
+        _check(load().smq_memcpy_htod(self.ptr + offset, arr.ctypes.data, arr.nbytes))
+
+    def download(self, dtype, count=None, offset=0):
+        dtype = np.dtype(dtype)
+        count = (self.nbytes - offset) // dtype.itemsize if count is None else count
+        out = np.empty(count, dtype)
+        if count:
+            _check(load().smq_memcpy_dtoh(out.ctypes.data, self.ptr + offset, out.nbytes))
+        return out
+
+    def fill(self, value=0):
+        _check(load().smq_memset(self.ptr, value, self.nbytes))
+
+    def at(self, offset):
+        return self.ptr + offset
+
+    def free(self):
+        if self.ptr:
+            load().smq_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def _p(x, offset=0):
+    if x is None:
+        return None
+    if isinstance(x, DeviceBuffer):
+        return x.ptr + offset
+    return int(x) + offset
+
+
+# ---- src/kernels.h:72-87
+def kernels_select(force_exact=False):
+    name = load().smq_kernels_select(int(bool(force_exact))).decode()
+    _check()
+    return name
+
+
+def kernels_set_fast(fast):
+    load().smq_kernels_set_fast(int(bool(fast)))
+
+
+def kernels_fast():
+    return bool(load().smq_kernels_fast())
+
+
+def gemm_scratch_bytes(nb):
+    return load().smq_gemm_scratch_bytes(nb)
+
+
+# ---- src/kernels.h:183-187
+def quantize_q8(x, n, d, q):
+    """QuantizeQ8 on device buffers: returns 0, or -1 for a non-finite input."""
+    r = load().smq_quantize_q8(_p(x), n, _p(d), _p(q))
+    if r != 0 and load().smq_last_status() != 0:
+        _check()
+    return r
+
+
+def quantize_q8_rows(x, rows, n, d, q):
+    _check(load().smq_quantize_q8_rows(_p(x), rows, n, _p(d), _p(q)))
+
+
+# ---- src/kernels.h:49-70
+def dot_q8(w, xd, xq, nb):
+    v = load().smq_dot_q8(_p(w), _p(xd), _p(xq), nb)
+    _check()
+    return v
+
+
+def dot_q5(w, xd, xq, nb):
+    v = load().smq_dot_q5(_p(w), _p(xd), _p(xq), nb)
+    _check()
+    return v
+
+
+def dot_q8_x4(w, xd, xq, nb, stride, out):
+    load().smq_dot_q8_x4(_p(w), _p(xd), _p(xq), nb, stride, _p(out))
+    _check()
+
+
+def dot_q5_x4(w, xd, xq, nb, stride, out):
+    load().smq_dot_q5_x4(_p(w), _p(xd), _p(xq), nb, stride, _p(out))
+    _check()
+
+
+def dot_q8_r4(w, row_bytes, xd, xq, nb, out):
+    load().smq_dot_q8_r4(_p(w), row_bytes, _p(xd), _p(xq), nb, _p(out))
+    _check()
+
+
+def dot_q5_r4(w, row_bytes, xd, xq, nb, out):
+    load().smq_dot_q5_r4(_p(w), row_bytes, _p(xd), _p(xq), nb, _p(out))
+    _check()
+
+
+def gemm_q8(w, row_bytes, xd, xq, nrows, ntok, nb, out, stride, scratch=None):
+    load().smq_gemm_q8(_p(w), row_bytes, _p(xd), _p(xq), nrows, ntok, nb, _p(out), stride, _p(scratch))
+    _check()
+
+
+def gemm_q5(w, row_bytes, xd, xq, nrows, ntok, nb, out, stride, scratch=None):
+    load().smq_gemm_q5(_p(w), row_bytes, _p(xd), _p(xq), nrows, ntok, nb, _p(out), stride, _p(scratch))
+    _check()
+
+
+# ---- src/model.c:236-310
+class QMat:
+    """model.h:15-19: a quantized matrix in device memory."""
+
+    def __init__(self, data, rows, cols, dtype=DTYPE_Q8, offset=0):
+        self.buf = data
+        self.offset = offset
+        self.rows, self.cols, self.dtype = rows, cols, dtype
+        self.nb = (cols + QK - 1) // QK
+        self.row_bytes = self.nb * (Q5_BLOCK_BYTES if dtype == DTYPE_Q5 else Q8_BLOCK_BYTES)
+
+    def _c(self):
+        return _QMat(_p(self.buf, self.offset), self.rows, self.cols, self.nb, self.dtype, self.row_bytes)
+
+
+def matmul(items, xd, xq, ntok):
+    """items: sequence of (QMat, bias DeviceBuffer or None, y DeviceBuffer)."""
+    cm = [w._c() for w, _, _ in items]
+    arr = (_MatItem * len(items))()
+    for i, (w, bias, y) in enumerate(items):
+        arr[i].w = ctypes.pointer(cm[i])
+        arr[i].bias = _p(bias)
+        arr[i].y = _p(y)
+    _check(load().smq_matmul(arr, len(items), _p(xd), _p(xq), ntok))
+
+
+def numeric_check():
+    """Raises SmqError(SM_ERR_NUMERIC) if a non-finite value was seen."""
+    _check(load().smq_numeric_check())
+
+
+# ---- src/kernels.h:193-196
+def dequantize_q8_row(w, cols, out):
+    load().smq_dequantize_q8_row(_p(w), cols, _p(out))
+    _check()
+
+
+def dequantize_q5_row(w, cols, out):
+    load().smq_dequantize_q5_row(_p(w), cols, _p(out))
+    _check()
+
+
+# ---- timing
+def timer_start():
+    _check(load().smq_timer_start())
+
+
+def timer_stop():
+    ms = load().smq_timer_stop()
+    _check()
+    return ms

@@ -1,0 +1,52 @@
+"""Builds libsmq_gfx950.so in place (hipcc, gfx950 only).
+
+Flags that the arithmetic contract depends on:
+  -ffp-contract=off                        no a*b+c fused into an FMA
+  -fhip-fp32-correctly-rounded-divide-sqrt correctly rounded amax/127, 1/scale
+  -fno-gpu-flush-denormals-to-zero         f32 denormals kept (tiny scales)
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+                                           no packed f32 math in device code
+"""
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB = os.path.join(HERE, "libsmq_gfx950.so")
+SOURCES = [os.path.join(HERE, "csrc", "smq_kernels.hip"), os.path.join(HERE, "csrc", "smq_api.cpp")]
+HEADERS = [os.path.join(HERE, "csrc", "smq_internal.h"), os.path.join(ROOT, "include", "smq.h")]
+
+FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-ffp-contract=off", "-fno-fast-math", "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-fno-gpu-flush-denormals-to-zero",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function",
+]
+
+
+def hipcc():
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
+        if cand and (os.path.isabs(cand) and os.path.exists(cand) or not os.path.isabs(cand)):
+            return cand
+    return "hipcc"
+
+
+def build(verbose=False):
+    cmd = [hipcc()] + FLAGS + ["-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc"),
+                               "-o", LIB + ".tmp"] + SOURCES
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    out = "\n".join(line for line in (res.stdout + res.stderr).splitlines()
+                    if "packed-fp32-ops" not in line)  # host pass does not know the feature: harmless
+    if res.returncode != 0:
+        sys.stderr.write(out + "\n")
+        raise RuntimeError("hipcc failed building libsmq_gfx950.so")
+    if verbose and out.strip():
+        sys.stderr.write(out + "\n")
+    os.replace(LIB + ".tmp", LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,432 @@
+/* C ABI of the gfx950 quantized matrix-product path (include/smq.h).
+ *
+ * Host side of the drop-in: validates shapes and buffer extents before any
+ * launch (a kernel must never be handed a grid or a pointer range it does not
+ * fit), maps the reference's entry points (src/kernels.h:49-87, 183-196;
+ * src/model.c:236-310) to launches on one stream, and keeps the reference's
+ * error model: a status code plus a thread-local message (src/util.c:24-61).
+ */
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+#include "smq.h"
+#include "smq_internal.h"
+
+namespace {
+
+struct Context {
+    bool ready = false;
+    int device = -1;
+    hipStream_t own = nullptr;
+    hipStream_t cur = nullptr;
+    int *flag = nullptr;    /* sticky numeric fault (quantize rows, matmul) */
+    int *qflag = nullptr;   /* per-call fault of the synchronous quantizer */
+    float *scalar = nullptr;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    int fast = 0;
+    int checks = 1;
+    char arch[64] = {0};
+    char backend[80] = {0};
+};
+
+Context g;
+thread_local smq_status t_status = SMQ_OK;
+thread_local char t_message[1024];
+
+smq_status set_status(smq_status s, const char *fmt, ...) {
+    t_status = s;
+    if (s == SMQ_OK) {
+        t_message[0] = 0;
+        return s;
+    }
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(t_message, sizeof(t_message), fmt, ap);
+    va_end(ap);
+    return s;
+}
+
+bool hip_ok(hipError_t e, const char *what) {
+    if (e == hipSuccess) return true;
+    set_status(e == hipErrorOutOfMemory ? SMQ_ERR_NOMEM : SMQ_ERR_STATE, "%s: %s", what, hipGetErrorString(e));
+    return false;
+}
+
+bool ready() {
+    if (g.ready) return true;
+    set_status(SMQ_ERR_STATE, "smq_init has not been called");
+    return false;
+}
+
+/* The byte range [p, p + bytes) must lie inside one device allocation. */
+bool extent_ok(const void *p, size_t bytes, const char *what) {
+    if (!bytes) return true;
+    if (!p) {
+        set_status(SMQ_ERR_RANGE, "%s is NULL", what);
+        return false;
+    }
+    if (!g.checks) return true;
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p) != hipSuccess) {
+        (void)hipGetLastError();
+        set_status(SMQ_ERR_RANGE, "%s is not a device allocation", what);
+        return false;
+    }
+    const uintptr_t b = (uintptr_t)base, q = (uintptr_t)p;
+    if (q < b || q - b > size || bytes > size - (q - b)) {
+        set_status(SMQ_ERR_RANGE, "%s: %zu bytes at offset %zu exceed its allocation of %zu bytes", what, bytes,
+                   (size_t)(q - b), size);
+        return false;
+    }
+    return true;
+}
+
+uint32_t block_bytes(bool q5) { return q5 ? smq::Q5_BYTES : smq::Q8_BYTES; }
+
+/* Validates one weight matrix and the activations of a launch. */
+bool check_operands(const unsigned char *w, size_t row_bytes, uint32_t nrows, uint32_t nb, bool q5, const float *xd,
+                    const int8_t *xq, uint32_t ntok, uint32_t xstride, const float *y, size_t y_stride,
+                    const char *who) {
+    if (!nrows || !ntok) return true;
+    if (!nb) {
+        set_status(SMQ_ERR_RANGE, "%s: nb is 0", who);
+        return false;
+    }
+    const size_t row_need = (size_t)nb * block_bytes(q5);
+    if (row_bytes < row_need) {
+        set_status(SMQ_ERR_RANGE, "%s: row_bytes %zu < nb*%u", who, row_bytes, block_bytes(q5));
+        return false;
+    }
+    if (xstride < nb && ntok > 1) {
+        set_status(SMQ_ERR_RANGE, "%s: activation stride %u < nb %u", who, xstride, nb);
+        return false;
+    }
+    if (y_stride < nrows && ntok > 1) {
+        set_status(SMQ_ERR_RANGE, "%s: output stride %zu < rows %u", who, y_stride, nrows);
+        return false;
+    }
+    const size_t acts = (size_t)(ntok - 1) * xstride + nb;
+    return extent_ok(w, (size_t)(nrows - 1) * row_bytes + row_need, "weights") &&
+           extent_ok(xd, acts * sizeof(float), "activation scales") && extent_ok(xq, acts * smq::QK, "activations") &&
+           extent_ok(y, ((size_t)(ntok - 1) * y_stride + nrows) * sizeof(float), "output");
+}
+
+smq::MatArgs one_item(const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq, uint32_t nrows,
+                      uint32_t ntok, uint32_t nb, uint32_t xstride, float *out, size_t stride) {
+    smq::MatArgs a;
+    memset(&a, 0, sizeof(a));
+    a.item[0].w = w;
+    a.item[0].row_bytes = row_bytes;
+    a.item[0].y = out;
+    a.item[0].y_stride = stride;
+    a.item[0].rows = nrows;
+    a.nitems = 1;
+    a.xd = xd;
+    a.xq = xq;
+    a.nb = nb;
+    a.ntok = ntok;
+    a.xstride = xstride;
+    return a;
+}
+
+void gemm_impl(bool q5, const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq, uint32_t nrows,
+               uint32_t ntok, uint32_t nb, uint32_t xstride, float *out, size_t stride, const char *who) {
+    if (!ready()) return;
+    if (!nrows || !ntok) return;
+    if (!check_operands(w, row_bytes, nrows, nb, q5, xd, xq, ntok, xstride, out, stride, who)) return;
+    hip_ok(smq::launch_matmul(one_item(w, row_bytes, xd, xq, nrows, ntok, nb, xstride, out, stride), q5, g.fast != 0,
+                              g.cur),
+           who);
+}
+
+float dot_impl(bool q5, const unsigned char *w, const float *xd, const int8_t *xq, uint32_t nb) {
+    if (!ready()) return 0.0f;
+    gemm_impl(q5, w, (size_t)nb * block_bytes(q5), xd, xq, 1, 1, nb, nb, g.scalar, 1, q5 ? "dot_q5" : "dot_q8");
+    if (t_status != SMQ_OK) return 0.0f;
+    float v = 0.0f;
+    if (!hip_ok(hipMemcpyAsync(&v, g.scalar, sizeof(v), hipMemcpyDeviceToHost, g.cur), "dot") ||
+        !hip_ok(hipStreamSynchronize(g.cur), "dot"))
+        return 0.0f;
+    return v;
+}
+
+}  // namespace
+
+extern "C" {
+
+smq_status smq_last_status(void) { return t_status; }
+const char *smq_last_error(void) { return t_message; }
+void smq_clear_error(void) { set_status(SMQ_OK, ""); }
+
+smq_status smq_init(int device) {
+    if (g.ready) {
+        if (device == g.device) return SMQ_OK;
+        return set_status(SMQ_ERR_STATE, "already initialised on device %d", g.device);
+    }
+    int count = 0;
+    if (!hip_ok(hipGetDeviceCount(&count), "hipGetDeviceCount")) return t_status;
+    if (device < 0 || device >= count) return set_status(SMQ_ERR_RANGE, "device %d of %d", device, count);
+    if (!hip_ok(hipSetDevice(device), "hipSetDevice")) return t_status;
+    hipDeviceProp_t prop;
+    if (!hip_ok(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties")) return t_status;
+    snprintf(g.arch, sizeof(g.arch), "%s", prop.gcnArchName);
+    char *colon = strchr(g.arch, ':');
+    if (colon) *colon = 0;
+    if (strcmp(g.arch, "gfx950") != 0)
+        return set_status(SMQ_ERR_STATE, "device %d is %s; this library is built for gfx950", device, g.arch);
+    /* Default priority only: streams of other priorities are not used here. */
+    if (!hip_ok(hipStreamCreateWithFlags(&g.own, hipStreamNonBlocking), "hipStreamCreate")) return t_status;
+    void *p = nullptr;
+    if (!hip_ok(hipMalloc(&p, 256), "hipMalloc")) return t_status;
+    g.flag = (int *)p;
+    g.qflag = (int *)p + 16;
+    g.scalar = (float *)p + 32;
+    if (!hip_ok(hipMemset(p, 0, 256), "hipMemset")) return t_status;
+    if (!hip_ok(hipEventCreate(&g.t0), "hipEventCreate") || !hip_ok(hipEventCreate(&g.t1), "hipEventCreate"))
+        return t_status;
+    g.cur = g.own;
+    g.device = device;
+    const char *env = getenv("SMQ_CHECKS");
+    g.checks = !(env && !strcmp(env, "0"));
+    g.ready = true;
+    return set_status(SMQ_OK, "");
+}
+
+void smq_shutdown(void) {
+    if (!g.ready) return;
+    (void)hipStreamSynchronize(g.cur);
+    (void)hipEventDestroy(g.t0);
+    (void)hipEventDestroy(g.t1);
+    (void)hipFree(g.flag);
+    (void)hipStreamDestroy(g.own);
+    g = Context();
+}
+
+void *smq_stream(void) { return g.cur; }
+
+smq_status smq_set_stream(void *s) {
+    if (!ready()) return t_status;
+    g.cur = s ? (hipStream_t)s : g.own;
+    return SMQ_OK;
+}
+
+smq_status smq_synchronize(void) {
+    if (!ready()) return t_status;
+    return hip_ok(hipStreamSynchronize(g.cur), "hipStreamSynchronize") ? SMQ_OK : t_status;
+}
+
+const char *smq_device_arch(void) { return g.ready ? g.arch : ""; }
+
+const char *smq_kernels_select(int force_exact) {
+    if (!g.ready && smq_init(0) != SMQ_OK) return "none";
+    if (force_exact) g.fast = 0;
+    snprintf(g.backend, sizeof(g.backend), "%s%s", g.arch, g.fast ? "-fast" : "");
+    return g.backend;
+}
+
+void smq_kernels_set_fast(int fast) { g.fast = fast ? 1 : 0; }
+int smq_kernels_fast(void) { return g.fast; }
+size_t smq_gemm_scratch_bytes(uint32_t nb) {
+    (void)nb;
+    return 0;
+}
+
+/* Bounds checking of every operand range against its allocation (on by
+ * default; SMQ_CHECKS=0 or smq_set_checks(0) turns it off for timing). */
+void smq_set_checks(int on) { g.checks = on ? 1 : 0; }
+
+int smq_quantize_q8(const float *x, uint32_t n, float *d, int8_t *q) {
+    if (!ready()) return -1;
+    const uint32_t nb = (n + smq::QK - 1) / smq::QK;
+    if (!n) return 0;
+    if (!extent_ok(x, (size_t)n * 4, "x") || !extent_ok(d, (size_t)nb * 4, "d") ||
+        !extent_ok(q, (size_t)nb * smq::QK, "q"))
+        return -1;
+    int bad = 0;
+    if (!hip_ok(hipMemsetAsync(g.qflag, 0, sizeof(int), g.cur), "quantize_q8") ||
+        !hip_ok(smq::launch_quantize_q8(x, 1, n, d, q, g.qflag, g.cur), "quantize_q8") ||
+        !hip_ok(hipMemcpyAsync(&bad, g.qflag, sizeof(int), hipMemcpyDeviceToHost, g.cur), "quantize_q8") ||
+        !hip_ok(hipStreamSynchronize(g.cur), "quantize_q8"))
+        return -1;
+    return bad ? -1 : 0;
+}
+
+smq_status smq_quantize_q8_rows(const float *x, uint32_t rows, uint32_t n, float *d, int8_t *q) {
+    if (!ready()) return t_status;
+    const uint32_t nb = (n + smq::QK - 1) / smq::QK;
+    if (!rows || !n) return SMQ_OK;
+    if (!extent_ok(x, (size_t)rows * n * 4, "x") || !extent_ok(d, (size_t)rows * nb * 4, "d") ||
+        !extent_ok(q, (size_t)rows * nb * smq::QK, "q"))
+        return t_status;
+    return hip_ok(smq::launch_quantize_q8(x, rows, n, d, q, g.flag, g.cur), "quantize_q8_rows") ? SMQ_OK : t_status;
+}
+
+float smq_dot_q8(const unsigned char *w, const float *xd, const int8_t *xq, uint32_t nb) {
+    return dot_impl(false, w, xd, xq, nb);
+}
+float smq_dot_q5(const unsigned char *w, const float *xd, const int8_t *xq, uint32_t nb) {
+    return dot_impl(true, w, xd, xq, nb);
+}
+
+void smq_dot_q8_x4(const unsigned char *w, const float *xd, const int8_t *xq, uint32_t nb, uint32_t stride,
+                   float *out) {
+    gemm_impl(false, w, (size_t)nb * smq::Q8_BYTES, xd, xq, 1, 4, nb, stride, out, 1, "dot_q8_x4");
+}
+void smq_dot_q5_x4(const unsigned char *w, const float *xd, const int8_t *xq, uint32_t nb, uint32_t stride,
+                   float *out) {
+    gemm_impl(true, w, (size_t)nb * smq::Q5_BYTES, xd, xq, 1, 4, nb, stride, out, 1, "dot_q5_x4");
+}
+void smq_dot_q8_r4(const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq, uint32_t nb,
+                   float *out) {
+    gemm_impl(false, w, row_bytes, xd, xq, 4, 1, nb, nb, out, 4, "dot_q8_r4");
+}
+void smq_dot_q5_r4(const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq, uint32_t nb,
+                   float *out) {
+    gemm_impl(true, w, row_bytes, xd, xq, 4, 1, nb, nb, out, 4, "dot_q5_r4");
+}
+
+void smq_gemm_q8(const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq, uint32_t nrows,
+                 uint32_t ntok, uint32_t nb, float *out, size_t stride, unsigned char *scratch) {
+    (void)scratch;
+    gemm_impl(false, w, row_bytes, xd, xq, nrows, ntok, nb, nb, out, stride, "gemm_q8");
+}
+void smq_gemm_q5(const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq, uint32_t nrows,
+                 uint32_t ntok, uint32_t nb, float *out, size_t stride, unsigned char *scratch) {
+    (void)scratch;
+    gemm_impl(true, w, row_bytes, xd, xq, nrows, ntok, nb, nb, out, stride, "gemm_q5");
+}
+
+smq_status smq_matmul(const smq_mat_item *items, uint32_t n, const float *xd, const int8_t *xq, uint32_t ntok) {
+    if (!ready()) return t_status;
+    if (!items || n < 1 || n > SMQ_MAX_ITEMS) return set_status(SMQ_ERR_RANGE, "matmul: %u items", n);
+    const uint32_t nb = items[0].w ? items[0].w->nb : 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        const smq_qmat *w = items[i].w;
+        if (!w) return set_status(SMQ_ERR_RANGE, "matmul: item %u has no matrix", i);
+        if (w->nb != nb) return set_status(SMQ_ERR_STATE, "internal error: matmul inputs differ in width");
+        if (w->dtype != 1 && w->dtype != 2) return set_status(SMQ_ERR_FORMAT, "matmul: dtype %u", w->dtype);
+        if (w->nb != (w->cols + smq::QK - 1) / smq::QK)
+            return set_status(SMQ_ERR_RANGE, "matmul: nb %u does not match %u columns", w->nb, w->cols);
+        if (!check_operands(w->data, w->row_bytes, w->rows, w->nb, w->dtype == 2, xd, xq, ntok, nb, items[i].y,
+                            w->rows, "matmul") ||
+            !extent_ok(items[i].bias, items[i].bias ? (size_t)w->rows * 4 : 0, "bias"))
+            return t_status;
+    }
+    if (!ntok) return SMQ_OK;
+    /* One launch per weight format present (items keep their relative order). */
+    for (int q5 = 0; q5 < 2; ++q5) {
+        smq::MatArgs a;
+        memset(&a, 0, sizeof(a));
+        a.xd = xd;
+        a.xq = xq;
+        a.nb = nb;
+        a.ntok = ntok;
+        a.xstride = nb;
+        a.flag = g.flag;
+        for (uint32_t i = 0; i < n; ++i) {
+            const smq_qmat *w = items[i].w;
+            if ((w->dtype == 2) != (q5 == 1) || !w->rows) continue;
+            smq::Item &it = a.item[a.nitems++];
+            it.w = w->data;
+            it.row_bytes = w->row_bytes;
+            it.bias = items[i].bias;
+            it.y = items[i].y;
+            it.y_stride = w->rows;
+            it.rows = w->rows;
+        }
+        if (a.nitems && !hip_ok(smq::launch_matmul(a, q5 == 1, g.fast != 0, g.cur), "matmul")) return t_status;
+    }
+    return SMQ_OK;
+}
+
+smq_status smq_numeric_check(void) {
+    if (!ready()) return t_status;
+    int bad = 0;
+    if (!hip_ok(hipStreamSynchronize(g.cur), "numeric_check") ||
+        !hip_ok(hipMemcpy(&bad, g.flag, sizeof(int), hipMemcpyDeviceToHost), "numeric_check"))
+        return t_status;
+    if (!bad) return SMQ_OK;
+    if (!hip_ok(hipMemset(g.flag, 0, sizeof(int)), "numeric_check")) return t_status;
+    /* the reference's message, model.c:309 */
+    return set_status(SMQ_ERR_NUMERIC, "non-finite activation; the checkpoint is outside the supported numeric range");
+}
+
+void smq_dequantize_q8_row(const unsigned char *w, uint32_t cols, float *out) {
+    if (!ready()) return;
+    const uint32_t nb = (cols + smq::QK - 1) / smq::QK;
+    if (!extent_ok(w, (size_t)nb * smq::Q8_BYTES, "w") || !extent_ok(out, (size_t)cols * 4, "out")) return;
+    hip_ok(smq::launch_dequantize_row(w, cols, out, false, g.cur), "dequantize_q8_row");
+}
+
+void smq_dequantize_q5_row(const unsigned char *w, uint32_t cols, float *out) {
+    if (!ready()) return;
+    const uint32_t nb = (cols + smq::QK - 1) / smq::QK;
+    if (!extent_ok(w, (size_t)nb * smq::Q5_BYTES, "w") || !extent_ok(out, (size_t)cols * 4, "out")) return;
+    hip_ok(smq::launch_dequantize_row(w, cols, out, true, g.cur), "dequantize_q5_row");
+}
+
+void *smq_malloc(size_t bytes) {
+    if (!ready()) return nullptr;
+    void *p = nullptr;
+    if (!hip_ok(hipMalloc(&p, bytes ? bytes : 1), "hipMalloc")) return nullptr;
+    return p;
+}
+
+void smq_free(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+smq_status smq_memcpy_htod(void *dst, const void *src, size_t bytes) {
+    if (!ready()) return t_status;
+    if (!bytes) return SMQ_OK;
+    if (!extent_ok(dst, bytes, "dst")) return t_status;
+    if (!hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g.cur), "memcpy htod") ||
+        !hip_ok(hipStreamSynchronize(g.cur), "memcpy htod"))
+        return t_status;
+    return SMQ_OK;
+}
+
+smq_status smq_memcpy_dtoh(void *dst, const void *src, size_t bytes) {
+    if (!ready()) return t_status;
+    if (!bytes) return SMQ_OK;
+    if (!extent_ok(src, bytes, "src")) return t_status;
+    if (!hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g.cur), "memcpy dtoh") ||
+        !hip_ok(hipStreamSynchronize(g.cur), "memcpy dtoh"))
+        return t_status;
+    return SMQ_OK;
+}
+
+smq_status smq_memcpy_dtod(void *dst, const void *src, size_t bytes) {
+    if (!ready()) return t_status;
+    if (!bytes) return SMQ_OK;
+    if (!extent_ok(src, bytes, "src") || !extent_ok(dst, bytes, "dst")) return t_status;
+    return hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g.cur), "memcpy dtod") ? SMQ_OK : t_status;
+}
+
+smq_status smq_memset(void *dst, int value, size_t bytes) {
+    if (!ready()) return t_status;
+    if (!bytes) return SMQ_OK;
+    if (!extent_ok(dst, bytes, "dst")) return t_status;
+    return hip_ok(hipMemsetAsync(dst, value, bytes, g.cur), "memset") ? SMQ_OK : t_status;
+}
+
+smq_status smq_timer_start(void) {
+    if (!ready()) return t_status;
+    return hip_ok(hipEventRecord(g.t0, g.cur), "timer") ? SMQ_OK : t_status;
+}
+
+double smq_timer_stop(void) {
+    if (!ready()) return -1.0;
+    float ms = 0.0f;
+    if (!hip_ok(hipEventRecord(g.t1, g.cur), "timer") || !hip_ok(hipEventSynchronize(g.t1), "timer") ||
+        !hip_ok(hipEventElapsedTime(&ms, g.t0, g.t1), "timer"))
+        return -1.0;
+    return (double)ms;
+}
+
+}  // extern "C"

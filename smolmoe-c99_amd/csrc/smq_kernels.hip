@@ -1,0 +1,604 @@
+/* gfx950 kernels of the quantized matrix-product path.
+ *
+ * Arithmetic contract (reference: src/kernels.c:36-79, docs/FORMAT.md:152-171):
+ * for weight row r and activation t, block b contributes eight exact int32 lane
+ * sums s_l (products 4l..4l+3); lane l accumulates acc_l = acc_l + d_b*float(s_l)
+ * with d_b = wscale_b * xscale_b, two roundings per step (one fmaf in fast
+ * mode), blocks in increasing order; the result is
+ * ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)). Each lane is a serial f32 chain of
+ * nb adds, so nothing below splits K across threads: parallelism comes from
+ * rows, tokens and the eight lanes, and from computing the per-block products
+ * away from the chain that adds them.
+ *
+ * Compiled with -ffp-contract=off (no fused multiply-add unless written as
+ * fmaf), correctly rounded f32 division and f32 denormals preserved.
+ */
+#include <float.h>
+
+#include "smq_internal.h"
+
+namespace smq {
+namespace {
+
+constexpr int WG = 256;
+
+typedef uint32_t u4a __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u3a __attribute__((ext_vector_type(3), aligned(4)));
+
+/* Exact int32 sum of four int8 products plus c (v_dot4_i32_i8). */
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+/* IEEE binary16 bits to float, exact for every input including subnormals
+ * (reference: src/f16.h:10-27): subnormal m * 2^-24 is exact in binary32. */
+__device__ __forceinline__ float half_to_float(uint32_t h) {
+    const uint32_t e = (h >> 10) & 31u, m = h & 1023u, sign = (h & 0x8000u) << 16;
+    if (e == 31u) return __uint_as_float(sign | 0x7f800000u | (m << 13));
+    if (e != 0u) return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
+    return __uint_as_float(__float_as_uint((float)m * 0x1p-24f) | sign);
+}
+
+/* One lane step of the contract: acc + d*f with two roundings, or fmaf. */
+template <bool FAST>
+__device__ __forceinline__ float lane_step(float acc, float d, int s) {
+    const float f = (float)s;
+    if (FAST) return __builtin_fmaf(d, f, acc);
+    const float p = d * f;
+    return acc + p;
+}
+
+/* The fixed lane reduction over eight consecutive threads (lane = tid & 7):
+ * thread 0 ends with ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)). IEEE addition is
+ * commutative, so the partner's copy of each pair sum is the same bits. */
+__device__ __forceinline__ float reduce8(float a) {
+    const float s = a + __shfl_xor(a, 4, 8);
+    const float t = s + __shfl_xor(s, 2, 8);
+    return t + __shfl_xor(t, 1, 8);
+}
+
+/* Q5 block fields (docs/FORMAT.md:124-134). */
+struct Q5Fields {
+    float scale;
+    uint32_t high;   /* bit j = bit 4 of element j */
+    uint32_t nib[4]; /* byte j: element j low nibble, element j+16 high nibble */
+};
+
+/* A pair of Q5 blocks is 44 bytes = 11 dwords: the first block's fields sit
+ * at 2-byte offsets inside the dwords, the second block's are dword aligned. */
+__device__ __forceinline__ void q5_parse_pair(const uint32_t d[11], Q5Fields &b0, Q5Fields &b1) {
+    b0.scale = half_to_float(d[0] & 0xffffu);
+    b0.high = __builtin_amdgcn_alignbit(d[1], d[0], 16);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) b0.nib[k] = __builtin_amdgcn_alignbit(d[k + 2], d[k + 1], 16);
+    b1.scale = half_to_float(d[5] >> 16);
+    b1.high = d[6];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) b1.nib[k] = d[7 + k];
+}
+
+/* Lane l's four 5-bit codes q in [0, 31] as bytes: low nibble | high bit << 4.
+ * The high bits 4l..4l+3 are spread to bit 0 of each byte by a multiply
+ * (x * 0x204081 moves bit i to bit 8i; the partial products do not overlap). */
+__device__ __forceinline__ uint32_t q5_codes(const Q5Fields &b, int l) {
+    const uint32_t nib = l < 4 ? (b.nib[l] & 0x0f0f0f0fu) : ((b.nib[l - 4] >> 4) & 0x0f0f0f0fu);
+    const uint32_t hb = (b.high >> (4 * l)) & 15u;
+    const uint32_t spread = __umul24(hb, 0x204081u) & 0x01010101u;
+    return nib | (spread << 4);
+}
+
+/* Signed weights q - 16 as int8 bytes: (q + 112) ^ 0x80 per byte, no carries. */
+__device__ __forceinline__ uint32_t q5_signed(const Q5Fields &b, int l) {
+    return (q5_codes(b, l) + 0x70707070u) ^ 0x80808080u;
+}
+
+__device__ __forceinline__ uint32_t find_item(const MatArgs &a, uint32_t tile) {
+    uint32_t it = 0;
+    if (a.nitems > 1 && tile >= a.item[1].tile_begin) it = 1;
+    if (a.nitems > 2 && tile >= a.item[2].tile_begin) it = 2;
+    if (a.nitems > 3 && tile >= a.item[3].tile_begin) it = 3;
+    return it;
+}
+
+__device__ __forceinline__ void store_out(const Item &I, int *flag, uint32_t t, uint32_t r, float v) {
+    if (I.bias) v = v + I.bias[r]; /* model.c:259-262 */
+    I.y[(size_t)t * I.y_stride + r] = v;
+    if (flag && !(fabsf(v) <= FLT_MAX)) *flag = 1;
+}
+
+/* ------------------------------------------------------------------------
+ * Decode GEMV (ntok == 1). Workgroup = RT rows x all K. K is walked in chunks
+ * of CB blocks. In each chunk every thread owns one task (one Q8 block, or
+ * one pair of Q5 blocks, of one row): it loads the block straight from HBM
+ * (prefetched one chunk ahead), and writes the eight lane products
+ * d*float(s_l) (fast mode: float(s_l) and d) into LDS. Then the RT*8 chain
+ * threads, one per (row, lane), add their CB products in block order. The
+ * serial part per thread is one add per block; the loads, dot4s and
+ * multiplies are spread over all 256 threads.
+ * LDS products: group g of four blocks holds [thread (r*8+l)][b%4], padded by
+ * four floats per group so writes from a wave fall in distinct banks.
+ * ---------------------------------------------------------------------- */
+template <bool Q5, bool FAST, int RT>
+__global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
+    constexpr int TB = Q5 ? 2 : 1;       /* blocks per task */
+    constexpr int TPR = WG / RT;         /* tasks per row per chunk */
+    constexpr int CB = TPR * TB;         /* blocks per chunk */
+    constexpr int GS = RT * 32 + 4;      /* floats per group of four blocks */
+    constexpr int NRAW = Q5 ? 11 : 9;    /* dwords per task */
+    __shared__ __attribute__((aligned(16))) float prod[2][(CB / 4) * GS];
+    __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? (CB / 4) * (RT * 4 + 4) : 4];
+    extern __shared__ __attribute__((aligned(16))) uint32_t act[];
+
+    const uint32_t nb = a.nb, tid = threadIdx.x;
+    uint32_t *act_q = act;                      /* nb*8 words of int8 x4 */
+    float *act_d = (float *)(act + nb * 8);     /* nb scales */
+    int *act_b = (int *)(act + nb * 9);         /* Q5: -16 * lane sums of x */
+
+    const Item &I = a.item[find_item(a, blockIdx.x)]; /* uniform index into the kernel arguments */
+    const uint32_t r0 = (blockIdx.x - I.tile_begin) * RT;
+
+    const uint32_t *xq32 = (const uint32_t *)a.xq;
+    for (uint32_t i = tid; i < nb * 8; i += WG) {
+        const uint32_t v = xq32[i];
+        act_q[i] = v;
+        if (Q5) act_b[i] = -16 * dot4(v, 0x01010101u, 0);
+    }
+    for (uint32_t i = tid; i < nb; i += WG) act_d[i] = a.xd[i];
+
+    const uint32_t tr = tid / TPR, ti = tid % TPR;
+    const bool row_ok = r0 + tr < I.rows;
+    const unsigned char *wrow = I.w + (size_t)(row_ok ? r0 + tr : 0) * I.row_bytes;
+    const uint32_t nchunks = (nb + CB - 1) / CB;
+
+    uint32_t raw[NRAW];
+    auto load_task = [&](uint32_t b) {
+        if (row_ok && b < nb) {
+            if (Q5) {
+                const unsigned char *p = wrow + (size_t)b * Q5_BYTES;
+                const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
+                const u3a v2 = *(const u3a *)(p + 32);
+                raw[0] = v0.x; raw[1] = v0.y; raw[2] = v0.z; raw[3] = v0.w;
+                raw[4] = v1.x; raw[5] = v1.y; raw[6] = v1.z; raw[7] = v1.w;
+                raw[8] = v2.x; raw[9] = v2.y; raw[10] = v2.z;
+            } else {
+                const unsigned char *p = wrow + (size_t)b * Q8_BYTES;
+                const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
+                raw[0] = v0.x; raw[1] = v0.y; raw[2] = v0.z; raw[3] = v0.w;
+                raw[4] = v1.x; raw[5] = v1.y; raw[6] = v1.z; raw[7] = v1.w;
+                raw[8] = *(const uint32_t *)(p + 32);
+            }
+        }
+    };
+    load_task(ti * TB);
+    __syncthreads(); /* activation staged */
+
+    float acc = 0.0f;
+    for (uint32_t c = 0; c < nchunks; ++c) {
+        const uint32_t bt = c * CB + ti * TB; /* first block of this task */
+        uint32_t cur[NRAW];
+#pragma unroll
+        for (int k = 0; k < NRAW; ++k) cur[k] = raw[k];
+        if (c + 1 < nchunks) load_task(bt + CB);
+
+        float *pb = prod[c & 1];
+        if (row_ok && bt < nb) {
+            if (Q5) {
+                Q5Fields f[2];
+                q5_parse_pair(cur, f[0], f[1]);
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const uint32_t b = bt + k, bb = ti * 2 + k;
+                    const float d = f[k].scale * act_d[b];
+                    float *dst = pb + (bb / 4) * GS + tr * 32 + (bb % 4);
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) {
+                        const int s = dot4(q5_codes(f[k], l), act_q[b * 8 + l], act_b[b * 8 + l]);
+                        dst[l * 4] = FAST ? (float)s : d * (float)s;
+                    }
+                    if (FAST) dsc[c & 1][(bb / 4) * (RT * 4 + 4) + tr * 4 + (bb % 4)] = d;
+                }
+            } else {
+                const uint32_t b = bt, bb = ti;
+                const float d = __uint_as_float(cur[0]) * act_d[b];
+                float *dst = pb + (bb / 4) * GS + tr * 32 + (bb % 4);
+#pragma unroll
+                for (int l = 0; l < 8; ++l) {
+                    const int s = dot4(cur[1 + l], act_q[b * 8 + l], 0);
+                    dst[l * 4] = FAST ? (float)s : d * (float)s;
+                }
+                if (FAST) dsc[c & 1][(bb / 4) * (RT * 4 + 4) + tr * 4 + (bb % 4)] = d;
+            }
+        }
+        __syncthreads();
+
+        if (tid < RT * 8) {
+            const uint32_t count = nb - c * CB < (uint32_t)CB ? nb - c * CB : (uint32_t)CB;
+            const float4 *pg = (const float4 *)pb + tid;
+            const float4 *dg = FAST ? (const float4 *)dsc[c & 1] + tid / 8 : nullptr;
+            uint32_t q = 0;
+            for (; q + 1 <= count / 4; ++q) {
+                const float4 v = pg[q * (GS / 4)];
+                if (FAST) {
+                    const float4 dv = dg[q * (RT + 1)];
+                    acc = __builtin_fmaf(dv.x, v.x, acc);
+                    acc = __builtin_fmaf(dv.y, v.y, acc);
+                    acc = __builtin_fmaf(dv.z, v.z, acc);
+                    acc = __builtin_fmaf(dv.w, v.w, acc);
+                } else {
+                    acc = acc + v.x;
+                    acc = acc + v.y;
+                    acc = acc + v.z;
+                    acc = acc + v.w;
+                }
+            }
+            const uint32_t rem = count - q * 4;
+            if (rem) {
+                const float4 v = pg[q * (GS / 4)];
+                if (FAST) {
+                    const float4 dv = dg[q * (RT + 1)];
+                    acc = __builtin_fmaf(dv.x, v.x, acc);
+                    if (rem > 1) acc = __builtin_fmaf(dv.y, v.y, acc);
+                    if (rem > 2) acc = __builtin_fmaf(dv.z, v.z, acc);
+                } else {
+                    acc = acc + v.x;
+                    if (rem > 1) acc = acc + v.y;
+                    if (rem > 2) acc = acc + v.z;
+                }
+            }
+        }
+    }
+
+    if (tid < RT * 8) {
+        const float v = reduce8(acc);
+        const uint32_t r = r0 + tid / 8;
+        if ((tid & 7) == 0 && r < I.rows) store_out(I, a.flag, 0, r, v);
+    }
+}
+
+/* ------------------------------------------------------------------------
+ * Exact prefill GEMM (ntok > 1). Workgroup tile = 32 rows x 16 tokens; K in
+ * chunks of 16 blocks staged in LDS (weights decoded once per block: Q5
+ * becomes signed int8 words, so the inner loop is the same for both formats).
+ * Thread (lane l, row group, token group) owns 4 rows x 4 tokens of lane l:
+ * sixteen serial chains, each step one dot4, one convert, one multiply for d,
+ * one multiply and one add. The next chunk's global loads are issued before
+ * the current chunk is computed.
+ * ---------------------------------------------------------------------- */
+constexpr int GT_R = 32, GT_T = 16, GT_CB = 16;
+constexpr int WQ_PITCH = GT_CB * 8 + 2; /* dwords; rows of a wave hit distinct banks */
+constexpr int SC_PITCH = GT_CB + 1;
+
+template <bool Q5, bool FAST>
+__global__ __launch_bounds__(WG) void k_gemm_exact(MatArgs a, uint32_t tok_tiles) {
+    __shared__ float wsl[GT_R][SC_PITCH];
+    __shared__ __attribute__((aligned(8))) uint32_t wql[GT_R][WQ_PITCH];
+    __shared__ float xdl[GT_T][SC_PITCH];
+    __shared__ __attribute__((aligned(8))) uint32_t xql[GT_T][WQ_PITCH];
+
+    const uint32_t tid = threadIdx.x, nb = a.nb;
+    /* XCD-aware order: workgroup i runs on XCD i % 8; give each XCD a
+     * contiguous range of tiles so the token tiles of one row tile share an L2. */
+    const uint32_t G = gridDim.x, xcd = blockIdx.x % 8u, k = blockIdx.x / 8u;
+    const uint32_t per = G / 8u, extra = G % 8u;
+    const uint32_t L = xcd * per + (xcd < extra ? xcd : extra) + k;
+    const uint32_t row_tile = L / tok_tiles, tok_tile = L % tok_tiles;
+
+    const Item &I = a.item[find_item(a, row_tile)];
+    const uint32_t r0 = (row_tile - I.tile_begin) * GT_R, t0 = tok_tile * GT_T;
+
+    /* staging roles */
+    const uint32_t srow = tid / 8, spart = tid % 8; /* weights: row, pair of blocks */
+    const bool srow_ok = r0 + srow < I.rows;
+    const unsigned char *wrow = I.w + (size_t)(srow_ok ? r0 + srow : 0) * I.row_bytes;
+    const uint32_t stok = tid / 16, spiece = tid % 16; /* activations */
+    const bool stok_ok = t0 + stok < a.ntok;
+    const size_t tok_base = (size_t)(stok_ok ? t0 + stok : 0) * a.xstride;
+
+    uint32_t wr[Q5 ? 11 : 18] = {};
+    u4a xr[2] = {};
+    float xs = 0.0f;
+    auto fetch = [&](uint32_t c) {
+        const uint32_t b = c * GT_CB + spart * 2;
+        if (Q5) {
+            if (srow_ok && b < nb) {
+                const unsigned char *p = wrow + (size_t)b * Q5_BYTES;
+                const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
+                const u3a v2 = *(const u3a *)(p + 32);
+                wr[0] = v0.x; wr[1] = v0.y; wr[2] = v0.z; wr[3] = v0.w;
+                wr[4] = v1.x; wr[5] = v1.y; wr[6] = v1.z; wr[7] = v1.w;
+                wr[8] = v2.x; wr[9] = v2.y; wr[10] = v2.z;
+            }
+        } else {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if (srow_ok && b + h < nb) {
+                    const unsigned char *p = wrow + (size_t)(b + h) * Q8_BYTES;
+                    const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
+                    wr[9 * h + 0] = v0.x; wr[9 * h + 1] = v0.y; wr[9 * h + 2] = v0.z; wr[9 * h + 3] = v0.w;
+                    wr[9 * h + 4] = v1.x; wr[9 * h + 5] = v1.y; wr[9 * h + 6] = v1.z; wr[9 * h + 7] = v1.w;
+                    wr[9 * h + 8] = *(const uint32_t *)(p + 32);
+                }
+            }
+        }
+        /* token stok, 16-byte pieces spiece and spiece+16 of the chunk's 512 bytes */
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t piece = spiece + 16 * h, b = c * GT_CB + piece / 2;
+            if (stok_ok && b < nb) xr[h] = *(const u4a *)(a.xq + (tok_base + c * GT_CB) * QK + piece * 16);
+        }
+        const uint32_t bx = c * GT_CB + spiece;
+        if (stok_ok && bx < nb) xs = a.xd[tok_base + bx];
+    };
+    auto stage = [&](uint32_t c) {
+        const uint32_t b = c * GT_CB + spart * 2;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t bb = spart * 2 + h;
+            const bool ok = srow_ok && b + h < nb;
+            uint32_t words[8];
+            float sc = 0.0f;
+            if (Q5) {
+                Q5Fields f[2];
+                q5_parse_pair(wr, f[0], f[1]);
+#pragma unroll
+                for (int l = 0; l < 8; ++l) words[l] = ok ? q5_signed(f[h], l) : 0u;
+                sc = ok ? f[h].scale : 0.0f;
+            } else {
+#pragma unroll
+                for (int l = 0; l < 8; ++l) words[l] = ok ? wr[9 * h + 1 + l] : 0u;
+                sc = ok ? __uint_as_float(wr[9 * h]) : 0.0f;
+            }
+            wsl[srow][bb] = sc;
+            uint2 *dst = (uint2 *)&wql[srow][bb * 8];
+#pragma unroll
+            for (int l = 0; l < 4; ++l) dst[l] = make_uint2(words[2 * l], words[2 * l + 1]);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t piece = spiece + 16 * h, b = c * GT_CB + piece / 2;
+            const bool ok = stok_ok && b < nb;
+            uint2 *dst = (uint2 *)&xql[stok][piece * 4];
+            dst[0] = ok ? make_uint2(xr[h].x, xr[h].y) : make_uint2(0u, 0u);
+            dst[1] = ok ? make_uint2(xr[h].z, xr[h].w) : make_uint2(0u, 0u);
+        }
+        const uint32_t bx = c * GT_CB + spiece;
+        xdl[stok][spiece] = (stok_ok && bx < nb) ? xs : 0.0f;
+    };
+
+    const uint32_t l = tid % 8, rg = (tid / 8) % 8, tg = tid / 64;
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+
+    const uint32_t nchunks = (nb + GT_CB - 1) / GT_CB;
+    fetch(0);
+    for (uint32_t c = 0; c < nchunks; ++c) {
+        stage(c);
+        __syncthreads();
+        if (c + 1 < nchunks) fetch(c + 1);
+        const uint32_t count = nb - c * GT_CB < (uint32_t)GT_CB ? nb - c * GT_CB : (uint32_t)GT_CB;
+        for (uint32_t bb = 0; bb < count; ++bb) {
+            float ws[4], xsc[4];
+            uint32_t w[4], x[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                ws[i] = wsl[rg * 4 + i][bb];
+                w[i] = wql[rg * 4 + i][bb * 8 + l];
+                xsc[i] = xdl[tg * 4 + i][bb];
+                x[i] = xql[tg * 4 + i][bb * 8 + l];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float d = ws[i] * xsc[j];
+                    acc[i][j] = lane_step<FAST>(acc[i][j], d, dot4(w[i], x[j], 0));
+                }
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float v = reduce8(acc[i][j]);
+            const int idx = i * 4 + j;
+            if (idx == (int)l || idx == (int)l + 8) {
+                const uint32_t r = r0 + rg * 4 + i, t = t0 + tg * 4 + j;
+                if (r < I.rows && t < a.ntok) store_out(I, a.flag, t, r, v);
+            }
+        }
+}
+
+/* ------------------------------------------------------------------------
+ * Generic path: any alignment, any width. One thread per (row, token), byte
+ * reads. Used for shapes the tiled kernels do not take (unaligned rows, odd
+ * Q5 widths, nb > MAX_FAST_NB); same contract, bit for bit.
+ * ---------------------------------------------------------------------- */
+__device__ __forceinline__ uint32_t ld_u32_bytes(const unsigned char *p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+template <bool Q5, bool FAST>
+__global__ __launch_bounds__(WG) void k_generic(MatArgs a, uint32_t total_rows) {
+    const uint64_t gi = (uint64_t)blockIdx.x * WG + threadIdx.x;
+    if (gi >= (uint64_t)total_rows * a.ntok) return;
+    const uint32_t t = (uint32_t)(gi / total_rows), fr = (uint32_t)(gi % total_rows);
+    const Item &I = a.item[find_item(a, fr)];
+    const uint32_t r = fr - I.tile_begin;
+    const unsigned char *row = I.w + (size_t)r * I.row_bytes;
+    const float *xd = a.xd + (size_t)t * a.xstride;
+    const int8_t *xq = a.xq + (size_t)t * a.xstride * QK;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (uint32_t b = 0; b < a.nb; ++b) {
+        float ws;
+        int8_t wv[32];
+        if (Q5) {
+            const unsigned char *blk = row + (size_t)b * Q5_BYTES;
+            ws = half_to_float((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+            const uint32_t high = ld_u32_bytes(blk + 2);
+            for (int j = 0; j < 16; ++j) {
+                wv[j] = (int8_t)((int)((blk[6 + j] & 15u) | (((high >> j) & 1u) << 4)) - 16);
+                wv[j + 16] = (int8_t)((int)((blk[6 + j] >> 4) | (((high >> (j + 16)) & 1u) << 4)) - 16);
+            }
+        } else {
+            const unsigned char *blk = row + (size_t)b * Q8_BYTES;
+            ws = __uint_as_float(ld_u32_bytes(blk));
+            for (int j = 0; j < 32; ++j) wv[j] = (int8_t)blk[4 + j];
+        }
+        const float d = ws * xd[b];
+        for (int l = 0; l < 8; ++l) {
+            int s = 0;
+            for (int k = 0; k < 4; ++k) s += (int)wv[4 * l + k] * (int)xq[b * QK + 4 * l + k];
+            acc[l] = lane_step<FAST>(acc[l], d, s);
+        }
+    }
+    const float p04 = acc[0] + acc[4], p15 = acc[1] + acc[5], p26 = acc[2] + acc[6], p37 = acc[3] + acc[7];
+    const float e = p04 + p26, o = p15 + p37;
+    store_out(I, a.flag, t, r, e + o);
+}
+
+/* ------------------------------------------------------------------------
+ * Activation quantizer (reference: src/kernels.c:912-935). One thread per
+ * element of the zero-padded row; a block of 32 is half a wave. amax is a
+ * max-reduction (order-free: max is exact); scale = amax / 127 (correctly
+ * rounded); inv = 1/scale when scale >= FLT_MIN, else 0; q = clamp(rint(x*inv)).
+ * ---------------------------------------------------------------------- */
+__global__ __launch_bounds__(WG) void k_quantize_q8(const float *x, uint32_t rows, uint32_t n, uint32_t nb, float *d,
+                                                    int8_t *q, int *flag) {
+    const uint64_t gi = (uint64_t)blockIdx.x * WG + threadIdx.x;
+    const uint64_t per_row = (uint64_t)nb * QK;
+    const bool in_range = gi < per_row * rows;
+    const uint32_t row = in_range ? (uint32_t)(gi / per_row) : 0u;
+    const uint32_t rem = (uint32_t)(gi % per_row), b = rem / QK, j = rem % QK;
+    const bool valid = in_range && b * QK + j < n;
+    const float v = valid ? x[(size_t)row * n + b * QK + j] : 0.0f;
+    const float av = fabsf(v);
+    int bad = valid && !(av <= FLT_MAX);
+    float m = av;
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(m, off, 32);
+        m = o > m ? o : m;
+        bad |= __shfl_xor(bad, off, 32);
+    }
+    if (!in_range) return;
+    const float scale = m / 127.0f;
+    const float inv = scale >= FLT_MIN ? 1.0f / scale : 0.0f;
+    int qv = 0;
+    if (valid) {
+        const float p = v * inv;
+        qv = (int)__builtin_rintf(p);
+        qv = qv > 127 ? 127 : (qv < -127 ? -127 : qv);
+    }
+    q[(size_t)row * per_row + rem] = (int8_t)qv;
+    if (j == 0) {
+        d[(size_t)row * nb + b] = scale;
+        if (bad && flag) *flag = 1;
+    }
+}
+
+/* Row dequantization (reference: src/kernels.c:1044-1062): scale * float(q). */
+template <bool Q5>
+__global__ __launch_bounds__(WG) void k_dequantize_row(const unsigned char *w, uint32_t cols, float *out) {
+    const uint32_t j = blockIdx.x * WG + threadIdx.x;
+    if (j >= cols) return;
+    const uint32_t b = j / QK, k = j % QK;
+    float scale;
+    int v;
+    if (Q5) {
+        const unsigned char *blk = w + (size_t)b * Q5_BYTES;
+        scale = half_to_float((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+        const uint32_t high = ld_u32_bytes(blk + 2);
+        const uint32_t lo = k < 16 ? (blk[6 + k] & 15u) : (uint32_t)(blk[6 + k - 16] >> 4);
+        v = (int)(lo | (((high >> k) & 1u) << 4)) - 16;
+    } else {
+        const unsigned char *blk = w + (size_t)b * Q8_BYTES;
+        scale = __uint_as_float(ld_u32_bytes(blk));
+        v = (int)(int8_t)blk[4 + k];
+    }
+    out[j] = scale * (float)v;
+}
+
+bool fast_layout(const MatArgs &a, bool q5) {
+    if (a.nb == 0 || a.nb > MAX_FAST_NB) return false;
+    if (((uintptr_t)a.xq | (uintptr_t)a.xd) & 3u) return false;
+    if (q5 && (a.nb & 1u)) return false;
+    for (uint32_t i = 0; i < a.nitems; ++i)
+        if ((((uintptr_t)a.item[i].w) | a.item[i].row_bytes) & 3u) return false;
+    return true;
+}
+
+template <bool Q5, bool FAST, int RT>
+hipError_t launch_gemv_rt(MatArgs a, hipStream_t s) {
+    uint32_t tiles = 0;
+    for (uint32_t i = 0; i < a.nitems; ++i) {
+        a.item[i].tile_begin = tiles;
+        tiles += (a.item[i].rows + RT - 1) / RT;
+    }
+    if (!tiles) return hipSuccess;
+    const size_t lds = (size_t)a.nb * (Q5 ? 17u : 9u) * 4u;
+    hipLaunchKernelGGL((k_gemv<Q5, FAST, RT>), dim3(tiles), dim3(WG), lds, s, a);
+    return hipGetLastError();
+}
+
+template <bool Q5, bool FAST>
+hipError_t launch_typed(MatArgs a, hipStream_t s) {
+    uint32_t total_rows = 0;
+    for (uint32_t i = 0; i < a.nitems; ++i) total_rows += a.item[i].rows;
+    if (!total_rows || !a.ntok || !a.nb) return hipSuccess;
+    if (fast_layout(a, Q5)) {
+        if (a.ntok == 1) {
+            if (total_rows <= 2048) return launch_gemv_rt<Q5, FAST, 4>(a, s);
+            if (total_rows <= 65536) return launch_gemv_rt<Q5, FAST, 8>(a, s);
+            return launch_gemv_rt<Q5, FAST, 16>(a, s);
+        }
+        uint32_t tiles = 0;
+        for (uint32_t i = 0; i < a.nitems; ++i) {
+            a.item[i].tile_begin = tiles;
+            tiles += (a.item[i].rows + GT_R - 1) / GT_R;
+        }
+        const uint32_t tok_tiles = (a.ntok + GT_T - 1) / GT_T;
+        hipLaunchKernelGGL((k_gemm_exact<Q5, FAST>), dim3(tiles * tok_tiles), dim3(WG), 0, s, a, tok_tiles);
+        return hipGetLastError();
+    }
+    uint32_t begin = 0;
+    for (uint32_t i = 0; i < a.nitems; ++i) {
+        a.item[i].tile_begin = begin;
+        begin += a.item[i].rows;
+    }
+    const uint64_t threads = (uint64_t)total_rows * a.ntok;
+    hipLaunchKernelGGL((k_generic<Q5, FAST>), dim3((uint32_t)((threads + WG - 1) / WG)), dim3(WG), 0, s, a,
+                       total_rows);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_matmul(const MatArgs &a, bool q5, bool fast, hipStream_t s) {
+    if (q5) return fast ? launch_typed<true, true>(a, s) : launch_typed<true, false>(a, s);
+    return fast ? launch_typed<false, true>(a, s) : launch_typed<false, false>(a, s);
+}
+
+hipError_t launch_quantize_q8(const float *x, uint32_t rows, uint32_t n, float *d, int8_t *q, int *flag,
+                              hipStream_t s) {
+    const uint32_t nb = (n + QK - 1) / QK;
+    const uint64_t threads = (uint64_t)rows * nb * QK;
+    if (!threads) return hipSuccess;
+    hipLaunchKernelGGL(k_quantize_q8, dim3((uint32_t)((threads + WG - 1) / WG)), dim3(WG), 0, s, x, rows, n, nb, d,
+                       q, flag);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequantize_row(const unsigned char *w, uint32_t cols, float *out, bool q5, hipStream_t s) {
+    if (!cols) return hipSuccess;
+    const dim3 grid((cols + WG - 1) / WG);
+    if (q5) hipLaunchKernelGGL(k_dequantize_row<true>, grid, dim3(WG), 0, s, w, cols, out);
+    else hipLaunchKernelGGL(k_dequantize_row<false>, grid, dim3(WG), 0, s, w, cols, out);
+    return hipGetLastError();
+}
+
+}  // namespace smq

@@ -1,0 +1,338 @@
+"""GPU parity: every entry point of the C ABI against the CPU oracle on the
+same seeded inputs. Integer and f32 results must be bit-identical (the
+contract is reproduced exactly); NaN results compare as NaN."""
+import sys
+
+import numpy as np
+import pytest
+
+from patterns import LcgUniform
+from smq_pkg import smq, synth
+
+pytestmark = pytest.mark.gpu
+
+Q8B, Q5B = 36, 22
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    arch = smq.init(0)
+    assert arch == "gfx950"
+    smq.kernels_set_fast(False)
+    assert smq.kernels_select() == "gfx950"
+    yield
+    smq.kernels_set_fast(False)
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def assert_same_f32(got, want, what=""):
+    got = np.asarray(got, np.float32)
+    want = np.asarray(want, np.float32)
+    assert got.shape == want.shape, what
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan), what
+    bad = np.nonzero(bits(got[~nan]) != bits(want[~nan]))[0]
+    assert bad.size == 0, f"{what}: {bad.size} mismatches, first at {bad[:5]}: " \
+                          f"{got[~nan][bad[:5]]} vs {want[~nan][bad[:5]]}"
+
+
+def gpu_quantize(x):
+    rows, n = x.shape
+    nb = (n + 31) // 32
+    xb = smq.DeviceBuffer.from_array(x)
+    d = smq.DeviceBuffer(rows * nb * 4)
+    q = smq.DeviceBuffer(rows * nb * 32)
+    smq.quantize_q8_rows(xb, rows, n, d, q)
+    smq.numeric_check()
+    return d, q, d.download(np.float32).reshape(rows, nb), q.download(np.int8).reshape(rows, nb * 32)
+
+
+# ------------------------------------------------------------------ quantize
+
+@pytest.mark.parametrize("spread", [1.0, 50.0, 1e-30, 1e30, 1e-37, 1e-39])
+def test_quantize_bit_exact(orc, spread):
+    g = LcgUniform(101)
+    for n in (1, 7, 31, 32, 33, 67, 896, 4864, 8960 + 5):
+        x = g.uniform(-spread, spread, 3 * n).reshape(3, n)
+        x[:, ::33] = 0.0
+        say("quantize", spread, n)
+        _, _, d, q = gpu_quantize(x)
+        s, wd, wq = orc.quantize_q8(x)
+        assert s == 0
+        assert np.array_equal(bits(d), bits(wd)), (spread, n)
+        assert np.array_equal(q, wq), (spread, n)
+
+
+def test_quantize_single_and_nonfinite(orc):
+    g = LcgUniform(5)
+    x = g.uniform(-3, 3, 100)
+    xb = smq.DeviceBuffer.from_array(x)
+    d = smq.DeviceBuffer(4 * 4)
+    q = smq.DeviceBuffer(4 * 32)
+    assert smq.quantize_q8(xb, 100, d, q) == 0
+    s, wd, wq = orc.quantize_q8(x)
+    assert np.array_equal(bits(d.download(np.float32)), bits(wd[0]))
+    assert np.array_equal(q.download(np.int8), wq[0])
+    for at in (0, 7, 31, 40, 66):  # tests/test_kernels.c:400-410
+        y = np.ones(67, np.float32)
+        y[at] = np.nan if at % 2 else np.inf
+        yb = smq.DeviceBuffer.from_array(y)
+        assert smq.quantize_q8(yb, 67, d, q) == -1
+    # the asynchronous row variant raises the sticky flag instead
+    y = np.ones((2, 64), np.float32)
+    y[1, 5] = -np.inf
+    yb = smq.DeviceBuffer.from_array(y)
+    smq.quantize_q8_rows(yb, 2, 64, d, q)
+    with pytest.raises(smq.SmqError) as e:
+        smq.numeric_check()
+    assert e.value.status == smq.SM_ERR_NUMERIC
+    smq.numeric_check()  # cleared
+
+
+# ------------------------------------------------------------------ gemm / gemv
+
+def run_gemm(w_host, row_bytes, x, nrows, ntok, nb, q5, stride=None, fast=False):
+    stride = nrows if stride is None else stride
+    dbuf, qbuf, xd, xq = gpu_quantize(x)
+    wb = smq.DeviceBuffer.from_array(w_host)
+    out = smq.DeviceBuffer(max(1, ntok * stride) * 4)
+    out.fill(0xFF)
+    smq.kernels_set_fast(fast)
+    try:
+        (smq.gemm_q5 if q5 else smq.gemm_q8)(wb, row_bytes, dbuf, qbuf, nrows, ntok, nb, out, stride)
+        got = out.download(np.float32)[:ntok * stride]
+    finally:
+        smq.kernels_set_fast(False)
+    return got, xd, xq
+
+
+def weights(q5, seed, rows, cols, sigma=0.02):
+    return (synth.q5_weights if q5 else synth.q8_weights)(seed, rows, cols, sigma).reshape(-1)
+
+
+CONFIG_SHAPES = [  # (name, q5, rows, cols, ntok)
+    ("c0", False, 896, 896, 1),
+    ("c1-gate", False, 4864, 896, 1),
+    ("c1-down", False, 896, 4864, 1),
+    ("c2-up", True, 8960, 1536, 1),
+    ("c2-down", True, 1536, 8960, 1),
+    ("c1-gate-b128", False, 4864, 896, 128),
+    ("c1-down-b128", False, 896, 4864, 128),
+    ("c2-up-b64", True, 8960, 1536, 64),
+    ("c2-down-b64", True, 1536, 8960, 64),
+]
+
+
+@pytest.mark.parametrize("name,q5,rows,cols,ntok", CONFIG_SHAPES)
+def test_config_shapes_bit_exact(orc, name, q5, rows, cols, ntok):
+    say("config", name)
+    nb = (cols + 31) // 32
+    w = weights(q5, 1000 + rows + cols, rows, cols)
+    x = synth.activations(2000 + cols + ntok, ntok, cols)
+    got, xd, xq = run_gemm(w, nb * (Q5B if q5 else Q8B), x, rows, ntok, nb, q5)
+    want = orc.gemm(w, nb * (Q5B if q5 else Q8B), xd, xq, rows, ntok, nb, q5=q5)
+    assert_same_f32(got, want, name)
+
+
+@pytest.mark.parametrize("ntok", [1, 64])
+def test_lm_head_bit_exact(orc, ntok):
+    """c3: 151936 x 896 Q8 against RMSNorm-scaled activations; batch 64 is
+    checked on every 16th row (the oracle is scalar)."""
+    rows, cols, nb = 151936, 896, 28
+    say("lm head", ntok)
+    w = weights(False, 1003, rows, cols)
+    raw = synth.activations(2003, ntok, cols)
+    x = np.stack([orc.rmsnorm(r, np.ones(cols, np.float32), 1e-6)[1] for r in raw])
+    got, xd, xq = run_gemm(w, nb * Q8B, x, rows, ntok, nb, False)
+    got = got.reshape(ntok, rows)
+    pick = np.arange(0, rows, 1 if ntok == 1 else 16)
+    wsub = w.reshape(rows, nb * Q8B)[pick].reshape(-1)
+    want = orc.gemm(wsub, nb * Q8B, xd, xq, len(pick), ntok, nb).reshape(ntok, len(pick))
+    assert_same_f32(got[:, pick], want, "lm head")
+
+
+def test_random_shapes_and_strides(orc):
+    """Ragged rows and tokens, odd widths (including odd Q5 widths, which take
+    the generic kernel), output strides wider than the row count."""
+    g = LcgUniform(77)
+    for trial in range(40):
+        q5 = trial % 2 == 1
+        nb = 1 + int(g.next(1)[0] % 40)
+        rows = 1 + int(g.next(1)[0] % 70)
+        ntok = 1 + int(g.next(1)[0] % 20)
+        stride = rows + int(g.next(1)[0] % 3)
+        cols = nb * 32 - int(g.next(1)[0] % 32)
+        fast = trial % 5 == 4
+        w = weights(q5, trial, rows, cols, 0.5)
+        x = g.uniform(-30, 30, ntok * cols).reshape(ntok, cols)
+        say("random", trial, q5, nb, rows, ntok, stride, fast)
+        got, xd, xq = run_gemm(w, nb * (Q5B if q5 else Q8B), x, rows, ntok, nb, q5, stride, fast)
+        want = orc.gemm(w, nb * (Q5B if q5 else Q8B), xd, xq, rows, ntok, nb, stride=stride, q5=q5, fast=fast)
+        m = np.zeros(ntok * stride, bool)
+        m.reshape(ntok, stride)[:, :rows] = True
+        assert_same_f32(got[m], want[m], f"trial {trial}")
+        assert np.all(bits(got[~m]) == 0xFFFFFFFF), "wrote outside the output rows"
+
+
+def test_fma_probe_exact_and_fast():
+    """tests/test_kernels.c:223-249: 0.0 with two roundings, 2^-12 with FMA."""
+    w = np.zeros(2 * Q8B, np.uint8)
+    w[0:4] = np.array([1.0], np.float32).view(np.uint8)
+    w[Q8B:Q8B + 4] = np.array([1.0 + 1.0 / 4096], np.float32).view(np.uint8)
+    w[4], w[5], w[Q8B + 4], w[Q8B + 5] = 127, 17, 127, 1
+    xq = np.zeros(4 * 64, np.int8)
+    for t in range(4):
+        xq[t * 64 + 0], xq[t * 64 + 1], xq[t * 64 + 32], xq[t * 64 + 33] = -32, -2, 32, 33
+    xd = np.ones(8, np.float32)
+    wb, qb, db = (smq.DeviceBuffer.from_array(a) for a in (w, xq, xd))
+    out = smq.DeviceBuffer(16 * 4)
+    assert smq.dot_q8(wb, db, qb, 2) == 0.0
+    smq.dot_q8_x4(wb, db, qb, 2, 2, out)
+    assert np.all(out.download(np.float32, 4) == 0.0)
+    smq.gemm_q8(wb, Q8B * 2, db, qb, 1, 4, 2, out, 1)
+    assert np.all(out.download(np.float32, 4) == 0.0)
+    smq.kernels_set_fast(True)
+    try:
+        assert smq.kernels_select() == "gfx950-fast"
+        assert smq.dot_q8(wb, db, qb, 2) == 2.0 ** -12
+        smq.gemm_q8(wb, Q8B * 2, db, qb, 1, 4, 2, out, 1)
+        assert np.all(out.download(np.float32, 4) == 2.0 ** -12)
+    finally:
+        smq.kernels_set_fast(False)
+    assert smq.kernels_select() == "gfx950"
+
+
+def test_backend_edges(orc):
+    """tests/test_kernels.c:251-278 edges through every GPU kernel shape."""
+    import struct
+    high = [0xFFFFFFFF, 0, 0xAAAAAAAA, 0x12345678]
+    low = [0xF0, 0xFF, 0x5A, 0x0F]
+    nb = 4
+    w5 = np.zeros(nb * Q5B, np.uint8)
+    w8 = np.zeros(nb * Q8B, np.uint8)
+    xq = np.zeros(nb * 32, np.int8)
+    j = np.arange(32)
+    for b in range(nb):
+        blk = w5[b * Q5B:(b + 1) * Q5B]
+        blk[0], blk[1] = 0x00, 0x3C
+        blk[2:6] = np.frombuffer(struct.pack("<I", high[b]), np.uint8)
+        blk[6:] = low[b]
+        w8[b * Q8B:b * Q8B + 4] = np.array([1.0], np.float32).view(np.uint8)
+        w8[b * Q8B + 4:(b + 1) * Q8B] = np.where(j % 2 == 1, -128, 127).astype(np.int8).view(np.uint8)
+        xq[b * 32:(b + 1) * 32] = np.where(b == 2, np.where(j % 3 != 0, 127, -127), -127)
+    xd = np.array([1.0, 0.5, 2.0, 0.25], np.float32)
+    for q5, w in ((True, w5), (False, w8)):
+        rows = 9
+        wrows = np.tile(w, rows)
+        want = orc.gemm(wrows, len(w), xd, xq, rows, 1, nb, q5=q5)
+        wb, qb, db = (smq.DeviceBuffer.from_array(a) for a in (wrows, xq, xd))
+        out = smq.DeviceBuffer(rows * 4)
+        (smq.gemm_q5 if q5 else smq.gemm_q8)(wb, len(w), db, qb, rows, 1, nb, out, rows)
+        assert_same_f32(out.download(np.float32), want, f"edges q5={q5}")
+        assert (smq.dot_q5 if q5 else smq.dot_q8)(wb, db, qb, nb) == want[0]
+
+
+def test_dot_variants(orc):
+    g = LcgUniform(12)
+    for q5 in (False, True):
+        nb = 28
+        bb = Q5B if q5 else Q8B
+        w = weights(q5, 5, 4, nb * 32, 1.0)
+        x = g.uniform(-8, 8, 4 * nb * 32).reshape(4, -1)
+        dbuf, qbuf, xd, xq = gpu_quantize(x)
+        wb = smq.DeviceBuffer.from_array(w)
+        out = smq.DeviceBuffer(4 * 4)
+        (smq.dot_q5_x4 if q5 else smq.dot_q8_x4)(wb, dbuf, qbuf, nb, nb, out)
+        want = [orc.dot(w[:nb * bb], xd[t], xq[t], nb, q5=q5) for t in range(4)]
+        assert_same_f32(out.download(np.float32), want, "x4")
+        (smq.dot_q5_r4 if q5 else smq.dot_q8_r4)(wb, nb * bb, dbuf, qbuf, nb, out)
+        want = [orc.dot(w[r * nb * bb:(r + 1) * nb * bb], xd[0], xq[0], nb, q5=q5) for r in range(4)]
+        assert_same_f32(out.download(np.float32), want, "r4")
+
+
+def test_unaligned_weights_take_the_generic_kernel(orc):
+    g = LcgUniform(3)
+    nb, rows, ntok = 9, 13, 3
+    for q5 in (False, True):
+        bb = Q5B if q5 else Q8B
+        w = weights(q5, 9, rows, nb * 32, 0.3)
+        x = g.uniform(-4, 4, ntok * nb * 32).reshape(ntok, -1)
+        dbuf, qbuf, xd, xq = gpu_quantize(x)
+        wb = smq.DeviceBuffer(len(w) + 8)
+        wb.upload(w, offset=1)
+        out = smq.DeviceBuffer(ntok * rows * 4)
+        (smq.gemm_q5 if q5 else smq.gemm_q8)(wb.at(1), nb * bb, dbuf, qbuf, rows, ntok, nb, out, rows)
+        want = orc.gemm(w, nb * bb, xd, xq, rows, ntok, nb, q5=q5)
+        assert_same_f32(out.download(np.float32), want, f"unaligned q5={q5}")
+
+
+def test_empty_and_bad_arguments():
+    wb = smq.DeviceBuffer(64)
+    out = smq.DeviceBuffer(64)
+    smq.gemm_q8(wb, 36, wb, wb, 0, 1, 1, out, 0)  # no rows: nothing to do
+    smq.gemm_q8(wb, 36, wb, wb, 1, 0, 1, out, 1)  # no tokens
+    with pytest.raises(smq.SmqError) as e:
+        smq.gemm_q8(wb, 36, wb, wb, 4, 1, 1, out, 4)  # 4 rows of 36 B exceed the 64-byte allocation
+    assert e.value.status == 4
+    with pytest.raises(smq.SmqError):
+        smq.gemm_q8(wb, 20, wb, wb, 1, 1, 1, out, 1)  # row_bytes < 36
+
+
+# ------------------------------------------------------------------ matmul glue
+
+def test_matmul_fused_items_bias_and_fault(orc):
+    """model.c:291-310: q/k/v share one input (896+128+128 rows), bias added,
+    outputs checked finite."""
+    g = LcgUniform(44)
+    cols, nb = 896, 28
+    shapes = [896, 128, 128]
+    for ntok in (1, 5):
+        x = synth.activations(9 + ntok, ntok, cols)
+        dbuf, qbuf, xd, xq = gpu_quantize(x)
+        items, wants = [], []
+        for i, rows in enumerate(shapes):
+            w = weights(False, 50 + i, rows, cols)
+            bias = g.uniform(-0.1, 0.1, rows)
+            wb = smq.DeviceBuffer.from_array(w)
+            bb = smq.DeviceBuffer.from_array(bias)
+            yb = smq.DeviceBuffer(ntok * rows * 4)
+            items.append((smq.QMat(wb, rows, cols), bb, yb))
+            ok, y = orc.mat_item(w, nb * Q8B, rows, bias, xd, xq, ntok, nb)
+            assert ok
+            wants.append(y)
+        smq.matmul(items, dbuf, qbuf, ntok)
+        smq.numeric_check()
+        for (_, _, yb), want in zip(items, wants):
+            assert_same_f32(yb.download(np.float32), want, f"matmul ntok={ntok}")
+    # an infinite weight scale makes a non-finite output: SM_ERR_NUMERIC
+    w = weights(False, 7, 4, cols)
+    w[0:4] = np.array([np.inf], np.float32).view(np.uint8)
+    wb = smq.DeviceBuffer.from_array(w)
+    yb = smq.DeviceBuffer(4 * 4)
+    smq.matmul([(smq.QMat(wb, 4, cols), None, yb)], dbuf, qbuf, 1)
+    with pytest.raises(smq.SmqError) as e:
+        smq.numeric_check()
+    assert e.value.status == smq.SM_ERR_NUMERIC
+    # items of different widths are an internal error, as in the reference
+    w2 = smq.DeviceBuffer.from_array(weights(False, 8, 4, 64))
+    with pytest.raises(smq.SmqError) as e:
+        smq.matmul([(smq.QMat(wb, 4, cols), None, yb), (smq.QMat(w2, 4, 64), None, yb)], dbuf, qbuf, 1)
+    assert e.value.status == 7
+
+
+def test_dequantize_rows(orc):
+    for q5 in (False, True):
+        for cols in (896, 45, 1):
+            w = weights(q5, cols, 1, cols, 0.7)
+            wb = smq.DeviceBuffer.from_array(w)
+            out = smq.DeviceBuffer(cols * 4)
+            (smq.dequantize_q5_row if q5 else smq.dequantize_q8_row)(wb, cols, out)
+            assert_same_f32(out.download(np.float32), orc.dequantize_row(w, cols, q5=q5), "dequant")

@@ -140,6 +140,16 @@ smq_status smq_numeric_check(void);
 void smq_dequantize_q8_row(const unsigned char *w, uint32_t cols, float *out);
 void smq_dequantize_q5_row(const unsigned char *w, uint32_t cols, float *out);
 
+/* ---- graph capture (no reference counterpart: amortizes launches) -------
+ * Work enqueued on the library stream between smq_capture_begin and
+ * smq_capture_end is recorded, not run, and replayed by smq_graph_launch
+ * (a HIP graph). Only asynchronous entry points may be captured: smq_gemm_*,
+ * smq_dot_*_x4/_r4, smq_matmul, smq_quantize_q8_rows, smq_dequantize_*. */
+smq_status smq_capture_begin(void);
+void *smq_capture_end(void);
+smq_status smq_graph_launch(void *graph);
+void smq_graph_destroy(void *graph);
+
 /* ---- device memory and timing helpers (plumbing for C hosts and tests) -- */
 void *smq_malloc(size_t bytes);
 void smq_free(void *p);

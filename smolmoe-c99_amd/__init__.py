@@ -86,6 +86,10 @@ _SIGS = {
     "smq_memcpy_dtoh": (ctypes.c_int, [_vp, _vp, _sz]),
     "smq_memcpy_dtod": (ctypes.c_int, [_vp, _vp, _sz]),
     "smq_memset": (ctypes.c_int, [_vp, ctypes.c_int, _sz]),
+    "smq_capture_begin": (ctypes.c_int, []),
+    "smq_capture_end": (_vp, []),
+    "smq_graph_launch": (ctypes.c_int, [_vp]),
+    "smq_graph_destroy": (None, [_vp]),
     "smq_timer_start": (ctypes.c_int, []),
     "smq_timer_stop": (ctypes.c_double, []),
 }
@@ -169,6 +173,10 @@ class DeviceBuffer:
         if count:
             _check(load().smq_memcpy_dtoh(out.ctypes.data, self.ptr + offset, out.nbytes))
         return out
+
+    def copy_from(self, other, nbytes=None):
+        n = other.nbytes if nbytes is None else nbytes
+        _check(load().smq_memcpy_dtod(self.ptr, other.ptr, n))
 
     def fill(self, value=0):
         _check(load().smq_memset(self.ptr, value, self.nbytes))
@@ -311,6 +319,41 @@ def dequantize_q8_row(w, cols, out):
 def dequantize_q5_row(w, cols, out):
     load().smq_dequantize_q5_row(_p(w), cols, _p(out))
     _check()
+
+
+# ---- graphs
+class Graph:
+    """A captured sequence of launches on the library stream (HIP graph)."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    def launch(self):
+        _check(load().smq_graph_launch(self.handle))
+
+    def destroy(self):
+        if self.handle:
+            load().smq_graph_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+def capture(fn):
+    """Runs fn() under stream capture and returns the replayable Graph."""
+    lib = load()
+    _check(lib.smq_capture_begin())
+    try:
+        fn()
+    finally:
+        handle = lib.smq_capture_end()
+    if not handle:
+        _check()
+    return Graph(handle)
 
 
 # ---- timing

@@ -415,6 +415,33 @@ smq_status smq_memset(void *dst, int value, size_t bytes) {
     return hip_ok(hipMemsetAsync(dst, value, bytes, g.cur), "memset") ? SMQ_OK : t_status;
 }
 
+smq_status smq_capture_begin(void) {
+    if (!ready()) return t_status;
+    if (g.cur != g.own) return set_status(SMQ_ERR_STATE, "capture needs the library stream");
+    return hip_ok(hipStreamBeginCapture(g.cur, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture") ? SMQ_OK
+                                                                                                        : t_status;
+}
+
+void *smq_capture_end(void) {
+    if (!ready()) return nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    if (!hip_ok(hipStreamEndCapture(g.cur, &graph), "hipStreamEndCapture")) return nullptr;
+    const bool ok = hip_ok(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+    (void)hipGraphDestroy(graph);
+    return ok ? (void *)exec : nullptr;
+}
+
+smq_status smq_graph_launch(void *graph) {
+    if (!ready()) return t_status;
+    if (!graph) return set_status(SMQ_ERR_RANGE, "graph is NULL");
+    return hip_ok(hipGraphLaunch((hipGraphExec_t)graph, g.cur), "hipGraphLaunch") ? SMQ_OK : t_status;
+}
+
+void smq_graph_destroy(void *graph) {
+    if (graph) (void)hipGraphExecDestroy((hipGraphExec_t)graph);
+}
+
 smq_status smq_timer_start(void) {
     if (!ready()) return t_status;
     return hip_ok(hipEventRecord(g.t0, g.cur), "timer") ? SMQ_OK : t_status;

@@ -14,6 +14,7 @@
  * fmaf), correctly rounded f32 division and f32 denormals preserved.
  */
 #include <float.h>
+#include <stdlib.h>
 
 #include "smq_internal.h"
 
@@ -106,107 +107,136 @@ __device__ __forceinline__ void store_out(const Item &I, int *flag, uint32_t t, 
     if (flag && !(fabsf(v) <= FLT_MAX)) *flag = 1;
 }
 
+/* DPP row shift by N lanes (row_shr:N): lane i reads lane i-N of its row of 16. */
+template <int N>
+__device__ __forceinline__ float shr_dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x110 + N, 0xf, 0xf, false));
+}
+
+/* The fixed lane reduction with DPP shifts (no LDS round trip). For eight
+ * consecutive threads holding lanes a0..a7, thread 4+i first holds
+ * a_i + a_{4+i} = s_i; thread 6 then s0 + s2 and thread 7 s1 + s3; thread 7
+ * ends with (s0+s2) + (s1+s3). Only thread 7 of each group is meaningful;
+ * every add is one the reference makes, with its operands swapped at most. */
+__device__ __forceinline__ float reduce8_to_lane7(float a) {
+    const float s = a + shr_dpp<4>(a);
+    const float t = s + shr_dpp<2>(s);
+    return t + shr_dpp<1>(t);
+}
+
 /* ------------------------------------------------------------------------
  * Decode GEMV (ntok == 1). Workgroup = RT rows x all K. K is walked in chunks
- * of CB blocks. In each chunk every thread owns one task (one Q8 block, or
- * one pair of Q5 blocks, of one row): it loads the block straight from HBM
- * (prefetched one chunk ahead), and writes the eight lane products
+ * of CB blocks (the launcher sizes RT so that one chunk usually covers K). In
+ * each chunk every thread owns one task (one Q8 block, or one pair of Q5
+ * blocks, of one row): it loads the block straight from HBM (the next chunk's
+ * task is prefetched into registers), and writes the eight lane products
  * d*float(s_l) (fast mode: float(s_l) and d) into LDS. Then the RT*8 chain
  * threads, one per (row, lane), add their CB products in block order. The
  * serial part per thread is one add per block; the loads, dot4s and
  * multiplies are spread over all 256 threads.
+ * STAGE: the activation is copied to LDS once per workgroup (large row counts,
+ * where it is reused by many tasks); otherwise each task reads its activation
+ * block directly (L1/L2 hits) and no barrier precedes the products.
  * LDS products: group g of four blocks holds [thread (r*8+l)][b%4], padded by
  * four floats per group so writes from a wave fall in distinct banks.
  * ---------------------------------------------------------------------- */
-template <bool Q5, bool FAST, int RT>
+template <bool Q5, bool FAST, int RT, bool STAGE>
 __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
-    constexpr int TB = Q5 ? 2 : 1;       /* blocks per task */
-    constexpr int TPR = WG / RT;         /* tasks per row per chunk */
-    constexpr int CB = TPR * TB;         /* blocks per chunk */
-    constexpr int GS = RT * 32 + 4;      /* floats per group of four blocks */
-    constexpr int NRAW = Q5 ? 11 : 9;    /* dwords per task */
+    constexpr int TB = Q5 ? 2 : 1;    /* blocks per task */
+    constexpr int TPR = WG / RT;      /* tasks per row per chunk */
+    constexpr int CB = TPR * TB;      /* blocks per chunk */
+    constexpr int GS = RT * 32 + 4;   /* floats per group of four blocks */
+    constexpr int DS = RT * 4 + 4;    /* fast mode: scales per group */
+    constexpr int NW = Q5 ? 11 : 9;   /* weight dwords per task */
+    constexpr int NX = STAGE ? 1 : TB * 8; /* activation words per task */
     __shared__ __attribute__((aligned(16))) float prod[2][(CB / 4) * GS];
-    __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? (CB / 4) * (RT * 4 + 4) : 4];
+    __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? (CB / 4) * DS : 4];
     extern __shared__ __attribute__((aligned(16))) uint32_t act[];
 
     const uint32_t nb = a.nb, tid = threadIdx.x;
-    uint32_t *act_q = act;                      /* nb*8 words of int8 x4 */
-    float *act_d = (float *)(act + nb * 8);     /* nb scales */
-    int *act_b = (int *)(act + nb * 9);         /* Q5: -16 * lane sums of x */
+    uint32_t *act_q = act;                  /* STAGE: nb*8 words of int8 x4 */
+    float *act_d = (float *)(act + nb * 8); /* STAGE: nb scales */
+    int *act_b = (int *)(act + nb * 9);     /* STAGE, Q5: -16 * lane sums of x */
 
     const Item &I = a.item[find_item(a, blockIdx.x)]; /* uniform index into the kernel arguments */
     const uint32_t r0 = (blockIdx.x - I.tile_begin) * RT;
 
-    const uint32_t *xq32 = (const uint32_t *)a.xq;
-    for (uint32_t i = tid; i < nb * 8; i += WG) {
-        const uint32_t v = xq32[i];
-        act_q[i] = v;
-        if (Q5) act_b[i] = -16 * dot4(v, 0x01010101u, 0);
+    if (STAGE) {
+        const uint32_t *xq32 = (const uint32_t *)a.xq;
+        for (uint32_t i = tid; i < nb * 8; i += WG) {
+            const uint32_t v = xq32[i];
+            act_q[i] = v;
+            if (Q5) act_b[i] = dot4(v, 0xf0f0f0f0u, 0); /* int8 0xf0 = -16 */
+        }
+        for (uint32_t i = tid; i < nb; i += WG) act_d[i] = a.xd[i];
     }
-    for (uint32_t i = tid; i < nb; i += WG) act_d[i] = a.xd[i];
 
     const uint32_t tr = tid / TPR, ti = tid % TPR;
     const bool row_ok = r0 + tr < I.rows;
     const unsigned char *wrow = I.w + (size_t)(row_ok ? r0 + tr : 0) * I.row_bytes;
     const uint32_t nchunks = (nb + CB - 1) / CB;
 
-    uint32_t raw[NRAW];
+    uint32_t wr[NW] = {}, xr[NX] = {};
+    float xs[TB] = {};
     auto load_task = [&](uint32_t b) {
         if (row_ok && b < nb) {
+            const unsigned char *p = wrow + (size_t)b * (Q5 ? Q5_BYTES : Q8_BYTES);
+            const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
+            wr[0] = v0.x; wr[1] = v0.y; wr[2] = v0.z; wr[3] = v0.w;
+            wr[4] = v1.x; wr[5] = v1.y; wr[6] = v1.z; wr[7] = v1.w;
             if (Q5) {
-                const unsigned char *p = wrow + (size_t)b * Q5_BYTES;
-                const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
                 const u3a v2 = *(const u3a *)(p + 32);
-                raw[0] = v0.x; raw[1] = v0.y; raw[2] = v0.z; raw[3] = v0.w;
-                raw[4] = v1.x; raw[5] = v1.y; raw[6] = v1.z; raw[7] = v1.w;
-                raw[8] = v2.x; raw[9] = v2.y; raw[10] = v2.z;
+                wr[8] = v2.x; wr[9] = v2.y; wr[10] = v2.z;
             } else {
-                const unsigned char *p = wrow + (size_t)b * Q8_BYTES;
-                const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
-                raw[0] = v0.x; raw[1] = v0.y; raw[2] = v0.z; raw[3] = v0.w;
-                raw[4] = v1.x; raw[5] = v1.y; raw[6] = v1.z; raw[7] = v1.w;
-                raw[8] = *(const uint32_t *)(p + 32);
+                wr[8] = *(const uint32_t *)(p + 32);
+            }
+            if (!STAGE) {
+                const unsigned char *xp = (const unsigned char *)a.xq + (size_t)b * QK;
+#pragma unroll
+                for (int k = 0; k < TB * 2; ++k) {
+                    const u4a v = *(const u4a *)(xp + 16 * k);
+                    xr[4 * k] = v.x; xr[4 * k + 1] = v.y; xr[4 * k + 2] = v.z; xr[4 * k + 3] = v.w;
+                }
+#pragma unroll
+                for (int k = 0; k < TB; ++k) xs[k] = a.xd[b + k];
             }
         }
     };
     load_task(ti * TB);
-    __syncthreads(); /* activation staged */
+    if (STAGE) __syncthreads(); /* activation staged */
 
     float acc = 0.0f;
     for (uint32_t c = 0; c < nchunks; ++c) {
         const uint32_t bt = c * CB + ti * TB; /* first block of this task */
-        uint32_t cur[NRAW];
+        uint32_t cw[NW], cx[NX];
+        float cs[TB];
 #pragma unroll
-        for (int k = 0; k < NRAW; ++k) cur[k] = raw[k];
+        for (int k = 0; k < NW; ++k) cw[k] = wr[k];
+#pragma unroll
+        for (int k = 0; k < NX; ++k) cx[k] = xr[k];
+#pragma unroll
+        for (int k = 0; k < TB; ++k) cs[k] = xs[k];
         if (c + 1 < nchunks) load_task(bt + CB);
 
         float *pb = prod[c & 1];
         if (row_ok && bt < nb) {
-            if (Q5) {
-                Q5Fields f[2];
-                q5_parse_pair(cur, f[0], f[1]);
+            Q5Fields f[2];
+            if (Q5) q5_parse_pair(cw, f[0], f[1]);
 #pragma unroll
-                for (int k = 0; k < 2; ++k) {
-                    const uint32_t b = bt + k, bb = ti * 2 + k;
-                    const float d = f[k].scale * act_d[b];
-                    float *dst = pb + (bb / 4) * GS + tr * 32 + (bb % 4);
-#pragma unroll
-                    for (int l = 0; l < 8; ++l) {
-                        const int s = dot4(q5_codes(f[k], l), act_q[b * 8 + l], act_b[b * 8 + l]);
-                        dst[l * 4] = FAST ? (float)s : d * (float)s;
-                    }
-                    if (FAST) dsc[c & 1][(bb / 4) * (RT * 4 + 4) + tr * 4 + (bb % 4)] = d;
-                }
-            } else {
-                const uint32_t b = bt, bb = ti;
-                const float d = __uint_as_float(cur[0]) * act_d[b];
+            for (int k = 0; k < TB; ++k) {
+                const uint32_t b = bt + k, bb = ti * TB + k;
+                const float wscale = Q5 ? f[k].scale : __uint_as_float(cw[0]);
+                const float d = wscale * (STAGE ? act_d[b] : cs[k]);
                 float *dst = pb + (bb / 4) * GS + tr * 32 + (bb % 4);
 #pragma unroll
                 for (int l = 0; l < 8; ++l) {
-                    const int s = dot4(cur[1 + l], act_q[b * 8 + l], 0);
+                    const uint32_t x = STAGE ? act_q[b * 8 + l] : cx[STAGE ? 0 : k * 8 + l];
+                    int s;
+                    if (Q5) s = dot4(q5_codes(f[k], l), x, STAGE ? act_b[b * 8 + l] : dot4(x, 0xf0f0f0f0u, 0));
+                    else s = dot4(cw[1 + l], x, 0);
                     dst[l * 4] = FAST ? (float)s : d * (float)s;
                 }
-                if (FAST) dsc[c & 1][(bb / 4) * (RT * 4 + 4) + tr * 4 + (bb % 4)] = d;
+                if (FAST) dsc[c & 1][(bb / 4) * DS + tr * 4 + (bb % 4)] = d;
             }
         }
         __syncthreads();
@@ -216,10 +246,10 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
             const float4 *pg = (const float4 *)pb + tid;
             const float4 *dg = FAST ? (const float4 *)dsc[c & 1] + tid / 8 : nullptr;
             uint32_t q = 0;
-            for (; q + 1 <= count / 4; ++q) {
+            for (; q < count / 4; ++q) {
                 const float4 v = pg[q * (GS / 4)];
                 if (FAST) {
-                    const float4 dv = dg[q * (RT + 1)];
+                    const float4 dv = dg[q * (DS / 4)];
                     acc = __builtin_fmaf(dv.x, v.x, acc);
                     acc = __builtin_fmaf(dv.y, v.y, acc);
                     acc = __builtin_fmaf(dv.z, v.z, acc);
@@ -235,7 +265,7 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
             if (rem) {
                 const float4 v = pg[q * (GS / 4)];
                 if (FAST) {
-                    const float4 dv = dg[q * (RT + 1)];
+                    const float4 dv = dg[q * (DS / 4)];
                     acc = __builtin_fmaf(dv.x, v.x, acc);
                     if (rem > 1) acc = __builtin_fmaf(dv.y, v.y, acc);
                     if (rem > 2) acc = __builtin_fmaf(dv.z, v.z, acc);
@@ -249,9 +279,9 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
     }
 
     if (tid < RT * 8) {
-        const float v = reduce8(acc);
+        const float v = reduce8_to_lane7(acc);
         const uint32_t r = r0 + tid / 8;
-        if ((tid & 7) == 0 && r < I.rows) store_out(I, a.flag, 0, r, v);
+        if ((tid & 7) == 7 && r < I.rows) store_out(I, a.flag, 0, r, v);
     }
 }
 
@@ -532,7 +562,7 @@ bool fast_layout(const MatArgs &a, bool q5) {
     return true;
 }
 
-template <bool Q5, bool FAST, int RT>
+template <bool Q5, bool FAST, int RT, bool STAGE>
 hipError_t launch_gemv_rt(MatArgs a, hipStream_t s) {
     uint32_t tiles = 0;
     for (uint32_t i = 0; i < a.nitems; ++i) {
@@ -540,9 +570,44 @@ hipError_t launch_gemv_rt(MatArgs a, hipStream_t s) {
         tiles += (a.item[i].rows + RT - 1) / RT;
     }
     if (!tiles) return hipSuccess;
-    const size_t lds = (size_t)a.nb * (Q5 ? 17u : 9u) * 4u;
-    hipLaunchKernelGGL((k_gemv<Q5, FAST, RT>), dim3(tiles), dim3(WG), lds, s, a);
+    const size_t lds = STAGE ? (size_t)a.nb * (Q5 ? 17u : 9u) * 4u : 0;
+    hipLaunchKernelGGL((k_gemv<Q5, FAST, RT, STAGE>), dim3(tiles), dim3(WG), lds, s, a);
     return hipGetLastError();
+}
+
+template <bool Q5, bool FAST, bool STAGE>
+hipError_t launch_gemv_stage(MatArgs a, int rt, hipStream_t s) {
+    switch (rt) {
+    case 1: return launch_gemv_rt<Q5, FAST, 1, STAGE>(a, s);
+    case 2: return launch_gemv_rt<Q5, FAST, 2, STAGE>(a, s);
+    case 4: return launch_gemv_rt<Q5, FAST, 4, STAGE>(a, s);
+    case 8: return launch_gemv_rt<Q5, FAST, 8, STAGE>(a, s);
+    default: return launch_gemv_rt<Q5, FAST, 16, STAGE>(a, s);
+    }
+}
+
+/* Rows per workgroup: the largest power of two (<= 8) whose chunk of 256
+ * tasks covers all nb blocks, so each workgroup needs one round of loads
+ * (Q5 keeps at least 2 rows: its wide rows run faster as two chunks of two
+ * rows than as one chunk of one). Measured on MI355X over rotated weights:
+ * 9728x896 Q8 4.7 us at 8 rows, 896x4864 Q8 4.6 us at 1 row, 1536x8960 Q5
+ * 7.4 us at 2 rows (9.9 us at 1). SMQ_GEMV_RT / SMQ_GEMV_STAGE override. */
+int gemv_rows_per_tile(uint32_t nb, bool q5, uint32_t total_rows) {
+    (void)total_rows;
+    const char *env = getenv("SMQ_GEMV_RT");
+    if (env && *env) return atoi(env);
+    const uint32_t cover = (q5 ? 512u : 256u) / nb;
+    int rt = q5 ? 2 : 1;
+    while (rt < 8 && (uint32_t)(rt * 2) <= cover) rt *= 2;
+    return rt;
+}
+
+/* Staging the activation in LDS never beat direct (L1/L2) reads on the
+ * measured shapes; the staged variant stays available for tuning. */
+bool gemv_stage(uint32_t total_rows) {
+    (void)total_rows;
+    const char *env = getenv("SMQ_GEMV_STAGE");
+    return env && *env && atoi(env) != 0;
 }
 
 template <bool Q5, bool FAST>
@@ -552,9 +617,9 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
     if (!total_rows || !a.ntok || !a.nb) return hipSuccess;
     if (fast_layout(a, Q5)) {
         if (a.ntok == 1) {
-            if (total_rows <= 2048) return launch_gemv_rt<Q5, FAST, 4>(a, s);
-            if (total_rows <= 65536) return launch_gemv_rt<Q5, FAST, 8>(a, s);
-            return launch_gemv_rt<Q5, FAST, 16>(a, s);
+            const int rt = gemv_rows_per_tile(a.nb, Q5, total_rows);
+            return gemv_stage(total_rows) ? launch_gemv_stage<Q5, FAST, true>(a, rt, s)
+                                          : launch_gemv_stage<Q5, FAST, false>(a, rt, s);
         }
         uint32_t tiles = 0;
         for (uint32_t i = 0; i < a.nitems; ++i) {

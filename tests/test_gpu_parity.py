@@ -336,3 +336,25 @@ def test_dequantize_rows(orc):
             out = smq.DeviceBuffer(cols * 4)
             (smq.dequantize_q5_row if q5 else smq.dequantize_q8_row)(wb, cols, out)
             assert_same_f32(out.download(np.float32), orc.dequantize_row(w, cols, q5=q5), "dequant")
+
+
+@pytest.mark.parametrize("rt", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("stage", [0, 1])
+def test_every_gemv_tile_variant(orc, rt, stage, monkeypatch):
+    """Forces each decode-GEMV variant (rows per workgroup, staged or direct
+    activation) through the launcher's tuning override, exact and fast, with
+    one- and multi-chunk widths."""
+    monkeypatch.setenv("SMQ_GEMV_RT", str(rt))
+    monkeypatch.setenv("SMQ_GEMV_STAGE", str(stage))
+    g = LcgUniform(1000 + rt * 10 + stage)
+    cases = [(False, 3, 37), (False, 28, 70), (False, 152, 9), (False, 300, 5), (True, 2, 41), (True, 48, 19),
+             (True, 280, 6), (True, 600, 3)]
+    for q5, nb, rows in cases:
+        for fast in (False, True):
+            cols = nb * 32
+            w = weights(q5, nb * 7 + rows, rows, cols, 0.3)
+            x = g.uniform(-5, 5, cols).reshape(1, cols)
+            say("variant", rt, stage, q5, nb, rows, fast)
+            got, xd, xq = run_gemm(w, nb * (Q5B if q5 else Q8B), x, rows, 1, nb, q5, fast=fast)
+            want = orc.gemm(w, nb * (Q5B if q5 else Q8B), xd, xq, rows, 1, nb, q5=q5, fast=fast)
+            assert_same_f32(got, want, f"rt={rt} stage={stage} q5={q5} nb={nb} fast={fast}")

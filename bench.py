@@ -206,6 +206,7 @@ def main():
     ms_per_step = timed_graph(step_graphs, args.steps)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     smq.numeric_check()
+    gpu_layer0 = [gu_out[0].download(np.float32), y_out[0].download(np.float32)]  # for the CPU parity gate
     log(f"bench: FFN step {ms_per_step * 1e3:.1f} us, {value:.0f} GB/s")
 
     # dominant kernel: gate+up GEMV (k_gemv<Q8, RT=8>), back-to-back launches
@@ -230,35 +231,46 @@ def main():
             "GBps": round(dec_bytes / (dec_ms * 1e-3) / 1e9, 1)}
         log(f"bench: decode matmuls {dec_ms * 1e3:.1f} us/token = {1000 / dec_ms:.0f} tok/s")
 
-        def single(name, fn, nbytes, reps=30):
-            gs = [smq.capture(lambda c=c: fn(c)) for c in range(2)]
-            timed_graph(gs, 3)
-            ms = timed_graph(gs, reps)
+        def single(name, fn, nbytes, per_graph, reps=10, note=None):
+            """Per-launch time of fn(i), i = 0..per_graph-1 captured in one graph
+            (fn picks distinct weight buffers by i), timed over `reps` replays."""
+            gs = [smq.capture(lambda: [fn(i) for i in range(per_graph)] and None)]
+            timed_graph(gs, 2)
+            ms = timed_graph(gs, reps) / per_graph
             extra[name] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
                            "pct_hbm_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
+            if note:
+                extra[name]["note"] = note
             log(f"bench: {name} {ms * 1e3:.2f} us {extra[name]['GBps']} GB/s")
 
         single("c3_lm_head_gemv_151936x896",
-               lambda c: smq.gemm_q8(head[c], 28 * 36, ax[0].d, ax[0].q, VOCAB, 1, 28, logits, VOCAB),
-               q8_bytes(VOCAB, DIM))
+               lambda i: smq.gemm_q8(head[i % 2], 28 * 36, ax[0].d, ax[0].q, VOCAB, 1, 28, logits, VOCAB),
+               q8_bytes(VOCAB, DIM), 16, note="2 copies of 153 MB alternated (306 MB > 256 MB Infinity Cache)")
         single("c1_down_gemv_896x4864",
-               lambda c: [smq.matmul([(copies[c][l].qmat("down"), None, y_out[l])], ah[l].d, ah[l].q, 1)
-                          for l in range(LAYERS)] and None, LAYERS * q8_bytes(DIM, HIDDEN))
-        extra["c1_down_gemv_896x4864"]["note"] = "24 launches per replay; figures per replay"
-        # prefill: exact GEMM at batch 128 on the gate+up shape
+               lambda i: smq.matmul([(copies[i // LAYERS % 2][i % LAYERS].qmat("down"), None, y_out[0])], ah[0].d,
+                                    ah[0].q, 1),
+               q8_bytes(DIM, HIDDEN), 2 * LAYERS, note="48 distinct 4.9 MB matrices in turn (235 MB)")
+        # prefill: exact GEMM and int8-MFMA GEMM at batch 128 on the fused gate+up shape
         px = Act(4000, 128, DIM)
         pout = smq.DeviceBuffer(128 * 2 * HIDDEN * 4)
-        single("c1_prefill_exact_gemm_9728x896_b128",
-               lambda c: smq.matmul([(copies[c][0].qmat("gate"), None, pout.ptr),
-                                     (copies[c][0].qmat("up"), None, pout.ptr + 128 * HIDDEN * 4)], px.d, px.q, 128),
-               q8_bytes(2 * HIDDEN, DIM, 128), reps=20)
+
+        def prefill(i):
+            layer = copies[i // LAYERS % 2][i % LAYERS]
+            smq.matmul([(layer.qmat("gate"), None, pout.ptr), (layer.qmat("up"), None, pout.ptr + 128 * HIDDEN * 4)],
+                       px.d, px.q, 128)
+
+        single("c1_prefill_exact_gemm_9728x896_b128", prefill, q8_bytes(2 * HIDDEN, DIM, 128), 8)
+        smq.set_prefill_mfma(True)
+        single("c1_prefill_mfma_gemm_9728x896_b128", prefill, q8_bytes(2 * HIDDEN, DIM, 128), 24)
+        smq.set_prefill_mfma(False)
         ops = 2 * 2 * HIDDEN * DIM * 128
-        e = extra["c1_prefill_exact_gemm_9728x896_b128"]
-        e["int_TOPS"] = round(ops / (e["us"] * 1e-6) / 1e12, 2)
+        for k in ("c1_prefill_exact_gemm_9728x896_b128", "c1_prefill_mfma_gemm_9728x896_b128"):
+            e = extra[k]
+            e["int_TOPS"] = round(ops / (e["us"] * 1e-6) / 1e12, 2)
+            e["pct_int8_peak"] = round(100 * ops / (e["us"] * 1e-6) / 5.0e15, 2)
         qx = Act(5, 1, HIDDEN)
         single("quantize_q8_4864",
-               lambda c: smq.quantize_q8_rows(qx.x, 1, HIDDEN, qx.d, qx.q), HIDDEN * 4 + HIDDEN + HIDDEN // 8,
-               reps=200)
+               lambda i: smq.quantize_q8_rows(qx.x, 1, HIDDEN, qx.d, qx.q), HIDDEN * 4 + HIDDEN + HIDDEN // 8, 32)
 
     cpu = None
     if not args.no_cpu:
@@ -267,9 +279,8 @@ def main():
             acts_h = [(synth_q(ah[l], HIDDEN)) for l in range(LAYERS)]
             ncpu = len(os.sched_getaffinity(0))
             threads = min(16, ncpu)
-            gpu_out = [gu_out[0].download(np.float32), y_out[0].download(np.float32)]
             kind, name, res, gate = cpu_baseline(copies[0], acts_x, acts_h, sorted({1, threads}), args.cpu_budget,
-                                                 gpu_out)
+                                                 gpu_layer0)
             best, nreps = res[threads]
             cpu = {"value": round(step_bytes / best / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": kind,
                    "gpu_bit_identical_layer0": gate,

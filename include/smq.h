@@ -113,6 +113,23 @@ void smq_gemm_q8(const unsigned char *w, size_t row_bytes, const float *xd, cons
                  uint32_t ntok, uint32_t nb, float *out, size_t stride, unsigned char *scratch);
 void smq_gemm_q5(const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq, uint32_t nrows,
                  uint32_t ntok, uint32_t nb, float *out, size_t stride, unsigned char *scratch);
+/* Prefill GEMM on int8 MFMA (no reference counterpart for its order: the
+ * reference has one order). The per-block int32 sums are exact; each output is
+ * acc = fma(wscale*xscale, float(blocksum), acc) over blocks in order, which
+ * matches the exact contract within 1e-5 relative (|err| <= 1e-5 * max|out|
+ * over a token's outputs). Same parameters as GemmQ8. Asynchronous. */
+void smq_gemm_q8_mfma(const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq, uint32_t nrows,
+                      uint32_t ntok, uint32_t nb, float *out, size_t stride, unsigned char *scratch);
+void smq_gemm_q5_mfma(const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq, uint32_t nrows,
+                      uint32_t ntok, uint32_t nb, float *out, size_t stride, unsigned char *scratch);
+/* The MFMA path's per-block int32 sums, sums[(t*nrows + r)*nb + b] (device),
+ * for the bit-exact integer check (test entry point, no reference counterpart). */
+void smq_block_sums(int q5, const unsigned char *w, size_t row_bytes, const int8_t *xq, uint32_t nrows,
+                    uint32_t ntok, uint32_t nb, int32_t *sums);
+/* Which kernel smq_matmul uses when ntok > 1: 0 = the exact GEMM (default,
+ * bit-identical to the reference), 1 = the int8-MFMA GEMM. */
+void smq_set_prefill_mfma(int on);
+
 /* ---- fused matmul with bias and finiteness (src/model.c:236-310) -------- */
 /* QMat (model.h:15-19): a weight matrix in device memory. dtype 1 = Q8, 2 = Q5
  * (docs/FORMAT.md:101). */

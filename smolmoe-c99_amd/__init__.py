@@ -76,6 +76,10 @@ _SIGS = {
     "smq_dot_q5_r4": (None, [_vp, _sz, _vp, _vp, _u32, _vp]),
     "smq_gemm_q8": (None, [_vp, _sz, _vp, _vp, _u32, _u32, _u32, _vp, _sz, _vp]),
     "smq_gemm_q5": (None, [_vp, _sz, _vp, _vp, _u32, _u32, _u32, _vp, _sz, _vp]),
+    "smq_gemm_q8_mfma": (None, [_vp, _sz, _vp, _vp, _u32, _u32, _u32, _vp, _sz, _vp]),
+    "smq_gemm_q5_mfma": (None, [_vp, _sz, _vp, _vp, _u32, _u32, _u32, _vp, _sz, _vp]),
+    "smq_block_sums": (None, [ctypes.c_int, _vp, _sz, _vp, _u32, _u32, _u32, _vp]),
+    "smq_set_prefill_mfma": (None, [ctypes.c_int]),
     "smq_matmul": (ctypes.c_int, [ctypes.POINTER(_MatItem), _u32, _vp, _vp, _u32]),
     "smq_numeric_check": (ctypes.c_int, []),
     "smq_dequantize_q8_row": (None, [_vp, _u32, _vp]),
@@ -277,6 +281,25 @@ def gemm_q8(w, row_bytes, xd, xq, nrows, ntok, nb, out, stride, scratch=None):
 def gemm_q5(w, row_bytes, xd, xq, nrows, ntok, nb, out, stride, scratch=None):
     load().smq_gemm_q5(_p(w), row_bytes, _p(xd), _p(xq), nrows, ntok, nb, _p(out), stride, _p(scratch))
     _check()
+
+
+def gemm_q8_mfma(w, row_bytes, xd, xq, nrows, ntok, nb, out, stride, scratch=None):
+    load().smq_gemm_q8_mfma(_p(w), row_bytes, _p(xd), _p(xq), nrows, ntok, nb, _p(out), stride, _p(scratch))
+    _check()
+
+
+def gemm_q5_mfma(w, row_bytes, xd, xq, nrows, ntok, nb, out, stride, scratch=None):
+    load().smq_gemm_q5_mfma(_p(w), row_bytes, _p(xd), _p(xq), nrows, ntok, nb, _p(out), stride, _p(scratch))
+    _check()
+
+
+def block_sums(q5, w, row_bytes, xq, nrows, ntok, nb, sums):
+    load().smq_block_sums(int(bool(q5)), _p(w), row_bytes, _p(xq), nrows, ntok, nb, _p(sums))
+    _check()
+
+
+def set_prefill_mfma(on):
+    load().smq_set_prefill_mfma(int(bool(on)))
 
 
 # ---- src/model.c:236-310

@@ -28,6 +28,7 @@ struct Context {
     float *scalar = nullptr;
     hipEvent_t t0 = nullptr, t1 = nullptr;
     int fast = 0;
+    int prefill_mfma = 0;
     int checks = 1;
     char arch[64] = {0};
     char backend[80] = {0};
@@ -141,6 +142,18 @@ void gemm_impl(bool q5, const unsigned char *w, size_t row_bytes, const float *x
     if (!check_operands(w, row_bytes, nrows, nb, q5, xd, xq, ntok, xstride, out, stride, who)) return;
     hip_ok(smq::launch_matmul(one_item(w, row_bytes, xd, xq, nrows, ntok, nb, xstride, out, stride), q5, g.fast != 0,
                               g.cur),
+           who);
+}
+
+void gemm_mfma_impl(bool q5, const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq,
+                    uint32_t nrows, uint32_t ntok, uint32_t nb, float *out, size_t stride, const char *who) {
+    if (!ready()) return;
+    if (!nrows || !ntok) return;
+    if (!check_operands(w, row_bytes, nrows, nb, q5, xd, xq, ntok, nb, out, stride, who)) return;
+    const smq::MatArgs a = one_item(w, row_bytes, xd, xq, nrows, ntok, nb, nb, out, stride);
+    /* rows or activations the MFMA staging cannot load take the exact GEMM */
+    hip_ok(smq::mfma_layout_ok(a, q5) ? smq::launch_matmul_mfma(a, q5, nullptr, g.cur)
+                                      : smq::launch_matmul(a, q5, g.fast != 0, g.cur),
            who);
 }
 
@@ -301,6 +314,45 @@ void smq_gemm_q5(const unsigned char *w, size_t row_bytes, const float *xd, cons
     gemm_impl(true, w, row_bytes, xd, xq, nrows, ntok, nb, nb, out, stride, "gemm_q5");
 }
 
+void smq_gemm_q8_mfma(const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq, uint32_t nrows,
+                      uint32_t ntok, uint32_t nb, float *out, size_t stride, unsigned char *scratch) {
+    (void)scratch;
+    gemm_mfma_impl(false, w, row_bytes, xd, xq, nrows, ntok, nb, out, stride, "gemm_q8_mfma");
+}
+void smq_gemm_q5_mfma(const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq, uint32_t nrows,
+                      uint32_t ntok, uint32_t nb, float *out, size_t stride, unsigned char *scratch) {
+    (void)scratch;
+    gemm_mfma_impl(true, w, row_bytes, xd, xq, nrows, ntok, nb, out, stride, "gemm_q5_mfma");
+}
+
+void smq_block_sums(int q5, const unsigned char *w, size_t row_bytes, const int8_t *xq, uint32_t nrows,
+                    uint32_t ntok, uint32_t nb, int32_t *sums) {
+    if (!ready()) return;
+    if (!nrows || !ntok) return;
+    if (!nb) {
+        set_status(SMQ_ERR_RANGE, "block_sums: nb is 0");
+        return;
+    }
+    const size_t row_need = (size_t)nb * block_bytes(q5 != 0);
+    if (row_bytes < row_need) {
+        set_status(SMQ_ERR_RANGE, "block_sums: row_bytes %zu < nb*%u", row_bytes, block_bytes(q5 != 0));
+        return;
+    }
+    if (!extent_ok(w, (size_t)(nrows - 1) * row_bytes + row_need, "weights") ||
+        !extent_ok(xq, (size_t)ntok * nb * smq::QK, "activations") ||
+        !extent_ok(sums, (size_t)ntok * nrows * nb * sizeof(int32_t), "sums"))
+        return;
+    /* scales are not read in this mode: xq stands in for the scale pointer */
+    smq::MatArgs a = one_item(w, row_bytes, (const float *)(const void *)xq, xq, nrows, ntok, nb, nb, nullptr, nrows);
+    if (!smq::mfma_layout_ok(a, q5 != 0)) {
+        set_status(SMQ_ERR_RANGE, "block_sums: rows and activations must be 4-byte aligned (and nb even for Q5)");
+        return;
+    }
+    hip_ok(smq::launch_matmul_mfma(a, q5 != 0, sums, g.cur), "block_sums");
+}
+
+void smq_set_prefill_mfma(int on) { g.prefill_mfma = on ? 1 : 0; }
+
 smq_status smq_matmul(const smq_mat_item *items, uint32_t n, const float *xd, const int8_t *xq, uint32_t ntok) {
     if (!ready()) return t_status;
     if (!items || n < 1 || n > SMQ_MAX_ITEMS) return set_status(SMQ_ERR_RANGE, "matmul: %u items", n);
@@ -339,7 +391,12 @@ smq_status smq_matmul(const smq_mat_item *items, uint32_t n, const float *xd, co
             it.y_stride = w->rows;
             it.rows = w->rows;
         }
-        if (a.nitems && !hip_ok(smq::launch_matmul(a, q5 == 1, g.fast != 0, g.cur), "matmul")) return t_status;
+        if (!a.nitems) continue;
+        const bool mfma = ntok > 1 && g.prefill_mfma && smq::mfma_layout_ok(a, q5 == 1);
+        if (!hip_ok(mfma ? smq::launch_matmul_mfma(a, q5 == 1, nullptr, g.cur)
+                         : smq::launch_matmul(a, q5 == 1, g.fast != 0, g.cur),
+                    "matmul"))
+            return t_status;
     }
     return SMQ_OK;
 }

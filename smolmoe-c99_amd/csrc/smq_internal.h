@@ -43,6 +43,11 @@ struct MatArgs {
 hipError_t launch_quantize_q8(const float *x, uint32_t rows, uint32_t n, float *d, int8_t *q, int *flag,
                               hipStream_t s);
 hipError_t launch_matmul(const MatArgs &a, bool q5, bool fast, hipStream_t s);
+/* Int8-MFMA prefill GEMM (relaxed block order). sums != NULL writes the exact
+ * per-block int32 sums, sums[(t*rows + r)*nb + b], instead of the outputs.
+ * mfma_layout_ok: 4-byte aligned rows and activations, even nb for Q5. */
+bool mfma_layout_ok(const MatArgs &a, bool q5);
+hipError_t launch_matmul_mfma(const MatArgs &a, bool q5, int32_t *sums, hipStream_t s);
 hipError_t launch_dequantize_row(const unsigned char *w, uint32_t cols, float *out, bool q5, hipStream_t s);
 
 }  // namespace smq

@@ -444,6 +444,192 @@ __global__ __launch_bounds__(WG) void k_gemm_exact(MatArgs a, uint32_t tok_tiles
 }
 
 /* ------------------------------------------------------------------------
+ * Prefill GEMM on int8 MFMA (relaxed block order). A Q8 block is exactly the
+ * K = 32 of v_mfma_i32_16x16x32_i8, so one MFMA per (16 rows x 16 tokens,
+ * block) yields the exact int32 block sums S; the epilogue then applies the
+ * block's scales, acc = fma(wscale * xscale, float(S), acc), blocks in order.
+ * The per-block integer sums are bit-exact; the f32 result differs from the
+ * eight-lane contract only in rounding (within 1e-5 relative).
+ * Workgroup tile: 32 rows x 64 tokens; wave w owns rows 16*(w/2).. and tokens
+ * 32*(w%2).. (two 16x16 tiles). K is staged in chunks of 8 blocks, stored in
+ * MFMA operand order so that a wave's operand read is one contiguous 512-byte
+ * run: A[block][k8 chunk][row] and B[block][k8 chunk][token], 8 bytes each.
+ * Operand layout (16x16x32 i8): lane l supplies A[l%16][8*(l/16)+0..7] and
+ * B[8*(l/16)+0..7][l%16]; it receives D[4*(l/16)+v][l%16], v = 0..3.
+ * SUMS writes the raw block sums instead (test entry point).
+ * ---------------------------------------------------------------------- */
+constexpr int MT_R = 32, MT_T = 64, MT_CB = 8;
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+template <bool Q5, bool SUMS>
+__global__ __launch_bounds__(WG) void k_gemm_mfma(MatArgs a, uint32_t tok_tiles, int32_t *sums) {
+    __shared__ __attribute__((aligned(16))) uint2 wqa[MT_CB][4][MT_R];
+    __shared__ __attribute__((aligned(16))) uint2 xqb[MT_CB][4][MT_T];
+    __shared__ __attribute__((aligned(16))) float wsl[MT_CB][MT_R];
+    __shared__ __attribute__((aligned(16))) float xsl[MT_CB][MT_T];
+
+    const uint32_t tid = threadIdx.x, nb = a.nb, l = tid % 64, w = tid / 64;
+    const uint32_t G = gridDim.x, xcd = blockIdx.x % 8u, kk = blockIdx.x / 8u;
+    const uint32_t per = G / 8u, extra = G % 8u;
+    const uint32_t L = xcd * per + (xcd < extra ? xcd : extra) + kk;
+    const uint32_t row_tile = L / tok_tiles, tok_tile = L % tok_tiles;
+    const Item &I = a.item[find_item(a, row_tile)];
+    const uint32_t r0 = (row_tile - I.tile_begin) * MT_R, t0 = tok_tile * MT_T;
+
+    /* staging roles: weights (row, pair of blocks), threads 0..127; a wave
+     * writes 32 consecutive rows of one block. Activations: a wave stages one
+     * (block, half) for 64 consecutive tokens (one contiguous LDS run). */
+    const uint32_t srow = tid % 32, spair = tid / 32;
+    const bool srow_ok = tid < 128 && r0 + srow < I.rows;
+    const unsigned char *wrow = I.w + (size_t)(srow_ok ? r0 + srow : 0) * I.row_bytes;
+
+    uint32_t wr[Q5 ? 11 : 18] = {};
+    u4a xr[4] = {};
+    float xs[2] = {};
+    auto fetch = [&](uint32_t c) {
+        const uint32_t b = c * MT_CB + spair * 2;
+        if (tid < 128) {
+            if (Q5) {
+                if (srow_ok && b < nb) {
+                    const unsigned char *p = wrow + (size_t)b * Q5_BYTES;
+                    const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
+                    const u3a v2 = *(const u3a *)(p + 32);
+                    wr[0] = v0.x; wr[1] = v0.y; wr[2] = v0.z; wr[3] = v0.w;
+                    wr[4] = v1.x; wr[5] = v1.y; wr[6] = v1.z; wr[7] = v1.w;
+                    wr[8] = v2.x; wr[9] = v2.y; wr[10] = v2.z;
+                }
+            } else {
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    if (srow_ok && b + h < nb) {
+                        const unsigned char *p = wrow + (size_t)(b + h) * Q8_BYTES;
+                        const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
+                        wr[9 * h + 0] = v0.x; wr[9 * h + 1] = v0.y; wr[9 * h + 2] = v0.z; wr[9 * h + 3] = v0.w;
+                        wr[9 * h + 4] = v1.x; wr[9 * h + 5] = v1.y; wr[9 * h + 6] = v1.z; wr[9 * h + 7] = v1.w;
+                        wr[9 * h + 8] = *(const uint32_t *)(p + 32);
+                    }
+            }
+        }
+        /* 64 tokens x 8 blocks x 32 bytes = 1024 pieces of 16 bytes, 4 per thread */
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const uint32_t piece = tid + WG * h, tok = piece % 64, rest = piece / 64, bb = rest / 2, half = rest % 2;
+            const uint32_t t = t0 + tok, b = c * MT_CB + bb;
+            if (t < a.ntok && b < nb)
+                xr[h] = *(const u4a *)(a.xq + ((size_t)t * a.xstride + b) * QK + half * 16);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t e = tid + WG * h, tok = e / MT_CB, bb = e % MT_CB;
+            const uint32_t t = t0 + tok, b = c * MT_CB + bb;
+            if (t < a.ntok && b < nb) xs[h] = a.xd[(size_t)t * a.xstride + b];
+        }
+    };
+    auto stage = [&](uint32_t c) {
+        if (tid < 128) {
+            const uint32_t b = c * MT_CB + spair * 2;
+            Q5Fields f[2];
+            if (Q5) q5_parse_pair(wr, f[0], f[1]);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t bb = spair * 2 + h;
+                const bool ok = srow_ok && b + h < nb;
+                uint32_t wv[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) wv[k] = ok ? (Q5 ? q5_signed(f[h], k) : wr[9 * h + 1 + k]) : 0u;
+                wsl[bb][srow] = ok ? (Q5 ? f[h].scale : __uint_as_float(wr[9 * h])) : 0.0f;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) wqa[bb][k][srow] = make_uint2(wv[2 * k], wv[2 * k + 1]);
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const uint32_t piece = tid + WG * h, tok = piece % 64, rest = piece / 64, bb = rest / 2, half = rest % 2;
+            const bool ok = t0 + tok < a.ntok && c * MT_CB + bb < nb;
+            xqb[bb][2 * half][tok] = ok ? make_uint2(xr[h].x, xr[h].y) : make_uint2(0u, 0u);
+            xqb[bb][2 * half + 1][tok] = ok ? make_uint2(xr[h].z, xr[h].w) : make_uint2(0u, 0u);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t e = tid + WG * h, tok = e / MT_CB, bb = e % MT_CB;
+            xsl[bb][tok] = (t0 + tok < a.ntok && c * MT_CB + bb < nb) ? xs[h] : 0.0f;
+        }
+    };
+
+    const uint32_t wrow0 = 16 * (w / 2), wtok0 = 32 * (w % 2);
+    float acc[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[j][v] = 0.0f;
+    const v4i zero = {0, 0, 0, 0};
+
+    const uint32_t nchunks = (nb + MT_CB - 1) / MT_CB;
+    fetch(0);
+    for (uint32_t c = 0; c < nchunks; ++c) {
+        stage(c);
+        __syncthreads();
+        if (c + 1 < nchunks) fetch(c + 1);
+        const uint32_t count = nb - c * MT_CB < (uint32_t)MT_CB ? nb - c * MT_CB : (uint32_t)MT_CB;
+        auto block_sums = [&](uint32_t bb, v4i S[2]) {
+            const uint2 av = wqa[bb][l / 16][wrow0 + l % 16];
+            const long A = (long)(((unsigned long)av.y << 32) | av.x);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint2 bv = xqb[bb][l / 16][wtok0 + 16 * j + l % 16];
+                const long B = (long)(((unsigned long)bv.y << 32) | bv.x);
+                S[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
+            }
+        };
+        auto epilogue = [&](uint32_t bb, const v4i S[2]) {
+            const float4 ws4 = *(const float4 *)&wsl[bb][wrow0 + 4 * (l / 16)];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if (SUMS) {
+                    const uint32_t t = t0 + wtok0 + 16 * j + l % 16, b = c * MT_CB + bb;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const uint32_t r = r0 + wrow0 + 4 * (l / 16) + v;
+                        if (r < I.rows && t < a.ntok) sums[((size_t)t * I.rows + r) * nb + b] = S[j][v];
+                    }
+                } else {
+                    const float xsc = xsl[bb][wtok0 + 16 * j + l % 16];
+                    acc[j][0] = __builtin_fmaf(ws4.x * xsc, (float)S[j][0], acc[j][0]);
+                    acc[j][1] = __builtin_fmaf(ws4.y * xsc, (float)S[j][1], acc[j][1]);
+                    acc[j][2] = __builtin_fmaf(ws4.z * xsc, (float)S[j][2], acc[j][2]);
+                    acc[j][3] = __builtin_fmaf(ws4.w * xsc, (float)S[j][3], acc[j][3]);
+                }
+            }
+        };
+        if (count == (uint32_t)MT_CB) {
+            /* all MFMAs of the chunk first (16 independent ones per wave), then
+             * the scale epilogue in block order */
+            v4i S[MT_CB][2];
+#pragma unroll
+            for (int bb = 0; bb < MT_CB; ++bb) block_sums(bb, S[bb]);
+#pragma unroll
+            for (int bb = 0; bb < MT_CB; ++bb) epilogue(bb, S[bb]);
+        } else {
+            for (uint32_t bb = 0; bb < count; ++bb) {
+                v4i S[2];
+                block_sums(bb, S);
+                epilogue(bb, S);
+            }
+        }
+        __syncthreads();
+    }
+    if (!SUMS) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t r = r0 + wrow0 + 4 * (l / 16) + v, t = t0 + wtok0 + 16 * j + l % 16;
+                if (r < I.rows && t < a.ntok) store_out(I, a.flag, t, r, acc[j][v]);
+            }
+    }
+}
+
+/* ------------------------------------------------------------------------
  * Generic path: any alignment, any width. One thread per (row, token), byte
  * reads. Used for shapes the tiled kernels do not take (unaligned rows, odd
  * Q5 widths, nb > MAX_FAST_NB); same contract, bit for bit.
@@ -641,7 +827,34 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <bool Q5, bool SUMS>
+hipError_t launch_mfma_typed(MatArgs a, int32_t *sums, hipStream_t s) {
+    uint32_t tiles = 0;
+    for (uint32_t i = 0; i < a.nitems; ++i) {
+        a.item[i].tile_begin = tiles;
+        tiles += (a.item[i].rows + MT_R - 1) / MT_R;
+    }
+    const uint32_t tok_tiles = (a.ntok + MT_T - 1) / MT_T;
+    if (!tiles || !tok_tiles || !a.nb) return hipSuccess;
+    hipLaunchKernelGGL((k_gemm_mfma<Q5, SUMS>), dim3(tiles * tok_tiles), dim3(WG), 0, s, a, tok_tiles, sums);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+bool mfma_layout_ok(const MatArgs &a, bool q5) {
+    if (a.nb == 0) return false;
+    if (((uintptr_t)a.xq | (uintptr_t)a.xd) & 3u) return false;
+    if (q5 && (a.nb & 1u)) return false;
+    for (uint32_t i = 0; i < a.nitems; ++i)
+        if ((((uintptr_t)a.item[i].w) | a.item[i].row_bytes) & 3u) return false;
+    return true;
+}
+
+hipError_t launch_matmul_mfma(const MatArgs &a, bool q5, int32_t *sums, hipStream_t s) {
+    if (sums) return q5 ? launch_mfma_typed<true, true>(a, sums, s) : launch_mfma_typed<false, true>(a, sums, s);
+    return q5 ? launch_mfma_typed<true, false>(a, nullptr, s) : launch_mfma_typed<false, false>(a, nullptr, s);
+}
 
 hipError_t launch_matmul(const MatArgs &a, bool q5, bool fast, hipStream_t s) {
     if (q5) return fast ? launch_typed<true, true>(a, s) : launch_typed<true, false>(a, s);

@@ -358,3 +358,70 @@ def test_every_gemv_tile_variant(orc, rt, stage, monkeypatch):
             got, xd, xq = run_gemm(w, nb * (Q5B if q5 else Q8B), x, rows, 1, nb, q5, fast=fast)
             want = orc.gemm(w, nb * (Q5B if q5 else Q8B), xd, xq, rows, 1, nb, q5=q5, fast=fast)
             assert_same_f32(got, want, f"rt={rt} stage={stage} q5={q5} nb={nb} fast={fast}")
+
+
+# ------------------------------------------------------------------ MFMA prefill
+
+def mfma_tolerance_ok(got, want, ntok, rows):
+    """North-star tolerance for the relaxed-order path: per token,
+    max_r |got - want| <= 1e-5 * max_r |want| (relative error in the max norm)."""
+    g = got.reshape(ntok, -1)[:, :rows].astype(np.float64)
+    w = want.reshape(ntok, -1)[:, :rows].astype(np.float64)
+    err = np.abs(g - w).max(axis=1)
+    scale = np.abs(w).max(axis=1)
+    return bool(np.all(err <= 1e-5 * scale)), float((err / np.maximum(scale, 1e-30)).max())
+
+
+MFMA_SHAPES = [("c1-gate-b128", False, 4864, 896, 128), ("c1-down-b128", False, 896, 4864, 128),
+               ("c2-up-b64", True, 8960, 1536, 64), ("c2-down-b64", True, 1536, 8960, 64),
+               ("ragged", False, 77, 416, 13), ("ragged-q5", True, 45, 64 * 5, 70), ("one-token", False, 33, 96, 1)]
+
+
+@pytest.mark.parametrize("name,q5,rows,cols,ntok", MFMA_SHAPES)
+def test_mfma_block_sums_exact_and_outputs_within_tolerance(orc, name, q5, rows, cols, ntok):
+    say("mfma", name)
+    nb = (cols + 31) // 32
+    bb = Q5B if q5 else Q8B
+    w = weights(q5, 3000 + rows, rows, cols)
+    x = synth.activations(4000 + cols + ntok, ntok, cols)
+    dbuf, qbuf, xd, xq = gpu_quantize(x)
+    wb = smq.DeviceBuffer.from_array(w)
+    # integer path: every per-block int32 sum bit-exact
+    sums = smq.DeviceBuffer(ntok * rows * nb * 4)
+    smq.block_sums(q5, wb, nb * bb, qbuf, rows, ntok, nb, sums)
+    want_sums = orc.block_sums(w, nb * bb, xq, rows, ntok, nb, q5=q5)
+    assert np.array_equal(sums.download(np.int32).reshape(ntok, rows, nb), want_sums), name
+    # f32 outputs within 1e-5 of the exact contract
+    out = smq.DeviceBuffer(ntok * rows * 4)
+    (smq.gemm_q5_mfma if q5 else smq.gemm_q8_mfma)(wb, nb * bb, dbuf, qbuf, rows, ntok, nb, out, rows)
+    want = orc.gemm(w, nb * bb, xd, xq, rows, ntok, nb, q5=q5)
+    ok, worst = mfma_tolerance_ok(out.download(np.float32), want, ntok, rows)
+    say("  worst normwise relative error", worst)
+    assert ok, (name, worst)
+
+
+def test_matmul_prefill_switch(orc):
+    """smq_matmul with ntok > 1 takes the MFMA GEMM when selected (bias and
+    finiteness still applied), the exact GEMM otherwise."""
+    cols, nb, ntok = 896, 28, 32
+    x = synth.activations(77, ntok, cols)
+    dbuf, qbuf, xd, xq = gpu_quantize(x)
+    items, wants = [], []
+    for i, rows in enumerate((896, 128)):
+        w = weights(False, 80 + i, rows, cols)
+        bias = synth.normal(90 + i, rows, 0.05)
+        items.append((smq.QMat(smq.DeviceBuffer.from_array(w), rows, cols), smq.DeviceBuffer.from_array(bias),
+                      smq.DeviceBuffer(ntok * rows * 4)))
+        wants.append(orc.mat_item(w, nb * Q8B, rows, bias, xd, xq, ntok, nb)[1])
+    try:
+        smq.set_prefill_mfma(True)
+        smq.matmul(items, dbuf, qbuf, ntok)
+        smq.numeric_check()
+        for (wq, _, y), want in zip(items, wants):
+            ok, worst = mfma_tolerance_ok(y.download(np.float32), want, ntok, wq.rows)
+            assert ok, worst
+    finally:
+        smq.set_prefill_mfma(False)
+    smq.matmul(items, dbuf, qbuf, ntok)
+    for (_, _, y), want in zip(items, wants):
+        assert_same_f32(y.download(np.float32), want, "exact prefill")

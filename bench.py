@@ -137,7 +137,69 @@ def cpu_baseline(model, acts_x, acts_h, threads_list, budget_s, gpu_out):
     return kind, name, out, gate
 
 
+def traffic_probe():
+    """Short program for rocprofv3 --pmc runs: 8 launches of the dominant
+    kernel (fused gate+up GEMV, 9728x896 Q8) on 8 distinct weight copies, then
+    one 256 MiB device-to-device copy whose FETCH_SIZE / WRITE_SIZE calibrate the
+    counters (expected 262,144 KiB each)."""
+    smq.init(0)
+    layer = Layer(1000)
+    ax = Act(2000, 1, DIM)
+    gu = smq.DeviceBuffer(2 * HIDDEN * 4)
+    mats = []
+    for _ in range(8):
+        g_ = smq.DeviceBuffer(layer.dev["gate"][0].nbytes)
+        u_ = smq.DeviceBuffer(layer.dev["up"][0].nbytes)
+        g_.copy_from(layer.dev["gate"][0])
+        u_.copy_from(layer.dev["up"][0])
+        mats.append((smq.QMat(g_, HIDDEN, DIM), smq.QMat(u_, HIDDEN, DIM)))
+    big = [smq.DeviceBuffer(256 << 20) for _ in range(2)]
+    big[0].fill(1)
+    smq.synchronize()
+    for g_, u_ in mats:
+        smq.matmul([(g_, None, gu.ptr), (u_, None, gu.ptr + HIDDEN * 4)], ax.d, ax.q, 1)
+    smq.synchronize()
+    big[1].copy_from(big[0])
+    smq.synchronize()
+    print("traffic probe done", flush=True)
+
+
+def summarize_pmc(fetch_dir, write_dir):
+    """Per-dispatch HBM traffic of the gate+up GEMV from two rocprofv3 --pmc
+    runs of --traffic-probe, scaled by the copy's counter reading."""
+    import csv
+    import glob
+
+    def read(d, counter):
+        rows = []
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            rows += [r for r in csv.DictReader(open(f)) if r["Counter_Name"] == counter]
+        gemv = [float(r["Counter_Value"]) for r in rows if "k_gemv" in r["Kernel_Name"]]
+        copy = sum(float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]
+                   and float(r["Counter_Value"]) > 1e5)
+        return gemv, copy
+
+    fetch, fcopy = read(fetch_dir, "FETCH_SIZE")
+    write, wcopy = read(write_dir, "WRITE_SIZE")
+    expect = 256 * 1024.0  # KiB moved by the 256 MiB copy
+    fscale, wscale = expect / fcopy, expect / wcopy
+    f_kib = float(np.median(fetch)) * fscale
+    w_kib = float(np.median(write)) * wscale
+    out = {"fetch_kib_raw_median": float(np.median(fetch)), "write_kib_raw_median": float(np.median(write)),
+           "copy_fetch_kib_raw": fcopy, "copy_write_kib_raw": wcopy, "fetch_scale": fscale, "write_scale": wscale,
+           "traffic_bytes": int((f_kib + w_kib) * 1024), "algorithmic_bytes": q8_bytes(2 * HIDDEN, DIM),
+           "dispatches": len(fetch)}
+    print(json.dumps(out))
+    return out
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "--traffic-probe":
+        traffic_probe()
+        return
+    if len(sys.argv) > 1 and sys.argv[1] == "--summarize-pmc":
+        summarize_pmc(sys.argv[2], sys.argv[3])
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
@@ -291,6 +353,12 @@ def main():
         except Exception as ex:  # the CPU leg must not hide the GPU result
             log(f"bench: cpu baseline failed: {ex!r}")
 
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "gemv_q8_gateup_9728x896_traffic.json")
+    if os.path.exists(tfile):  # measured by two rocprofv3 --pmc runs of --traffic-probe (see that file)
+        with open(tfile) as f:
+            traffic = json.load(f).get("traffic_bytes")
+
     line = {
         "metric": "Q8_0/Q5_0 GEMV HBM GB/s (% of peak); decode tok/s at Qwen2.5-0.5B shape",
         "value": round(value, 1),
@@ -311,7 +379,7 @@ def main():
         "ffn_decode_tok_s": round(1000.0 / ms_per_step, 1),
         "roofline": {"kernel": "k_gemv<Q8,exact,RT=8,direct> (fused gate+up, 9728x896)", "bound": "hbm",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_per_launch": gu_bytes, "us_per_launch": round(gu_ms * 1e3, 3)},
         "cpu_baseline": cpu,
         "extra": extra,

@@ -93,6 +93,26 @@ int smq_quantize_q8(const float *x, uint32_t n, float *d, int8_t *q);
  * input raises the sticky numeric flag read by smq_numeric_check. */
 smq_status smq_quantize_q8_rows(const float *x, uint32_t rows, uint32_t n, float *d, int8_t *q);
 
+/* ---- activation producers (src/model.c:347-415, src/vecmath.c:61-93) ----
+ * The caller's per-token row work (row_work, model.c:354-362) for `rows` rows
+ * of n floats (n <= 16384): optional RMSNorm with weight `norm` (NULL: none)
+ * and eps (model.c:334-342, sequential f32 sum of squares); optional gated
+ * activation with `gate` (act 0 = none, 1 = SwiGLU vecmath.c:78-81,
+ * 2 = GeGLU vecmath.c:86-93, both with the deterministic binary64 exp of
+ * vecmath.c:61-76); the f32 result stored to y when y != NULL (y may alias
+ * src, as silu_quantize updates m->up in place); then quantize_q8 into
+ * d + r*nb, q + r*nb*32. Bit-identical to the reference. A non-finite sum,
+ * scale or value raises the sticky numeric flag. Asynchronous. */
+smq_status smq_row_quantize(const float *src, const float *norm, float eps, const float *gate, int act, uint32_t rows,
+                            uint32_t n, float *y, float *d, int8_t *q);
+/* norm_quantize (model.c:393-400): RMSNorm then quantize. */
+smq_status smq_norm_quantize(const float *src, const float *norm, float eps, uint32_t rows, uint32_t n, float *y,
+                             float *d, int8_t *q);
+/* silu_quantize (model.c:409-415): up *= act(gate) in place, then quantize;
+ * gemma3 != 0 selects GeGLU. */
+smq_status smq_silu_quantize(float *up, const float *gate, int gemma3, uint32_t rows, uint32_t n, float *d,
+                             int8_t *q);
+
 /* ---- dot products and gemm (src/kernels.h:49-70) -------------------------
  * Parameter lists are those of DotQ8, DotQ8x4, DotQ8R4 and GemmQ8. out is a
  * device array; smq_dot_q8/q5 return the value (synchronous). */

@@ -72,6 +72,14 @@ class Oracle:
         lib.orc_q8_weight_rows.argtypes = [_f32p, _u32, _u32, _u8p]
         lib.orc_quantize_q5_row.argtypes = [_f32p, _u32, _u8p]
         lib.orc_dequantize_row.argtypes = [ctypes.c_int, _u8p, _u32, _f32p]
+        lib.orc_exp2_table.restype = ctypes.POINTER(ctypes.c_uint64)
+        lib.orc_exp_det.restype = ctypes.c_float
+        lib.orc_exp_det.argtypes = [ctypes.c_float]
+        lib.orc_silu_mul.argtypes = [_f32p, _f32p, _sz]
+        lib.orc_gelu_mul.argtypes = [_f32p, _f32p, _sz]
+        lib.orc_row_work.restype = ctypes.c_int
+        lib.orc_row_work.argtypes = [_f32p, _f32p, ctypes.c_float, _f32p, ctypes.c_int, _u32, _u32, _f32p, _f32p,
+                                     _i8p]
         lib.orc_time_gemm_pass.restype = ctypes.c_double
         lib.orc_time_gemm_pass.argtypes = [ctypes.c_void_p, ctypes.POINTER(_u8p), ctypes.POINTER(_u32),
                                            ctypes.POINTER(_u32), ctypes.POINTER(_f32p), ctypes.POINTER(_i8p), _u32,
@@ -155,6 +163,35 @@ class Oracle:
         self.lib.orc_split_range(total, index, count, ctypes.byref(b), ctypes.byref(e))
         return b.value, e.value
 
+    # -- deterministic exp and gated activations
+    def exp2_table(self):
+        t = self.lib.orc_exp2_table()
+        return [t[i] for i in range(32)]
+
+    def exp_det(self, x):
+        return self.lib.orc_exp_det(float(x))
+
+    def act_mul(self, up, gate, gelu=False):
+        up = np.array(up, np.float32, copy=True)
+        gate = np.ascontiguousarray(gate, np.float32)
+        fn = self.lib.orc_gelu_mul if gelu else self.lib.orc_silu_mul
+        fn(_ptr(up, _f32p), _ptr(gate, _f32p), up.shape[0])
+        return up
+
+    def row_work(self, src, rows, n, norm=None, eps=1e-6, gate=None, gelu=False):
+        """model.c:354-362 over `rows` rows: (ok, y, d, q)."""
+        src = np.ascontiguousarray(src, np.float32)
+        nb = (n + 31) // 32
+        y = np.zeros(rows * n, np.float32)
+        d = np.zeros(rows * nb, np.float32)
+        q = np.zeros(rows * nb * 32, np.int8)
+        np_ = None if norm is None else np.ascontiguousarray(norm, np.float32)
+        gp = None if gate is None else np.ascontiguousarray(gate, np.float32)
+        ok = self.lib.orc_row_work(_ptr(src, _f32p), None if np_ is None else _ptr(np_, _f32p), eps,
+                                   None if gp is None else _ptr(gp, _f32p), int(gelu), rows, n, _ptr(y, _f32p),
+                                   _ptr(d, _f32p), _ptr(q, _i8p))
+        return bool(ok), y, d, q
+
     # -- offline weight rules
     def q8_weight_rows(self, x):
         x = np.ascontiguousarray(x, np.float32)
@@ -231,6 +268,10 @@ class Reference:
         lib.dequantize_q5_row.argtypes = [_u8p, _u32, _f32p]
         lib.gemm_scratch_bytes.restype = _sz
         lib.gemm_scratch_bytes.argtypes = [_u32]
+        lib.exp_det.restype = ctypes.c_float
+        lib.exp_det.argtypes = [ctypes.c_float]
+        lib.silu_mul_scalar.argtypes = [_f32p, _f32p, _sz]
+        lib.gelu_mul_scalar.argtypes = [_f32p, _f32p, _sz]
 
     def quantize_q8(self, x, avx2=False):
         x = np.ascontiguousarray(x, np.float32)
@@ -267,6 +308,16 @@ class Reference:
         fn = self.lib.dequantize_q5_row if q5 else self.lib.dequantize_q8_row
         fn(_ptr(w, _u8p), cols, _ptr(out, _f32p))
         return out
+
+    def exp_det(self, x):
+        return self.lib.exp_det(float(x))
+
+    def act_mul(self, up, gate, gelu=False):
+        up = np.array(up, np.float32, copy=True)
+        gate = np.ascontiguousarray(gate, np.float32)
+        fn = self.lib.gelu_mul_scalar if gelu else self.lib.silu_mul_scalar
+        fn(_ptr(up, _f32p), _ptr(gate, _f32p), up.shape[0])
+        return up
 
     def fn_addr(self, name):
         return ctypes.cast(getattr(self.lib, name), ctypes.c_void_p).value

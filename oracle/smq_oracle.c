@@ -304,6 +304,100 @@ int orc_rmsnorm(const float *x, const float *w, float *y, uint32_t n, float eps)
     return 0;
 }
 
+/* ---- deterministic exp and the gated activations (src/vecmath.c:19-93) - */
+
+/* vecmath.c:44-52: bits of 2^(j/32) (correctly rounded binary64) minus j<<47;
+ * regenerated from the mathematics by oracle/gen_exp_table.py. */
+static const uint64_t ORC_EXP2[32] = {
+    0x3ff0000000000000u, 0x3fefd9b0d3158574u, 0x3fefb5586cf9890fu, 0x3fef9301d0125b51u,
+    0x3fef72b83c7d517bu, 0x3fef54873168b9aau, 0x3fef387a6e756238u, 0x3fef1e9df51fdee1u,
+    0x3fef06fe0a31b715u, 0x3feef1a7373aa9cbu, 0x3feedea64c123422u, 0x3feece086061892du,
+    0x3feebfdad5362a27u, 0x3feeb42b569d4f82u, 0x3feeab07dd485429u, 0x3feea47eb03a5585u,
+    0x3feea09e667f3bcdu, 0x3fee9f75e8ec5f74u, 0x3feea11473eb0187u, 0x3feea589994cce13u,
+    0x3feeace5422aa0dbu, 0x3feeb737b0cdc5e5u, 0x3feec49182a3f090u, 0x3feed503b23e255du,
+    0x3feee89f995ad3adu, 0x3feeff76f2fb5e47u, 0x3fef199bdd85529cu, 0x3fef3720dcef9069u,
+    0x3fef5818dcfba487u, 0x3fef7c97337b9b5fu, 0x3fefa4afa2a490dau, 0x3fefd0765b6e4540u,
+};
+
+const uint64_t *orc_exp2_table(void) { return ORC_EXP2; }
+
+/* vecmath.c:61-76: e^x = 2^(k/32) * e^(r ln2/32) with k = round(32x/ln2)
+ * taken from the low bits after adding 1.5*2^52, r the remainder, a degree-4
+ * Taylor polynomial evaluated with separate multiplies and adds (no FMA),
+ * everything in binary64, one rounding to binary32. Clamped to [-104, 89]. */
+float orc_exp_det(float x) {
+    const double inv_ln2_n = 0x1.71547652b82fep+5, shift = 0x1.8p+52;
+    const double a = 0x1.62e42fefa39efp-1 / 32;
+    const double c1 = a, c2 = a * a / 2, c3 = a * a * a / 6, c4 = a * a * a * a / 24;
+    double z, kd, r, p, scale;
+    uint64_t ki, sb;
+    if (x != x) return x;
+    if (x > 89.0f) x = 89.0f;
+    if (x < -104.0f) x = -104.0f;
+    z = inv_ln2_n * (double)x;
+    kd = z + shift;
+    memcpy(&ki, &kd, 8);
+    kd = kd - shift;
+    r = z - kd;
+    p = c4 * r + c3;
+    p = p * r + c2;
+    p = p * r + c1;
+    p = p * r + 1.0;
+    sb = ORC_EXP2[ki & 31u] + (ki << 47);
+    memcpy(&scale, &sb, 8);
+    return (float)(p * scale);
+}
+
+/* vecmath.c:78-81: up *= gate / (1 + e^-gate). */
+void orc_silu_mul(float *up, const float *gate, size_t n) {
+    size_t i;
+    for (i = 0; i < n; ++i) {
+        float den = 1.0f + orc_exp_det(-gate[i]);
+        float s = gate[i] / den;
+        up[i] = up[i] * s;
+    }
+}
+
+/* vecmath.c:86-93: up *= g / (1 + e^-(1.5957691216 (g + 0.044715 g^3))). */
+void orc_gelu_mul(float *up, const float *gate, size_t n) {
+    size_t i;
+    for (i = 0; i < n; ++i) {
+        float g = gate[i];
+        float g3 = 0.044715f * g * g * g;
+        float u = 1.5957691216f * (g + g3);
+        float den = 1.0f + orc_exp_det(-u);
+        float s = g / den;
+        up[i] = up[i] * s;
+    }
+}
+
+/* model.c:354-362 row_work for `rows` token rows of n values: optional RMSNorm
+ * (norm != NULL, into y), optional gated activation (gate != NULL: y *= act),
+ * then quantize_q8 into d/q. Returns 1 when every row was finite. y holds the
+ * pre-quantization rows (the source rows themselves when no norm is given). */
+int orc_row_work(const float *src, const float *norm, float eps, const float *gate, int gelu, uint32_t rows,
+                 uint32_t n, float *y, float *d, int8_t *q) {
+    uint32_t r, nb = (n + 31u) / 32u;
+    int ok = 1;
+    for (r = 0; r < rows; ++r) {
+        float *row = y + (size_t)r * n;
+        if (norm) {
+            if (orc_rmsnorm(src + (size_t)r * n, norm, row, n, eps)) {
+                ok = 0;
+                continue;
+            }
+        } else if (row != src + (size_t)r * n) {
+            memcpy(row, src + (size_t)r * n, (size_t)n * 4);
+        }
+        if (gate) {
+            if (gelu) orc_gelu_mul(row, gate + (size_t)r * n, n);
+            else orc_silu_mul(row, gate + (size_t)r * n, n);
+        }
+        if (orc_quantize_q8(row, n, d + (size_t)r * nb, q + (size_t)r * nb * 32u)) ok = 0;
+    }
+    return ok;
+}
+
 /* ---- offline weight rules --------------------------------------------- */
 
 /* tools/q8pack.c:38-44 (also scripts/smoe/quant.ts:73-97): per block

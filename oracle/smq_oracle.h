@@ -33,6 +33,13 @@ int orc_mat_item(int q5, int fast, const unsigned char *w, size_t row_bytes, uin
                  const float *xd, const int8_t *xq, uint32_t ntok, uint32_t nb, float *y);
 int orc_rmsnorm(const float *x, const float *w, float *y, uint32_t n, float eps);
 
+const uint64_t *orc_exp2_table(void);
+float orc_exp_det(float x);
+void orc_silu_mul(float *up, const float *gate, size_t n);
+void orc_gelu_mul(float *up, const float *gate, size_t n);
+int orc_row_work(const float *src, const float *norm, float eps, const float *gate, int gelu, uint32_t rows,
+                 uint32_t n, float *y, float *d, int8_t *q);
+
 void orc_q8_weight_rows(const float *x, uint32_t rows, uint32_t cols, unsigned char *out);
 void orc_quantize_q5_row(const float *x, uint32_t cols, unsigned char *out);
 void orc_dequantize_row(int q5, const unsigned char *w, uint32_t cols, float *out);

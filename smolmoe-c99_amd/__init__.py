@@ -68,6 +68,9 @@ _SIGS = {
     "smq_set_checks": (None, [ctypes.c_int]),
     "smq_quantize_q8": (ctypes.c_int, [_vp, _u32, _vp, _vp]),
     "smq_quantize_q8_rows": (ctypes.c_int, [_vp, _u32, _u32, _vp, _vp]),
+    "smq_row_quantize": (ctypes.c_int, [_vp, _vp, ctypes.c_float, _vp, ctypes.c_int, _u32, _u32, _vp, _vp, _vp]),
+    "smq_norm_quantize": (ctypes.c_int, [_vp, _vp, ctypes.c_float, _u32, _u32, _vp, _vp, _vp]),
+    "smq_silu_quantize": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _u32, _u32, _vp, _vp]),
     "smq_dot_q8": (ctypes.c_float, [_vp, _vp, _vp, _u32]),
     "smq_dot_q5": (ctypes.c_float, [_vp, _vp, _vp, _u32]),
     "smq_dot_q8_x4": (None, [_vp, _vp, _vp, _u32, _u32, _vp]),
@@ -238,6 +241,19 @@ def quantize_q8(x, n, d, q):
 
 def quantize_q8_rows(x, rows, n, d, q):
     _check(load().smq_quantize_q8_rows(_p(x), rows, n, _p(d), _p(q)))
+
+
+# ---- src/model.c:347-415
+def row_quantize(src, rows, n, d, q, norm=None, eps=1e-6, gate=None, act=0, y=None):
+    _check(load().smq_row_quantize(_p(src), _p(norm), eps, _p(gate), act, rows, n, _p(y), _p(d), _p(q)))
+
+
+def norm_quantize(src, norm, eps, rows, n, y, d, q):
+    _check(load().smq_norm_quantize(_p(src), _p(norm), eps, rows, n, _p(y), _p(d), _p(q)))
+
+
+def silu_quantize(up, gate, rows, n, d, q, gemma3=False):
+    _check(load().smq_silu_quantize(_p(up), _p(gate), int(bool(gemma3)), rows, n, _p(d), _p(q)))
 
 
 # ---- src/kernels.h:49-70

@@ -279,6 +279,36 @@ smq_status smq_quantize_q8_rows(const float *x, uint32_t rows, uint32_t n, float
     return hip_ok(smq::launch_quantize_q8(x, rows, n, d, q, g.flag, g.cur), "quantize_q8_rows") ? SMQ_OK : t_status;
 }
 
+smq_status smq_row_quantize(const float *src, const float *norm, float eps, const float *gate, int act, uint32_t rows,
+                            uint32_t n, float *y, float *d, int8_t *q) {
+    if (!ready()) return t_status;
+    if (!rows || !n) return SMQ_OK;
+    if (n > smq::MAX_ROW) return set_status(SMQ_ERR_RANGE, "row_quantize: %u columns exceed %u", n, smq::MAX_ROW);
+    if (act < 0 || act > 2) return set_status(SMQ_ERR_RANGE, "row_quantize: activation %d", act);
+    if (act && !gate) return set_status(SMQ_ERR_RANGE, "row_quantize: activation without gate");
+    const uint32_t nb = (n + smq::QK - 1) / smq::QK;
+    const size_t cells = (size_t)rows * n;
+    if (!extent_ok(src, cells * 4, "src") || !extent_ok(norm, norm ? (size_t)n * 4 : 0, "norm") ||
+        !extent_ok(gate, act ? cells * 4 : 0, "gate") || !extent_ok(y, y ? cells * 4 : 0, "y") ||
+        !extent_ok(d, (size_t)rows * nb * 4, "d") || !extent_ok(q, (size_t)rows * nb * smq::QK, "q"))
+        return t_status;
+    return hip_ok(smq::launch_row_quantize(src, norm, eps, act ? gate : nullptr, act, rows, n, y, d, q, g.flag, g.cur),
+                  "row_quantize")
+               ? SMQ_OK
+               : t_status;
+}
+
+smq_status smq_norm_quantize(const float *src, const float *norm, float eps, uint32_t rows, uint32_t n, float *y,
+                             float *d, int8_t *q) {
+    if (!norm) return set_status(SMQ_ERR_RANGE, "norm_quantize: norm is NULL");
+    return smq_row_quantize(src, norm, eps, nullptr, 0, rows, n, y, d, q);
+}
+
+smq_status smq_silu_quantize(float *up, const float *gate, int gemma3, uint32_t rows, uint32_t n, float *d,
+                             int8_t *q) {
+    return smq_row_quantize(up, nullptr, 0.0f, gate, gemma3 ? 2 : 1, rows, n, up, d, q);
+}
+
 float smq_dot_q8(const unsigned char *w, const float *xd, const int8_t *xq, uint32_t nb) {
     return dot_impl(false, w, xd, xq, nb);
 }

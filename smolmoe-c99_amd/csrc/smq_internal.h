@@ -48,6 +48,11 @@ hipError_t launch_matmul(const MatArgs &a, bool q5, bool fast, hipStream_t s);
  * mfma_layout_ok: 4-byte aligned rows and activations, even nb for Q5. */
 bool mfma_layout_ok(const MatArgs &a, bool q5);
 hipError_t launch_matmul_mfma(const MatArgs &a, bool q5, int32_t *sums, hipStream_t s);
+/* Activation producer rows (model.c:354-415): optional RMSNorm, optional
+ * gated activation (act 1 = SwiGLU, 2 = GeGLU), optional f32 store, Q8. */
+constexpr uint32_t MAX_ROW = 16384;
+hipError_t launch_row_quantize(const float *src, const float *norm, float eps, const float *gate, int act,
+                               uint32_t rows, uint32_t n, float *y, float *d, int8_t *q, int *flag, hipStream_t s);
 hipError_t launch_dequantize_row(const unsigned char *w, uint32_t cols, float *out, bool q5, hipStream_t s);
 
 }  // namespace smq

@@ -161,14 +161,27 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
     const Item &I = a.item[find_item(a, blockIdx.x)]; /* uniform index into the kernel arguments */
     const uint32_t r0 = (blockIdx.x - I.tile_begin) * RT;
 
+    /* STAGE: this thread's share of the activation is loaded first, the
+     * weights next, and the activation is written to LDS afterwards, so the
+     * wait before that write covers only the older activation loads. */
+    constexpr int SA = STAGE ? (MAX_FAST_NB * 8 + WG - 1) / WG : 1; /* staged words per thread */
+    uint32_t sav[SA];
+    float sdv[STAGE ? 2 : 1];
     if (STAGE) {
+        /* unconditional loads from clamped (in-range) indices; only the LDS
+         * writes below are guarded */
         const uint32_t *xq32 = (const uint32_t *)a.xq;
-        for (uint32_t i = tid; i < nb * 8; i += WG) {
-            const uint32_t v = xq32[i];
-            act_q[i] = v;
-            if (Q5) act_b[i] = dot4(v, 0xf0f0f0f0u, 0); /* int8 0xf0 = -16 */
+        const uint32_t nw = nb * 8;
+#pragma unroll
+        for (int k = 0; k < SA; ++k) {
+            const uint32_t i = tid + k * WG;
+            if (k * WG < nw) sav[k] = xq32[i < nw ? i : nw - 1];
         }
-        for (uint32_t i = tid; i < nb; i += WG) act_d[i] = a.xd[i];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t i = tid + k * WG;
+            if (k * WG < nb) sdv[k] = a.xd[i < nb ? i : nb - 1];
+        }
     }
 
     const uint32_t tr = tid / TPR, ti = tid % TPR;
@@ -203,7 +216,24 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
         }
     };
     load_task(ti * TB);
-    if (STAGE) __syncthreads(); /* activation staged */
+    if (STAGE) {
+        /* keep the weight loads issued here, ahead of the barrier below */
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < SA; ++k) {
+            const uint32_t i = tid + k * WG;
+            if (i < nb * 8) {
+                act_q[i] = sav[k];
+                if (Q5) act_b[i] = dot4(sav[k], 0xf0f0f0f0u, 0); /* int8 0xf0 = -16 */
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t i = tid + k * WG;
+            if (i < nb) act_d[i] = sdv[k];
+        }
+        __syncthreads(); /* activation staged */
+    }
 
     float acc = 0.0f;
     for (uint32_t c = 0; c < nchunks; ++c) {
@@ -717,6 +747,161 @@ __global__ __launch_bounds__(WG) void k_quantize_q8(const float *x, uint32_t row
     }
 }
 
+/* ------------------------------------------------------------------------
+ * Activation producers (reference: src/model.c:334-415, src/vecmath.c:61-93).
+ * One workgroup of 1024 threads per token row: optional RMSNorm (sequential
+ * f32 sum of squares, model.c:337 — the squares are formed in parallel, one
+ * lane adds them in element order), optional SwiGLU / GeGLU with the binary64
+ * exp below, then the Q8 block quantization of kernels.c:912-935, written
+ * straight to d/q. Element i lives in thread i % 1024, register i / 1024.
+ * ---------------------------------------------------------------------- */
+/* 2^(j/32) correctly rounded to binary64, minus j << 47 (vecmath.c:44-52). */
+__constant__ uint64_t EXP2_TABLE[32] = {
+    0x3ff0000000000000u, 0x3fefd9b0d3158574u, 0x3fefb5586cf9890fu, 0x3fef9301d0125b51u,
+    0x3fef72b83c7d517bu, 0x3fef54873168b9aau, 0x3fef387a6e756238u, 0x3fef1e9df51fdee1u,
+    0x3fef06fe0a31b715u, 0x3feef1a7373aa9cbu, 0x3feedea64c123422u, 0x3feece086061892du,
+    0x3feebfdad5362a27u, 0x3feeb42b569d4f82u, 0x3feeab07dd485429u, 0x3feea47eb03a5585u,
+    0x3feea09e667f3bcdu, 0x3fee9f75e8ec5f74u, 0x3feea11473eb0187u, 0x3feea589994cce13u,
+    0x3feeace5422aa0dbu, 0x3feeb737b0cdc5e5u, 0x3feec49182a3f090u, 0x3feed503b23e255du,
+    0x3feee89f995ad3adu, 0x3feeff76f2fb5e47u, 0x3fef199bdd85529cu, 0x3fef3720dcef9069u,
+    0x3fef5818dcfba487u, 0x3fef7c97337b9b5fu, 0x3fefa4afa2a490dau, 0x3fefd0765b6e4540u,
+};
+
+/* e^x in binary64, rounded once (vecmath.c:61-76): k = round(32x/ln2) from the
+ * low bits of z + 1.5*2^52, remainder r, degree-4 Taylor polynomial of
+ * e^(r ln2/32) with separate multiplies and adds, times 2^(k/32). */
+__device__ __forceinline__ float exp_det(float x) {
+    const double inv_ln2_n = 0x1.71547652b82fep+5, shift = 0x1.8p+52;
+    const double ea = 0x1.62e42fefa39efp-1 / 32;
+    const double c1 = ea, c2 = ea * ea / 2, c3 = ea * ea * ea / 6, c4 = ea * ea * ea * ea / 24;
+    if (x != x) return x;
+    x = x > 89.0f ? 89.0f : (x < -104.0f ? -104.0f : x);
+    const double z = inv_ln2_n * (double)x;
+    double kd = z + shift;
+    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd = kd - shift;
+    const double r = z - kd;
+    double p = c4 * r + c3;
+    p = p * r + c2;
+    p = p * r + c1;
+    p = p * r + 1.0;
+    const double scale = __longlong_as_double((long long)(EXP2_TABLE[ki & 31u] + (ki << 47)));
+    return (float)(p * scale);
+}
+
+constexpr int RW_WG = 1024;
+constexpr int RW_EPT = 16; /* elements per thread: rows up to 16384 */
+
+template <bool NORM, int ACT>
+__global__ __launch_bounds__(RW_WG) void k_row_quantize(const float *src, const float *norm, float eps,
+                                                       const float *gate, uint32_t n, float *yout, float *d,
+                                                       int8_t *q, int *flag) {
+    extern __shared__ __attribute__((aligned(16))) float sq_lds[]; /* NORM: the n squares */
+    __shared__ float s_inv;
+    __shared__ int s_bad;
+    const uint32_t tid = threadIdx.x, row = blockIdx.x, nb = (n + QK - 1) / QK, np = nb * QK;
+    const float *x = src + (size_t)row * n;
+    float v[RW_EPT];
+#pragma unroll
+    for (int k = 0; k < RW_EPT; ++k) {
+        const uint32_t i = tid + k * RW_WG;
+        v[k] = i < n ? x[i] : 0.0f;
+    }
+    if (NORM) {
+#pragma unroll
+        for (int k = 0; k < RW_EPT; ++k) {
+            const uint32_t i = tid + k * RW_WG;
+            if (i < n) sq_lds[i] = v[k] * v[k];
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float sq = 0.0f;
+            uint32_t i = 0;
+            for (; i + 4 <= n; i += 4) {
+                const float4 p4 = *(const float4 *)&sq_lds[i];
+                sq = sq + p4.x;
+                sq = sq + p4.y;
+                sq = sq + p4.z;
+                sq = sq + p4.w;
+            }
+            for (; i < n; ++i) sq = sq + sq_lds[i];
+            const float inv = 1.0f / sqrtf(sq / (float)n + eps); /* model.c:338 */
+            s_inv = inv;
+            s_bad = !(fabsf(sq) <= FLT_MAX) || !(fabsf(inv) <= FLT_MAX);
+        }
+        __syncthreads();
+        const float inv = s_inv;
+        if (s_bad && tid == 0 && flag) *flag = 1;
+#pragma unroll
+        for (int k = 0; k < RW_EPT; ++k) {
+            const uint32_t i = tid + k * RW_WG;
+            if (i < n) {
+                const float t = v[k] * inv;
+                v[k] = t * norm[i]; /* model.c:340 */
+            }
+        }
+    }
+    if (ACT) {
+        const float *g = gate + (size_t)row * n;
+#pragma unroll
+        for (int k = 0; k < RW_EPT; ++k) {
+            const uint32_t i = tid + k * RW_WG;
+            if (i < n) {
+                const float gv = g[i];
+                float e;
+                if (ACT == 1) {
+                    e = exp_det(-gv);
+                } else {
+                    const float g3 = 0.044715f * gv * gv * gv;
+                    const float u = 1.5957691216f * (gv + g3);
+                    e = exp_det(-u);
+                }
+                const float den = 1.0f + e;
+                const float sg = gv / den;
+                v[k] = v[k] * sg;
+            }
+        }
+    }
+    if (yout) {
+#pragma unroll
+        for (int k = 0; k < RW_EPT; ++k) {
+            const uint32_t i = tid + k * RW_WG;
+            if (i < n) yout[(size_t)row * n + i] = v[k];
+        }
+    }
+    /* Q8 blocks: 32 consecutive elements = 32 consecutive threads of one k */
+#pragma unroll
+    for (int k = 0; k < RW_EPT; ++k) {
+        const uint32_t i = tid + k * RW_WG;
+        if (k * RW_WG >= np) break; /* uniform */
+        const bool valid = i < n;
+        const float av = fabsf(v[k]);
+        int bad = valid && !(av <= FLT_MAX);
+        float m = valid ? av : 0.0f;
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) {
+            const float o = __shfl_xor(m, off, 32);
+            m = o > m ? o : m;
+            bad |= __shfl_xor(bad, off, 32);
+        }
+        if (i < np) {
+            const float scale = m / 127.0f;
+            const float inv = scale >= FLT_MIN ? 1.0f / scale : 0.0f;
+            int qv = 0;
+            if (valid) {
+                const float p = v[k] * inv;
+                qv = (int)__builtin_rintf(p);
+                qv = qv > 127 ? 127 : (qv < -127 ? -127 : qv);
+            }
+            q[(size_t)row * np + i] = (int8_t)qv;
+            if ((i & 31u) == 0) {
+                d[(size_t)row * nb + i / QK] = scale;
+                if (bad && flag) *flag = 1;
+            }
+        }
+    }
+}
+
 /* Row dequantization (reference: src/kernels.c:1044-1062): scale * float(q). */
 template <bool Q5>
 __global__ __launch_bounds__(WG) void k_dequantize_row(const unsigned char *w, uint32_t cols, float *out) {
@@ -868,6 +1053,27 @@ hipError_t launch_quantize_q8(const float *x, uint32_t rows, uint32_t n, float *
     if (!threads) return hipSuccess;
     hipLaunchKernelGGL(k_quantize_q8, dim3((uint32_t)((threads + WG - 1) / WG)), dim3(WG), 0, s, x, rows, n, nb, d,
                        q, flag);
+    return hipGetLastError();
+}
+
+hipError_t launch_row_quantize(const float *src, const float *norm, float eps, const float *gate, int act,
+                               uint32_t rows, uint32_t n, float *y, float *d, int8_t *q, int *flag, hipStream_t s) {
+    if (!rows || !n) return hipSuccess;
+    if (n > (uint32_t)(RW_WG * RW_EPT)) return hipErrorInvalidValue;
+    const size_t lds = norm ? (size_t)n * sizeof(float) : 0;
+    const dim3 grid(rows), block(RW_WG);
+#define SMQ_RQ(NORM, ACT) \
+    hipLaunchKernelGGL((k_row_quantize<NORM, ACT>), grid, block, lds, s, src, norm, eps, gate, n, y, d, q, flag)
+    if (norm) {
+        if (act == 1) SMQ_RQ(true, 1);
+        else if (act == 2) SMQ_RQ(true, 2);
+        else SMQ_RQ(true, 0);
+    } else {
+        if (act == 1) SMQ_RQ(false, 1);
+        else if (act == 2) SMQ_RQ(false, 2);
+        else SMQ_RQ(false, 0);
+    }
+#undef SMQ_RQ
     return hipGetLastError();
 }
 

@@ -425,3 +425,70 @@ def test_matmul_prefill_switch(orc):
     smq.matmul(items, dbuf, qbuf, ntok)
     for (_, _, y), want in zip(items, wants):
         assert_same_f32(y.download(np.float32), want, "exact prefill")
+
+
+# ------------------------------------------------------------------ activation producers
+
+@pytest.mark.parametrize("n", [896, 4864, 8960, 100, 1])
+def test_norm_quantize_bit_exact(orc, n):
+    """RMSNorm (sequential f32 sum) then Q8, against the oracle's row_work."""
+    g = LcgUniform(300 + n)
+    rows = 5
+    x = g.uniform(-3, 3, rows * n)
+    w = g.uniform(0.5, 1.5, n)
+    nb = (n + 31) // 32
+    xb, wb = smq.DeviceBuffer.from_array(x), smq.DeviceBuffer.from_array(w)
+    y, d, q = smq.DeviceBuffer(rows * n * 4), smq.DeviceBuffer(rows * nb * 4), smq.DeviceBuffer(rows * nb * 32)
+    smq.norm_quantize(xb, wb, 1e-6, rows, n, y, d, q)
+    smq.numeric_check()
+    ok, wy, wd, wq = orc.row_work(x, rows, n, norm=w, eps=1e-6)
+    assert ok
+    assert_same_f32(y.download(np.float32), wy, "rmsnorm y")
+    assert_same_f32(d.download(np.float32), wd, "rmsnorm d")
+    assert np.array_equal(q.download(np.int8), wq)
+
+
+@pytest.mark.parametrize("gelu", [False, True])
+def test_silu_quantize_bit_exact(orc, gelu):
+    """SwiGLU / GeGLU with the binary64 exp, in place, then Q8; gate values
+    cover the exp clamps, infinities and NaN-free extremes."""
+    g = LcgUniform(400 + gelu)
+    rows, n = 3, 4864
+    nb = n // 32
+    up = g.uniform(-4, 4, rows * n)
+    gate = g.uniform(-30, 30, rows * n)
+    gate[::97] = np.array([88.7, 88.8, -88.7, -88.72, -88.8, -89.0, 103.0, 120.0, 1e-30, -1e-30, 0.0, -0.0, 200.0,
+                           -200.0], np.float32)[np.arange(len(gate[::97])) % 14]
+    ub, gb = smq.DeviceBuffer.from_array(up), smq.DeviceBuffer.from_array(gate)
+    d, q = smq.DeviceBuffer(rows * nb * 4), smq.DeviceBuffer(rows * nb * 32)
+    smq.silu_quantize(ub, gb, rows, n, d, q, gemma3=gelu)
+    ok, wy, wd, wq = orc.row_work(up, rows, n, gate=gate, gelu=gelu)
+    nonfinite = not ok
+    if nonfinite:
+        with pytest.raises(smq.SmqError):
+            smq.numeric_check()
+    else:
+        smq.numeric_check()
+    assert_same_f32(ub.download(np.float32), wy, "activation in place")
+    if not nonfinite:
+        assert_same_f32(d.download(np.float32), wd, "activation d")
+        assert np.array_equal(q.download(np.int8), wq)
+
+
+def test_row_quantize_flags_nonfinite(orc):
+    rows, n = 2, 64
+    x = np.ones(rows * n, np.float32)
+    x[70] = np.inf
+    xb = smq.DeviceBuffer.from_array(x)
+    wb = smq.DeviceBuffer.from_array(np.ones(n, np.float32))
+    d, q = smq.DeviceBuffer(rows * 2 * 4), smq.DeviceBuffer(rows * 64)
+    smq.norm_quantize(xb, wb, 1e-6, rows, n, None, d, q)
+    with pytest.raises(smq.SmqError) as e:
+        smq.numeric_check()
+    assert e.value.status == smq.SM_ERR_NUMERIC
+    smq.row_quantize(xb, rows, n, d, q)  # plain quantize of an inf: also flagged
+    with pytest.raises(smq.SmqError):
+        smq.numeric_check()
+    with pytest.raises(smq.SmqError) as e:
+        smq.row_quantize(xb, rows, 20000, d, q)
+    assert e.value.status == 4

@@ -444,3 +444,80 @@ def test_rmsnorm_sequential(orc):
     inv = np.float32(1) / np.sqrt(np.float32(sq / np.float32(896) + np.float32(1e-6)))
     assert s == 0
     assert np.array_equal(f32_bits(y), f32_bits(((x * inv).astype(np.float32) * w).astype(np.float32)))
+
+
+# ---------------------------------------------------------------- exp_det and gated activations
+
+def test_exp_table_is_the_mathematics(orc):
+    """The oracle's exp_det table equals 2^(j/32) correctly rounded (computed
+    independently in 60-digit decimal), minus j << 47."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("gen_exp_table", os.path.join(
+        os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle", "gen_exp_table.py"))
+    gen = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gen)
+    assert orc.exp2_table() == gen.exp2_table()
+
+
+def test_exp_det_accuracy_and_specials(orc):
+    """tests/test_kernels.c:330-357: at most 1 ulp from the correctly rounded
+    e^x, at most 1 in 10^4 not correctly rounded; clamps and NaN."""
+    xs = (-103.5 + 192.2 * np.arange(200001) / 200000.0).astype(np.float32)
+    got = np.array([orc.exp_det(float(v)) for v in xs], np.float32)
+    want = np.exp(xs.astype(np.float64)).astype(np.float32)
+    gi, wi = got.view(np.int32).astype(np.int64), want.view(np.int32).astype(np.int64)
+    d = np.abs(gi - wi)
+    assert d.max() <= 1
+    assert (d != 0).sum() <= len(xs) // 10000
+    assert orc.exp_det(0.0) == 1.0
+    assert orc.exp_det(89.0) == np.inf and orc.exp_det(np.inf) == np.inf
+    assert orc.exp_det(-110.0) == 0.0 and orc.exp_det(-np.inf) == 0.0
+    assert orc.exp_det(-100.0) > 0.0
+    assert np.isnan(orc.exp_det(np.nan))
+
+
+def test_exp_det_and_activations_match_reference(orc, ref):
+    g = LcgUniform(17)
+    xs = np.concatenate([g.uniform(-110, 95, 20000), np.array([0.0, -0.0, 88.7, 88.8, -88.7, -88.72, -88.8, -89.0,
+                                                               103.0, 120.0, 1e-30, -1e-30, np.inf, -np.inf,
+                                                               np.nan], np.float32)])
+    a = np.array([orc.exp_det(float(v)) for v in xs], np.float32)
+    b = np.array([ref.exp_det(float(v)) for v in xs], np.float32)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    gate = np.concatenate([g.uniform(-30, 30, 3000), xs[-15:]]).astype(np.float32)
+    up = g.uniform(-4, 4, gate.shape[0])
+    for gelu in (False, True):
+        mine, theirs = orc.act_mul(up, gate, gelu), ref.act_mul(up, gate, gelu)
+        nan = np.isnan(theirs)
+        assert np.array_equal(np.isnan(mine), nan)
+        assert np.array_equal(mine[~nan].view(np.uint32), theirs[~nan].view(np.uint32))
+
+
+def test_silu_against_float64(orc):
+    # tests/test_kernels.c:372-381
+    g = LcgUniform(23)
+    gate = g.uniform(-30, 30, 2000)
+    up = g.uniform(-4, 4, 2000)
+    got = orc.act_mul(up, gate)
+    want = up.astype(np.float64) * (gate / (1.0 + np.exp(-gate.astype(np.float64))))
+    assert np.all(np.abs(got - want) <= 1e-6 * np.abs(want) + 1e-30)
+
+
+def test_row_work_composes(orc):
+    g = LcgUniform(29)
+    rows, n = 3, 100
+    src = g.uniform(-3, 3, rows * n)
+    norm = g.uniform(0.5, 1.5, n)
+    ok, y, d, q = orc.row_work(src, rows, n, norm=norm, eps=1e-6)
+    assert ok
+    for r in range(rows):
+        s, yr = orc.rmsnorm(src[r * n:(r + 1) * n], norm, 1e-6)
+        assert np.array_equal(y[r * n:(r + 1) * n].view(np.uint32), yr.view(np.uint32))
+        st, dr, qr = orc.quantize_q8(yr)
+        assert np.array_equal(d[r * 4:(r + 1) * 4].view(np.uint32), dr[0].view(np.uint32))
+    gate = g.uniform(-5, 5, rows * n)
+    ok, y2, d2, q2 = orc.row_work(src, rows, n, gate=gate)
+    assert ok and np.array_equal(y2.view(np.uint32), orc.act_mul(src, gate).view(np.uint32))
+    bad = src.copy()
+    bad[5] = np.inf
+    assert not orc.row_work(bad, rows, n, norm=norm)[0]

@@ -80,6 +80,12 @@ class Oracle:
         lib.orc_row_work.restype = ctypes.c_int
         lib.orc_row_work.argtypes = [_f32p, _f32p, ctypes.c_float, _f32p, ctypes.c_int, _u32, _u32, _f32p, _f32p,
                                      _i8p]
+        lib.orc_dot_f32.restype = ctypes.c_float
+        lib.orc_dot_f32.argtypes = [_f32p, _f32p, _u32]
+        lib.orc_rope.argtypes = [_f32p, _u32, _u32, _u32, _f32p, _f32p]
+        lib.orc_attend_f32.argtypes = [_f32p, _f32p, _f32p, _u32, _u32, _u32, _u32, _f32p, _f32p]
+        lib.orc_argmax.restype = _u32
+        lib.orc_argmax.argtypes = [_f32p, _u32, _u8p]
         lib.orc_time_gemm_pass.restype = ctypes.c_double
         lib.orc_time_gemm_pass.argtypes = [ctypes.c_void_p, ctypes.POINTER(_u8p), ctypes.POINTER(_u32),
                                            ctypes.POINTER(_u32), ctypes.POINTER(_f32p), ctypes.POINTER(_i8p), _u32,
@@ -192,6 +198,37 @@ class Oracle:
                                    _ptr(d, _f32p), _ptr(q, _i8p))
         return bool(ok), y, d, q
 
+    # -- attention pieces
+    def dot_f32(self, a, b):
+        a = np.ascontiguousarray(a, np.float32)
+        b = np.ascontiguousarray(b, np.float32)
+        return self.lib.orc_dot_f32(_ptr(a, _f32p), _ptr(b, _f32p), a.shape[0])
+
+    def rope(self, x, heads, hd, pairs, cs, sn):
+        x = np.array(x, np.float32, copy=True)
+        cs = np.ascontiguousarray(cs, np.float32)
+        sn = np.ascontiguousarray(sn, np.float32)
+        self.lib.orc_rope(_ptr(x, _f32p), heads, hd, pairs, _ptr(cs, _f32p), _ptr(sn, _f32p))
+        return x
+
+    def attend_f32(self, q, keys, values, stride, hd, start, pos):
+        q = np.ascontiguousarray(q, np.float32)
+        keys = np.ascontiguousarray(keys, np.float32)
+        values = np.ascontiguousarray(values, np.float32)
+        scores = np.zeros(pos + 1, np.float32)
+        out = np.zeros(hd, np.float32)
+        self.lib.orc_attend_f32(_ptr(q, _f32p), _ptr(keys, _f32p), _ptr(values, _f32p), stride, hd, start, pos,
+                                _ptr(scores, _f32p), _ptr(out, _f32p))
+        return out
+
+    def argmax(self, logits, banned=None):
+        logits = np.ascontiguousarray(logits, np.float32)
+        bp = None
+        if banned is not None:
+            banned = np.ascontiguousarray(banned, np.uint8)
+            bp = _ptr(banned, _u8p)
+        return self.lib.orc_argmax(_ptr(logits, _f32p), logits.shape[0], bp)
+
     # -- offline weight rules
     def q8_weight_rows(self, x):
         x = np.ascontiguousarray(x, np.float32)
@@ -271,6 +308,9 @@ class Reference:
         lib.exp_det.restype = ctypes.c_float
         lib.exp_det.argtypes = [ctypes.c_float]
         lib.silu_mul_scalar.argtypes = [_f32p, _f32p, _sz]
+        lib.dot_f32.restype = ctypes.c_float
+        lib.dot_f32.argtypes = [_f32p, _f32p, _u32]
+        lib.attend_f32_scalar.argtypes = [_f32p, _f32p, _f32p, _u32, _u32, _u32, _u32, _f32p, _f32p]
         lib.gelu_mul_scalar.argtypes = [_f32p, _f32p, _sz]
 
     def quantize_q8(self, x, avx2=False):
@@ -318,6 +358,21 @@ class Reference:
         fn = self.lib.gelu_mul_scalar if gelu else self.lib.silu_mul_scalar
         fn(_ptr(up, _f32p), _ptr(gate, _f32p), up.shape[0])
         return up
+
+    def dot_f32(self, a, b):
+        a = np.ascontiguousarray(a, np.float32)
+        b = np.ascontiguousarray(b, np.float32)
+        return self.lib.dot_f32(_ptr(a, _f32p), _ptr(b, _f32p), a.shape[0])
+
+    def attend_f32(self, q, keys, values, stride, hd, start, pos):
+        q = np.ascontiguousarray(q, np.float32)
+        keys = np.ascontiguousarray(keys, np.float32)
+        values = np.ascontiguousarray(values, np.float32)
+        scores = np.zeros(pos + 1, np.float32)
+        out = np.zeros(hd, np.float32)
+        self.lib.attend_f32_scalar(_ptr(q, _f32p), _ptr(keys, _f32p), _ptr(values, _f32p), stride, hd, start, pos,
+                                   _ptr(scores, _f32p), _ptr(out, _f32p))
+        return out
 
     def fn_addr(self, name):
         return ctypes.cast(getattr(self.lib, name), ctypes.c_void_p).value

@@ -398,6 +398,76 @@ int orc_row_work(const float *src, const float *norm, float eps, const float *ga
     return ok;
 }
 
+/* ---- attention pieces (src/model.c:425-491, src/kernels.c:1119-1176) ---- */
+
+/* kernels.c:1119-1127: eight lanes over full groups of 8, lane reduction,
+ * then the tail added in order. */
+float orc_dot_f32(const float *a, const float *b, uint32_t n) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0}, sum;
+    uint32_t i, l;
+    for (i = 0; i + 8 <= n; i += 8)
+        for (l = 0; l < 8; ++l) {
+            float p = a[i + l] * b[i + l];
+            acc[l] = acc[l] + p;
+        }
+    sum = lanes_reduce(acc);
+    for (; i < n; ++i) {
+        float p = a[i] * b[i];
+        sum = sum + p;
+    }
+    return sum;
+}
+
+/* model.c:442-450: adjacent pairs (2i, 2i+1), i < pairs, of each head. */
+void orc_rope(float *x, uint32_t heads, uint32_t hd, uint32_t pairs, const float *cs, const float *sn) {
+    uint32_t h, i;
+    for (h = 0; h < heads; ++h, x += hd)
+        for (i = 0; i < pairs; ++i) {
+            float a = x[2 * i], b = x[2 * i + 1];
+            float ac = a * cs[i], bs = b * sn[i], as = a * sn[i], bc = b * cs[i];
+            x[2 * i] = ac - bs;
+            x[2 * i + 1] = as + bc;
+        }
+}
+
+/* kernels.c:1154-1176 attend_f32: scores = dot * (1/sqrt(hd)); softmax with
+ * the maximum subtracted, exp_det, sequential total, one reciprocal; then
+ * out = sum over positions (in order) of (score * inv) * value. */
+void orc_attend_f32(const float *q, const float *keys, const float *values, uint32_t stride, uint32_t hd,
+                    uint32_t start, uint32_t pos, float *scores, float *out) {
+    uint32_t p, j;
+    float factor = 1.0f / sqrtf((float)hd), high = -FLT_MAX, total = 0.0f, inv;
+    for (p = start; p <= pos; ++p) {
+        float s = orc_dot_f32(q, keys + (size_t)p * stride, hd);
+        scores[p] = s * factor;
+    }
+    for (p = start; p <= pos; ++p)
+        if (scores[p] > high) high = scores[p];
+    for (p = start; p <= pos; ++p) {
+        scores[p] = orc_exp_det(scores[p] - high);
+        total = total + scores[p];
+    }
+    inv = 1.0f / total;
+    for (j = 0; j < hd; ++j) out[j] = 0.0f;
+    for (p = start; p <= pos; ++p) {
+        float w = scores[p] * inv;
+        const float *v = values + (size_t)p * stride;
+        for (j = 0; j < hd; ++j) {
+            float t = w * v[j];
+            out[j] = out[j] + t;
+        }
+    }
+}
+
+/* sampler.c:57-63: first non-banned id, replaced by any later id whose logit
+ * is strictly greater. Returns UINT32_MAX when every id is banned. */
+uint32_t orc_argmax(const float *logits, uint32_t n, const unsigned char *banned) {
+    uint32_t i, best = UINT32_MAX;
+    for (i = 0; i < n; ++i)
+        if (!(banned && banned[i]) && (best == UINT32_MAX || logits[i] > logits[best])) best = i;
+    return best;
+}
+
 /* ---- offline weight rules --------------------------------------------- */
 
 /* tools/q8pack.c:38-44 (also scripts/smoe/quant.ts:73-97): per block

@@ -40,6 +40,12 @@ void orc_gelu_mul(float *up, const float *gate, size_t n);
 int orc_row_work(const float *src, const float *norm, float eps, const float *gate, int gelu, uint32_t rows,
                  uint32_t n, float *y, float *d, int8_t *q);
 
+float orc_dot_f32(const float *a, const float *b, uint32_t n);
+void orc_rope(float *x, uint32_t heads, uint32_t hd, uint32_t pairs, const float *cs, const float *sn);
+void orc_attend_f32(const float *q, const float *keys, const float *values, uint32_t stride, uint32_t hd,
+                    uint32_t start, uint32_t pos, float *scores, float *out);
+uint32_t orc_argmax(const float *logits, uint32_t n, const unsigned char *banned);
+
 void orc_q8_weight_rows(const float *x, uint32_t rows, uint32_t cols, unsigned char *out);
 void orc_quantize_q5_row(const float *x, uint32_t cols, unsigned char *out);
 void orc_dequantize_row(int q5, const unsigned char *w, uint32_t cols, float *out);

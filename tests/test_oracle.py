@@ -521,3 +521,77 @@ def test_row_work_composes(orc):
     bad = src.copy()
     bad[5] = np.inf
     assert not orc.row_work(bad, rows, n, norm=norm)[0]
+
+
+# ---------------------------------------------------------------- attention pieces
+
+def test_dot_f32_and_attention_match_reference(orc, ref):
+    """kernels.c:1119-1176 and tests/test_kernels.c:458-484: strided KV, every
+    head size 2..24, start offsets, a -0.0 key."""
+    g = LcgUniform(41)
+    for trial in range(60):
+        hd = 2 + int(g.next(1)[0] % 70)
+        npos = 1 + int(g.next(1)[0] % 90)
+        start = int(g.next(1)[0] % npos)
+        stride = hd + int(g.next(1)[0] % 9)
+        q = g.uniform(-4, 4, hd)
+        keys = g.uniform(-3, 3, npos * stride)
+        values = g.uniform(-3, 3, npos * stride)
+        keys[0] = -0.0
+        assert np.array_equal(f32_bits(orc.dot_f32(q, keys[:hd])), f32_bits(ref.dot_f32(q, keys[:hd])))
+        a = orc.attend_f32(q, keys, values, stride, hd, start, npos - 1)
+        b = ref.attend_f32(q, keys, values, stride, hd, start, npos - 1)
+        assert np.array_equal(f32_bits(a), f32_bits(b)), trial
+
+
+def test_attention_closed_form(orc):
+    g = LcgUniform(43)
+    hd, npos = 64, 40
+    q = g.uniform(-1, 1, hd)
+    keys = g.uniform(-1, 1, npos * hd).reshape(npos, hd)
+    values = g.uniform(-1, 1, npos * hd).reshape(npos, hd)
+    s = keys.astype(np.float64) @ q.astype(np.float64) / np.sqrt(hd)
+    p = np.exp(s - s.max())
+    want = (p / p.sum()) @ values.astype(np.float64)
+    got = orc.attend_f32(q, keys.reshape(-1), values.reshape(-1), hd, hd, 0, npos - 1)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+def test_rope_closed_form(orc):
+    g = LcgUniform(47)
+    heads, hd, pairs = 3, 16, 6
+    x = g.uniform(-2, 2, heads * hd)
+    ang = g.uniform(-3, 3, pairs)
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    y = orc.rope(x, heads, hd, pairs, cs, sn)
+    xr = x.reshape(heads, hd).astype(np.float64)
+    yr = y.reshape(heads, hd)
+    for i in range(pairs):
+        a, b = xr[:, 2 * i], xr[:, 2 * i + 1]
+        assert np.allclose(yr[:, 2 * i], a * cs[i] - b * sn[i], atol=1e-6)
+        assert np.allclose(yr[:, 2 * i + 1], a * sn[i] + b * cs[i], atol=1e-6)
+    assert np.array_equal(yr[:, 2 * pairs:], x.reshape(heads, hd)[:, 2 * pairs:])
+
+
+def test_argmax_semantics(orc):
+    """sampler.c:57-63 by brute force: lowest id on ties, banned skipped, a
+    NaN only wins as the first candidate."""
+    def brute(l, banned):
+        best = None
+        for i, v in enumerate(l):
+            if banned is not None and banned[i]:
+                continue
+            if best is None or v > l[best]:
+                best = i
+        return 0xFFFFFFFF if best is None else best
+    g = LcgUniform(53)
+    for trial in range(200):
+        n = 1 + int(g.next(1)[0] % 300)
+        l = np.round(g.uniform(-3, 3, n) * 2) / 2  # many ties
+        banned = (g.next(n) % np.uint64(5) == 0).astype(np.uint8) if trial % 2 else None
+        if trial % 7 == 0:
+            l[int(g.next(1)[0] % n)] = np.nan
+        if trial % 11 == 0:
+            l[0] = np.nan
+        assert orc.argmax(l, banned) == brute(l, banned), trial
+    assert orc.argmax(np.zeros(3, np.float32), np.ones(3, np.uint8)) == 0xFFFFFFFF

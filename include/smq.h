@@ -158,11 +158,15 @@ typedef struct smq_qmat {
     uint32_t rows, cols, nb, dtype;
     size_t row_bytes;
 } smq_qmat;
-/* MatItem (model.c:236-240): y[token*w->rows + row] = dot + bias[row]. */
+/* MatItem (model.c:236-240): y[token*w->rows + row] = dot + bias[row].
+ * accumulate != 0 adds the result into y instead (y = y + result: the
+ * residual add_rows of model.c:452-455 fused into the store, model.c:540,
+ * 643); the finiteness check still looks at the result before the add. */
 typedef struct smq_mat_item {
     const smq_qmat *w; /* host pointer to the descriptor */
     const float *bias; /* device, may be NULL */
     float *y;          /* device */
+    int accumulate;
 } smq_mat_item;
 #define SMQ_MAX_ITEMS 4
 /* Up to SMQ_MAX_ITEMS matrices with the same nb sharing one quantized input,
@@ -172,6 +176,44 @@ smq_status smq_matmul(const smq_mat_item *items, uint32_t n, const float *xd, co
 /* Synchronizes, then returns SMQ_ERR_NUMERIC (and clears the flag) if any
  * quantize or matmul since the last check saw a non-finite value. */
 smq_status smq_numeric_check(void);
+
+/* ---- decoder pieces around the matmuls ----------------------------------
+ * Device-resident steps of the reference's forward pass (src/model.c:425-542,
+ * 669-677) and its greedy choice (src/sampler.c:57-63). `pos_dev`, when not
+ * NULL, is a device int32 read by the kernel in place of pos0, so a captured
+ * decode step replays at successive positions. */
+typedef struct smq_attn_shape {
+    uint32_t heads, kv_heads, head_dim; /* query heads, KV heads (heads % kv_heads == 0) */
+    uint32_t rotary_pairs;              /* rotary_dim / 2 (config.c:25-47) */
+    uint32_t window;                    /* sliding window, 0 = full causal (model.c:466-470) */
+    uint32_t context;                   /* positions the caches hold */
+} smq_attn_shape;
+/* model.c:511-526: for each of ntok tokens at position p = pos0 + t, rotate
+ * q[t] (heads*head_dim) and k[t] (kv_heads*head_dim) in place by the table
+ * rows cos_table[p], sin_table[p] (rotary_pairs floats each, model.c:425-450),
+ * then store k[t] and v[t] into keys[p] and values[p] (kv_heads*head_dim f32
+ * each). A position at or past context raises the numeric flag instead. */
+smq_status smq_rope_kv(float *q, float *k, const float *v, uint32_t ntok, const smq_attn_shape *shape,
+                       const float *cos_table, const float *sin_table, float *keys, float *values, uint32_t pos0,
+                       const int32_t *pos_dev);
+/* model.c:459-491 with attend_f32 (kernels.c:1154-1176): causal attention of
+ * each query head of ntok tokens over keys/values[start .. p], p = pos0 + t,
+ * in the reference's order (8-lane dot, exp_det softmax, sums in position
+ * order), writing att[t] (heads*head_dim). Bit identical to the reference. */
+smq_status smq_attention(const float *q, const float *keys, const float *values, float *att, uint32_t ntok,
+                         const smq_attn_shape *shape, uint32_t pos0, const int32_t *pos_dev);
+/* sampler.c:57-63: *token = first non-banned id, replaced by any later
+ * non-banned id with a strictly greater logit (NaN never wins unless it is
+ * the first candidate). banned may be NULL. UINT32_MAX if every id is banned. */
+smq_status smq_argmax(const float *logits, uint32_t vocab, const unsigned char *banned, uint32_t *token);
+/* model.c:669-677: x[t] = dequantized row tokens[t] of the embedding matrix
+ * (embed->cols floats). Ids must be < embed->rows (checked by the caller, as
+ * model.c:671-672 does; an id out of range raises the numeric flag). */
+smq_status smq_embed(const smq_qmat *embed, const uint32_t *tokens, uint32_t ntok, float *x);
+/* Decode-loop bookkeeping on the device: history[*count] = *token when
+ * *count < capacity, then ++*count and ++*pos (lets a captured step advance). */
+smq_status smq_decode_advance(int32_t *pos, uint32_t *count, const uint32_t *token, uint32_t *history,
+                              uint32_t capacity);
 
 /* ---- dequantization (src/kernels.h:193-196, kernels.c:1044-1062) -------- */
 void smq_dequantize_q8_row(const unsigned char *w, uint32_t cols, float *out);

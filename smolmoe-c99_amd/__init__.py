@@ -29,7 +29,7 @@ DTYPE_Q8, DTYPE_Q5 = 1, 2
 # src/util.h:28-37
 STATUS = {0: "SM_OK", 1: "SM_ERR", 2: "SM_ERR_IO", 3: "SM_ERR_FORMAT", 4: "SM_ERR_RANGE", 5: "SM_ERR_NUMERIC",
           6: "SM_ERR_NOMEM", 7: "SM_ERR_STATE"}
-SM_ERR_NUMERIC = 5
+SM_ERR_FORMAT, SM_ERR_RANGE, SM_ERR_NUMERIC, SM_ERR_STATE = 3, 4, 5, 7
 
 
 class SmqError(RuntimeError):
@@ -48,7 +48,12 @@ class _QMat(ctypes.Structure):
 
 
 class _MatItem(ctypes.Structure):
-    _fields_ = [("w", ctypes.POINTER(_QMat)), ("bias", _vp), ("y", _vp)]
+    _fields_ = [("w", ctypes.POINTER(_QMat)), ("bias", _vp), ("y", _vp), ("accumulate", ctypes.c_int)]
+
+
+class _AttnShape(ctypes.Structure):
+    _fields_ = [("heads", _u32), ("kv_heads", _u32), ("head_dim", _u32), ("rotary_pairs", _u32), ("window", _u32),
+                ("context", _u32)]
 
 
 _SIGS = {
@@ -85,6 +90,11 @@ _SIGS = {
     "smq_set_prefill_mfma": (None, [ctypes.c_int]),
     "smq_matmul": (ctypes.c_int, [ctypes.POINTER(_MatItem), _u32, _vp, _vp, _u32]),
     "smq_numeric_check": (ctypes.c_int, []),
+    "smq_rope_kv": (ctypes.c_int, [_vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _vp, _vp, _vp, _vp, _u32, _vp]),
+    "smq_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _u32, _vp]),
+    "smq_argmax": (ctypes.c_int, [_vp, _u32, _vp, _vp]),
+    "smq_embed": (ctypes.c_int, [ctypes.POINTER(_QMat), _vp, _u32, _vp]),
+    "smq_decode_advance": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32]),
     "smq_dequantize_q8_row": (None, [_vp, _u32, _vp]),
     "smq_dequantize_q5_row": (None, [_vp, _u32, _vp]),
     "smq_malloc": (_vp, [_sz]),
@@ -334,14 +344,43 @@ class QMat:
 
 
 def matmul(items, xd, xq, ntok):
-    """items: sequence of (QMat, bias DeviceBuffer or None, y DeviceBuffer)."""
-    cm = [w._c() for w, _, _ in items]
+    """items: sequence of (QMat, bias DeviceBuffer or None, y DeviceBuffer[,
+    accumulate]); accumulate adds the result into y (the residual add)."""
+    cm = [it[0]._c() for it in items]
     arr = (_MatItem * len(items))()
-    for i, (w, bias, y) in enumerate(items):
+    for i, it in enumerate(items):
         arr[i].w = ctypes.pointer(cm[i])
-        arr[i].bias = _p(bias)
-        arr[i].y = _p(y)
+        arr[i].bias = _p(it[1])
+        arr[i].y = _p(it[2])
+        arr[i].accumulate = int(bool(it[3])) if len(it) > 3 else 0
     _check(load().smq_matmul(arr, len(items), _p(xd), _p(xq), ntok))
+
+
+# ---- decoder pieces (src/model.c:425-542, 669-677; src/sampler.c:57-63)
+def attn_shape(heads, kv_heads, head_dim, rotary_pairs, window, context):
+    return _AttnShape(heads, kv_heads, head_dim, rotary_pairs, window, context)
+
+
+def rope_kv(q, k, v, ntok, shape, cos_table, sin_table, keys, values, pos0=0, pos_dev=None):
+    _check(load().smq_rope_kv(_p(q), _p(k), _p(v), ntok, ctypes.byref(shape), _p(cos_table), _p(sin_table),
+                              _p(keys), _p(values), pos0, _p(pos_dev)))
+
+
+def attention(q, keys, values, att, ntok, shape, pos0=0, pos_dev=None):
+    _check(load().smq_attention(_p(q), _p(keys), _p(values), _p(att), ntok, ctypes.byref(shape), pos0, _p(pos_dev)))
+
+
+def argmax(logits, vocab, banned, token):
+    _check(load().smq_argmax(_p(logits), vocab, _p(banned), _p(token)))
+
+
+def embed(w, tokens, ntok, x):
+    c = w._c()
+    _check(load().smq_embed(ctypes.byref(c), _p(tokens), ntok, _p(x)))
+
+
+def decode_advance(pos, count, token, history, capacity):
+    _check(load().smq_decode_advance(_p(pos), _p(count), _p(token), _p(history), capacity))
 
 
 def numeric_check():

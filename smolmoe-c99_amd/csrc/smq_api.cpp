@@ -420,6 +420,7 @@ smq_status smq_matmul(const smq_mat_item *items, uint32_t n, const float *xd, co
             it.y = items[i].y;
             it.y_stride = w->rows;
             it.rows = w->rows;
+            it.accumulate = items[i].accumulate != 0;
         }
         if (!a.nitems) continue;
         const bool mfma = ntok > 1 && g.prefill_mfma && smq::mfma_layout_ok(a, q5 == 1);
@@ -441,6 +442,106 @@ smq_status smq_numeric_check(void) {
     if (!hip_ok(hipMemset(g.flag, 0, sizeof(int)), "numeric_check")) return t_status;
     /* the reference's message, model.c:309 */
     return set_status(SMQ_ERR_NUMERIC, "non-finite activation; the checkpoint is outside the supported numeric range");
+}
+
+static bool attn_shape(const smq_attn_shape *in, smq::AttnShape *out, const char *who) {
+    if (!in) {
+        set_status(SMQ_ERR_RANGE, "%s: shape is NULL", who);
+        return false;
+    }
+    if (!in->heads || !in->kv_heads || in->heads % in->kv_heads || !in->head_dim || in->head_dim % 2 ||
+        in->head_dim > smq::MAX_HEAD_DIM || 2 * in->rotary_pairs > in->head_dim || !in->context ||
+        in->context > smq::MAX_ATT_POSITIONS) {
+        set_status(SMQ_ERR_RANGE, "%s: unsupported shape (heads %u, kv_heads %u, head_dim %u <= %u, pairs %u, context %u <= %u)",
+                   who, in->heads, in->kv_heads, in->head_dim, smq::MAX_HEAD_DIM, in->rotary_pairs, in->context,
+                   smq::MAX_ATT_POSITIONS);
+        return false;
+    }
+    out->heads = in->heads;
+    out->kv_heads = in->kv_heads;
+    out->head_dim = in->head_dim;
+    out->q_dim = in->heads * in->head_dim;
+    out->kv_dim = in->kv_heads * in->head_dim;
+    out->pairs = in->rotary_pairs;
+    out->window = in->window;
+    out->context = in->context;
+    return true;
+}
+
+smq_status smq_rope_kv(float *q, float *k, const float *v, uint32_t ntok, const smq_attn_shape *shape,
+                       const float *cos_table, const float *sin_table, float *keys, float *values, uint32_t pos0,
+                       const int32_t *pos_dev) {
+    if (!ready()) return t_status;
+    smq::AttnShape sh;
+    if (!attn_shape(shape, &sh, "rope_kv")) return t_status;
+    if (!ntok) return SMQ_OK;
+    if (!pos_dev && (pos0 > sh.context || ntok > sh.context - pos0))
+        return set_status(SMQ_ERR_RANGE, "token batch exceeds context"); /* model.c:667-668 */
+    const size_t table = (size_t)sh.context * sh.pairs * 4, cache = (size_t)sh.context * sh.kv_dim * 4;
+    if (!extent_ok(q, (size_t)ntok * sh.q_dim * 4, "q") || !extent_ok(k, (size_t)ntok * sh.kv_dim * 4, "k") ||
+        !extent_ok(v, (size_t)ntok * sh.kv_dim * 4, "v") || !extent_ok(cos_table, table, "cos table") ||
+        !extent_ok(sin_table, table, "sin table") || !extent_ok(keys, cache, "keys") ||
+        !extent_ok(values, cache, "values") || !extent_ok(pos_dev, pos_dev ? 4 : 0, "pos"))
+        return t_status;
+    return hip_ok(smq::launch_rope_kv(q, k, v, ntok, sh, cos_table, sin_table, keys, values, pos0, pos_dev, g.flag,
+                                      g.cur),
+                  "rope_kv")
+               ? SMQ_OK
+               : t_status;
+}
+
+smq_status smq_attention(const float *q, const float *keys, const float *values, float *att, uint32_t ntok,
+                         const smq_attn_shape *shape, uint32_t pos0, const int32_t *pos_dev) {
+    if (!ready()) return t_status;
+    smq::AttnShape sh;
+    if (!attn_shape(shape, &sh, "attention")) return t_status;
+    if (!ntok) return SMQ_OK;
+    if (!pos_dev && (pos0 > sh.context || ntok > sh.context - pos0))
+        return set_status(SMQ_ERR_RANGE, "token batch exceeds context");
+    const size_t cache = (size_t)sh.context * sh.kv_dim * 4;
+    if (!extent_ok(q, (size_t)ntok * sh.q_dim * 4, "q") || !extent_ok(att, (size_t)ntok * sh.q_dim * 4, "att") ||
+        !extent_ok(keys, cache, "keys") || !extent_ok(values, cache, "values") ||
+        !extent_ok(pos_dev, pos_dev ? 4 : 0, "pos"))
+        return t_status;
+    return hip_ok(smq::launch_attention(q, keys, values, att, ntok, sh, pos0, pos_dev, g.flag, g.cur), "attention")
+               ? SMQ_OK
+               : t_status;
+}
+
+smq_status smq_argmax(const float *logits, uint32_t vocab, const unsigned char *banned, uint32_t *token) {
+    if (!ready()) return t_status;
+    if (!vocab) return set_status(SMQ_ERR_RANGE, "argmax: empty vocabulary");
+    if (!extent_ok(logits, (size_t)vocab * 4, "logits") || !extent_ok(banned, banned ? vocab : 0, "banned") ||
+        !extent_ok(token, 4, "token"))
+        return t_status;
+    return hip_ok(smq::launch_argmax(logits, vocab, banned, token, g.cur), "argmax") ? SMQ_OK : t_status;
+}
+
+smq_status smq_embed(const smq_qmat *embed, const uint32_t *tokens, uint32_t ntok, float *x) {
+    if (!ready()) return t_status;
+    if (!embed || (embed->dtype != 1 && embed->dtype != 2) || embed->nb != (embed->cols + smq::QK - 1) / smq::QK ||
+        embed->row_bytes < (size_t)embed->nb * block_bytes(embed->dtype == 2))
+        return set_status(SMQ_ERR_FORMAT, "embed: invalid matrix descriptor");
+    if (!ntok) return SMQ_OK;
+    if (!extent_ok(embed->data, (size_t)embed->rows * embed->row_bytes, "embed") ||
+        !extent_ok(tokens, (size_t)ntok * 4, "tokens") || !extent_ok(x, (size_t)ntok * embed->cols * 4, "x"))
+        return t_status;
+    return hip_ok(smq::launch_embed(embed->data, embed->row_bytes, embed->dtype == 2, embed->rows, tokens, ntok,
+                                    embed->cols, x, g.flag, g.cur),
+                  "embed")
+               ? SMQ_OK
+               : t_status;
+}
+
+smq_status smq_decode_advance(int32_t *pos, uint32_t *count, const uint32_t *token, uint32_t *history,
+                              uint32_t capacity) {
+    if (!ready()) return t_status;
+    if (!extent_ok(pos, 4, "pos") || !extent_ok(count, 4, "count") || !extent_ok(token, 4, "token") ||
+        !extent_ok(history, (size_t)capacity * 4, "history"))
+        return t_status;
+    return hip_ok(smq::launch_decode_advance(pos, count, token, history, capacity, g.cur), "decode_advance")
+               ? SMQ_OK
+               : t_status;
 }
 
 void smq_dequantize_q8_row(const unsigned char *w, uint32_t cols, float *out) {

@@ -27,6 +27,7 @@ struct Item {
     size_t y_stride;
     uint32_t rows;
     uint32_t tile_begin; /* first workgroup tile of this item */
+    int accumulate;      /* y += result (the residual add of model.c:540, 643) */
 };
 
 struct MatArgs {
@@ -53,6 +54,25 @@ hipError_t launch_matmul_mfma(const MatArgs &a, bool q5, int32_t *sums, hipStrea
 constexpr uint32_t MAX_ROW = 16384;
 hipError_t launch_row_quantize(const float *src, const float *norm, float eps, const float *gate, int act,
                                uint32_t rows, uint32_t n, float *y, float *d, int8_t *q, int *flag, hipStream_t s);
+/* Decoder pieces (model.c:425-542, 673-676; sampler.c:57-63). pos_dev, when
+ * not NULL, supplies the first position from device memory (graph replay).
+ * RoPE tables hold `pairs` floats per absolute position; caches hold kv_dim
+ * floats per position, `context` positions. */
+constexpr uint32_t MAX_HEAD_DIM = 256;
+constexpr uint32_t MAX_ATT_POSITIONS = 16384; /* one f32 score per position in LDS */
+struct AttnShape {
+    uint32_t heads, kv_heads, head_dim, q_dim, kv_dim, pairs, window, context;
+};
+hipError_t launch_rope_kv(float *q, float *k, const float *v, uint32_t ntok, const AttnShape &sh, const float *cs,
+                          const float *sn, float *kcache, float *vcache, uint32_t pos0, const int32_t *pos_dev,
+                          int *flag, hipStream_t s);
+hipError_t launch_attention(const float *q, const float *kcache, const float *vcache, float *att, uint32_t ntok,
+                            const AttnShape &sh, uint32_t pos0, const int32_t *pos_dev, int *flag, hipStream_t s);
+hipError_t launch_decode_advance(int32_t *pos, uint32_t *count, const uint32_t *token, uint32_t *history,
+                                 uint32_t capacity, hipStream_t s);
+hipError_t launch_argmax(const float *logits, uint32_t n, const unsigned char *banned, uint32_t *out, hipStream_t s);
+hipError_t launch_embed(const unsigned char *w, size_t row_bytes, bool q5, uint32_t vocab, const uint32_t *tokens,
+                        uint32_t ntok, uint32_t cols, float *out, int *flag, hipStream_t s);
 hipError_t launch_dequantize_row(const unsigned char *w, uint32_t cols, float *out, bool q5, hipStream_t s);
 
 }  // namespace smq

@@ -103,8 +103,10 @@ __device__ __forceinline__ uint32_t find_item(const MatArgs &a, uint32_t tile) {
 
 __device__ __forceinline__ void store_out(const Item &I, int *flag, uint32_t t, uint32_t r, float v) {
     if (I.bias) v = v + I.bias[r]; /* model.c:259-262 */
-    I.y[(size_t)t * I.y_stride + r] = v;
     if (flag && !(fabsf(v) <= FLT_MAX)) *flag = 1;
+    float *cell = &I.y[(size_t)t * I.y_stride + r];
+    if (I.accumulate) v = *cell + v; /* residual: x += out (model.c:452-455) */
+    *cell = v;
 }
 
 /* DPP row shift by N lanes (row_shr:N): lane i reads lane i-N of its row of 16. */
@@ -902,6 +904,223 @@ __global__ __launch_bounds__(RW_WG) void k_row_quantize(const float *src, const 
     }
 }
 
+/* ------------------------------------------------------------------------
+ * Decoder pieces around the matmuls.
+ * ---------------------------------------------------------------------- */
+
+/* RoPE on q and k, then k and v into the KV cache (model.c:511-526): one
+ * workgroup per token. Adjacent pairs (2i, 2i+1), i < pairs, of every head
+ * rotate by the (cos, sin) table row of the token's absolute position
+ * (model.c:442-450); the other coordinates pass through. The cache holds
+ * kv_dim floats per position; a position at or past the context is refused
+ * (flag) rather than written. */
+__global__ __launch_bounds__(256) void k_rope_kv(float *q, float *k, const float *v, AttnShape sh, const float *cs,
+                                                 const float *sn, float *kcache, float *vcache, uint32_t pos0,
+                                                 const int32_t *pos_dev, int *flag) {
+    const uint32_t t = blockIdx.x, tid = threadIdx.x;
+    const uint32_t p = (pos_dev ? (uint32_t)*pos_dev : pos0) + t;
+    if (p >= sh.context) {
+        if (tid == 0 && flag) *flag = 1;
+        return;
+    }
+    float *qt = q + (size_t)t * sh.q_dim;
+    float *kt = k + (size_t)t * sh.kv_dim;
+    const float *vt = v + (size_t)t * sh.kv_dim;
+    const float *ct = cs + (size_t)p * sh.pairs, *st = sn + (size_t)p * sh.pairs;
+    float *kslot = kcache + (size_t)p * sh.kv_dim;
+    float *vslot = vcache + (size_t)p * sh.kv_dim;
+    const uint32_t qpairs = sh.heads * sh.pairs, kpairs = sh.kv_heads * sh.pairs;
+    for (uint32_t i = tid; i < qpairs + kpairs; i += 256) {
+        const bool isq = i < qpairs;
+        const uint32_t j = isq ? i : i - qpairs, h = j / sh.pairs, pr = j % sh.pairs;
+        float *x = (isq ? qt : kt) + (size_t)h * sh.head_dim + 2 * pr;
+        const float a = x[0], b = x[1];
+        const float ac = a * ct[pr], bs = b * st[pr], as = a * st[pr], bc = b * ct[pr];
+        const float r0 = ac - bs, r1 = as + bc;
+        x[0] = r0;
+        x[1] = r1;
+        if (!isq) {
+            kslot[(size_t)h * sh.head_dim + 2 * pr] = r0;
+            kslot[(size_t)h * sh.head_dim + 2 * pr + 1] = r1;
+        }
+    }
+    /* the unrotated tail of each k head, and all of v */
+    for (uint32_t i = tid; i < sh.kv_dim; i += 256) {
+        vslot[i] = vt[i];
+        if (i % sh.head_dim >= 2 * sh.pairs) kslot[i] = kt[i];
+    }
+}
+
+/* One query head of one token over KV positions [start, pos]
+ * (kernels.c:1154-1176, model.c:459-491): scores in parallel, each a dot_f32
+ * in its eight-lane order (kernels.c:1119-1127) times 1/sqrt(hd); the maximum
+ * (order-free); exp_det(s - max) in parallel; the total summed in position
+ * order by one lane; weights s*inv; then head_dim lanes each add their
+ * output coordinate over positions in order. */
+__global__ __launch_bounds__(256) void k_attend(const float *q, const float *kcache, const float *vcache, float *att,
+                                                AttnShape sh, uint32_t pos0, const int32_t *pos_dev, int *flag) {
+    extern __shared__ __attribute__((aligned(16))) float sc[];
+    __shared__ float qv[MAX_HEAD_DIM];
+    __shared__ float red[256];
+    __shared__ float s_inv;
+    const uint32_t tid = threadIdx.x, t = blockIdx.x / sh.heads, h = blockIdx.x % sh.heads;
+    const uint32_t hd = sh.head_dim, kh = h / (sh.heads / sh.kv_heads);
+    const uint32_t pos = (pos_dev ? (uint32_t)*pos_dev : pos0) + t;
+    const uint32_t start = sh.window && pos >= sh.window ? pos - sh.window + 1 : 0, np = pos - start + 1;
+    if (pos >= sh.context) { /* the scores row holds at most context positions */
+        if (tid == 0 && flag) *flag = 1;
+        return;
+    }
+    const float *qh = q + (size_t)t * sh.q_dim + (size_t)h * hd;
+    for (uint32_t j = tid; j < hd; j += 256) qv[j] = qh[j];
+    __syncthreads();
+    const float factor = 1.0f / sqrtf((float)hd);
+    for (uint32_t i = tid; i < np; i += 256) {
+        const float *kp = kcache + (size_t)(start + i) * sh.kv_dim + (size_t)kh * hd;
+        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        uint32_t e = 0;
+        for (; e + 8 <= hd; e += 8)
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                const float pr = qv[e + l] * kp[e + l];
+                acc[l] = acc[l] + pr;
+            }
+        const float p04 = acc[0] + acc[4], p15 = acc[1] + acc[5], p26 = acc[2] + acc[6], p37 = acc[3] + acc[7];
+        const float ev = p04 + p26, od = p15 + p37;
+        float sum = ev + od;
+        for (; e < hd; ++e) {
+            const float pr = qv[e] * kp[e];
+            sum = sum + pr;
+        }
+        sc[i] = sum * factor;
+    }
+    __syncthreads();
+    float m = -FLT_MAX;
+    for (uint32_t i = tid; i < np; i += 256) m = sc[i] > m ? sc[i] : m;
+    red[tid] = m;
+    __syncthreads();
+    for (uint32_t w = 128; w > 0; w >>= 1) {
+        if (tid < w) red[tid] = red[tid + w] > red[tid] ? red[tid + w] : red[tid];
+        __syncthreads();
+    }
+    const float high = red[0];
+    for (uint32_t i = tid; i < np; i += 256) sc[i] = exp_det(sc[i] - high);
+    __syncthreads();
+    if (tid == 0) {
+        float total = 0.0f;
+        for (uint32_t i = 0; i < np; ++i) total = total + sc[i];
+        s_inv = 1.0f / total;
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    for (uint32_t i = tid; i < np; i += 256) sc[i] = sc[i] * inv;
+    __syncthreads();
+    for (uint32_t j = tid; j < hd; j += 256) {
+        const float *vp = vcache + (size_t)start * sh.kv_dim + (size_t)kh * hd + j;
+        float o = 0.0f;
+        uint32_t i = 0;
+        for (; i + 8 <= np; i += 8) {
+            float vv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) vv[u] = vp[(size_t)(i + u) * sh.kv_dim];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float pr = sc[i + u] * vv[u];
+                o = o + pr;
+            }
+        }
+        for (; i < np; ++i) {
+            const float pr = sc[i] * vp[(size_t)i * sh.kv_dim];
+            o = o + pr;
+        }
+        att[(size_t)t * sh.q_dim + (size_t)h * hd + j] = o;
+    }
+}
+
+/* Greedy choice (sampler.c:57-63): the first non-banned id, replaced by any
+ * later id with a strictly greater logit. Equivalently: the lowest id of the
+ * largest non-NaN logit, unless the first candidate itself is NaN. */
+__global__ __launch_bounds__(1024) void k_argmax(const float *logits, uint32_t n, const unsigned char *banned,
+                                                 uint32_t *out) {
+    __shared__ float bv[1024];
+    __shared__ uint32_t bi[1024], bf[1024];
+    const uint32_t tid = threadIdx.x;
+    float best = 0.0f;
+    uint32_t besti = UINT32_MAX, first = UINT32_MAX;
+    for (uint32_t i = tid; i < n; i += 1024) {
+        if (banned && banned[i]) continue;
+        if (first == UINT32_MAX) first = i;
+        const float v = logits[i];
+        if (v != v) continue;
+        if (besti == UINT32_MAX || v > best) {
+            best = v;
+            besti = i;
+        }
+    }
+    bv[tid] = best;
+    bi[tid] = besti;
+    bf[tid] = first;
+    __syncthreads();
+    for (uint32_t w = 512; w > 0; w >>= 1) {
+        if (tid < w) {
+            const uint32_t oi = bi[tid + w];
+            const float ov = bv[tid + w];
+            if (oi != UINT32_MAX &&
+                (bi[tid] == UINT32_MAX || ov > bv[tid] || (ov == bv[tid] && oi < bi[tid]))) {
+                bv[tid] = ov;
+                bi[tid] = oi;
+            }
+            if (bf[tid + w] < bf[tid]) bf[tid] = bf[tid + w];
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        const uint32_t f = bf[0];
+        *out = (f != UINT32_MAX && logits[f] != logits[f]) ? f : bi[0];
+    }
+}
+
+/* Bookkeeping after one replayed decode step: history[*count] = *token
+ * (bounded by capacity), then ++*count and ++*pos. One lane. */
+__global__ __launch_bounds__(64) void k_decode_advance(int32_t *pos, uint32_t *count, const uint32_t *token,
+                                                       uint32_t *history, uint32_t capacity) {
+    if (threadIdx.x != 0) return;
+    const uint32_t c = *count;
+    if (c < capacity) history[c] = *token;
+    *count = c + 1;
+    *pos = *pos + 1;
+}
+
+/* Embedding rows (model.c:669-677): x[t] = dequantized row tokens[t]
+ * (kernels.c:1044-1062). */
+template <bool Q5>
+__global__ __launch_bounds__(256) void k_embed(const unsigned char *w, size_t row_bytes, uint32_t vocab,
+                                               const uint32_t *tokens, uint32_t cols, float *out, int *flag) {
+    const uint32_t t = blockIdx.x, tok = tokens[t];
+    if (tok >= vocab) { /* ids are checked on the host; this only keeps the read in bounds */
+        if (threadIdx.x == 0 && flag) *flag = 1;
+        return;
+    }
+    const unsigned char *row = w + (size_t)tok * row_bytes;
+    for (uint32_t j = threadIdx.x; j < cols; j += 256) {
+        const uint32_t b = j / QK, kk = j % QK;
+        float scale;
+        int v;
+        if (Q5) {
+            const unsigned char *blk = row + (size_t)b * Q5_BYTES;
+            scale = half_to_float((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+            const uint32_t high = ld_u32_bytes(blk + 2);
+            const uint32_t lo = kk < 16 ? (blk[6 + kk] & 15u) : (uint32_t)(blk[6 + kk - 16] >> 4);
+            v = (int)(lo | (((high >> kk) & 1u) << 4)) - 16;
+        } else {
+            const unsigned char *blk = row + (size_t)b * Q8_BYTES;
+            scale = __uint_as_float(ld_u32_bytes(blk));
+            v = (int)(int8_t)blk[4 + kk];
+        }
+        out[(size_t)t * cols + j] = scale * (float)v;
+    }
+}
+
 /* Row dequantization (reference: src/kernels.c:1044-1062): scale * float(q). */
 template <bool Q5>
 __global__ __launch_bounds__(WG) void k_dequantize_row(const unsigned char *w, uint32_t cols, float *out) {
@@ -1074,6 +1293,43 @@ hipError_t launch_row_quantize(const float *src, const float *norm, float eps, c
         else SMQ_RQ(false, 0);
     }
 #undef SMQ_RQ
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_kv(float *q, float *k, const float *v, uint32_t ntok, const AttnShape &sh, const float *cs,
+                          const float *sn, float *kcache, float *vcache, uint32_t pos0, const int32_t *pos_dev,
+                          int *flag, hipStream_t s) {
+    if (!ntok) return hipSuccess;
+    hipLaunchKernelGGL(k_rope_kv, dim3(ntok), dim3(256), 0, s, q, k, v, sh, cs, sn, kcache, vcache, pos0, pos_dev,
+                       flag);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention(const float *q, const float *kcache, const float *vcache, float *att, uint32_t ntok,
+                            const AttnShape &sh, uint32_t pos0, const int32_t *pos_dev, int *flag, hipStream_t s) {
+    if (!ntok) return hipSuccess;
+    if (sh.context > MAX_ATT_POSITIONS || sh.head_dim > MAX_HEAD_DIM) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_attend, dim3(ntok * sh.heads), dim3(256), (size_t)sh.context * sizeof(float), s, q, kcache,
+                       vcache, att, sh, pos0, pos_dev, flag);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float *logits, uint32_t n, const unsigned char *banned, uint32_t *out, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, logits, n, banned, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed(const unsigned char *w, size_t row_bytes, bool q5, uint32_t vocab, const uint32_t *tokens,
+                        uint32_t ntok, uint32_t cols, float *out, int *flag, hipStream_t s) {
+    if (!ntok) return hipSuccess;
+    if (q5) hipLaunchKernelGGL(k_embed<true>, dim3(ntok), dim3(256), 0, s, w, row_bytes, vocab, tokens, cols, out, flag);
+    else hipLaunchKernelGGL(k_embed<false>, dim3(ntok), dim3(256), 0, s, w, row_bytes, vocab, tokens, cols, out, flag);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_advance(int32_t *pos, uint32_t *count, const uint32_t *token, uint32_t *history,
+                                 uint32_t capacity, hipStream_t s) {
+    hipLaunchKernelGGL(k_decode_advance, dim3(1), dim3(64), 0, s, pos, count, token, history, capacity);
     return hipGetLastError();
 }
 

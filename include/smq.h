@@ -55,6 +55,10 @@ typedef enum smq_status {
 smq_status smq_last_status(void);
 const char *smq_last_error(void);
 void smq_clear_error(void);
+/* Records a status and message for the calling thread, as sm_set does
+ * (src/util.h:40-43), so host code layered on this library (the forward pass
+ * in smq_model.h) reports through the same smq_last_error. Returns status. */
+smq_status smq_set_error(smq_status status, const char *message);
 
 /* ---- context ------------------------------------------------------------
  * One device per process (the reference's kernel table is process-global,

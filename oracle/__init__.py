@@ -4,9 +4,12 @@ Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import this package, and only as the checker. The GPU
 product never imports it.
 
-``Oracle`` wraps ``liboracle.so`` (the C restatement, ``smq_oracle.c``).
-``Reference`` wraps ``_ref/libsmref.so``: the reference's own kernel sources
-compiled where they lie (``oracle/Makefile``), present when it was built.
+``Oracle`` wraps ``liboracle.so`` (the C restatement, ``smq_oracle.c``);
+``OracleModel`` runs its restated forward pass (``smq_forward.c``) over a
+checkpoint's tensors. ``Reference`` wraps ``_ref/libsmref.so``: the
+reference's own kernel sources compiled where they lie (``oracle/Makefile``),
+present when it was built; ``ReferenceModel`` wraps ``_ref/libsmref_model.so``,
+the reference's own model layer behind a small driver (``ref_model.c``).
 """
 import ctypes
 import os
@@ -38,6 +41,23 @@ def build():
     if os.path.isdir("/root/reference/src"):
         targets.append("ref")
     subprocess.run(["make", "-s", "-B", "-C", HERE] + targets, check=True)
+
+
+class _OrcLayer(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("attn_norm", "ffn_norm", "q_bias", "k_bias", "v_bias", "q", "k", "v",
+                                               "o", "gate", "up", "down")] + \
+               [(n + "_dtype", _u32) for n in ("q", "k", "v", "o", "gate", "up", "down")]
+
+
+class _OrcModel(ctypes.Structure):
+    _fields_ = [(n, _u32) for n in ("dim", "hidden", "layers", "heads", "kv_heads", "head_dim", "vocab", "rotary_dim",
+                                    "window", "context", "llama3_rope", "llama3_original")] + \
+               [("eps", ctypes.c_float), ("theta", ctypes.c_float), ("local_theta", ctypes.c_float),
+                ("rope_factor", ctypes.c_double),
+                ("llama3_factor", ctypes.c_double), ("llama3_low", ctypes.c_double),
+                ("llama3_high", ctypes.c_double), ("embed", ctypes.c_void_p), ("head", ctypes.c_void_p),
+                ("embed_dtype", _u32), ("head_dtype", _u32), ("final_norm", ctypes.c_void_p),
+                ("layer", ctypes.POINTER(_OrcLayer)), ("keys", ctypes.c_void_p), ("values", ctypes.c_void_p)]
 
 
 class Oracle:
@@ -86,6 +106,9 @@ class Oracle:
         lib.orc_attend_f32.argtypes = [_f32p, _f32p, _f32p, _u32, _u32, _u32, _u32, _f32p, _f32p]
         lib.orc_argmax.restype = _u32
         lib.orc_argmax.argtypes = [_f32p, _u32, _u8p]
+        lib.orc_forward.restype = ctypes.c_int
+        lib.orc_forward.argtypes = [ctypes.POINTER(_OrcModel), ctypes.POINTER(_u32), _u32, _u32, ctypes.c_int,
+                                    _f32p]
         lib.orc_time_gemm_pass.restype = ctypes.c_double
         lib.orc_time_gemm_pass.argtypes = [ctypes.c_void_p, ctypes.POINTER(_u8p), ctypes.POINTER(_u32),
                                            ctypes.POINTER(_u32), ctypes.POINTER(_f32p), ctypes.POINTER(_i8p), _u32,
@@ -376,3 +399,174 @@ class Reference:
 
     def fn_addr(self, name):
         return ctypes.cast(getattr(self.lib, name), ctypes.c_void_p).value
+
+
+class OracleModel:
+    """The restated forward pass (smq_forward.c) over one-expert checkpoint
+    tensors. `cfg` is the config as key=value pairs (the text's keys);
+    `tensors` maps names to (dtype, rows, cols, ..., array) with the array
+    last (uint8 rows for Q8/Q5, float32 for F32). The KV cache lives here."""
+
+    def __init__(self, orc, cfg, tensors, context):
+        dim, heads = int(cfg["dim"]), int(cfg["heads"])
+        hd = int(cfg.get("head_dim", dim // heads))
+        self.orc, self.context = orc, context
+        self.vocab = int(cfg["vocab_size"])
+        self.layers = int(cfg["layers"])
+        self.kv_dim = int(cfg["kv_heads"]) * hd
+        self._keep = []
+
+        def arr(name, dtype):
+            t = tensors[name]
+            a = np.ascontiguousarray(t[-1], dtype)
+            self._keep.append(a)
+            return a.ctypes.data, int(t[0])
+
+        m = _OrcModel()
+        m.dim, m.hidden, m.layers, m.heads = dim, int(cfg["hidden_dim"]), self.layers, heads
+        m.kv_heads, m.head_dim, m.vocab = int(cfg["kv_heads"]), hd, self.vocab
+        m.rotary_dim = int(cfg.get("rotary_dim", hd))
+        m.window = int(cfg.get("sliding_window", 0))
+        m.context = context
+        # config.c parses reals with strtod and narrows eps and theta to float
+        m.eps = float(np.float32(float(cfg["rms_eps"])))
+        m.theta = float(np.float32(float(cfg["rope_theta"])))
+        m.local_theta = float(np.float32(float(cfg.get("rope_local_theta", cfg["rope_theta"]))))
+        m.rope_factor = float(cfg.get("rope_attention_factor", 1.0))
+        l3 = "rope_llama3_factor" in cfg
+        m.llama3_rope = int(l3)
+        if l3:
+            m.llama3_factor = float(cfg["rope_llama3_factor"])
+            m.llama3_low = float(cfg["rope_llama3_low_freq_factor"])
+            m.llama3_high = float(cfg["rope_llama3_high_freq_factor"])
+            m.llama3_original = int(cfg["rope_llama3_original_context"])
+        m.embed, m.embed_dtype = arr("embed", np.uint8)
+        m.head, m.head_dtype = arr("lm_head" if "lm_head" in tensors else "embed", np.uint8)
+        m.final_norm, _ = arr("final_norm", np.float32)
+        layers = (_OrcLayer * self.layers)()
+        qwen = cfg.get("architecture") == "smolmoe_qwen2"
+        for i in range(self.layers):
+            p, L = f"l.{i}.", layers[i]
+            L.attn_norm, _ = arr(p + "attn_norm", np.float32)
+            L.ffn_norm, _ = arr(p + "ffn_norm", np.float32)
+            if qwen:
+                L.q_bias, _ = arr(p + "q_bias", np.float32)
+                L.k_bias, _ = arr(p + "k_bias", np.float32)
+                L.v_bias, _ = arr(p + "v_bias", np.float32)
+            for n, key in (("q", "q"), ("k", "k"), ("v", "v"), ("o", "o"), ("gate", "e.0.gate"), ("up", "e.0.up"),
+                           ("down", "e.0.down")):
+                ptr, dt = arr(p + key, np.uint8)
+                setattr(L, n, ptr)
+                setattr(L, n + "_dtype", dt)
+        self.keys = np.zeros((self.layers, context, self.kv_dim), np.float32)
+        self.values = np.zeros((self.layers, context, self.kv_dim), np.float32)
+        m.layer = layers
+        m.keys, m.values = self.keys.ctypes.data, self.values.ctypes.data
+        self._layers, self._m = layers, m
+
+    def forward(self, tokens, pos0, mode=1):
+        """-> (ok, logits [rows, vocab]); ok False where the reference fails
+        with SM_ERR_NUMERIC."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        rows = 0 if mode == 0 else (t.size if mode == 2 else 1)
+        logits = np.zeros((max(rows, 1), self.vocab), np.float32)
+        ok = self.orc.lib.orc_forward(ctypes.byref(self._m), _ptr(t, ctypes.POINTER(_u32)), t.size, pos0, mode,
+                                      _ptr(logits, _f32p))
+        if ok < 0:
+            raise MemoryError("orc_forward allocation failed")
+        self.last_logits = logits[rows - 1] if rows else None
+        return bool(ok), logits[:rows]
+
+    def generate(self, pos, ntokens, banned=None):
+        """main.c:580-597 with temperature 0: out[0] from the last logits."""
+        out = []
+        for i in range(ntokens):
+            out.append(self.orc.argmax(self.last_logits, banned))
+            if i + 1 < ntokens:
+                ok, _ = self.forward([out[-1]], pos + i, 1)
+                assert ok
+        return np.array(out, np.uint32)
+
+
+class ReferenceModel:
+    """The reference's own model layer (model.c, modelfile.c, config.c,
+    sampler.c, ...) compiled from its sources with ref_model.c as driver."""
+
+    PATH = os.path.join(HERE, "_ref", "libsmref_model.so")
+
+    @classmethod
+    def available(cls):
+        return os.path.exists(cls.PATH)
+
+    _lib = None
+
+    @classmethod
+    def _load(cls):
+        if cls._lib is None:
+            lib = ctypes.CDLL(cls.PATH)
+            vp = ctypes.c_void_p
+            lib.ref_last_error.restype = ctypes.c_char_p
+            lib.ref_backend.restype = ctypes.c_char_p
+            lib.ref_backend.argtypes = [ctypes.c_int, ctypes.c_int]
+            lib.ref_model_open.restype = vp
+            lib.ref_model_open.argtypes = [ctypes.c_char_p, ctypes.c_char_p, _u32, _u32, _u32, _u32]
+            lib.ref_model_close.argtypes = [vp]
+            lib.ref_model_forward.argtypes = [vp, vp, _u32, _u32, ctypes.c_int]
+            lib.ref_model_prefill.argtypes = [vp, vp, _u32, _u32, ctypes.c_int]
+            lib.ref_model_logits.restype = vp
+            lib.ref_model_logits.argtypes = [vp]
+            lib.ref_model_kv.restype = vp
+            lib.ref_model_kv.argtypes = [vp, _u32, ctypes.c_int]
+            lib.ref_model_vocab.restype = _u32
+            lib.ref_model_vocab.argtypes = [vp]
+            lib.ref_model_set_banned.argtypes = [vp, vp]
+            lib.ref_model_generate.argtypes = [vp, _u32, _u32, vp]
+            cls._lib = lib
+        return cls._lib
+
+    def __init__(self, path, config_path=None, context=256, batch=64, logit_rows=1, threads=1, scalar=False):
+        lib = self._load()
+        self.backend = lib.ref_backend(int(scalar), 0).decode()
+        self._h = lib.ref_model_open(path.encode(), config_path.encode() if config_path else None, context, batch,
+                                     logit_rows, threads)
+        if not self._h:
+            raise RuntimeError(lib.ref_last_error().decode())
+        self.vocab = lib.ref_model_vocab(self._h)
+        self.context, self.logit_rows = context, logit_rows
+
+    def close(self):
+        if self._h:
+            self._lib.ref_model_close(self._h)
+            self._h = None
+
+    def _status(self, st):
+        if st != 0:
+            raise RuntimeError(f"status {st}: {self._lib.ref_last_error().decode()}")
+
+    def forward(self, tokens, pos0, mode=1):
+        t = np.ascontiguousarray(tokens, np.uint32)
+        return self._lib.ref_model_forward(self._h, t.ctypes.data, t.size, pos0, mode)
+
+    def prefill(self, tokens, pos0=0, last_logits=True):
+        t = np.ascontiguousarray(tokens, np.uint32)
+        self._status(self._lib.ref_model_prefill(self._h, t.ctypes.data, t.size, pos0, int(bool(last_logits))))
+
+    def logits(self, rows=1):
+        p = self._lib.ref_model_logits(self._h)
+        return np.ctypeslib.as_array(ctypes.cast(p, _f32p), (rows, self.vocab)).copy()
+
+    def kv(self, layer, values, positions, kv_dim):
+        p = self._lib.ref_model_kv(self._h, layer, int(bool(values)))
+        return np.ctypeslib.as_array(ctypes.cast(p, _f32p), (positions, kv_dim)).copy()
+
+    def set_banned(self, banned=None):
+        if banned is None:
+            self._lib.ref_model_set_banned(self._h, None)
+        else:
+            b = np.ascontiguousarray(banned, np.uint8)
+            self._lib.ref_model_set_banned(self._h, b.ctypes.data)
+
+    def generate(self, pos, ntokens):
+        out = np.zeros(ntokens, np.uint32)
+        self._status(self._lib.ref_model_generate(self._h, pos, ntokens, out.ctypes.data))
+        return out

@@ -60,6 +60,7 @@ _SIGS = {
     "smq_last_status": (ctypes.c_int, []),
     "smq_last_error": (ctypes.c_char_p, []),
     "smq_clear_error": (None, []),
+    "smq_set_error": (ctypes.c_int, [ctypes.c_int, ctypes.c_char_p]),
     "smq_init": (ctypes.c_int, [ctypes.c_int]),
     "smq_shutdown": (None, []),
     "smq_stream": (_vp, []),

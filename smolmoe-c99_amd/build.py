@@ -1,4 +1,5 @@
-"""Builds libsmq_gfx950.so in place (hipcc, gfx950 only).
+"""Builds libsmq_gfx950.so (hipcc, gfx950 only) and the C host forward pass
+libsmq_model.so (gcc, linked against it) in place.
 
 Flags that the arithmetic contract depends on:
   -ffp-contract=off                        no a*b+c fused into an FMA
@@ -16,6 +17,11 @@ ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libsmq_gfx950.so")
 SOURCES = [os.path.join(HERE, "csrc", "smq_kernels.hip"), os.path.join(HERE, "csrc", "smq_api.cpp")]
 HEADERS = [os.path.join(HERE, "csrc", "smq_internal.h"), os.path.join(ROOT, "include", "smq.h")]
+MODEL_LIB = os.path.join(HERE, "libsmq_model.so")
+MODEL_SOURCES = [os.path.join(HERE, "host", "smq_model.c")]
+# The host side keeps IEEE double/float as written (RoPE tables in double).
+MODEL_FLAGS = ["-std=c99", "-O2", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math", "-Wall", "-Wextra",
+               "-Werror"]
 
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
@@ -45,6 +51,14 @@ def build(verbose=False):
     if verbose and out.strip():
         sys.stderr.write(out + "\n")
     os.replace(LIB + ".tmp", LIB)
+    cmd = [os.environ.get("CC", "gcc")] + MODEL_FLAGS + ["-I", os.path.join(ROOT, "include"), "-o",
+                                                         MODEL_LIB + ".tmp"] + MODEL_SOURCES + \
+        ["-L", HERE, "-lsmq_gfx950", "-Wl,-rpath,$ORIGIN", "-lm"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr + "\n")
+        raise RuntimeError("gcc failed building libsmq_model.so")
+    os.replace(MODEL_LIB + ".tmp", MODEL_LIB)
     return LIB
 
 

@@ -175,6 +175,9 @@ extern "C" {
 smq_status smq_last_status(void) { return t_status; }
 const char *smq_last_error(void) { return t_message; }
 void smq_clear_error(void) { set_status(SMQ_OK, ""); }
+smq_status smq_set_error(smq_status status, const char *message) {
+    return set_status(status, "%s", message ? message : "");
+}
 
 smq_status smq_init(int device) {
     if (g.ready) {

@@ -9,3 +9,5 @@ if ROOT not in sys.path:
 
 smq = importlib.import_module("smolmoe-c99_amd")
 synth = importlib.import_module("smolmoe-c99_amd.synth")
+smoe = importlib.import_module("smolmoe-c99_amd.smoe")
+smodel = importlib.import_module("smolmoe-c99_amd.model")

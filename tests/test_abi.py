@@ -1,18 +1,21 @@
-"""CPU checks of the C-ABI library: it loads, exports every entry point that
-include/smq.h declares, and reports a missing GPU as a status (no compute)."""
+"""CPU checks of the C-ABI libraries: they load, export every entry point
+that include/smq.h and include/smq_model.h declare, and report a missing GPU
+as a status (no compute)."""
 import ctypes
 import os
 import re
 
 import pytest
 
-from smq_pkg import smq
+from smq_pkg import smodel, smq
 
-HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "smq.h")
+INCLUDE = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
+HEADER = os.path.join(INCLUDE, "smq.h")
+MODEL_HEADER = os.path.join(INCLUDE, "smq_model.h")
 
 
-def declared():
-    text = open(HEADER).read()
+def declared(header=HEADER):
+    text = open(header).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(smq_[a-z0-9_]+)\s*\(", text)))
 
@@ -50,3 +53,21 @@ def test_calls_without_init_report_state_error(lib):
     assert l.smq_last_status() == 7  # SM_ERR_STATE
     assert b"smq_init" in l.smq_last_error()
     l.smq_clear_error()
+
+
+def test_model_library_exports_its_header():
+    if not os.path.exists(smodel.MODEL_LIB):
+        pytest.fail("libsmq_model.so is not built: run __graft_entry__.build()")
+    lib = ctypes.CDLL(smodel.MODEL_LIB)
+    names = declared(MODEL_HEADER)
+    assert len(names) >= 15
+    assert not [n for n in names if not hasattr(lib, n)]
+    assert set(names) == set(smodel.exported_symbols())
+
+
+def test_model_open_without_init_reports_state_error(tmp_path):
+    smodel.load_model_lib()
+    path = tmp_path / "empty.smoe"
+    path.write_bytes(b"SMOEQ8\0\x01" + b"\0" * 8)
+    with pytest.raises(smq.SmqError):
+        smodel.Model(str(path), context=8, batch=1)

@@ -206,6 +206,12 @@ smq_status smq_rope_kv(float *q, float *k, const float *v, uint32_t ntok, const 
  * order), writing att[t] (heads*head_dim). Bit identical to the reference. */
 smq_status smq_attention(const float *q, const float *keys, const float *values, float *att, uint32_t ntok,
                          const smq_attn_shape *shape, uint32_t pos0, const int32_t *pos_dev);
+/* smq_attention followed by quantize_attention (model.c:402-406): att rows
+ * also quantized to Q8 into xd (ntok*nb f32) and xq (ntok*nb*32), nb =
+ * ceil(heads*head_dim / 32); one launch when head_dim % 32 == 0. */
+smq_status smq_attention_q8(const float *q, const float *keys, const float *values, float *att, uint32_t ntok,
+                            const smq_attn_shape *shape, uint32_t pos0, const int32_t *pos_dev, float *xd,
+                            int8_t *xq);
 /* sampler.c:57-63: *token = first non-banned id, replaced by any later
  * non-banned id with a strictly greater logit (NaN never wins unless it is
  * the first candidate). banned may be NULL. UINT32_MAX if every id is banned. */

@@ -136,6 +136,15 @@ smq_status smq_model_set_banned(smq_model *m, const unsigned char *banned);
  * reference would (the tokens up to EOS are the same). */
 smq_status smq_model_generate(smq_model *m, uint32_t pos, uint32_t ntokens, uint32_t *out);
 
+/* No reference counterpart (the reference's fixtures are built the same way by
+ * tests/support/fixture.ts and its Q8 writer tools/q8pack.c:38-44): writes a
+ * synthetic one-expert checkpoint for config_text (SMOEQ8 v3, the config
+ * embedded): matrices N(0, sigma) packed to Q8, norm weights 1, Qwen2
+ * biases N(0, sigma), seeded per tensor name; tied stores lm_head as an
+ * alias of embed. Host only (no GPU); `threads` worker threads. */
+smq_status smq_synth_checkpoint(const char *path, const char *config_text, uint64_t seed, float sigma, int tied,
+                                uint32_t threads);
+
 #ifdef __cplusplus
 }
 #endif

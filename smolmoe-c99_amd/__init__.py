@@ -93,6 +93,7 @@ _SIGS = {
     "smq_numeric_check": (ctypes.c_int, []),
     "smq_rope_kv": (ctypes.c_int, [_vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _vp, _vp, _vp, _vp, _u32, _vp]),
     "smq_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _u32, _vp]),
+    "smq_attention_q8": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _u32, _vp, _vp, _vp]),
     "smq_argmax": (ctypes.c_int, [_vp, _u32, _vp, _vp]),
     "smq_embed": (ctypes.c_int, [ctypes.POINTER(_QMat), _vp, _u32, _vp]),
     "smq_decode_advance": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32]),
@@ -369,6 +370,11 @@ def rope_kv(q, k, v, ntok, shape, cos_table, sin_table, keys, values, pos0=0, po
 
 def attention(q, keys, values, att, ntok, shape, pos0=0, pos_dev=None):
     _check(load().smq_attention(_p(q), _p(keys), _p(values), _p(att), ntok, ctypes.byref(shape), pos0, _p(pos_dev)))
+
+
+def attention_q8(q, keys, values, att, ntok, shape, xd, xq, pos0=0, pos_dev=None):
+    _check(load().smq_attention_q8(_p(q), _p(keys), _p(values), _p(att), ntok, ctypes.byref(shape), pos0,
+                                   _p(pos_dev), _p(xd), _p(xq)))
 
 
 def argmax(logits, vocab, banned, token):

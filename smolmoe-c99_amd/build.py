@@ -18,7 +18,7 @@ LIB = os.path.join(HERE, "libsmq_gfx950.so")
 SOURCES = [os.path.join(HERE, "csrc", "smq_kernels.hip"), os.path.join(HERE, "csrc", "smq_api.cpp")]
 HEADERS = [os.path.join(HERE, "csrc", "smq_internal.h"), os.path.join(ROOT, "include", "smq.h")]
 MODEL_LIB = os.path.join(HERE, "libsmq_model.so")
-MODEL_SOURCES = [os.path.join(HERE, "host", "smq_model.c")]
+MODEL_SOURCES = [os.path.join(HERE, "host", "smq_model.c"), os.path.join(HERE, "host", "smq_synth.c")]
 # The host side keeps IEEE double/float as written (RoPE tables in double).
 MODEL_FLAGS = ["-std=c99", "-O2", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math", "-Wall", "-Wextra",
                "-Werror"]
@@ -53,7 +53,7 @@ def build(verbose=False):
     os.replace(LIB + ".tmp", LIB)
     cmd = [os.environ.get("CC", "gcc")] + MODEL_FLAGS + ["-I", os.path.join(ROOT, "include"), "-o",
                                                          MODEL_LIB + ".tmp"] + MODEL_SOURCES + \
-        ["-L", HERE, "-lsmq_gfx950", "-Wl,-rpath,$ORIGIN", "-lm"]
+        ["-L", HERE, "-lsmq_gfx950", "-Wl,-rpath,$ORIGIN", "-lm", "-lpthread"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr + "\n")

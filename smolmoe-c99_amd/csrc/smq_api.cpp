@@ -506,7 +506,36 @@ smq_status smq_attention(const float *q, const float *keys, const float *values,
         !extent_ok(keys, cache, "keys") || !extent_ok(values, cache, "values") ||
         !extent_ok(pos_dev, pos_dev ? 4 : 0, "pos"))
         return t_status;
-    return hip_ok(smq::launch_attention(q, keys, values, att, ntok, sh, pos0, pos_dev, g.flag, g.cur), "attention")
+    return hip_ok(smq::launch_attention(q, keys, values, att, ntok, sh, pos0, pos_dev, g.flag, nullptr, nullptr, g.cur),
+                  "attention")
+               ? SMQ_OK
+               : t_status;
+}
+
+smq_status smq_attention_q8(const float *q, const float *keys, const float *values, float *att, uint32_t ntok,
+                            const smq_attn_shape *shape, uint32_t pos0, const int32_t *pos_dev, float *xd,
+                            int8_t *xq) {
+    if (!ready()) return t_status;
+    smq::AttnShape sh;
+    if (!attn_shape(shape, &sh, "attention_q8")) return t_status;
+    if (!ntok) return SMQ_OK;
+    if (!pos_dev && (pos0 > sh.context || ntok > sh.context - pos0))
+        return set_status(SMQ_ERR_RANGE, "token batch exceeds context");
+    const size_t cache = (size_t)sh.context * sh.kv_dim * 4, nbq = (sh.q_dim + smq::QK - 1) / smq::QK;
+    if (!extent_ok(q, (size_t)ntok * sh.q_dim * 4, "q") || !extent_ok(att, (size_t)ntok * sh.q_dim * 4, "att") ||
+        !extent_ok(keys, cache, "keys") || !extent_ok(values, cache, "values") ||
+        !extent_ok(pos_dev, pos_dev ? 4 : 0, "pos") || !extent_ok(xd, ntok * nbq * 4, "xd") ||
+        !extent_ok(xq, ntok * nbq * smq::QK, "xq"))
+        return t_status;
+    if (sh.head_dim % smq::QK == 0) /* each head owns whole blocks: quantized in the same kernel */
+        return hip_ok(smq::launch_attention(q, keys, values, att, ntok, sh, pos0, pos_dev, g.flag, xd, xq, g.cur),
+                      "attention_q8")
+                   ? SMQ_OK
+                   : t_status;
+    return hip_ok(smq::launch_attention(q, keys, values, att, ntok, sh, pos0, pos_dev, g.flag, nullptr, nullptr,
+                                        g.cur),
+                  "attention_q8") &&
+                   hip_ok(smq::launch_quantize_q8(att, ntok, sh.q_dim, xd, xq, g.flag, g.cur), "attention_q8")
                ? SMQ_OK
                : t_status;
 }

@@ -67,7 +67,8 @@ hipError_t launch_rope_kv(float *q, float *k, const float *v, uint32_t ntok, con
                           const float *sn, float *kcache, float *vcache, uint32_t pos0, const int32_t *pos_dev,
                           int *flag, hipStream_t s);
 hipError_t launch_attention(const float *q, const float *kcache, const float *vcache, float *att, uint32_t ntok,
-                            const AttnShape &sh, uint32_t pos0, const int32_t *pos_dev, int *flag, hipStream_t s);
+                            const AttnShape &sh, uint32_t pos0, const int32_t *pos_dev, int *flag, float *xd,
+                            int8_t *xq, hipStream_t s);
 hipError_t launch_decode_advance(int32_t *pos, uint32_t *count, const uint32_t *token, uint32_t *history,
                                  uint32_t capacity, hipStream_t s);
 hipError_t launch_argmax(const float *logits, uint32_t n, const unsigned char *banned, uint32_t *out, hipStream_t s);

@@ -749,6 +749,58 @@ __global__ __launch_bounds__(WG) void k_quantize_q8(const float *x, uint32_t row
     }
 }
 
+/* s = ((0 + a[0]) + a[1]) + ... + a[n-1] in f32, by one lane: the order of
+ * the reference's sequential loops (model.c:337, kernels.c:1150). a is
+ * 16-byte aligned LDS. Two register batches alternate so that the reads of
+ * one batch are in flight while the other is added (the scheduling barriers
+ * keep the compiler from sinking the reads below the adds). */
+__device__ __forceinline__ void add_batch(float &s, const float4 (&v)[8]) {
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        s = s + v[b].x;
+        s = s + v[b].y;
+        s = s + v[b].z;
+        s = s + v[b].w;
+    }
+}
+__device__ __forceinline__ void read_batch(float4 (&v)[8], const float4 *p) {
+#pragma unroll
+    for (int b = 0; b < 8; ++b) v[b] = p[b];
+}
+__device__ __forceinline__ float serial_sum_lds(const float *a, uint32_t n) {
+    const float4 *a4 = (const float4 *)a;
+    const uint32_t batches = n / 32; /* 32 floats = 8 float4 per batch */
+    float s = 0.0f;
+    uint32_t c = 0;
+    if (batches) {
+        float4 x[8], y[8];
+        read_batch(x, a4);
+        for (; c + 2 <= batches; c += 2) {
+            read_batch(y, a4 + 8 * (c + 1));
+            __builtin_amdgcn_sched_barrier(0);
+            add_batch(s, x);
+            read_batch(x, a4 + 8 * (c + 2 < batches ? c + 2 : c + 1)); /* clamped re-read past the end */
+            __builtin_amdgcn_sched_barrier(0);
+            add_batch(s, y);
+        }
+        if (c < batches) {
+            add_batch(s, x);
+            ++c;
+        }
+    }
+    const uint32_t rest = n - c * 32; /* < 32: read together, then added in order */
+    if (rest) {
+        const float *t = a + c * 32;
+        float v[32];
+#pragma unroll
+        for (uint32_t u = 0; u < 32; ++u) v[u] = t[u < rest ? u : rest - 1];
+#pragma unroll
+        for (uint32_t u = 0; u < 32; ++u)
+            if (u < rest) s = s + v[u];
+    }
+    return s;
+}
+
 /* ------------------------------------------------------------------------
  * Activation producers (reference: src/model.c:334-415, src/vecmath.c:61-93).
  * One workgroup of 1024 threads per token row: optional RMSNorm (sequential
@@ -817,16 +869,7 @@ __global__ __launch_bounds__(RW_WG) void k_row_quantize(const float *src, const 
         }
         __syncthreads();
         if (tid == 0) {
-            float sq = 0.0f;
-            uint32_t i = 0;
-            for (; i + 4 <= n; i += 4) {
-                const float4 p4 = *(const float4 *)&sq_lds[i];
-                sq = sq + p4.x;
-                sq = sq + p4.y;
-                sq = sq + p4.z;
-                sq = sq + p4.w;
-            }
-            for (; i < n; ++i) sq = sq + sq_lds[i];
+            const float sq = serial_sum_lds(sq_lds, n);
             const float inv = 1.0f / sqrtf(sq / (float)n + eps); /* model.c:338 */
             s_inv = inv;
             s_bad = !(fabsf(sq) <= FLT_MAX) || !(fabsf(inv) <= FLT_MAX);
@@ -951,89 +994,302 @@ __global__ __launch_bounds__(256) void k_rope_kv(float *q, float *k, const float
     }
 }
 
-/* One query head of one token over KV positions [start, pos]
- * (kernels.c:1154-1176, model.c:459-491): scores in parallel, each a dot_f32
- * in its eight-lane order (kernels.c:1119-1127) times 1/sqrt(hd); the maximum
- * (order-free); exp_det(s - max) in parallel; the total summed in position
- * order by one lane; weights s*inv; then head_dim lanes each add their
- * output coordinate over positions in order. */
-__global__ __launch_bounds__(256) void k_attend(const float *q, const float *kcache, const float *vcache, float *att,
-                                                AttnShape sh, uint32_t pos0, const int32_t *pos_dev, int *flag) {
-    extern __shared__ __attribute__((aligned(16))) float sc[];
-    __shared__ float qv[MAX_HEAD_DIM];
-    __shared__ float red[256];
+/* Attention of one query head of one token over KV positions [start, pos]
+ * (kernels.c:1154-1176, model.c:459-491), for the 32 output coordinates
+ * [32g, 32g+32) of the head: workgroup (t, h, g), 512 threads.
+ *  0. the first pass of V rows and each thread's first two K rows are
+ *     requested before anything else, so their latencies overlap;
+ *  1. scores: one thread per position, the 8-lane dot_f32 of kernels.c:1119-
+ *     1127 (acc[l] += q[e+l]*k[e+l] over groups of 8, lane tree, tail in
+ *     order), times 1/sqrt(hd);
+ *  2. the maximum (order-free) and exp_det(s - max) in parallel;
+ *  3. the total in position order by one lane, inv = 1/total;
+ *  4. the products (s_p*inv)*v_p[j] of ATT_CH rows at a time go to LDS in
+ *     parallel, then lane j of wave 0 adds them in position order while the
+ *     next rows load.
+ * Every workgroup of a head recomputes steps 1-3 (the same values), so a
+ * head's value sums spread over ceil(hd/32) workgroups. With xd/xq
+ * (head_dim % 32 == 0) the workgroup also quantizes its block of the
+ * attention row (quantize_attention, model.c:402-406). */
+constexpr uint32_t ATT_WG = 512;
+constexpr uint32_t ATT_JW = 32;   /* output coordinates per workgroup: one Q8 block */
+constexpr uint32_t ATT_CH = 256;  /* value rows per LDS pass */
+constexpr uint32_t ATT_CHP = ATT_CH + 4; /* products column pitch: lanes' 16-byte reads spread over banks */
+constexpr uint32_t ATT_PRE = ATT_CH * ATT_JW / 4 / ATT_WG; /* float4 V loads per thread per pass */
+constexpr uint32_t ATT_KT = 256;  /* K rows per LDS tile (head_dim <= 64) */
+constexpr uint32_t ATT_KTL = ATT_KT * 16 / ATT_WG; /* float4 K loads per thread per tile */
+constexpr uint32_t ATT_SHARED = ATT_KT * 68 > ATT_CHP * ATT_JW ? ATT_KT * 68 : ATT_CHP * ATT_JW; /* floats */
+
+struct DotAcc {
+    float a[8];
+};
+
+/* acc[l] += q[8g+l] * k[8g+l] for the groups g of kr (2 float4 each). */
+__device__ __forceinline__ void dot_groups(DotAcc &acc, const float4 *kr, const float4 *q4, uint32_t g0,
+                                           uint32_t ng) {
+#pragma unroll
+    for (uint32_t e = 0; e < 8; ++e) {
+        if (e < ng) {
+            const float4 ka = kr[2 * e], kb = kr[2 * e + 1];
+            const float4 qa = q4[2 * (g0 + e)], qb = q4[2 * (g0 + e) + 1];
+            float p;
+            p = qa.x * ka.x; acc.a[0] = acc.a[0] + p;
+            p = qa.y * ka.y; acc.a[1] = acc.a[1] + p;
+            p = qa.z * ka.z; acc.a[2] = acc.a[2] + p;
+            p = qa.w * ka.w; acc.a[3] = acc.a[3] + p;
+            p = qb.x * kb.x; acc.a[4] = acc.a[4] + p;
+            p = qb.y * kb.y; acc.a[5] = acc.a[5] + p;
+            p = qb.z * kb.z; acc.a[6] = acc.a[6] + p;
+            p = qb.w * kb.w; acc.a[7] = acc.a[7] + p;
+        }
+    }
+}
+
+/* The lane tree of kernels.c:40-50, then the tail elements in order. */
+__device__ __forceinline__ float dot_finish(const DotAcc &acc, const float *qv, const float *kp, uint32_t from,
+                                            uint32_t hd) {
+    const float p04 = acc.a[0] + acc.a[4], p15 = acc.a[1] + acc.a[5], p26 = acc.a[2] + acc.a[6],
+                p37 = acc.a[3] + acc.a[7];
+    const float ev = p04 + p26, od = p15 + p37;
+    float sum = ev + od;
+    for (uint32_t e = from; e < hd; ++e) {
+        const float p = qv[e] * kp[e];
+        sum = sum + p;
+    }
+    return sum;
+}
+
+/* K tile rows [tb, tb + ATT_KT) of one head (head_dim = 4*q4n <= 64) into
+ * registers: float4 f = tid + u*ATT_WG is element 4c of row f / q4n. Rows
+ * past np re-read the last row (in bounds, never used). */
+__device__ __forceinline__ void att_load_tile(float4 (&kr)[ATT_KTL], const float *kbase, uint32_t kvd, uint32_t q4n,
+                                              uint32_t np, uint32_t tb, uint32_t tid) {
+    const uint32_t trows = np - tb < ATT_KT ? np - tb : ATT_KT;
+#pragma unroll
+    for (uint32_t u = 0; u < ATT_KTL; ++u) {
+        const uint32_t f = tid + u * ATT_WG, r = f / q4n, c = f - r * q4n;
+        const uint32_t rr = r < trows ? r : trows - 1;
+        kr[u] = *(const float4 *)(kbase + (size_t)(tb + rr) * kvd + 4 * c);
+    }
+}
+__device__ __forceinline__ void att_store_tile(float *kt, const float4 (&kr)[ATT_KTL], uint32_t q4n, uint32_t kpitch,
+                                               uint32_t trows, uint32_t tid) {
+#pragma unroll
+    for (uint32_t u = 0; u < ATT_KTL; ++u) {
+        const uint32_t f = tid + u * ATT_WG, r = f / q4n, c = f - r * q4n;
+        if (r < trows) *(float4 *)&kt[r * kpitch + 4 * c] = kr[u];
+    }
+}
+
+__global__ __launch_bounds__(ATT_WG) void k_attend(const float *q, const float *kcache, const float *vcache, float *att,
+                                                   AttnShape sh, uint32_t pos0, const int32_t *pos_dev, int *flag,
+                                                   float *xd, int8_t *xq) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    __shared__ __attribute__((aligned(16))) float qv[MAX_HEAD_DIM];
+    __shared__ float red[ATT_WG / 64];
     __shared__ float s_inv;
-    const uint32_t tid = threadIdx.x, t = blockIdx.x / sh.heads, h = blockIdx.x % sh.heads;
-    const uint32_t hd = sh.head_dim, kh = h / (sh.heads / sh.kv_heads);
+    const uint32_t tid = threadIdx.x, hd = sh.head_dim, ngrp = (hd + ATT_JW - 1) / ATT_JW;
+    const uint32_t g = blockIdx.x % ngrp, th = blockIdx.x / ngrp, t = th / sh.heads, h = th % sh.heads;
+    const uint32_t kh = h / (sh.heads / sh.kv_heads), kvd = sh.kv_dim, j0 = g * ATT_JW;
+    const uint32_t jw = hd - j0 < ATT_JW ? hd - j0 : ATT_JW; /* coordinates this group owns */
     const uint32_t pos = (pos_dev ? (uint32_t)*pos_dev : pos0) + t;
-    const uint32_t start = sh.window && pos >= sh.window ? pos - sh.window + 1 : 0, np = pos - start + 1;
     if (pos >= sh.context) { /* the scores row holds at most context positions */
         if (tid == 0 && flag) *flag = 1;
         return;
     }
-    const float *qh = q + (size_t)t * sh.q_dim + (size_t)h * hd;
-    for (uint32_t j = tid; j < hd; j += 256) qv[j] = qh[j];
-    __syncthreads();
-    const float factor = 1.0f / sqrtf((float)hd);
-    for (uint32_t i = tid; i < np; i += 256) {
-        const float *kp = kcache + (size_t)(start + i) * sh.kv_dim + (size_t)kh * hd;
-        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        uint32_t e = 0;
-        for (; e + 8 <= hd; e += 8)
+    const uint32_t start = sh.window && pos >= sh.window ? pos - sh.window + 1 : 0, np = pos - start + 1;
+    float *sc = lds;
+    float *prod = lds + ((sh.context + 3) & ~3u); /* [ATT_JW][ATT_CHP]: column j holds its rows in order */
+    const bool vec = (hd & 3) == 0 && ((uintptr_t)kcache & 15) == 0 && ((uintptr_t)vcache & 15) == 0;
+    const float *kbase = kcache + (size_t)start * kvd + (size_t)kh * hd;
+    const float *vbase = vcache + (size_t)start * kvd + (size_t)kh * hd + j0;
+    const uint32_t groups = hd / 8;
+
+    /* 0. V pass 0 and the first K rows, requested up front */
+    const uint32_t fq = ATT_JW / 4; /* float4 per row segment */
+    const uint32_t frow = tid / fq, fcol = (tid % fq) * 4;
+    float4 pre[ATT_PRE];
+    auto load_pass = [&](uint32_t p0) __attribute__((always_inline)) {
 #pragma unroll
-            for (int l = 0; l < 8; ++l) {
-                const float pr = qv[e + l] * kp[e + l];
-                acc[l] = acc[l] + pr;
+        for (uint32_t u = 0; u < ATT_PRE; ++u) {
+            const uint32_t r = frow + u * (ATT_WG / fq), p = p0 + r;
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (p < np) {
+                const float *src = vbase + (size_t)p * kvd + fcol;
+                if (vec && fcol + 4 <= jw) {
+                    v = *(const float4 *)src;
+                } else {
+                    if (fcol + 0 < jw) v.x = src[0];
+                    if (fcol + 1 < jw) v.y = src[1];
+                    if (fcol + 2 < jw) v.z = src[2];
+                    if (fcol + 3 < jw) v.w = src[3];
+                }
             }
-        const float p04 = acc[0] + acc[4], p15 = acc[1] + acc[5], p26 = acc[2] + acc[6], p37 = acc[3] + acc[7];
-        const float ev = p04 + p26, od = p15 + p37;
-        float sum = ev + od;
-        for (; e < hd; ++e) {
-            const float pr = qv[e] * kp[e];
-            sum = sum + pr;
+            pre[u] = v;
         }
-        sc[i] = sum * factor;
+    };
+    load_pass(0);
+    /* K tiles (head_dim <= 64): rows loaded coalesced (hd/4 float4 per row,
+     * consecutive threads along a row), stored row-major in LDS with a pitch
+     * of hd+4 floats so that the row-per-thread 16-byte reads below do not
+     * conflict. */
+    const bool fast = vec && hd <= 64;
+    const uint32_t q4n = hd / 4, kpitch = hd + 4;
+    float *kt = prod; /* shares the products region (used later) */
+    const float *qh = q + (size_t)t * sh.q_dim + (size_t)h * hd;
+    for (uint32_t j = tid; j < hd; j += ATT_WG) qv[j] = qh[j];
+    __syncthreads();
+
+    /* 1. scores */
+    const float factor = 1.0f / sqrtf((float)hd);
+    const float4 *q4 = (const float4 *)qv;
+    uint32_t i = tid;
+    if (fast) {
+        for (uint32_t tb = 0; tb < np; tb += ATT_KT) {
+            const uint32_t trows = np - tb < ATT_KT ? np - tb : ATT_KT;
+            float4 kr[ATT_KTL];
+            att_load_tile(kr, kbase, kvd, q4n, np, tb, tid);
+            att_store_tile(kt, kr, q4n, kpitch, trows, tid);
+            __syncthreads();
+            if (tid < trows) {
+                const float4 *row = (const float4 *)&kt[tid * kpitch];
+                float4 k4[16];
+#pragma unroll
+                for (uint32_t u = 0; u < 16; ++u) k4[u] = row[u < q4n ? u : q4n - 1];
+                DotAcc acc = {{0, 0, 0, 0, 0, 0, 0, 0}};
+                dot_groups(acc, k4, q4, 0, groups);
+                sc[tb + tid] = dot_finish(acc, qv, kbase + (size_t)(tb + tid) * kvd, groups * 8, hd) * factor;
+            }
+            __syncthreads();
+        }
+        i = np;
+    }
+    for (; i < np; i += ATT_WG) { /* further rows, or head_dim > 64 */
+        const float *kp = kbase + (size_t)i * kvd;
+        DotAcc acc = {{0, 0, 0, 0, 0, 0, 0, 0}};
+        if (vec) {
+            const float4 *k4 = (const float4 *)kp;
+            for (uint32_t g0 = 0; g0 < groups; g0 += 8) { /* 64 floats of the row in flight */
+                const uint32_t ng = groups - g0 < 8 ? groups - g0 : 8, last = 2 * ng - 1;
+                float4 kr[16];
+#pragma unroll
+                for (uint32_t u = 0; u < 16; ++u) kr[u] = k4[2 * g0 + (u < last ? u : last)];
+                dot_groups(acc, kr, q4, g0, ng);
+            }
+        } else {
+            for (uint32_t e = 0; e < groups; ++e)
+#pragma unroll
+                for (int l = 0; l < 8; ++l) {
+                    const float p = qv[8 * e + l] * kp[8 * e + l];
+                    acc.a[l] = acc.a[l] + p;
+                }
+        }
+        sc[i] = dot_finish(acc, qv, kp, groups * 8, hd) * factor;
     }
     __syncthreads();
+
+    /* 2. max (order-free; NaN never wins, as in softmax_inv), exp */
     float m = -FLT_MAX;
-    for (uint32_t i = tid; i < np; i += 256) m = sc[i] > m ? sc[i] : m;
-    red[tid] = m;
-    __syncthreads();
-    for (uint32_t w = 128; w > 0; w >>= 1) {
-        if (tid < w) red[tid] = red[tid + w] > red[tid] ? red[tid + w] : red[tid];
-        __syncthreads();
+    for (uint32_t r = tid; r < np; r += ATT_WG) m = sc[r] > m ? sc[r] : m;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
     }
-    const float high = red[0];
-    for (uint32_t i = tid; i < np; i += 256) sc[i] = exp_det(sc[i] - high);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
-    if (tid == 0) {
-        float total = 0.0f;
-        for (uint32_t i = 0; i < np; ++i) total = total + sc[i];
-        s_inv = 1.0f / total;
-    }
+    float high = red[0];
+#pragma unroll
+    for (uint32_t w = 1; w < ATT_WG / 64; ++w) high = red[w] > high ? red[w] : high;
+    for (uint32_t r = tid; r < np; r += ATT_WG) sc[r] = exp_det(sc[r] - high);
+    __syncthreads();
+
+    /* 3. the total in position order */
+    if (tid == 0) s_inv = 1.0f / serial_sum_lds(sc, np);
     __syncthreads();
     const float inv = s_inv;
-    for (uint32_t i = tid; i < np; i += 256) sc[i] = sc[i] * inv;
-    __syncthreads();
-    for (uint32_t j = tid; j < hd; j += 256) {
-        const float *vp = vcache + (size_t)start * sh.kv_dim + (size_t)kh * hd + j;
-        float o = 0.0f;
-        uint32_t i = 0;
-        for (; i + 8 <= np; i += 8) {
-            float vv[8];
+
+    /* 4. weighted values: products in parallel, sums in order */
+    float o = 0.0f;
+    for (uint32_t p0 = 0; p0 < np; p0 += ATT_CH) {
+        /* kernels.c:1165: w = scores[p] * inv, then w * v[j] */
 #pragma unroll
-            for (int u = 0; u < 8; ++u) vv[u] = vp[(size_t)(i + u) * sh.kv_dim];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const float pr = sc[i + u] * vv[u];
-                o = o + pr;
+        for (uint32_t u = 0; u < ATT_PRE; ++u) {
+            const uint32_t r = frow + u * (ATT_WG / fq), p = p0 + r;
+            if (p < np) {
+                const float w = sc[p] * inv;
+                prod[(fcol + 0) * ATT_CHP + r] = w * pre[u].x;
+                prod[(fcol + 1) * ATT_CHP + r] = w * pre[u].y;
+                prod[(fcol + 2) * ATT_CHP + r] = w * pre[u].z;
+                prod[(fcol + 3) * ATT_CHP + r] = w * pre[u].w;
             }
         }
-        for (; i < np; ++i) {
-            const float pr = sc[i] * vp[(size_t)i * sh.kv_dim];
-            o = o + pr;
+        __syncthreads();
+        if (p0 + ATT_CH < np) load_pass(p0 + ATT_CH); /* next pass in flight during the sums */
+        if (tid < ATT_JW) {
+            /* lane j adds its column's rows in order: 16-byte reads, one batch of
+             * 8 reads in flight while the previous batch is added */
+            const uint32_t rows = np - p0 < ATT_CH ? np - p0 : ATT_CH, nbat = rows / 32;
+            const float *colp = prod + tid * ATT_CHP;
+            float acc = o;
+            uint32_t c = 0;
+            if (nbat) {
+                float4 x[8], y[8];
+                read_batch(x, (const float4 *)colp);
+                for (; c + 2 <= nbat; c += 2) {
+                    read_batch(y, (const float4 *)colp + 8 * (c + 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                    add_batch(acc, x);
+                    read_batch(x, (const float4 *)colp + 8 * (c + 2 < nbat ? c + 2 : c + 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                    add_batch(acc, y);
+                }
+                if (c < nbat) {
+                    add_batch(acc, x);
+                    ++c;
+                }
+            }
+            const uint32_t rest = rows - c * 32;
+            if (rest) {
+                const float *tl = colp + c * 32;
+                float v[32];
+#pragma unroll
+                for (uint32_t u = 0; u < 32; ++u) v[u] = tl[u < rest ? u : rest - 1];
+#pragma unroll
+                for (uint32_t u = 0; u < 32; ++u)
+                    if (u < rest) acc = acc + v[u];
+            }
+            o = acc;
         }
-        att[(size_t)t * sh.q_dim + (size_t)h * hd + j] = o;
+        __syncthreads();
+    }
+    if (tid < ATT_JW) {
+        const bool valid = tid < jw;
+        if (valid) att[(size_t)t * sh.q_dim + (size_t)h * hd + j0 + tid] = o;
+        if (xd) { /* this workgroup's 32 coordinates are one block (kernels.c:912-935) */
+            const float v = valid ? o : 0.0f, av = fabsf(v);
+            float mx = av;
+            int bad = valid && !(av <= FLT_MAX);
+#pragma unroll
+            for (int off = 16; off >= 1; off >>= 1) {
+                const float ot = __shfl_xor(mx, off, 32);
+                mx = ot > mx ? ot : mx;
+                bad |= __shfl_xor(bad, off, 32);
+            }
+            const float scale = mx / 127.0f;
+            const float qinv = scale >= FLT_MIN ? 1.0f / scale : 0.0f;
+            const uint32_t nbq = (sh.q_dim + QK - 1) / QK, blk = (h * hd + j0) / QK;
+            if (valid) {
+                const float pq = v * qinv;
+                int qi = (int)__builtin_rintf(pq);
+                qi = qi > 127 ? 127 : (qi < -127 ? -127 : qi);
+                xq[((size_t)t * nbq + blk) * QK + tid] = (int8_t)qi;
+            }
+            if (tid == 0) {
+                xd[(size_t)t * nbq + blk] = scale;
+                if (bad && flag) *flag = 1;
+            }
+        }
     }
 }
 
@@ -1306,11 +1562,23 @@ hipError_t launch_rope_kv(float *q, float *k, const float *v, uint32_t ntok, con
 }
 
 hipError_t launch_attention(const float *q, const float *kcache, const float *vcache, float *att, uint32_t ntok,
-                            const AttnShape &sh, uint32_t pos0, const int32_t *pos_dev, int *flag, hipStream_t s) {
+                            const AttnShape &sh, uint32_t pos0, const int32_t *pos_dev, int *flag, float *xd,
+                            int8_t *xq, hipStream_t s) {
     if (!ntok) return hipSuccess;
-    if (sh.context > MAX_ATT_POSITIONS || sh.head_dim > MAX_HEAD_DIM) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_attend, dim3(ntok * sh.heads), dim3(256), (size_t)sh.context * sizeof(float), s, q, kcache,
-                       vcache, att, sh, pos0, pos_dev, flag);
+    if (sh.context > MAX_ATT_POSITIONS || sh.head_dim > MAX_HEAD_DIM || sh.head_dim < 1 ||
+        (xd && sh.head_dim % QK))
+        return hipErrorInvalidValue;
+    const size_t lds = (((size_t)sh.context + 3) / 4 * 4 + (size_t)ATT_SHARED) * sizeof(float);
+    static bool raised = false;
+    if (!raised) { /* dynamic LDS beyond the 64 KiB default for long contexts */
+        const hipError_t e = hipFuncSetAttribute((const void *)k_attend, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)(((size_t)MAX_ATT_POSITIONS + ATT_SHARED) * sizeof(float)));
+        if (e != hipSuccess) return e;
+        raised = true;
+    }
+    const uint32_t groups = (sh.head_dim + ATT_JW - 1) / ATT_JW;
+    hipLaunchKernelGGL(k_attend, dim3(ntok * sh.heads * groups), dim3(ATT_WG), lds, s, q, kcache, vcache, att, sh, pos0,
+                       pos_dev, flag, xd, xq);
     return hipGetLastError();
 }
 

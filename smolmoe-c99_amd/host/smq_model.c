@@ -844,8 +844,7 @@ static smq_status attention_block(smq_model *m, uint32_t l, uint32_t n, uint32_t
     TRY(smq_matmul(qkv, 3, m->xd, m->xq, n));
     TRY(smq_rope_kv(m->q, m->k, m->v, n, &m->shape, m->rope_cos, m->rope_sin, m->keys + base, m->values + base, pos0,
                     pos_dev));
-    TRY(smq_attention(m->q, m->keys + base, m->values + base, m->att, n, &m->shape, pos0, pos_dev));
-    TRY(smq_quantize_q8_rows(m->att, n, m->q_dim, m->xd, m->xq));
+    TRY(smq_attention_q8(m->q, m->keys + base, m->values + base, m->att, n, &m->shape, pos0, pos_dev, m->xd, m->xq));
     qkv[0] = mat(&L->o, NULL, m->x, 1); /* x += o(att) */
     return smq_matmul(qkv, 1, m->xd, m->xq, n);
 }

@@ -55,6 +55,8 @@ _SIGS = {
     "smq_model_kv_layer": (_vp, [_vp, _u32, ctypes.c_int]),
     "smq_model_set_banned": (ctypes.c_int, [_vp, _vp]),
     "smq_model_generate": (ctypes.c_int, [_vp, _u32, _u32, _vp]),
+    "smq_synth_checkpoint": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_uint64, ctypes.c_float,
+                                            ctypes.c_int, _u32]),
 }
 
 _mlib = None
@@ -91,6 +93,13 @@ def config_read(path):
     c = Config()
     _check(load_model_lib().smq_config_read(path.encode(), ctypes.byref(c)))
     return c
+
+
+def synth_checkpoint(path, config_text, seed=1, sigma=0.02, tied=True, threads=8):
+    """Writes a synthetic one-expert checkpoint (smq_synth_checkpoint)."""
+    _check(load_model_lib().smq_synth_checkpoint(path.encode(), config_text.encode(), seed, sigma, int(bool(tied)),
+                                                 threads))
+    return path
 
 
 class ModelFile:

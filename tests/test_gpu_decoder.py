@@ -91,6 +91,9 @@ ATT_CASES = [
     (3, 1, 6, 0, 40, 4, 30, 1.0),        # hd < 8: tail only
     (2, 2, 64, 0, 300, 2, 290, 30.0),    # wide scores: exp underflows to 0
     (8, 8, 128, 3, 17, 17, 0, 1.0),      # every position, tiny window
+    (2, 1, 64, 0, 8192, 1, 8000, 1.0),   # 63 value chunks through both buffers
+    (4, 2, 128, 0, 2048, 2, 1500, 1.0),  # head_dim 128: 64-position chunks
+    (2, 1, 256, 0, 600, 1, 590, 1.0),    # head_dim 256: four outputs per lane
 ]
 
 
@@ -108,6 +111,31 @@ def test_attention(orc, heads, kv_heads, hd, window, context, ntok, pos0, scale)
     smq.numeric_check()
     want = attend_expect(orc, q, keys, values, heads, kv_heads, hd, window, pos0, ntok)
     assert_same_f32(att.download(np.float32).reshape(ntok, qd), want, "att")
+
+
+@pytest.mark.parametrize("heads,kv_heads,hd,window,context,ntok,pos0", [
+    (14, 2, 64, 0, 1024, 1, 700),   # decode: one launch quantizes its head's blocks
+    (4, 2, 96, 7, 300, 9, 100),     # head_dim 96: three blocks, the last lane group half used
+    (3, 1, 40, 0, 64, 5, 20),       # head_dim % 32 != 0: attention, then a separate quantize
+])
+def test_attention_q8(orc, heads, kv_heads, hd, window, context, ntok, pos0):
+    say("attention_q8", heads, kv_heads, hd, window, context, ntok, pos0)
+    qd, kd = heads * hd, kv_heads * hd
+    nb = (qd + 31) // 32
+    q = synth.normal(24, ntok * qd).reshape(ntok, qd)
+    keys = synth.normal(25, context * kd).reshape(context, kd)
+    values = synth.normal(26, context * kd).reshape(context, kd)
+    qb, kb, vb = dev(q), dev(keys), dev(values)
+    att = smq.DeviceBuffer(ntok * qd * 4)
+    xd, xq = smq.DeviceBuffer(ntok * nb * 4), smq.DeviceBuffer(ntok * nb * 32)
+    shape = smq.attn_shape(heads, kv_heads, hd, hd // 2, window, context)
+    smq.attention_q8(qb, kb, vb, att, ntok, shape, xd, xq, pos0)
+    smq.numeric_check()
+    want = attend_expect(orc, q, keys, values, heads, kv_heads, hd, window, pos0, ntok)
+    assert_same_f32(att.download(np.float32).reshape(ntok, qd), want, "att")
+    _, wd, wq = orc.quantize_q8(want)
+    assert_same_f32(xd.download(np.float32).reshape(ntok, nb), wd.reshape(ntok, nb), "att scales")
+    assert np.array_equal(xq.download(np.int8).reshape(ntok, nb * 32), wq.reshape(ntok, nb * 32))
 
 
 def test_attention_position_from_device(orc):

@@ -3,12 +3,15 @@
 
 Workload (the shape its metric is quoted on): the
 Q8 FFN matmuls of one Qwen2.5-0.5B decode token through all 24 layers —
-per layer the fused gate+up GEMV (2 x 4864 x 896, one launch, as the
-reference fuses them: src/model.c:547-561) and the down GEMV (896 x 4864).
-A step streams 24 distinct layers of weights (353 MB); two device copies of
-the model alternate between steps (706 MB > the 256 MB Infinity Cache), so
-every step reads its weights from HBM. Inputs are resident in HBM before the
-timed region; each step replays one captured HIP graph of the 48 launches.
+per layer the gate and up GEMVs (4864 x 896) and the down GEMV (896 x 4864),
+each with its layer's own quantized activation. A step streams 24 distinct
+layers of weights (353 MB) as two grouped launches of the persistent
+decode GEMV (48 gate/up GEMVs, then 24 down GEMVs: smq_gemv_grouped); two
+device copies of the model alternate between steps (706 MB > the 256 MB
+Infinity Cache), so every step reads its weights from HBM. Inputs are resident
+in HBM before the timed region; each step replays one captured HIP graph. The
+same step as 48 launches in layer order (what a decode token must do, each
+layer waiting for the previous one) is reported beside it.
 
 value = algorithmic bytes per step (weight blocks + int8 activations + f32
 activation scales + f32 outputs) / measured step time, in GB/s.
@@ -16,9 +19,12 @@ activation scales + f32 outputs) / measured step time, in GB/s.
 Also reported: the roofline of the dominant kernel (the gate+up GEMV; average
 launch duration from HIP events around back-to-back launches), the full
 decode-token matmul set (q/k/v fused + o + gate/up + down for 24 layers plus
-the LM head: 97 launches) as decode tok/s, the other BASELINE shapes, and the
+the LM head: 97 launches) as decode tok/s, the other BASELINE shapes, the
 reference's own AVX2 kernel (compiled from its sources, oracle/_ref) timed on
-this host's cores on the same weights.
+this host's cores on the same weights, and configs[4]: the whole random-init
+Qwen2.5-0.5B-shaped decoder through the device-resident forward (prefill 512
+ids, then 128 greedy decode steps as graph replays) with the reference's own
+model_forward on the same checkpoint as CPU rate and bit-exactness gate.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -138,26 +144,21 @@ def cpu_baseline(model, acts_x, acts_h, threads_list, budget_s, gpu_out):
 
 
 def traffic_probe():
-    """Short program for rocprofv3 --pmc runs: 8 launches of the dominant
-    kernel (fused gate+up GEMV, 9728x896 Q8) on 8 distinct weight copies, then
-    one 256 MiB device-to-device copy whose FETCH_SIZE / WRITE_SIZE calibrate the
-    counters (expected 262,144 KiB each)."""
+    """Short program for rocprofv3 --pmc runs: 4 launches of the dominant
+    kernel (the grouped gate/up launch: 48 GEMVs 4864x896 Q8, 235 MB) alternating
+    two model copies, then one 256 MiB device-to-device copy whose FETCH_SIZE /
+    WRITE_SIZE calibrate the counters (expected 262,144 KiB each)."""
     smq.init(0)
-    layer = Layer(1000)
-    ax = Act(2000, 1, DIM)
-    gu = smq.DeviceBuffer(2 * HIDDEN * 4)
-    mats = []
-    for _ in range(8):
-        g_ = smq.DeviceBuffer(layer.dev["gate"][0].nbytes)
-        u_ = smq.DeviceBuffer(layer.dev["up"][0].nbytes)
-        g_.copy_from(layer.dev["gate"][0])
-        u_.copy_from(layer.dev["up"][0])
-        mats.append((smq.QMat(g_, HIDDEN, DIM), smq.QMat(u_, HIDDEN, DIM)))
+    model = [Layer(1000 + 16 * l) for l in range(LAYERS)]
+    copies = [model, [layer.copy() for layer in model]]
+    ax = [Act(2000 + l, 1, DIM) for l in range(LAYERS)]
+    gu = [smq.DeviceBuffer(2 * HIDDEN * 4) for _ in range(LAYERS)]
     big = [smq.DeviceBuffer(256 << 20) for _ in range(2)]
     big[0].fill(1)
     smq.synchronize()
-    for g_, u_ in mats:
-        smq.matmul([(g_, None, gu.ptr), (u_, None, gu.ptr + HIDDEN * 4)], ax.d, ax.q, 1)
+    for i in range(4):
+        smq.gemv_grouped([(layer.qmat(k), None, gu[l].ptr + (HIDDEN * 4 if k == "up" else 0), False, ax[l].d,
+                           ax[l].q) for l, layer in enumerate(copies[i % 2]) for k in ("gate", "up")])
     smq.synchronize()
     big[1].copy_from(big[0])
     smq.synchronize()
@@ -165,8 +166,9 @@ def traffic_probe():
 
 
 def summarize_pmc(fetch_dir, write_dir):
-    """Per-dispatch HBM traffic of the gate+up GEMV from two rocprofv3 --pmc
-    runs of --traffic-probe, scaled by the copy's counter reading."""
+    """Per-dispatch HBM traffic of the grouped gate/up launch from two
+    rocprofv3 --pmc runs of --traffic-probe, scaled by the copy's counter
+    reading."""
     import csv
     import glob
 
@@ -174,7 +176,7 @@ def summarize_pmc(fetch_dir, write_dir):
         rows = []
         for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
             rows += [r for r in csv.DictReader(open(f)) if r["Counter_Name"] == counter]
-        gemv = [float(r["Counter_Value"]) for r in rows if "k_gemv" in r["Kernel_Name"]]
+        gemv = [float(r["Counter_Value"]) for r in rows if "k_gemv_pin" in r["Kernel_Name"]]
         copy = sum(float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]
                    and float(r["Counter_Value"]) > 1e5)
         return gemv, copy
@@ -187,7 +189,7 @@ def summarize_pmc(fetch_dir, write_dir):
     w_kib = float(np.median(write)) * wscale
     out = {"fetch_kib_raw_median": float(np.median(fetch)), "write_kib_raw_median": float(np.median(write)),
            "copy_fetch_kib_raw": fcopy, "copy_write_kib_raw": wcopy, "fetch_scale": fscale, "write_scale": wscale,
-           "traffic_bytes": int((f_kib + w_kib) * 1024), "algorithmic_bytes": q8_bytes(2 * HIDDEN, DIM),
+           "traffic_bytes": int((f_kib + w_kib) * 1024), "algorithmic_bytes": LAYERS * q8_bytes(2 * HIDDEN, DIM),
            "dispatches": len(fetch)}
     print(json.dumps(out))
     return out
@@ -256,31 +258,61 @@ def main():
             ffn_layer(layer, l)
         smq.gemm_q8(hd, 28 * 36, ax[0].d, ax[0].q, VOCAB, 1, 28, logits, VOCAB)
 
-    # one checked eager step (bounds checks on), then timing without host checks
+    def gateup_group(m):
+        """the 48 gate/up GEMVs of all layers (each layer's own activation): one launch"""
+        smq.gemv_grouped([(layer.qmat(k), None, gu_out[l].ptr + (HIDDEN * 4 if k == "up" else 0), False,
+                           ax[l].d, ax[l].q) for l, layer in enumerate(m) for k in ("gate", "up")])
+
+    def down_group(m):
+        smq.gemv_grouped([(layer.qmat("down"), None, y_out[l], False, ah[l].d, ah[l].q) for l, layer in enumerate(m)])
+
+    def ffn_streamed(m):
+        gateup_group(m)
+        down_group(m)
+
+    # one checked eager pass of each form (bounds checks on), then timing without host checks
     ffn_step(copies[0])
     smq.numeric_check()
+    seq_layer0 = [gu_out[0].download(np.float32), y_out[0].download(np.float32)]
+    for b in gu_out + y_out:
+        b.fill(0)
+    ffn_streamed(copies[0])
+    smq.numeric_check()
     smq.set_checks(False)
-
-    step_graphs = [smq.capture(lambda m=m: ffn_step(m)) for m in copies]
     step_bytes = LAYERS * (q8_bytes(2 * HIDDEN, DIM) + q8_bytes(DIM, HIDDEN))
+
+    # headline: the 72 GEMVs of the 24-layer FFN step streamed in two launches
+    step_graphs = [smq.capture(lambda m=m: ffn_streamed(m)) for m in copies]
     for i in range(args.warmup):
         step_graphs[i % 2].launch()
     ms_per_step = timed_graph(step_graphs, args.steps)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     smq.numeric_check()
     gpu_layer0 = [gu_out[0].download(np.float32), y_out[0].download(np.float32)]  # for the CPU parity gate
-    log(f"bench: FFN step {ms_per_step * 1e3:.1f} us, {value:.0f} GB/s")
+    same_as_sequential = all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(gpu_layer0, seq_layer0))
+    log(f"bench: FFN step streamed {ms_per_step * 1e3:.1f} us, {value:.0f} GB/s")
 
-    # dominant kernel: gate+up GEMV (k_gemv<Q8, RT=8>), back-to-back launches
-    gu_graphs = [smq.capture(lambda m=m: gateup_only(m)) for m in copies]
+    # dominant kernel: the gate/up group launch (k_gemv_pin<exact, RT=16, NT=512, D=2>, 235 MB)
+    gu_graphs = [smq.capture(lambda m=m: gateup_group(m)) for m in copies]
     timed_graph(gu_graphs, 4)
     reps = max(20, args.steps)
-    gu_ms = timed_graph(gu_graphs, reps) / LAYERS
-    gu_bytes = q8_bytes(2 * HIDDEN, DIM)
+    gu_ms = timed_graph(gu_graphs, reps)
+    gu_bytes = LAYERS * q8_bytes(2 * HIDDEN, DIM)
     gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
-    log(f"bench: gate+up GEMV {gu_ms * 1e3:.2f} us/launch, {gu_gbs:.0f} GB/s")
+    log(f"bench: gate/up group {gu_ms * 1e3:.2f} us/launch, {gu_gbs:.0f} GB/s")
 
-    extra = {}
+    # the same step as 48 dependent-order launches (as a decode must run them)
+    seq_graphs = [smq.capture(lambda m=m: ffn_step(m)) for m in copies]
+    timed_graph(seq_graphs, 4)
+    seq_ms = timed_graph(seq_graphs, max(20, args.steps))
+    one_ms = timed_graph([smq.capture(lambda m=m: gateup_only(m)) for m in copies], max(20, args.steps)) / LAYERS
+    extra = {"ffn_step_sequential": {
+        "what": "the same 24-layer FFN step as 48 launches in layer order (gate+up fused, down), one graph",
+        "us_per_step": round(seq_ms * 1e3, 2), "GBps": round(step_bytes / (seq_ms * 1e-3) / 1e9, 1),
+        "gateup_single_launch_us": round(one_ms * 1e3, 3),
+        "gateup_single_launch_GBps": round(q8_bytes(2 * HIDDEN, DIM) / (one_ms * 1e-3) / 1e9, 1),
+        "bit_identical_to_streamed": same_as_sequential}}
+    log(f"bench: FFN step sequential {seq_ms * 1e3:.1f} us")
     if not args.no_extra:
         dec_graphs = [smq.capture(lambda m=m, h=h: decode_matmuls(m, h)) for m, h in zip(copies, head)]
         timed_graph(dec_graphs, 4)
@@ -334,6 +366,9 @@ def main():
         single("quantize_q8_4864",
                lambda i: smq.quantize_q8_rows(qx.x, 1, HIDDEN, qx.d, qx.q), HIDDEN * 4 + HIDDEN + HIDDEN // 8, 32)
 
+    if not args.no_extra:
+        model_forward_extra(args, extra)
+
     cpu = None
     if not args.no_cpu:
         try:
@@ -354,7 +389,7 @@ def main():
             log(f"bench: cpu baseline failed: {ex!r}")
 
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", "gemv_q8_gateup_9728x896_traffic.json")
+    tfile = os.path.join(ROOT, "profiles", "gemv_pin_q8_gateup_group_traffic.json")
     if os.path.exists(tfile):  # measured by two rocprofv3 --pmc runs of --traffic-probe (see that file)
         with open(tfile) as f:
             traffic = json.load(f).get("traffic_bytes")
@@ -373,11 +408,14 @@ def main():
         "dtype": "int8",
         "data": "synthetic: seeded N(0,0.02) weights packed by the q8pack rule, N(0,1) activations quantized on GPU",
         "config": {"workload": "configs[1]: Qwen2.5-0.5B Q8 FFN matmuls, batch 1 (decode GEMV), all 24 layers "
-                               "(gate+up fused 9728x896 + down 896x4864 per layer), 353 MB/step, 2 model copies "
-                               "alternated", "bytes_per_step": step_bytes, "parallelism": "none (1 GPU)"},
+                               "(gate 4864x896, up 4864x896, down 896x4864 per layer, each with its layer's "
+                               "activation), 353 MB/step streamed as two grouped launches (48 gate/up, 24 down), "
+                               "2 model copies alternated", "bytes_per_step": step_bytes,
+                   "parallelism": "none (1 GPU)"},
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
-        "ffn_decode_tok_s": round(1000.0 / ms_per_step, 1),
-        "roofline": {"kernel": "k_gemv<Q8,exact,RT=8,direct> (fused gate+up, 9728x896)", "bound": "hbm",
+        "decode_tok_s": extra.get("c4_qwen05_forward", {}).get("decode_tok_s"),
+        "roofline": {"kernel": "k_gemv_pin<exact,RT=16,NT=512,D=2> (48 gate/up GEMVs 4864x896, one launch)",
+                     "bound": "hbm",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_per_launch": gu_bytes, "us_per_launch": round(gu_ms * 1e3, 3)},
@@ -386,6 +424,87 @@ def main():
         "wall_s": round(time.time() - t_start, 1),
     }
     print(json.dumps(line), flush=True)
+
+
+def model_forward_extra(args, extra):
+    """the whole Qwen2.5-0.5B-shaped decoder (random-init Q8 weights,
+    tied head) through the device-resident forward: prefill 512 random ids in
+    one batch, then 128 greedy decode steps replayed as captured graphs. With
+    the reference's own model layer built (oracle/_ref), the same checkpoint on
+    the host cores gives the CPU rate and the parity gate (logits after the
+    prompt, the first greedy tokens)."""
+    import tempfile
+    smoe = importlib.import_module("smolmoe-c99_amd.smoe")
+    smodel = importlib.import_module("smolmoe-c99_amd.model")
+    ncpu = len(os.sched_getaffinity(0))
+    path = os.path.join(tempfile.gettempdir(), f"smq_bench_qwen05_{os.getpid()}.smoe")
+    try:
+        t0 = time.time()
+        smodel.synth_checkpoint(path, smoe.config_text(smoe.QWEN05), seed=4000, sigma=0.02, tied=True,
+                                threads=min(16, ncpu))
+        t_synth = time.time() - t0
+        smq.set_checks(True)
+        m = smodel.Model(path, context=1024, batch=512, logit_rows=1)
+        banned = np.zeros(smoe.QWEN05["vocab_size"], np.uint8)
+        banned[256] = 1  # BOS (sampler.c:57-63 skips banned ids)
+        m.set_banned(banned)
+        prompt = np.random.default_rng(3000).integers(0, smoe.QWEN05["vocab_size"], 512).astype(np.uint32)
+        m.forward(prompt, 0, smodel.LOGITS_LAST)  # warm-up: first launches, graph capture
+        m.generate(512, 5)
+        smq.set_checks(False)
+        runs = []
+        for _ in range(3):
+            t0 = time.time()
+            m.forward(prompt, 0, smodel.LOGITS_LAST)
+            t1 = time.time()
+            gl = m.logits(1)
+            t1b = time.time()
+            toks = m.generate(512, 129)
+            t2 = time.time()
+            runs.append((t1 - t0, t2 - t1b))
+        pre_s = min(r[0] for r in runs)
+        dec_s = min(r[1] for r in runs)
+        smq.set_prefill_mfma(True)
+        t0 = time.time()
+        m.forward(prompt, 0, smodel.LOGITS_LAST)
+        mfma_s = time.time() - t0
+        smq.set_prefill_mfma(False)
+        e = {"what": "Qwen2.5-0.5B shape (24 layers, 896/4864, GQA 14/2, vocab 151936, tied), random-init Q8, "
+                     "prefill 512 ids in one batch then 128 greedy decode steps (HIP graph per step), BOS banned",
+             "decode_tok_s": round(128 / dec_s, 1), "decode_ms_per_token": round(dec_s / 128 * 1e3, 3),
+             "prefill_tok_s": round(512 / pre_s, 1), "prefill_ms": round(pre_s * 1e3, 2),
+             "prefill_mfma_tok_s": round(512 / mfma_s, 1),
+             "prefill_mfma_note": "int8-MFMA prefill: exact int32 block sums, f32 block order relaxed (not bit-exact)",
+             "decode_roofline_tok_s": round(8e12 / 555.7e6, 1), "weights_bytes_per_token": 555706368,
+             "synth_s": round(t_synth, 2), "first_tokens": toks[:8].tolist()}
+        del m
+        if not args.no_cpu:
+            import oracle
+            if oracle.ReferenceModel.available():
+                th = min(16, ncpu)
+                r = oracle.ReferenceModel(path, context=1024, batch=512, logit_rows=1, threads=th)
+                r.set_banned(banned)
+                t0 = time.time()
+                r.prefill(prompt, 0, True)
+                t1 = time.time()
+                rl = r.logits(1)
+                rt = r.generate(512, 9)
+                t2 = time.time()
+                e["cpu_reference"] = {"kind": "reference", "backend": r.backend, "threads": th,
+                                      "prefill_tok_s": round(512 / (t1 - t0), 1),
+                                      "decode_tok_s": round(8 / (t2 - t1), 2),
+                                      "sample": "the reference's own model_forward (src/model.c built from its "
+                                                "sources) on the same checkpoint: prefill 512, 8 decode steps"}
+                e["gpu_logits_bit_identical"] = bool(np.array_equal(gl.view(np.uint32), rl.view(np.uint32)))
+                e["gpu_tokens_identical_first9"] = toks[:9].tolist() == rt.tolist()
+                r.close()
+        extra["c4_qwen05_forward"] = e
+        log(f"bench: qwen0.5B forward: prefill {e['prefill_tok_s']} tok/s, decode {e['decode_tok_s']} tok/s")
+    except Exception as ex:  # the model leg must not hide the matmul result
+        log(f"bench: model forward leg failed: {ex!r}")
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
 
 
 def synth_q(act, cols):

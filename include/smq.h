@@ -177,6 +177,24 @@ typedef struct smq_mat_item {
  * in one launch. A non-finite output raises the sticky numeric flag.
  * Asynchronous; SMQ_ERR_STATE if the items differ in width (model.c:298). */
 smq_status smq_matmul(const smq_mat_item *items, uint32_t n, const float *xd, const int8_t *xq, uint32_t ntok);
+/* No reference counterpart (the reference runs such matrices one matmul
+ * after another, e.g. its experts in routed_experts, model.c:587-606):
+ * independent decode GEMVs (one token each) in one launch. Item i computes
+ * y_i[r] = dot(w_i row r, x_i) (+ bias_i[r]; added into y_i when accumulate),
+ * with its own quantized activation x_i = (xd_i, xq_i). All items share nb
+ * and the weight format; every output is bit-identical to smq_matmul's.
+ * Persistent workgroups stream all items' weights back to back. At most
+ * SMQ_MAX_GROUP items; asynchronous; the numeric flag as smq_matmul. */
+#define SMQ_MAX_GROUP 48
+typedef struct smq_group_item {
+    const smq_qmat *w;  /* host pointer to the descriptor */
+    const float *bias;  /* device, may be NULL */
+    float *y;           /* device */
+    int accumulate;
+    const float *xd;    /* device: nb scales */
+    const int8_t *xq;   /* device: nb*32 values */
+} smq_group_item;
+smq_status smq_gemv_grouped(const smq_group_item *items, uint32_t n);
 /* Synchronizes, then returns SMQ_ERR_NUMERIC (and clears the flag) if any
  * quantize or matmul since the last check saw a non-finite value. */
 smq_status smq_numeric_check(void);

@@ -51,6 +51,11 @@ class _MatItem(ctypes.Structure):
     _fields_ = [("w", ctypes.POINTER(_QMat)), ("bias", _vp), ("y", _vp), ("accumulate", ctypes.c_int)]
 
 
+class _GroupItem(ctypes.Structure):
+    _fields_ = [("w", ctypes.POINTER(_QMat)), ("bias", _vp), ("y", _vp), ("accumulate", ctypes.c_int),
+                ("xd", _vp), ("xq", _vp)]
+
+
 class _AttnShape(ctypes.Structure):
     _fields_ = [("heads", _u32), ("kv_heads", _u32), ("head_dim", _u32), ("rotary_pairs", _u32), ("window", _u32),
                 ("context", _u32)]
@@ -91,6 +96,7 @@ _SIGS = {
     "smq_set_prefill_mfma": (None, [ctypes.c_int]),
     "smq_matmul": (ctypes.c_int, [ctypes.POINTER(_MatItem), _u32, _vp, _vp, _u32]),
     "smq_numeric_check": (ctypes.c_int, []),
+    "smq_gemv_grouped": (ctypes.c_int, [ctypes.POINTER(_GroupItem), _u32]),
     "smq_rope_kv": (ctypes.c_int, [_vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _vp, _vp, _vp, _vp, _u32, _vp]),
     "smq_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _u32, _vp]),
     "smq_attention_q8": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _u32, _vp, _vp, _vp]),
@@ -356,6 +362,21 @@ def matmul(items, xd, xq, ntok):
         arr[i].y = _p(it[2])
         arr[i].accumulate = int(bool(it[3])) if len(it) > 3 else 0
     _check(load().smq_matmul(arr, len(items), _p(xd), _p(xq), ntok))
+
+
+def gemv_grouped(items):
+    """items: sequence of (QMat, bias or None, y, accumulate, xd, xq): independent
+    one-token GEMVs with their own activations, one launch."""
+    cm = [it[0]._c() for it in items]
+    arr = (_GroupItem * len(items))()
+    for i, it in enumerate(items):
+        arr[i].w = ctypes.pointer(cm[i])
+        arr[i].bias = _p(it[1])
+        arr[i].y = _p(it[2])
+        arr[i].accumulate = int(bool(it[3]))
+        arr[i].xd = _p(it[4])
+        arr[i].xq = _p(it[5])
+    _check(load().smq_gemv_grouped(arr, len(items)))
 
 
 # ---- decoder pieces (src/model.c:425-542, 669-677; src/sampler.c:57-63)

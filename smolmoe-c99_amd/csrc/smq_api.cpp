@@ -435,6 +435,54 @@ smq_status smq_matmul(const smq_mat_item *items, uint32_t n, const float *xd, co
     return SMQ_OK;
 }
 
+smq_status smq_gemv_grouped(const smq_group_item *items, uint32_t n) {
+    if (!ready()) return t_status;
+    if (!items || n < 1 || n > SMQ_MAX_GROUP) return set_status(SMQ_ERR_RANGE, "gemv_grouped: %u items", n);
+    const smq_qmat *w0 = items[0].w;
+    if (!w0) return set_status(SMQ_ERR_RANGE, "gemv_grouped: item 0 has no matrix");
+    smq::GroupArgs ga;
+    memset(&ga, 0, sizeof(ga));
+    ga.nb = w0->nb;
+    ga.flag = g.flag;
+    for (uint32_t i = 0; i < n; ++i) {
+        const smq_qmat *w = items[i].w;
+        if (!w) return set_status(SMQ_ERR_RANGE, "gemv_grouped: item %u has no matrix", i);
+        if (w->nb != ga.nb || w->dtype != w0->dtype)
+            return set_status(SMQ_ERR_STATE, "gemv_grouped: items differ in width or format");
+        if (w->dtype != 1 && w->dtype != 2) return set_status(SMQ_ERR_FORMAT, "gemv_grouped: dtype %u", w->dtype);
+        if (w->nb != (w->cols + smq::QK - 1) / smq::QK)
+            return set_status(SMQ_ERR_RANGE, "gemv_grouped: nb %u does not match %u columns", w->nb, w->cols);
+        if (!check_operands(w->data, w->row_bytes, w->rows, w->nb, w->dtype == 2, items[i].xd, items[i].xq, 1, w->nb,
+                            items[i].y, w->rows, "gemv_grouped") ||
+            !extent_ok(items[i].bias, items[i].bias ? (size_t)w->rows * 4 : 0, "bias"))
+            return t_status;
+        smq::GroupItem &it = ga.item[ga.nitems++];
+        it.w = w->data;
+        it.row_bytes = w->row_bytes;
+        it.bias = items[i].bias;
+        it.y = items[i].y;
+        it.xd = items[i].xd;
+        it.xq = items[i].xq;
+        it.rows = w->rows;
+        it.accumulate = items[i].accumulate != 0;
+    }
+    const bool q5 = w0->dtype == 2;
+    if (!smq::group_layout_ok(ga, q5)) {
+        /* unaligned rows or activations, or very wide rows: one matmul per item */
+        for (uint32_t i = 0; i < n; ++i) {
+            smq_mat_item mi;
+            mi.w = items[i].w;
+            mi.bias = items[i].bias;
+            mi.y = items[i].y;
+            mi.accumulate = items[i].accumulate;
+            const smq_status st = smq_matmul(&mi, 1, items[i].xd, items[i].xq, 1);
+            if (st != SMQ_OK) return st;
+        }
+        return SMQ_OK;
+    }
+    return hip_ok(smq::launch_gemv_grouped(ga, q5, g.fast != 0, g.cur), "gemv_grouped") ? SMQ_OK : t_status;
+}
+
 smq_status smq_numeric_check(void) {
     if (!ready()) return t_status;
     int bad = 0;

@@ -40,6 +40,30 @@ struct MatArgs {
     int *flag; /* set to 1 on a non-finite output; may be NULL */
 };
 
+/* Grouped decode GEMV (ntok == 1): independent matrices with the same nb,
+ * each with its own activation, streamed by persistent workgroups. */
+constexpr uint32_t MAX_GROUP_ITEMS = 48;
+struct GroupItem {
+    const unsigned char *w;
+    size_t row_bytes;
+    const float *bias;
+    float *y;
+    const float *xd;
+    const int8_t *xq;
+    uint32_t rows;
+    uint32_t tile_begin;
+    int accumulate;
+    uint32_t wg_begin, nwg; /* pinned launch: this item's workgroups */
+};
+struct GroupArgs {
+    GroupItem item[MAX_GROUP_ITEMS];
+    uint32_t nitems, nb, total_tiles;
+    int *flag;
+};
+/* Layout the streaming kernel needs: 4-byte aligned rows, Q5 nb even. */
+bool group_layout_ok(const GroupArgs &g, bool q5);
+hipError_t launch_gemv_grouped(GroupArgs &g, bool q5, bool fast, hipStream_t s);
+
 /* Launchers; each returns the hipError_t of its launch. */
 hipError_t launch_quantize_q8(const float *x, uint32_t rows, uint32_t n, float *d, int8_t *q, int *flag,
                               hipStream_t s);

@@ -15,6 +15,7 @@
  */
 #include <float.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include "smq_internal.h"
 
@@ -124,6 +125,72 @@ __device__ __forceinline__ float reduce8_to_lane7(float a) {
     const float s = a + shr_dpp<4>(a);
     const float t = s + shr_dpp<2>(s);
     return t + shr_dpp<1>(t);
+}
+
+/* One chain thread's step over `count` (<= 4*NQ) products in block order:
+ * float4 p[q*ps] holds blocks 4q..4q+3 (fast mode: their scales in
+ * d[q*dst]). Up to eight float4 are read at once before the first add
+ * (clamped indices); the adds run in block order: acc = acc + p (exact) or
+ * fma(d, p, acc). */
+template <bool FAST, int G>
+__device__ __forceinline__ void chain_read(float4 (&v)[G], float4 (&w)[G], const float4 *p, uint32_t ps,
+                                           const float4 *d, uint32_t dst, uint32_t q0, uint32_t nq) {
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+        const uint32_t qq = q0 + (uint32_t)u < nq ? q0 + (uint32_t)u : nq - 1;
+        v[u] = p[qq * ps];
+        if (FAST) w[u] = d[qq * dst];
+    }
+}
+template <bool FAST, int G>
+__device__ __forceinline__ void chain_add(float &acc, const float4 (&v)[G], const float4 (&w)[G], uint32_t q0,
+                                          uint32_t count) {
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+        const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+        const float f[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (4 * (q0 + (uint32_t)u) + (uint32_t)c < count) acc = FAST ? __builtin_fmaf(f[c], e[c], acc) : acc + e[c];
+    }
+}
+template <bool FAST, int NQ>
+__device__ __forceinline__ void chain_sum(float &acc, const float4 *p, uint32_t ps, const float4 *d, uint32_t dst,
+                                          uint32_t count) {
+    const uint32_t nq = (count + 3) / 4;
+    if (NQ <= 8) { /* short rows: every read at once */
+        float4 x[NQ <= 8 ? NQ : 1], xw[NQ <= 8 ? NQ : 1];
+        chain_read<FAST, NQ <= 8 ? NQ : 1>(x, xw, p, ps, d, dst, 0, nq);
+        chain_add<FAST, NQ <= 8 ? NQ : 1>(acc, x, xw, 0, count);
+        return;
+    }
+    /* wide rows (a few chain threads, many blocks): whole float4 first (the
+     * compiler unrolls this loop and batches its reads), then the tail */
+    const uint32_t full = count / 4;
+    uint32_t q = 0;
+    for (; q < full; ++q) {
+        const float4 v = p[q * ps];
+        if (FAST) {
+            const float4 dv = d[q * dst];
+            acc = __builtin_fmaf(dv.x, v.x, acc);
+            acc = __builtin_fmaf(dv.y, v.y, acc);
+            acc = __builtin_fmaf(dv.z, v.z, acc);
+            acc = __builtin_fmaf(dv.w, v.w, acc);
+        } else {
+            acc = acc + v.x;
+            acc = acc + v.y;
+            acc = acc + v.z;
+            acc = acc + v.w;
+        }
+    }
+    const uint32_t rem = count - 4 * full;
+    if (rem) {
+        const float4 v = p[q * ps];
+        const float4 dv = FAST ? d[q * dst] : v;
+        acc = FAST ? __builtin_fmaf(dv.x, v.x, acc) : acc + v.x;
+        if (rem > 1) acc = FAST ? __builtin_fmaf(dv.y, v.y, acc) : acc + v.y;
+        if (rem > 2) acc = FAST ? __builtin_fmaf(dv.z, v.z, acc) : acc + v.z;
+    }
 }
 
 /* ------------------------------------------------------------------------
@@ -275,38 +342,8 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
 
         if (tid < RT * 8) {
             const uint32_t count = nb - c * CB < (uint32_t)CB ? nb - c * CB : (uint32_t)CB;
-            const float4 *pg = (const float4 *)pb + tid;
-            const float4 *dg = FAST ? (const float4 *)dsc[c & 1] + tid / 8 : nullptr;
-            uint32_t q = 0;
-            for (; q < count / 4; ++q) {
-                const float4 v = pg[q * (GS / 4)];
-                if (FAST) {
-                    const float4 dv = dg[q * (DS / 4)];
-                    acc = __builtin_fmaf(dv.x, v.x, acc);
-                    acc = __builtin_fmaf(dv.y, v.y, acc);
-                    acc = __builtin_fmaf(dv.z, v.z, acc);
-                    acc = __builtin_fmaf(dv.w, v.w, acc);
-                } else {
-                    acc = acc + v.x;
-                    acc = acc + v.y;
-                    acc = acc + v.z;
-                    acc = acc + v.w;
-                }
-            }
-            const uint32_t rem = count - q * 4;
-            if (rem) {
-                const float4 v = pg[q * (GS / 4)];
-                if (FAST) {
-                    const float4 dv = dg[q * (DS / 4)];
-                    acc = __builtin_fmaf(dv.x, v.x, acc);
-                    if (rem > 1) acc = __builtin_fmaf(dv.y, v.y, acc);
-                    if (rem > 2) acc = __builtin_fmaf(dv.z, v.z, acc);
-                } else {
-                    acc = acc + v.x;
-                    if (rem > 1) acc = acc + v.y;
-                    if (rem > 2) acc = acc + v.z;
-                }
-            }
+            chain_sum<FAST, CB / 4>(acc, (const float4 *)pb + tid, GS / 4,
+                                    FAST ? (const float4 *)dsc[c & 1] + tid / 8 : nullptr, DS / 4, count);
         }
     }
 
@@ -314,6 +351,345 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
         const float v = reduce8_to_lane7(acc);
         const uint32_t r = r0 + tid / 8;
         if ((tid & 7) == 7 && r < I.rows) store_out(I, a.flag, 0, r, v);
+    }
+}
+
+/* ------------------------------------------------------------------------
+ * Streaming decode GEMV: the same tasks, LDS products and in-order chains as
+ * k_gemv, run by persistent workgroups that each walk the (tile, chunk) steps
+ * of a contiguous range of tiles over the items. The next
+ * step's weight and activation blocks are requested before the current
+ * step's products are formed, so each workgroup keeps one step of loads in
+ * flight while it computes; a launch then streams all its items' weights
+ * without per-tile launch or drain gaps. Items are independent matrices with
+ * the same nb, each with its own activation (a group of experts, or many
+ * layers' weights in a bandwidth run).
+ * ---------------------------------------------------------------------- */
+__device__ __forceinline__ uint32_t find_group_item(const GroupArgs &g, uint32_t tile) {
+    uint32_t lo = 0, hi = g.nitems; /* last item with tile_begin <= tile */
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) / 2;
+        if (g.item[mid].tile_begin <= tile) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+/* One task of a streaming step: this thread's weight block(s) and
+ * activation block(s), and, for the output row the thread may store, its bias
+ * and prior output, all in registers. Every task issues the same loads (an
+ * invalid one reads row 0, block 0 of its item and is then ignored), so the
+ * in-order load counter lets a step wait for its own task only. */
+template <bool Q5>
+struct StreamTask {
+    uint32_t w[Q5 ? 11 : 9];
+    uint32_t x[Q5 ? 16 : 8];
+    float s[Q5 ? 2 : 1];
+    float bias, prior;
+    bool ok;
+};
+
+/* The item under one of a workgroup's cursors, with its fields held in
+ * registers (reloaded only when the cursor crosses into the next item), and
+ * the (tile, chunk) position that cursor stands at. */
+struct StreamCursor {
+    const unsigned char *w;
+    const float *bias, *xd;
+    float *y;
+    const int8_t *xq;
+    size_t row_bytes;
+    uint32_t rows, tile_begin, next_begin, idx, tile, chunk;
+    int accumulate;
+};
+__device__ __forceinline__ void cursor_load(StreamCursor &c, const GroupArgs &g) {
+    const GroupItem &I = g.item[c.idx];
+    c.w = I.w;
+    c.row_bytes = I.row_bytes;
+    c.bias = I.bias;
+    c.y = I.y;
+    c.xd = I.xd;
+    c.xq = I.xq;
+    c.rows = I.rows;
+    c.tile_begin = I.tile_begin;
+    c.accumulate = I.accumulate;
+    c.next_begin = c.idx + 1 < g.nitems ? g.item[c.idx + 1].tile_begin : 0xffffffffu;
+}
+__device__ __forceinline__ void cursor_start(StreamCursor &c, const GroupArgs &g, uint32_t tile) {
+    c.idx = find_group_item(g, tile);
+    c.tile = tile;
+    c.chunk = 0;
+    cursor_load(c, g);
+}
+/* next (tile, chunk) step; crossing items reloads the fields */
+__device__ __forceinline__ void cursor_step(StreamCursor &c, const GroupArgs &g, uint32_t nchunks) {
+    if (++c.chunk == nchunks) {
+        c.chunk = 0;
+        if (++c.tile >= c.next_begin) {
+            while (c.tile >= c.next_begin) {
+                ++c.idx;
+                c.next_begin = c.idx + 1 < g.nitems ? g.item[c.idx + 1].tile_begin : 0xffffffffu;
+            }
+            cursor_load(c, g);
+        }
+    }
+}
+
+template <bool Q5, int RT, int NT>
+__device__ __forceinline__ void stream_load(StreamTask<Q5> &T, const StreamCursor &c, uint32_t nb, bool real,
+                                            uint32_t tid, uint32_t tr, uint32_t ti) {
+    constexpr int TB = Q5 ? 2 : 1, CB = (NT / RT) * TB;
+    const uint32_t row0 = (c.tile - c.tile_begin) * RT;
+    const uint32_t row = row0 + tr, b = c.chunk * CB + ti * TB;
+    T.ok = real && row < c.rows && b < nb;
+    const unsigned char *p = c.w + (T.ok ? (size_t)row * c.row_bytes + (size_t)b * (Q5 ? Q5_BYTES : Q8_BYTES) : 0);
+    const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
+    T.w[0] = v0.x; T.w[1] = v0.y; T.w[2] = v0.z; T.w[3] = v0.w;
+    T.w[4] = v1.x; T.w[5] = v1.y; T.w[6] = v1.z; T.w[7] = v1.w;
+    if (Q5) {
+        const u3a v2 = *(const u3a *)(p + 32);
+        T.w[8] = v2.x; T.w[9] = v2.y; T.w[10] = v2.z;
+    } else {
+        T.w[8] = *(const uint32_t *)(p + 32);
+    }
+    const uint32_t bx = T.ok ? b : 0;
+    const unsigned char *xp = (const unsigned char *)c.xq + (size_t)bx * QK;
+#pragma unroll
+    for (int k = 0; k < TB * 2; ++k) {
+        const u4a v = *(const u4a *)(xp + 16 * k);
+        T.x[4 * k] = v.x; T.x[4 * k + 1] = v.y; T.x[4 * k + 2] = v.z; T.x[4 * k + 3] = v.w;
+    }
+#pragma unroll
+    for (int k = 0; k < TB; ++k) T.s[k] = c.xd[bx + k];
+    /* the chain thread's output row of this tile (used at its last chunk) */
+    const uint32_t orow = row0 + (tid < RT * 8 ? tid / 8 : 0);
+    const uint32_t oc = orow < c.rows ? orow : 0;
+    T.bias = *(c.bias ? c.bias + oc : c.xd); /* an unused read when absent keeps the load count uniform */
+    T.prior = *(c.accumulate ? c.y + oc : c.xd);
+}
+
+/* Products of one task into the LDS buffer pb (and, fast mode, its scale). */
+template <bool Q5, bool FAST, int RT>
+__device__ __forceinline__ void stream_products(const StreamTask<Q5> &T, float *pb, float *db, uint32_t tr,
+                                                uint32_t ti) {
+    constexpr int TB = Q5 ? 2 : 1, GS = RT * 32 + 4, DS = RT * 4 + 4;
+    if (!T.ok) return;
+    Q5Fields f[2];
+    if (Q5) q5_parse_pair(T.w, f[0], f[1]);
+#pragma unroll
+    for (int q = 0; q < TB; ++q) {
+        const uint32_t bb = ti * TB + q;
+        const float wscale = Q5 ? f[q].scale : __uint_as_float(T.w[0]);
+        const float d = wscale * T.s[q];
+        float *dst = pb + (bb / 4) * GS + tr * 32 + (bb % 4);
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            const uint32_t x = T.x[q * 8 + l];
+            int sv;
+            if (Q5) sv = dot4(q5_codes(f[q], l), x, dot4(x, 0xf0f0f0f0u, 0));
+            else sv = dot4(T.w[1 + l], x, 0);
+            dst[l * 4] = FAST ? (float)sv : d * (float)sv;
+        }
+        if (FAST) db[(bb / 4) * DS + tr * 4 + (bb % 4)] = d;
+    }
+}
+
+/* Chain threads (tid < RT*8): this step's products in block order; at the
+ * last chunk of a tile, the lane tree and the store (bias and prior output
+ * were loaded with the tile's first chunk: no load waits here). */
+template <bool Q5, bool FAST, int RT, int NT>
+__device__ __forceinline__ void stream_chain(float &acc, float &bias, float &prior, const StreamTask<Q5> &T,
+                                             const float *pb, const float *db, const StreamCursor &c, uint32_t nb,
+                                             uint32_t nchunks, int *flag, uint32_t tid) {
+    constexpr int TB = Q5 ? 2 : 1, CB = (NT / RT) * TB, GS = RT * 32 + 4, DS = RT * 4 + 4;
+    if (c.chunk == 0) {
+        bias = T.bias;
+        prior = T.prior;
+    }
+    const uint32_t count = nb - c.chunk * CB < (uint32_t)CB ? nb - c.chunk * CB : (uint32_t)CB;
+    chain_sum<FAST, CB / 4>(acc, (const float4 *)pb + tid, GS / 4, FAST ? (const float4 *)db + tid / 8 : nullptr,
+                            DS / 4, count);
+    if (c.chunk + 1 == nchunks) {
+        const float v = reduce8_to_lane7(acc);
+        const uint32_t r = (c.tile - c.tile_begin) * RT + tid / 8;
+        if ((tid & 7) == 7 && r < c.rows) {
+            float o = v;
+            if (c.bias) o = o + bias; /* model.c:259-262 */
+            if (flag && !(fabsf(o) <= FLT_MAX)) *flag = 1;
+            if (c.accumulate) o = prior + o;
+            c.y[r] = o;
+        }
+        acc = 0.0f;
+    }
+}
+
+template <bool Q5, bool FAST, int RT, int NT>
+__global__ __launch_bounds__(NT) void k_gemv_stream(GroupArgs g) {
+    constexpr int TB = Q5 ? 2 : 1;
+    constexpr int CB = (NT / RT) * TB;
+    constexpr int GS = RT * 32 + 4;
+    constexpr int DS = RT * 4 + 4;
+    __shared__ __attribute__((aligned(16))) float prod[2][(CB / 4) * GS];
+    __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? (CB / 4) * DS : 4];
+
+    const uint32_t tid = threadIdx.x, tr = tid / (NT / RT), ti = tid % (NT / RT), nb = g.nb;
+    const uint32_t nchunks = (nb + CB - 1) / CB;
+    /* this workgroup's tiles: a contiguous range (consecutive rows, mostly one item) */
+    const uint32_t t0 = (uint32_t)((uint64_t)g.total_tiles * blockIdx.x / gridDim.x);
+    const uint32_t t1 = (uint32_t)((uint64_t)g.total_tiles * (blockIdx.x + 1) / gridDim.x);
+    const uint32_t my_steps = (t1 - t0) * nchunks;
+    if (!my_steps) return;
+
+    /* two tasks in flight: A holds even steps, B odd ones; the load cursor
+     * runs two steps ahead of the chain cursor */
+    StreamCursor cl, cc;
+    cursor_start(cl, g, t0);
+    cc = cl;
+    StreamTask<Q5> A, B;
+    stream_load<Q5, RT, NT>(A, cl, nb, true, tid, tr, ti);
+    cursor_step(cl, g, nchunks);
+    stream_load<Q5, RT, NT>(B, cl, nb, my_steps > 1, tid, tr, ti);
+    float acc = 0.0f, bias = 0.0f, prior = 0.0f;
+    for (uint32_t k = 0; k < my_steps; k += 2) {
+        /* even step k from A; then A loads step k + 2 */
+        stream_products<Q5, FAST, RT>(A, prod[0], dsc[0], tr, ti);
+        __syncthreads();
+        if (tid < RT * 8) stream_chain<Q5, FAST, RT, NT>(acc, bias, prior, A, prod[0], dsc[0], cc, nb, nchunks, g.flag, tid);
+        cursor_step(cc, g, nchunks);
+        if (k + 2 < my_steps) cursor_step(cl, g, nchunks);
+        stream_load<Q5, RT, NT>(A, cl, nb, k + 2 < my_steps, tid, tr, ti);
+        if (k + 1 >= my_steps) break;
+        /* odd step k + 1 from B; then B loads step k + 3 */
+        stream_products<Q5, FAST, RT>(B, prod[1], dsc[FAST ? 1 : 0], tr, ti);
+        __syncthreads();
+        if (tid < RT * 8)
+            stream_chain<Q5, FAST, RT, NT>(acc, bias, prior, B, prod[1], dsc[FAST ? 1 : 0], cc, nb, nchunks, g.flag, tid);
+        cursor_step(cc, g, nchunks);
+        if (k + 3 < my_steps) cursor_step(cl, g, nchunks);
+        stream_load<Q5, RT, NT>(B, cl, nb, k + 3 < my_steps, tid, tr, ti);
+    }
+}
+
+/* ------------------------------------------------------------------------
+ * Pinned streaming GEMV (Q8, nb <= PIN_NB): each workgroup belongs to one
+ * item (the launcher gives every item a share of the resident workgroups
+ * in proportion to its rows) and walks a contiguous range of that item's
+ * tiles. Its activation is staged in LDS once, so a task is just the nine
+ * weight dwords (plus the row's bias and prior output for the chain
+ * threads), and D tasks stay in flight per thread. Products and chains as in
+ * k_gemv: exact per-lane order, the fixed lane tree.
+ * ---------------------------------------------------------------------- */
+constexpr uint32_t PIN_NB = 64;
+
+struct PinTask {
+    uint32_t w[9];
+    float bias, prior;
+    bool ok;
+};
+
+__device__ __forceinline__ uint32_t find_pin_item(const GroupArgs &g, uint32_t wg) {
+    uint32_t lo = 0, hi = g.nitems; /* last item with wg_begin <= wg */
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) / 2;
+        if (g.item[mid].wg_begin <= wg) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+template <bool FAST, int RT, int NT, int D>
+__global__ __launch_bounds__(NT) void k_gemv_pin(GroupArgs g) {
+    constexpr int TPR = NT / RT, CB = TPR, GS = RT * 32 + 4, DS = RT * 4 + 4;
+    __shared__ __attribute__((aligned(16))) float prod[2][(CB / 4) * GS];
+    __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? (CB / 4) * DS : 4];
+    __shared__ __attribute__((aligned(16))) uint32_t act_q[PIN_NB * 8];
+    __shared__ float act_d[PIN_NB];
+
+    const uint32_t tid = threadIdx.x, tr = tid / TPR, ti = tid % TPR, nb = g.nb;
+    const GroupItem &I = g.item[find_pin_item(g, blockIdx.x)];
+    const uint32_t wg = blockIdx.x - I.wg_begin, item_tiles = (I.rows + RT - 1) / RT;
+    const uint32_t t0 = (uint32_t)((uint64_t)item_tiles * wg / I.nwg);
+    const uint32_t t1 = (uint32_t)((uint64_t)item_tiles * (wg + 1) / I.nwg);
+    const uint32_t nchunks = (nb + CB - 1) / CB, my_steps = (t1 - t0) * nchunks;
+    const unsigned char *wbase = I.w;
+    const size_t row_bytes = I.row_bytes;
+    const uint32_t rows = I.rows;
+    const float *bias_p = I.bias, *xd = I.xd;
+    float *y = I.y;
+    const bool accum = I.accumulate != 0;
+
+    /* the activation, once (kernels.c:912-935 layout: nb scales, nb*8 words) */
+    const uint32_t *xq32 = (const uint32_t *)I.xq;
+    for (uint32_t i = tid; i < nb * 8; i += NT) act_q[i] = xq32[i];
+    for (uint32_t i = tid; i < nb; i += NT) act_d[i] = xd[i];
+
+    /* step s: tile t0 + s / nchunks, chunk s % nchunks (counters, no division per step) */
+    auto load = [&](PinTask &T, uint32_t tile, uint32_t chunk, bool real) __attribute__((always_inline)) {
+        const uint32_t row0 = tile * RT, row = row0 + tr, b = chunk * CB + ti;
+        T.ok = real && row < rows && b < nb;
+        const unsigned char *p = wbase + (T.ok ? (size_t)row * row_bytes + (size_t)b * Q8_BYTES : 0);
+        const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
+        T.w[0] = v0.x; T.w[1] = v0.y; T.w[2] = v0.z; T.w[3] = v0.w;
+        T.w[4] = v1.x; T.w[5] = v1.y; T.w[6] = v1.z; T.w[7] = v1.w;
+        T.w[8] = *(const uint32_t *)(p + 32);
+        const uint32_t orow = row0 + (tid < RT * 8 ? tid / 8 : 0), oc = orow < rows ? orow : 0;
+        T.bias = *(bias_p ? bias_p + oc : xd); /* unused reads when absent keep the load count uniform */
+        T.prior = *(accum ? y + oc : xd);
+    };
+    PinTask T[D];
+    uint32_t lt = t0, lc = 0; /* load cursor */
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+        load(T[j], lt, lc, (uint32_t)j < my_steps);
+        if (++lc == nchunks) { lc = 0; ++lt; }
+    }
+    __syncthreads(); /* activation staged */
+    uint32_t ct = t0, cc = 0; /* chain cursor */
+    float acc = 0.0f, bias = 0.0f, prior = 0.0f;
+    for (uint32_t k = 0; k < my_steps; k += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            if (k + j >= my_steps) break;
+            float *pb = prod[(k + j) & 1];
+            float *db = dsc[FAST ? (k + j) & 1 : 0];
+            if (T[j].ok) {
+                const uint32_t b = cc * CB + ti;
+                const float d = __uint_as_float(T[j].w[0]) * act_d[b];
+                float *dst = pb + (ti / 4) * GS + tr * 32 + (ti % 4);
+                const u4a xa = *(const u4a *)&act_q[b * 8], xb = *(const u4a *)&act_q[b * 8 + 4];
+                const uint32_t xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+                for (int l = 0; l < 8; ++l) {
+                    const int sv = dot4(T[j].w[1 + l], xs[l], 0);
+                    dst[l * 4] = FAST ? (float)sv : d * (float)sv;
+                }
+                if (FAST) db[(ti / 4) * DS + tr * 4 + (ti % 4)] = d;
+            }
+            __syncthreads();
+            if (tid < RT * 8) {
+                if (cc == 0) {
+                    bias = T[j].bias;
+                    prior = T[j].prior;
+                }
+                const uint32_t count = nb - cc * CB < (uint32_t)CB ? nb - cc * CB : (uint32_t)CB;
+                chain_sum<FAST, CB / 4>(acc, (const float4 *)pb + tid, GS / 4,
+                                        FAST ? (const float4 *)db + tid / 8 : nullptr, DS / 4, count);
+                if (cc + 1 == nchunks) {
+                    const float v = reduce8_to_lane7(acc);
+                    const uint32_t r = ct * RT + tid / 8;
+                    if ((tid & 7) == 7 && r < rows) {
+                        float o = v;
+                        if (bias_p) o = o + bias; /* model.c:259-262 */
+                        if (g.flag && !(fabsf(o) <= FLT_MAX)) *g.flag = 1;
+                        if (accum) o = prior + o;
+                        y[r] = o;
+                    }
+                    acc = 0.0f;
+                }
+            }
+            if (++cc == nchunks) { cc = 0; ++ct; }
+            load(T[j], lt, lc, k + j + D < my_steps);
+            if (++lc == nchunks) { lc = 0; ++lt; }
+        }
     }
 }
 
@@ -1448,12 +1824,94 @@ int gemv_rows_per_tile(uint32_t nb, bool q5, uint32_t total_rows) {
     return rt;
 }
 
+/* Single launches of many tiles (the LM head: 18992 tiles of 8 rows) run on
+ * the persistent streaming kernel; a few thousand tiles fit the device in one
+ * wave of workgroups and keep the one-tile-per-workgroup kernel.
+ * SMQ_GEMV_STREAM=0/1 forces either. */
+bool gemv_stream(uint32_t total_rows, int rt) {
+    const char *env = getenv("SMQ_GEMV_STREAM");
+    if (env && *env) return atoi(env) != 0;
+    return (total_rows + rt - 1) / rt > 4096;
+}
+
 /* Staging the activation in LDS never beat direct (L1/L2) reads on the
  * measured shapes; the staged variant stays available for tuning. */
 bool gemv_stage(uint32_t total_rows) {
     (void)total_rows;
     const char *env = getenv("SMQ_GEMV_STAGE");
     return env && *env && atoi(env) != 0;
+}
+
+/* Persistent grid: as many workgroups as fit on the device at once (the
+ * occupancy query runs once per kernel), never more than the tiles. */
+template <bool Q5, bool FAST, int RT, int NT>
+hipError_t launch_gemv_stream_rt(GroupArgs &g, hipStream_t s) {
+    static int resident = 0;
+    uint32_t tiles = 0;
+    for (uint32_t i = 0; i < g.nitems; ++i) {
+        g.item[i].tile_begin = tiles;
+        tiles += (g.item[i].rows + RT - 1) / RT;
+    }
+    g.total_tiles = tiles;
+    if (!tiles) return hipSuccess;
+    if (!resident) {
+        int per_cu = 0, dev = 0, cus = 0;
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemv_stream<Q5, FAST, RT, NT>, NT, 0);
+        if (e == hipSuccess) e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        resident = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+    }
+    const uint32_t grid = tiles < (uint32_t)resident ? tiles : (uint32_t)resident;
+    hipLaunchKernelGGL((k_gemv_stream<Q5, FAST, RT, NT>), dim3(grid), dim3(NT), 0, s, g);
+    return hipGetLastError();
+}
+
+template <bool Q5, bool FAST>
+hipError_t launch_gemv_stream_typed(GroupArgs &g, int rt, hipStream_t s) {
+    switch (rt) {
+    case 1: return launch_gemv_stream_rt<Q5, FAST, 1, WG>(g, s);
+    case 2: return launch_gemv_stream_rt<Q5, FAST, 2, WG>(g, s);
+    case 4: return launch_gemv_stream_rt<Q5, FAST, 4, WG>(g, s);
+    case 8: return launch_gemv_stream_rt<Q5, FAST, 8, WG>(g, s);
+    default: return launch_gemv_stream_rt<Q5, FAST, 16, WG>(g, s);
+    }
+}
+
+/* Pinned launch: every item gets a share of the resident workgroups in
+ * proportion to its tiles (at least one), each a contiguous tile range. */
+template <bool FAST>
+hipError_t launch_gemv_pin(GroupArgs &g, hipStream_t s) {
+    constexpr int RT = 16, NT = 512, D = 2;
+    static int resident = 0;
+    if (!resident) {
+        int per_cu = 0, dev = 0, cus = 0;
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemv_pin<FAST, RT, NT, D>, NT, 0);
+        if (e == hipSuccess) e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        resident = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+    }
+    uint64_t tiles = 0;
+    for (uint32_t i = 0; i < g.nitems; ++i) tiles += (g.item[i].rows + RT - 1) / RT;
+    if (!tiles) return hipSuccess;
+    uint32_t wgs = 0;
+    for (uint32_t i = 0; i < g.nitems; ++i) {
+        const uint32_t t = (g.item[i].rows + RT - 1) / RT;
+        uint32_t n = (uint32_t)(((uint64_t)resident * t + tiles / 2) / tiles);
+        n = n < 1 ? 1 : (n > t ? t : n);
+        g.item[i].wg_begin = wgs;
+        g.item[i].nwg = n;
+        wgs += n;
+    }
+    hipLaunchKernelGGL((k_gemv_pin<FAST, RT, NT, D>), dim3(wgs), dim3(NT), 0, s, g);
+    return hipGetLastError();
+}
+
+bool gemv_pin_ok(const GroupArgs &g, bool q5) {
+    const char *env = getenv("SMQ_GEMV_PIN");
+    if (env && *env && atoi(env) == 0) return false;
+    return !q5 && g.nb <= PIN_NB;
 }
 
 template <bool Q5, bool FAST>
@@ -1464,6 +1922,26 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
     if (fast_layout(a, Q5)) {
         if (a.ntok == 1) {
             const int rt = gemv_rows_per_tile(a.nb, Q5, total_rows);
+            if (gemv_stream(total_rows, rt) && !gemv_stage(total_rows)) {
+                /* many tiles: persistent workgroups stream them (same products and order) */
+                GroupArgs g;
+                memset(&g, 0, sizeof(g));
+                g.nb = a.nb;
+                g.flag = a.flag;
+                for (uint32_t i = 0; i < a.nitems; ++i) {
+                    GroupItem &it = g.item[g.nitems++];
+                    it.w = a.item[i].w;
+                    it.row_bytes = a.item[i].row_bytes;
+                    it.bias = a.item[i].bias;
+                    it.y = a.item[i].y;
+                    it.xd = a.xd;
+                    it.xq = a.xq;
+                    it.rows = a.item[i].rows;
+                    it.accumulate = a.item[i].accumulate;
+                }
+                if (gemv_pin_ok(g, Q5)) return launch_gemv_pin<FAST>(g, s);
+                return launch_gemv_stream_typed<Q5, FAST>(g, rt, s);
+            }
             return gemv_stage(total_rows) ? launch_gemv_stage<Q5, FAST, true>(a, rt, s)
                                           : launch_gemv_stage<Q5, FAST, false>(a, rt, s);
         }
@@ -1550,6 +2028,22 @@ hipError_t launch_row_quantize(const float *src, const float *norm, float eps, c
     }
 #undef SMQ_RQ
     return hipGetLastError();
+}
+
+bool group_layout_ok(const GroupArgs &g, bool q5) {
+    if (!g.nb || g.nb > MAX_FAST_NB || (q5 && (g.nb & 1u))) return false;
+    for (uint32_t i = 0; i < g.nitems; ++i)
+        if ((((uintptr_t)g.item[i].w) | g.item[i].row_bytes | (uintptr_t)g.item[i].xq) & 3u) return false;
+    return true;
+}
+
+hipError_t launch_gemv_grouped(GroupArgs &g, bool q5, bool fast, hipStream_t s) {
+    if (!g.nitems) return hipSuccess;
+    if (!group_layout_ok(g, q5)) return hipErrorInvalidValue;
+    if (gemv_pin_ok(g, q5)) return fast ? launch_gemv_pin<true>(g, s) : launch_gemv_pin<false>(g, s);
+    const int rt = gemv_rows_per_tile(g.nb, q5, 0);
+    if (q5) return fast ? launch_gemv_stream_typed<true, true>(g, rt, s) : launch_gemv_stream_typed<true, false>(g, rt, s);
+    return fast ? launch_gemv_stream_typed<false, true>(g, rt, s) : launch_gemv_stream_typed<false, false>(g, rt, s);
 }
 
 hipError_t launch_rope_kv(float *q, float *k, const float *v, uint32_t ntok, const AttnShape &sh, const float *cs,

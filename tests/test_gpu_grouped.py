@@ -1,0 +1,95 @@
+"""GPU parity of the streaming decode GEMV: grouped launches of independent
+matrices with their own activations (smq_gemv_grouped) and single launches
+large enough to take the persistent kernel (the LM head shape), against the
+CPU oracle, bit for bit, in the exact and the fast (FMA) contract."""
+import numpy as np
+import pytest
+
+from checks import assert_same_f32, say
+from smq_pkg import smq, synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    assert smq.init(0) == "gfx950"
+    smq.kernels_set_fast(False)
+    smq.kernels_select()
+    yield
+    smq.kernels_set_fast(False)
+
+
+def dev(a):
+    return smq.DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+def quantized(seed, cols):
+    x = synth.activations(seed, 1, cols)
+    nb = (cols + 31) // 32
+    xb = dev(x)
+    d, q = smq.DeviceBuffer(nb * 4), smq.DeviceBuffer(nb * 32)
+    smq.quantize_q8_rows(xb, 1, cols, d, q)
+    return d, q, d.download(np.float32), q.download(np.int8)
+
+
+GROUP_CASES = [
+    # q5, cols, rows of each item, fast
+    (False, 896, [4864, 4864, 896, 128, 7], False),   # FFN/QKV shapes and a ragged tail tile
+    (False, 4864, [896, 896, 33], False),             # wide rows: several chunks per tile
+    (True, 1536, [8960, 1536, 5], False),             # Q5 pairs
+    (False, 896, [4864, 100], True),                  # fast contract (lane FMA)
+    (True, 8960, [1536, 3], True),
+]
+
+
+@pytest.mark.parametrize("q5,cols,rows,fast", GROUP_CASES)
+def test_grouped_gemv(orc, q5, cols, rows, fast):
+    say("grouped", q5, cols, rows, fast)
+    smq.kernels_set_fast(fast)
+    nb = (cols + 31) // 32
+    bb = 22 if q5 else 36
+    items, want = [], []
+    for i, r in enumerate(rows):
+        w = (synth.q5_weights if q5 else synth.q8_weights)(100 + i, r, cols)
+        bias = synth.normal(200 + i, r, 0.02) if i % 2 == 0 else None
+        acc = i % 3 == 1
+        y0 = synth.normal(300 + i, r) if acc else np.zeros(r, np.float32)
+        d, q, hd, hq = quantized(400 + i, cols)
+        ok, prod = orc.mat_item(w, nb * bb, r, bias, hd, hq, 1, nb, q5=q5, fast=fast)
+        assert ok
+        want.append(y0 + prod if acc else prod)
+        mat = smq.QMat(dev(w), r, cols, smq.DTYPE_Q5 if q5 else smq.DTYPE_Q8)
+        items.append((mat, dev(bias) if bias is not None else None, dev(y0), acc, d, q))
+    smq.gemv_grouped(items)
+    smq.numeric_check()
+    for i, (it, wnt) in enumerate(zip(items, want)):
+        assert_same_f32(it[2].download(np.float32), wnt, f"item {i}")
+    smq.kernels_set_fast(False)
+
+
+def test_grouped_rejects_mixed_widths():
+    a = smq.QMat(dev(synth.q8_weights(1, 8, 64)), 8, 64)
+    b = smq.QMat(dev(synth.q8_weights(2, 8, 96)), 8, 96)
+    d, q, _, _ = quantized(3, 64)
+    y = smq.DeviceBuffer(8 * 4)
+    with pytest.raises(smq.SmqError) as e:
+        smq.gemv_grouped([(a, None, y, False, d, q), (b, None, y, False, d, q)])
+    assert e.value.status == smq.SM_ERR_STATE
+
+
+@pytest.mark.parametrize("fast", [False, True])
+def test_lm_head_streams(orc, fast):
+    """151936 x 896: one matmul launch of 18992 tiles takes the persistent kernel."""
+    say("lm head stream", fast)
+    smq.kernels_set_fast(fast)
+    rows, cols, nb = 151936, 896, 28
+    w = synth.q8_weights(7, rows, cols)
+    d, q, hd, hq = quantized(8, cols)
+    y = smq.DeviceBuffer(rows * 4)
+    smq.matmul([(smq.QMat(dev(w), rows, cols), None, y)], d, q, 1)
+    smq.numeric_check()
+    ok, want = orc.mat_item(w, nb * 36, rows, None, hd, hq, 1, nb, fast=fast)
+    assert ok
+    assert_same_f32(y.download(np.float32), want, "lm head")
+    smq.kernels_set_fast(False)

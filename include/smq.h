@@ -197,6 +197,36 @@ typedef struct smq_group_item {
 smq_status smq_gemv_grouped(const smq_group_item *items, uint32_t n);
 /* Synchronizes, then returns SMQ_ERR_NUMERIC (and clears the flag) if any
  * quantize or matmul since the last check saw a non-finite value. */
+/* ---- fused decode matmuls (one token) --------------------------------------
+ * The activation of a decode matmul formed inside the matmul's own launch:
+ * norm_quantize + matmul (model.c:503-509, 636-638) and silu_quantize +
+ * matmul (model.c:639-643) without the activation round trip. Outputs are
+ * bit-identical to the two-call forms, which these calls fall back to where
+ * a shape does not fit the fused kernel (then the Q8 blocks go to the
+ * scratch buffers). */
+#define SMQ_ACT_Q8 0   /* xd, xq: the quantized activation */
+#define SMQ_ACT_NORM 1 /* RMSNorm of x with norm and eps (model.c:334-342), then Q8 */
+#define SMQ_ACT_F32 2  /* Q8 of the f32 row x (kernels.c:912-935) */
+typedef struct smq_act {
+    int kind;
+    uint32_t cols;          /* elements: the matrices' cols */
+    const float *x;         /* NORM, F32: cols floats */
+    const float *norm;      /* NORM: cols floats */
+    float eps;              /* NORM */
+    const float *xd;        /* Q8: ceil(cols/32) scales */
+    const int8_t *xq;       /* Q8: ceil(cols/32)*32 values */
+    float *xd_scratch;      /* NORM, F32: room for the Q8 blocks if the call falls back */
+    int8_t *xq_scratch;
+} smq_act;
+/* smq_matmul of one token with the activation `act`. */
+smq_status smq_matmul_act(const smq_mat_item *items, uint32_t n, const smq_act *act);
+/* The gate/up pair of a dense FFN (model.c:636-640): h[r] = up[r] *
+ * act(gate[r]) with act 1 SwiGLU, 2 GeGLU (vecmath.c:78-93), gate and up the
+ * matmuls of `act` (same rows and cols, no bias); a non-finite gate or up
+ * raises the numeric flag. gate_scratch (gate->rows floats) holds the gate
+ * row if the call falls back. */
+smq_status smq_matmul_glu(const smq_qmat *gate, const smq_qmat *up, const smq_act *act, int glu, float *h,
+                          float *gate_scratch);
 smq_status smq_numeric_check(void);
 
 /* ---- decoder pieces around the matmuls ----------------------------------
@@ -230,6 +260,14 @@ smq_status smq_attention(const float *q, const float *keys, const float *values,
 smq_status smq_attention_q8(const float *q, const float *keys, const float *values, float *att, uint32_t ntok,
                             const smq_attn_shape *shape, uint32_t pos0, const int32_t *pos_dev, float *xd,
                             int8_t *xq);
+/* One decoding token (model.c:511-542 for ntok = 1): smq_rope_kv, then
+ * smq_attention_q8, as one launch where the shape allows (head_dim 64,
+ * 16-byte aligned q, k, v and caches; otherwise the two calls). q and k are the unrotated QKV outputs; afterwards their contents
+ * are unspecified (rotated or not). keys/values[p] receive the rotated k and
+ * v of this position, att the attention row, xd/xq its Q8 blocks. */
+smq_status smq_attention_rope_q8(float *q, float *k, const float *v, const smq_attn_shape *shape,
+                                 const float *cos_table, const float *sin_table, float *keys, float *values,
+                                 float *att, uint32_t pos0, const int32_t *pos_dev, float *xd, int8_t *xq);
 /* sampler.c:57-63: *token = first non-banned id, replaced by any later
  * non-banned id with a strictly greater logit (NaN never wins unless it is
  * the first candidate). banned may be NULL. UINT32_MAX if every id is banned. */
@@ -242,6 +280,12 @@ smq_status smq_embed(const smq_qmat *embed, const uint32_t *tokens, uint32_t nto
  * *count < capacity, then ++*count and ++*pos (lets a captured step advance). */
 smq_status smq_decode_advance(int32_t *pos, uint32_t *count, const uint32_t *token, uint32_t *history,
                               uint32_t capacity);
+/* smq_argmax then smq_decode_advance in one call (the greedy step of the
+ * reference's generation loop, main.c:580-600, on device state). Calls on one
+ * stream share the library's argmax workspace; concurrent calls on different
+ * streams race. */
+smq_status smq_argmax_advance(const float *logits, uint32_t vocab, const unsigned char *banned, uint32_t *token,
+                              int32_t *pos, uint32_t *count, uint32_t *history, uint32_t capacity);
 
 /* ---- dequantization (src/kernels.h:193-196, kernels.c:1044-1062) -------- */
 void smq_dequantize_q8_row(const unsigned char *w, uint32_t cols, float *out);

@@ -56,6 +56,11 @@ class _GroupItem(ctypes.Structure):
                 ("xd", _vp), ("xq", _vp)]
 
 
+class _Act(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int), ("cols", _u32), ("x", _vp), ("norm", _vp), ("eps", ctypes.c_float),
+                ("xd", _vp), ("xq", _vp), ("xd_scratch", _vp), ("xq_scratch", _vp)]
+
+
 class _AttnShape(ctypes.Structure):
     _fields_ = [("heads", _u32), ("kv_heads", _u32), ("head_dim", _u32), ("rotary_pairs", _u32), ("window", _u32),
                 ("context", _u32)]
@@ -96,6 +101,9 @@ _SIGS = {
     "smq_set_prefill_mfma": (None, [ctypes.c_int]),
     "smq_matmul": (ctypes.c_int, [ctypes.POINTER(_MatItem), _u32, _vp, _vp, _u32]),
     "smq_numeric_check": (ctypes.c_int, []),
+    "smq_matmul_act": (ctypes.c_int, [ctypes.POINTER(_MatItem), _u32, ctypes.POINTER(_Act)]),
+    "smq_matmul_glu": (ctypes.c_int, [ctypes.POINTER(_QMat), ctypes.POINTER(_QMat), ctypes.POINTER(_Act), ctypes.c_int,
+                                      _vp, _vp]),
     "smq_gemv_grouped": (ctypes.c_int, [ctypes.POINTER(_GroupItem), _u32]),
     "smq_rope_kv": (ctypes.c_int, [_vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _vp, _vp, _vp, _vp, _u32, _vp]),
     "smq_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _u32, _vp]),
@@ -103,6 +111,8 @@ _SIGS = {
     "smq_argmax": (ctypes.c_int, [_vp, _u32, _vp, _vp]),
     "smq_embed": (ctypes.c_int, [ctypes.POINTER(_QMat), _vp, _u32, _vp]),
     "smq_decode_advance": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32]),
+    "smq_attention_rope_q8": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp]),
+    "smq_argmax_advance": (ctypes.c_int, [_vp, _u32, _vp, _vp, _vp, _vp, _vp, _u32]),
     "smq_dequantize_q8_row": (None, [_vp, _u32, _vp]),
     "smq_dequantize_q5_row": (None, [_vp, _u32, _vp]),
     "smq_malloc": (_vp, [_sz]),
@@ -364,6 +374,40 @@ def matmul(items, xd, xq, ntok):
     _check(load().smq_matmul(arr, len(items), _p(xd), _p(xq), ntok))
 
 
+ACT_Q8, ACT_NORM, ACT_F32 = 0, 1, 2
+
+
+def act(kind, cols, x=None, norm=None, eps=1e-6, xd=None, xq=None, xd_scratch=None, xq_scratch=None):
+    """The activation of a fused decode matmul (smq_act); holds its buffers."""
+    a = _Act(kind, cols, _p(x), _p(norm), eps, _p(xd), _p(xq), _p(xd_scratch), _p(xq_scratch))
+    a._keep = (x, norm, xd, xq, xd_scratch, xq_scratch)  # the device buffers live as long as the descriptor
+    return a
+
+
+def _items(items):
+    cm = [it[0]._c() for it in items]
+    arr = (_MatItem * len(items))()
+    for i, it in enumerate(items):
+        arr[i].w = ctypes.pointer(cm[i])
+        arr[i].bias = _p(it[1])
+        arr[i].y = _p(it[2])
+        arr[i].accumulate = int(bool(it[3])) if len(it) > 3 else 0
+    return arr, cm
+
+
+def matmul_act(items, activation):
+    """smq_matmul_act: one token, the activation formed in the matmul's launch."""
+    arr, _keep = _items(items)
+    _check(load().smq_matmul_act(arr, len(items), ctypes.byref(activation)))
+
+
+def matmul_glu(gate, up, activation, glu, h, gate_scratch=None):
+    """smq_matmul_glu: h = up * act(gate) of one token (glu 1 SwiGLU, 2 GeGLU)."""
+    g, u = gate._c(), up._c()
+    _check(load().smq_matmul_glu(ctypes.byref(g), ctypes.byref(u), ctypes.byref(activation), glu, _p(h),
+                                 _p(gate_scratch)))
+
+
 def gemv_grouped(items):
     """items: sequence of (QMat, bias or None, y, accumulate, xd, xq): independent
     one-token GEMVs with their own activations, one launch."""
@@ -398,6 +442,11 @@ def attention_q8(q, keys, values, att, ntok, shape, xd, xq, pos0=0, pos_dev=None
                                    _p(pos_dev), _p(xd), _p(xq)))
 
 
+def attention_rope_q8(q, k, v, shape, cos_table, sin_table, keys, values, att, xd, xq, pos0=0, pos_dev=None):
+    _check(load().smq_attention_rope_q8(_p(q), _p(k), _p(v), ctypes.byref(shape), _p(cos_table), _p(sin_table),
+                                        _p(keys), _p(values), _p(att), pos0, _p(pos_dev), _p(xd), _p(xq)))
+
+
 def argmax(logits, vocab, banned, token):
     _check(load().smq_argmax(_p(logits), vocab, _p(banned), _p(token)))
 
@@ -409,6 +458,11 @@ def embed(w, tokens, ntok, x):
 
 def decode_advance(pos, count, token, history, capacity):
     _check(load().smq_decode_advance(_p(pos), _p(count), _p(token), _p(history), capacity))
+
+
+def argmax_advance(logits, vocab, banned, token, pos, count, history, capacity):
+    _check(load().smq_argmax_advance(_p(logits), vocab, _p(banned), _p(token), _p(pos), _p(count), _p(history),
+                                     capacity))
 
 
 def numeric_check():

@@ -15,8 +15,10 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libsmq_gfx950.so")
-SOURCES = [os.path.join(HERE, "csrc", "smq_kernels.hip"), os.path.join(HERE, "csrc", "smq_api.cpp")]
-HEADERS = [os.path.join(HERE, "csrc", "smq_internal.h"), os.path.join(ROOT, "include", "smq.h")]
+SOURCES = [os.path.join(HERE, "csrc", f) for f in ("smq_kernels.hip", "smq_fused.hip", "smq_api.cpp")]
+HEADERS = [os.path.join(HERE, "csrc", "smq_internal.h"), os.path.join(HERE, "csrc", "smq_device.h"),
+           os.path.join(ROOT, "include", "smq.h")]
+OBJ_DIR = os.path.join(HERE, "_build")
 MODEL_LIB = os.path.join(HERE, "libsmq_model.so")
 MODEL_SOURCES = [os.path.join(HERE, "host", "smq_model.c"), os.path.join(HERE, "host", "smq_synth.c")]
 # The host side keeps IEEE double/float as written (RoPE tables in double).
@@ -39,17 +41,36 @@ def hipcc():
     return "hipcc"
 
 
+def _quiet(text):
+    """hipcc's host pass does not know the packed-fp32 feature: that note is harmless."""
+    return "\n".join(line for line in text.splitlines() if "packed-fp32-ops" not in line)
+
+
 def build(verbose=False):
-    cmd = [hipcc()] + FLAGS + ["-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc"),
-                               "-o", LIB + ".tmp"] + SOURCES
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    out = "\n".join(line for line in (res.stdout + res.stderr).splitlines()
-                    if "packed-fp32-ops" not in line)  # host pass does not know the feature: harmless
-    if res.returncode != 0:
-        sys.stderr.write(out + "\n")
+    """Compiles each source to an object in parallel, then links the library."""
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc")]
+    compile_flags = [f for f in FLAGS if f != "-shared"]
+    jobs = []
+    for src in SOURCES:
+        obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
+        cmd = [hipcc()] + compile_flags + inc + ["-c", src, "-o", obj]
+        jobs.append((src, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+    failed = False
+    for src, obj, proc in jobs:
+        out = _quiet(proc.communicate()[0])
+        if proc.returncode != 0:
+            sys.stderr.write(out + "\n")
+            failed = True
+        elif verbose and out.strip():
+            sys.stderr.write(out + "\n")
+    if failed:
         raise RuntimeError("hipcc failed building libsmq_gfx950.so")
-    if verbose and out.strip():
-        sys.stderr.write(out + "\n")
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB + ".tmp"] + [obj for _, obj, _ in jobs]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(_quiet(res.stdout + res.stderr) + "\n")
+        raise RuntimeError("hipcc failed linking libsmq_gfx950.so")
     os.replace(LIB + ".tmp", LIB)
     cmd = [os.environ.get("CC", "gcc")] + MODEL_FLAGS + ["-I", os.path.join(ROOT, "include"), "-o",
                                                          MODEL_LIB + ".tmp"] + MODEL_SOURCES + \

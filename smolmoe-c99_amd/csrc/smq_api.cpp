@@ -26,6 +26,7 @@ struct Context {
     int *flag = nullptr;    /* sticky numeric fault (quantize rows, matmul) */
     int *qflag = nullptr;   /* per-call fault of the synchronous quantizer */
     float *scalar = nullptr;
+    void *argmax_parts = nullptr; /* smq::MAX_ARGMAX_PARTS partials of the two-stage argmax */
     hipEvent_t t0 = nullptr, t1 = nullptr;
     int fast = 0;
     int prefill_mfma = 0;
@@ -203,6 +204,8 @@ smq_status smq_init(int device) {
     g.qflag = (int *)p + 16;
     g.scalar = (float *)p + 32;
     if (!hip_ok(hipMemset(p, 0, 256), "hipMemset")) return t_status;
+    if (!hip_ok(hipMalloc(&g.argmax_parts, (size_t)smq::MAX_ARGMAX_PARTS * smq::ARGMAX_PART_BYTES), "hipMalloc"))
+        return t_status;
     if (!hip_ok(hipEventCreate(&g.t0), "hipEventCreate") || !hip_ok(hipEventCreate(&g.t1), "hipEventCreate"))
         return t_status;
     g.cur = g.own;
@@ -219,6 +222,7 @@ void smq_shutdown(void) {
     (void)hipEventDestroy(g.t0);
     (void)hipEventDestroy(g.t1);
     (void)hipFree(g.flag);
+    (void)hipFree(g.argmax_parts);
     (void)hipStreamDestroy(g.own);
     g = Context();
 }
@@ -483,6 +487,199 @@ smq_status smq_gemv_grouped(const smq_group_item *items, uint32_t n) {
     return hip_ok(smq::launch_gemv_grouped(ga, q5, g.fast != 0, g.cur), "gemv_grouped") ? SMQ_OK : t_status;
 }
 
+/* Validates a fused-call activation for matrices of `cols` columns. */
+static bool act_ok(const smq_act *act, uint32_t cols, const char *who) {
+    if (!act) {
+        set_status(SMQ_ERR_RANGE, "%s: activation is NULL", who);
+        return false;
+    }
+    if (act->cols != cols) {
+        set_status(SMQ_ERR_RANGE, "%s: activation has %u columns, the matrices %u", who, act->cols, cols);
+        return false;
+    }
+    const size_t nb = (cols + smq::QK - 1) / smq::QK;
+    switch (act->kind) {
+    case SMQ_ACT_Q8:
+        return extent_ok(act->xd, nb * 4, "activation scales") && extent_ok(act->xq, nb * smq::QK, "activations");
+    case SMQ_ACT_NORM:
+        if (!extent_ok(act->norm, (size_t)cols * 4, "norm weights")) return false;
+        /* fall through */
+    case SMQ_ACT_F32:
+        return extent_ok(act->x, (size_t)cols * 4, "x") &&
+               extent_ok(act->xd_scratch, act->xd_scratch ? nb * 4 : 0, "scale scratch") &&
+               extent_ok(act->xq_scratch, act->xq_scratch ? nb * smq::QK : 0, "value scratch");
+    default:
+        set_status(SMQ_ERR_RANGE, "%s: activation kind %d", who, act->kind);
+        return false;
+    }
+}
+
+/* The unfused form: the activation's Q8 blocks into (xd, xq). */
+static bool act_materialize(const smq_act *act, const float **xd, const int8_t **xq, const char *who) {
+    if (act->kind == SMQ_ACT_Q8) {
+        *xd = act->xd;
+        *xq = act->xq;
+        return true;
+    }
+    if (!act->xd_scratch || !act->xq_scratch) {
+        set_status(SMQ_ERR_RANGE, "%s: this shape needs the scratch buffers", who);
+        return false;
+    }
+    const hipError_t e = act->kind == SMQ_ACT_NORM
+                             ? smq::launch_row_quantize(act->x, act->norm, act->eps, nullptr, 0, 1, act->cols, nullptr,
+                                                        act->xd_scratch, act->xq_scratch, g.flag, g.cur)
+                             : smq::launch_quantize_q8(act->x, 1, act->cols, act->xd_scratch, act->xq_scratch, g.flag,
+                                                       g.cur);
+    if (!hip_ok(e, who)) return false;
+    *xd = act->xd_scratch;
+    *xq = act->xq_scratch;
+    return true;
+}
+
+static void fused_act(smq::FusedArgs &f, const smq_act *act) {
+    f.n = act->cols;
+    f.src = act->x;
+    f.norm = act->norm;
+    f.eps = act->eps;
+    f.xd = act->xd;
+    f.xq = act->xq;
+    f.flag = g.flag;
+}
+
+/* One launch of the fused kernel covers at most this many workgroup tiles
+ * (about one resident wave): every workgroup repeats the prologue. */
+static const uint32_t FUSED_MAX_TILES = 4096;
+/* Rows x padded columns up to which an f32 activation is quantized in the matmul's own launch. */
+static const uint64_t FUSED_F32_WORK = (uint64_t)1 << 20;
+
+smq_status smq_matmul_act(const smq_mat_item *items, uint32_t n, const smq_act *act) {
+    if (!ready()) return t_status;
+    if (!items || n < 1 || n > SMQ_MAX_ITEMS) return set_status(SMQ_ERR_RANGE, "matmul_act: %u items", n);
+    const uint32_t nb = items[0].w ? items[0].w->nb : 0, cols = items[0].w ? items[0].w->cols : 0;
+    uint32_t total_rows = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        const smq_qmat *w = items[i].w;
+        if (!w) return set_status(SMQ_ERR_RANGE, "matmul_act: item %u has no matrix", i);
+        if (w->nb != nb || w->cols != cols)
+            return set_status(SMQ_ERR_STATE, "internal error: matmul inputs differ in width");
+        if (w->dtype != 1 && w->dtype != 2) return set_status(SMQ_ERR_FORMAT, "matmul_act: dtype %u", w->dtype);
+        if (w->nb != (w->cols + smq::QK - 1) / smq::QK)
+            return set_status(SMQ_ERR_RANGE, "matmul_act: nb %u does not match %u columns", w->nb, w->cols);
+        if (w->row_bytes < (size_t)w->nb * block_bytes(w->dtype == 2))
+            return set_status(SMQ_ERR_RANGE, "matmul_act: row_bytes %zu < nb*%u", w->row_bytes,
+                              block_bytes(w->dtype == 2));
+        if (!extent_ok(w->data, w->rows ? (size_t)(w->rows - 1) * w->row_bytes + (size_t)w->nb * block_bytes(w->dtype == 2) : 0,
+                       "weights") ||
+            !extent_ok(items[i].y, (size_t)w->rows * 4, "output") ||
+            !extent_ok(items[i].bias, items[i].bias ? (size_t)w->rows * 4 : 0, "bias"))
+            return t_status;
+        total_rows += w->rows;
+    }
+    if (!nb) return set_status(SMQ_ERR_RANGE, "matmul_act: nb is 0");
+    if (!act_ok(act, cols, "matmul_act")) return t_status;
+    if (!total_rows) return SMQ_OK;
+    if (act->kind == SMQ_ACT_Q8) return smq_matmul(items, n, act->xd, act->xq, 1);
+    /* fused: one launch per weight format present, each forming the activation itself */
+    bool fused = true;
+    smq::FusedArgs fa[2];
+    for (int q5 = 0; q5 < 2; ++q5) {
+        smq::FusedArgs &f = fa[q5];
+        memset(&f, 0, sizeof(f));
+        f.nb = nb;
+        fused_act(f, act);
+        uint32_t tiles = 0;
+        for (uint32_t i = 0; i < n; ++i) {
+            const smq_qmat *w = items[i].w;
+            if ((w->dtype == 2) != (q5 == 1) || !w->rows) continue;
+            smq::Item &it = f.item[f.nitems++];
+            it.w = w->data;
+            it.row_bytes = w->row_bytes;
+            it.bias = items[i].bias;
+            it.y = items[i].y;
+            it.y_stride = w->rows;
+            it.rows = w->rows;
+            it.accumulate = items[i].accumulate != 0;
+            tiles += w->rows; /* rows: an upper bound of the tiles */
+        }
+        /* every workgroup forms the activation: an f32 row is quantized once, apart, when the
+         * repeated work would outweigh a launch (the down projection's 896 workgroups x 4864) */
+        const uint64_t np = (uint64_t)nb * smq::QK;
+        if (f.nitems && (g.fast || !smq::fused_layout_ok(f, q5 == 1, act->kind) || tiles / 8 > FUSED_MAX_TILES ||
+                         (act->kind == SMQ_ACT_F32 && (uint64_t)tiles * np > FUSED_F32_WORK)))
+            fused = false;
+    }
+    if (fused) {
+        for (int q5 = 0; q5 < 2; ++q5)
+            if (fa[q5].nitems &&
+                !hip_ok(smq::launch_matmul_fused(fa[q5], q5 == 1, act->kind, false, g.cur), "matmul_act"))
+                return t_status;
+        return SMQ_OK;
+    }
+    const float *xd = nullptr;
+    const int8_t *xq = nullptr;
+    if (!act_materialize(act, &xd, &xq, "matmul_act")) return t_status;
+    return smq_matmul(items, n, xd, xq, 1);
+}
+
+smq_status smq_matmul_glu(const smq_qmat *gate, const smq_qmat *up, const smq_act *act, int glu, float *h,
+                          float *gate_scratch) {
+    if (!ready()) return t_status;
+    if (!gate || !up) return set_status(SMQ_ERR_RANGE, "matmul_glu: NULL matrix");
+    if (gate->rows != up->rows || gate->cols != up->cols || gate->nb != up->nb)
+        return set_status(SMQ_ERR_STATE, "matmul_glu: gate %ux%u and up %ux%u differ", gate->rows, gate->cols,
+                          up->rows, up->cols);
+    if (glu != 1 && glu != 2) return set_status(SMQ_ERR_RANGE, "matmul_glu: activation %d", glu);
+    if (!extent_ok(h, (size_t)up->rows * 4, "h")) return t_status;
+    smq_mat_item it[2];
+    it[0].w = gate;
+    it[0].bias = nullptr;
+    it[0].y = gate_scratch;
+    it[0].accumulate = 0;
+    it[1].w = up;
+    it[1].bias = nullptr;
+    it[1].y = h;
+    it[1].accumulate = 0;
+    if (gate->dtype == up->dtype && (gate->dtype == 1 || gate->dtype == 2) && act && act->cols == gate->cols &&
+        gate->nb == (gate->cols + smq::QK - 1) / smq::QK) {
+        smq::FusedArgs f;
+        memset(&f, 0, sizeof(f));
+        f.nb = gate->nb;
+        fused_act(f, act);
+        f.nitems = 2;
+        for (int k = 0; k < 2; ++k) {
+            const smq_qmat *w = k ? up : gate;
+            f.item[k].w = w->data;
+            f.item[k].row_bytes = w->row_bytes;
+            f.item[k].rows = w->rows;
+        }
+        f.h = h;
+        f.rows = gate->rows;
+        f.act = glu;
+        const bool q5 = gate->dtype == 2;
+        if (!g.fast && act->kind == SMQ_ACT_NORM && smq::fused_layout_ok(f, q5, act->kind) &&
+            gate->rows / 4 <= FUSED_MAX_TILES) {
+            for (int k = 0; k < 2; ++k) {
+                const smq_qmat *w = k ? up : gate;
+                if (w->row_bytes < (size_t)w->nb * block_bytes(q5))
+                    return set_status(SMQ_ERR_RANGE, "matmul_glu: row_bytes %zu < nb*%u", w->row_bytes, block_bytes(q5));
+                if (!extent_ok(w->data, w->rows ? (size_t)(w->rows - 1) * w->row_bytes + (size_t)w->nb * block_bytes(q5) : 0,
+                               "weights"))
+                    return t_status;
+            }
+            if (!act_ok(act, gate->cols, "matmul_glu")) return t_status;
+            if (!gate->rows) return SMQ_OK;
+            return hip_ok(smq::launch_matmul_fused(f, q5, act->kind, true, g.cur), "matmul_glu")
+                       ? SMQ_OK
+                       : t_status;
+        }
+    }
+    /* the two-call form: gate and up, then h = up * act(gate) */
+    if (!gate_scratch) return set_status(SMQ_ERR_RANGE, "matmul_glu: this shape needs gate_scratch");
+    const smq_status st = smq_matmul_act(it, 2, act);
+    if (st != SMQ_OK) return st;
+    return hip_ok(smq::launch_glu(h, gate_scratch, up->rows, glu, g.cur), "matmul_glu") ? SMQ_OK : t_status;
+}
+
 smq_status smq_numeric_check(void) {
     if (!ready()) return t_status;
     int bad = 0;
@@ -588,13 +785,59 @@ smq_status smq_attention_q8(const float *q, const float *keys, const float *valu
                : t_status;
 }
 
+smq_status smq_attention_rope_q8(float *q, float *k, const float *v, const smq_attn_shape *shape,
+                                 const float *cos_table, const float *sin_table, float *keys, float *values,
+                                 float *att, uint32_t pos0, const int32_t *pos_dev, float *xd, int8_t *xq) {
+    if (!ready()) return t_status;
+    smq::AttnShape sh;
+    if (!attn_shape(shape, &sh, "attention_rope_q8")) return t_status;
+    if (!pos_dev && pos0 >= sh.context) return set_status(SMQ_ERR_RANGE, "token batch exceeds context");
+    const size_t table = (size_t)sh.context * sh.pairs * 4, cache = (size_t)sh.context * sh.kv_dim * 4;
+    const size_t nbq = (sh.q_dim + smq::QK - 1) / smq::QK;
+    if (!extent_ok(q, (size_t)sh.q_dim * 4, "q") || !extent_ok(k, (size_t)sh.kv_dim * 4, "k") ||
+        !extent_ok(v, (size_t)sh.kv_dim * 4, "v") || !extent_ok(cos_table, table, "cos table") ||
+        !extent_ok(sin_table, table, "sin table") || !extent_ok(keys, cache, "keys") ||
+        !extent_ok(values, cache, "values") || !extent_ok(att, (size_t)sh.q_dim * 4, "att") ||
+        !extent_ok(pos_dev, pos_dev ? 4 : 0, "pos") || !extent_ok(xd, nbq * 4, "xd") ||
+        !extent_ok(xq, nbq * smq::QK, "xq"))
+        return t_status;
+    const bool aligned = !((uintptr_t)q & 15) && !((uintptr_t)k & 15) && !((uintptr_t)v & 15);
+    if (aligned && smq::attention_rows_ok(sh, q, keys, values))
+        return hip_ok(smq::launch_attention_rope(q, k, v, cos_table, sin_table, keys, values, att, sh, pos0, pos_dev,
+                                                 g.flag, xd, xq, g.cur),
+                      "attention_rope_q8")
+                   ? SMQ_OK
+                   : t_status;
+    /* other shapes: the two-step form (q and k are left rotated) */
+    if (smq_rope_kv(q, k, v, 1, shape, cos_table, sin_table, keys, values, pos0, pos_dev) != SMQ_OK) return t_status;
+    return smq_attention_q8(q, keys, values, att, 1, shape, pos0, pos_dev, xd, xq);
+}
+
 smq_status smq_argmax(const float *logits, uint32_t vocab, const unsigned char *banned, uint32_t *token) {
     if (!ready()) return t_status;
     if (!vocab) return set_status(SMQ_ERR_RANGE, "argmax: empty vocabulary");
     if (!extent_ok(logits, (size_t)vocab * 4, "logits") || !extent_ok(banned, banned ? vocab : 0, "banned") ||
         !extent_ok(token, 4, "token"))
         return t_status;
-    return hip_ok(smq::launch_argmax(logits, vocab, banned, token, g.cur), "argmax") ? SMQ_OK : t_status;
+    return hip_ok(smq::launch_argmax(logits, vocab, banned, token, g.argmax_parts, nullptr, nullptr, nullptr, 0, g.cur),
+                  "argmax")
+               ? SMQ_OK
+               : t_status;
+}
+
+smq_status smq_argmax_advance(const float *logits, uint32_t vocab, const unsigned char *banned, uint32_t *token,
+                              int32_t *pos, uint32_t *count, uint32_t *history, uint32_t capacity) {
+    if (!ready()) return t_status;
+    if (!vocab) return set_status(SMQ_ERR_RANGE, "argmax: empty vocabulary");
+    if (!extent_ok(logits, (size_t)vocab * 4, "logits") || !extent_ok(banned, banned ? vocab : 0, "banned") ||
+        !extent_ok(token, 4, "token") || !extent_ok(pos, 4, "pos") || !extent_ok(count, 4, "count") ||
+        !extent_ok(history, (size_t)capacity * 4, "history"))
+        return t_status;
+    if (!pos || !count || (capacity && !history)) return set_status(SMQ_ERR_RANGE, "argmax_advance: NULL argument");
+    return hip_ok(smq::launch_argmax(logits, vocab, banned, token, g.argmax_parts, pos, count, history, capacity, g.cur),
+                  "argmax_advance")
+               ? SMQ_OK
+               : t_status;
 }
 
 smq_status smq_embed(const smq_qmat *embed, const uint32_t *tokens, uint32_t ntok, float *x) {

@@ -1,0 +1,314 @@
+/* Fused decode GEMV (one token) for gfx950: the activation producer of the
+ * reference's decode step (model.c:334-415) run as the prologue of the
+ * matmul that consumes it, and the gated product of a gate/up pair run as
+ * its store (vecmath.c:78-93). */
+#include <float.h>
+
+#include "smq_device.h"
+#include "smq_internal.h"
+
+namespace smq {
+namespace {
+
+/* ------------------------------------------------------------------------
+ * Fused decode GEMV (one token): the activation is formed inside the
+ * launch, and for a gate/up pair the gated product is formed in the store.
+ *  PRO_NORM  RMSNorm of the f32 row src with weights norm (model.c:334-342:
+ *            squares in parallel, their sum in element order by one lane,
+ *            inv = 1/sqrtf(sum/n + eps), (x*inv)*w) and its Q8 blocks
+ *            (kernels.c:912-935), computed by every workgroup for itself;
+ *  PRO_F32   the Q8 blocks of the f32 row src.
+ *  EPI_STORE each item's rows: + bias, finiteness, y or y += (as k_gemv);
+ *  EPI_GLU   items 0 and 1 are gate and up with the same rows; a workgroup
+ *            owns RT/2 rows of each and stores h[r] = up[r] * (g / (1 +
+ *            exp_det(-g))) (SwiGLU) or the GeGLU form (vecmath.c:78-93).
+ * Every workgroup issues its first weight loads before the prologue, so the
+ * prologue's loads and serial sum overlap the weight fetch. Products, chains
+ * and the lane tree are those of k_gemv (exact per-lane order).
+ * ---------------------------------------------------------------------- */
+constexpr int PRO_NORM = 1, PRO_F32 = 2; /* SMQ_ACT_NORM, SMQ_ACT_F32 */
+constexpr uint32_t FU_BATCH = 32; /* prologue loads in flight per thread */
+static_assert(FU_BATCH * WG == MAX_NORM_K, "one batch holds the widest RMSNorm row");
+constexpr int EPI_STORE = 0, EPI_GLU = 1;
+
+__device__ __forceinline__ uint32_t find_fused_item(const FusedArgs &a, uint32_t tile) {
+    uint32_t it = 0;
+    if (a.nitems > 1 && tile >= a.item[1].tile_begin) it = 1;
+    if (a.nitems > 2 && tile >= a.item[2].tile_begin) it = 2;
+    if (a.nitems > 3 && tile >= a.item[3].tile_begin) it = 3;
+    return it;
+}
+
+template <bool Q5, bool FAST, int RT, int PRO, int EPI>
+__global__ __launch_bounds__(WG) void k_gemv_fused(FusedArgs a) {
+    constexpr int TB = Q5 ? 2 : 1;    /* blocks per task */
+    constexpr int TPR = WG / RT;      /* tasks per row per chunk */
+    constexpr int CB = TPR * TB;      /* blocks per chunk */
+    constexpr int GS = RT * 32 + 4;   /* floats per group of four blocks */
+    constexpr int DS = RT * 4 + 4;    /* fast mode: scales per group */
+    constexpr int NW = Q5 ? 11 : 9;   /* weight dwords per task */
+    static_assert(EPI != EPI_GLU || (RT % 2 == 0 && RT * 8 <= 64), "gate/up slots share wave 0");
+    __shared__ __attribute__((aligned(16))) float prod[2][(CB / 4) * GS];
+    __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? (CB / 4) * DS : 4];
+    __shared__ float s_inv;
+    __shared__ int s_bad;
+    extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];
+
+    const uint32_t nb = a.nb, tid = threadIdx.x, np = nb * QK, n = a.n;
+    const uint32_t n4 = PRO == PRO_NORM ? (n + 3) & ~3u : 0u;
+    float *sq = (float *)dyn, *xs = sq + n4, *ws = xs + n4; /* PRO_NORM: squares, x, weights */
+    uint32_t *act_q = dyn + 3 * n4;
+    float *act_d = (float *)(act_q + nb * 8);
+    int *act_b = (int *)(act_d + nb); /* Q5: -16 * lane sums of x */
+
+    /* this thread's weight row */
+    const uint32_t tr = tid / TPR, ti = tid % TPR;
+    const unsigned char *wrow;
+    size_t row_bytes;
+    bool row_ok;
+    uint32_t item = 0, r0 = 0;
+    if (EPI == EPI_GLU) {
+        constexpr uint32_t half = RT / 2 > 0 ? RT / 2 : 1;
+        const uint32_t row = blockIdx.x * half + tr % half;
+        const Item &I = a.item[tr < half ? 0 : 1];
+        row_ok = row < a.rows;
+        row_bytes = I.row_bytes;
+        wrow = I.w + (size_t)(row_ok ? row : 0) * row_bytes;
+    } else {
+        item = find_fused_item(a, blockIdx.x);
+        const Item &I = a.item[item];
+        r0 = (blockIdx.x - I.tile_begin) * RT;
+        row_ok = r0 + tr < I.rows;
+        row_bytes = I.row_bytes;
+        wrow = I.w + (size_t)(row_ok ? r0 + tr : 0) * row_bytes;
+    }
+    const uint32_t nchunks = (nb + CB - 1) / CB;
+    uint32_t wr[NW] = {};
+    auto load_task = [&](uint32_t b) {
+        if (row_ok && b < nb) {
+            const unsigned char *p = wrow + (size_t)b * (Q5 ? Q5_BYTES : Q8_BYTES);
+            const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
+            wr[0] = v0.x; wr[1] = v0.y; wr[2] = v0.z; wr[3] = v0.w;
+            wr[4] = v1.x; wr[5] = v1.y; wr[6] = v1.z; wr[7] = v1.w;
+            if constexpr (Q5) {
+                const u3a v2 = *(const u3a *)(p + 32);
+                wr[8] = v2.x; wr[9] = v2.y; wr[10] = v2.z;
+            } else {
+                wr[8] = *(const uint32_t *)(p + 32);
+            }
+        }
+    };
+    load_task(ti * TB);
+
+    /* prologue: the activation into LDS, loaded in batches of FU_BATCH
+     * elements per thread (a batch's loads all issue before any is used). The
+     * weight loads above stay in flight meanwhile. */
+    static_assert(PRO == PRO_NORM || PRO == PRO_F32, "a given Q8 activation takes k_gemv");
+    {
+        const uint32_t ke = (np + WG - 1) / WG; /* NORM: <= FU_BATCH (n <= MAX_NORM_K) */
+        int bad = 0;
+        int8_t *q8 = (int8_t *)act_q;
+        if (PRO == PRO_NORM) {
+            /* x, w and the squares to LDS; then the sum in order; then (x*inv)*w. (The
+             * batch loop, one trip for n <= MAX_NORM_K, keeps the batch registers'
+             * live range short: 5 workgroups per CU.) */
+            for (uint32_t k0 = 0; k0 < ke; k0 += FU_BATCH) {
+                float xv[FU_BATCH], wv[FU_BATCH];
+#pragma unroll
+                for (uint32_t k = 0; k < FU_BATCH; ++k) {
+                    const uint32_t i = tid + (k0 + k) * WG;
+                    xv[k] = i < n ? a.src[i] : 0.0f;
+                    wv[k] = i < n ? a.norm[i] : 0.0f;
+                }
+#pragma unroll
+                for (uint32_t k = 0; k < FU_BATCH; ++k) {
+                    const uint32_t i = tid + (k0 + k) * WG;
+                    if (i < n) {
+                        sq[i] = xv[k] * xv[k];
+                        xs[i] = xv[k];
+                        ws[i] = wv[k];
+                    }
+                }
+            }
+            __syncthreads();
+            if (tid == 0) {
+                const float ss = serial_sum_lds(sq, n);
+                const float iv = 1.0f / sqrtf(ss / (float)n + a.eps); /* model.c:338 */
+                s_inv = iv;
+                s_bad = !(fabsf(ss) <= FLT_MAX) || !(fabsf(iv) <= FLT_MAX);
+            }
+            __syncthreads();
+            const float inv = s_inv;
+            if (tid == 0 && s_bad && a.flag) *a.flag = 1;
+#pragma unroll
+            for (uint32_t k = 0; k < FU_BATCH; ++k) { /* uniform; a block's 32 lanes are all below np or past it */
+                const uint32_t i = tid + k * WG;
+                if (k < ke && i < np) {
+                    const bool valid = i < n;
+                    float v = 0.0f;
+                    if (valid) {
+                        const float t = xs[i] * inv;
+                        v = t * ws[i]; /* model.c:340 */
+                    }
+                    stage_q8(v, valid, i, q8, act_d, bad);
+                }
+            }
+        } else {
+            for (uint32_t k0 = 0; k0 < ke; k0 += FU_BATCH) {
+                float xv[FU_BATCH];
+#pragma unroll
+                for (uint32_t k = 0; k < FU_BATCH; ++k) {
+                    const uint32_t i = tid + (k0 + k) * WG;
+                    xv[k] = i < n ? a.src[i] : 0.0f;
+                }
+#pragma unroll
+                for (uint32_t k = 0; k < FU_BATCH; ++k) {
+                    const uint32_t i = tid + (k0 + k) * WG;
+                    if (i < np) stage_q8(xv[k], i < n, i, q8, act_d, bad); /* uniform per block */
+                }
+            }
+        }
+        if (bad && a.flag) *a.flag = 1;
+    }
+    if (Q5) {
+        __syncthreads();
+        for (uint32_t i = tid; i < nb * 8; i += WG) act_b[i] = dot4(act_q[i], 0xf0f0f0f0u, 0); /* int8 0xf0 = -16 */
+    }
+    __syncthreads(); /* activation staged */
+
+    float acc = 0.0f;
+    for (uint32_t c = 0; c < nchunks; ++c) {
+        const uint32_t bt = c * CB + ti * TB;
+        uint32_t cw[NW];
+#pragma unroll
+        for (int k = 0; k < NW; ++k) cw[k] = wr[k];
+        if (c + 1 < nchunks) load_task(bt + CB);
+        float *pb = prod[c & 1];
+        if (row_ok && bt < nb) {
+            Q5Fields f[2];
+            if (Q5) q5_parse_pair(cw, f[0], f[1]);
+#pragma unroll
+            for (int k = 0; k < TB; ++k) {
+                const uint32_t b = bt + k, bb = ti * TB + k;
+                const float wscale = Q5 ? f[k].scale : __uint_as_float(cw[0]);
+                const float d = wscale * act_d[b];
+                float *dst = pb + (bb / 4) * GS + tr * 32 + (bb % 4);
+#pragma unroll
+                for (int l = 0; l < 8; ++l) {
+                    const uint32_t x = act_q[b * 8 + l];
+                    int sv;
+                    if (Q5) sv = dot4(q5_codes(f[k], l), x, act_b[b * 8 + l]);
+                    else sv = dot4(cw[1 + l], x, 0);
+                    dst[l * 4] = FAST ? (float)sv : d * (float)sv;
+                }
+                if (FAST) dsc[c & 1][(bb / 4) * DS + tr * 4 + (bb % 4)] = d;
+            }
+        }
+        __syncthreads();
+        if (tid < RT * 8) {
+            const uint32_t count = nb - c * CB < (uint32_t)CB ? nb - c * CB : (uint32_t)CB;
+            chain_sum<FAST, CB / 4>(acc, (const float4 *)pb + tid, GS / 4,
+                                    FAST ? (const float4 *)dsc[c & 1] + tid / 8 : nullptr, DS / 4, count);
+        }
+    }
+
+    if (EPI == EPI_GLU) {
+        if (tid < 64) { /* every row slot is in wave 0 */
+            const float v = reduce8_to_lane7(acc);
+            const float u = __shfl_down(v, RT * 4, 64); /* up slot tr + RT/2 */
+            const uint32_t row = blockIdx.x * (RT / 2 > 0 ? RT / 2 : 1) + tid / 8;
+            if ((tid & 7) == 7 && tid < RT * 4 && row < a.rows) {
+                const float gv = v;
+                if (a.flag && (!(fabsf(gv) <= FLT_MAX) || !(fabsf(u) <= FLT_MAX))) *a.flag = 1; /* model.c:309 */
+                float e;
+                if (a.act == 2) {
+                    const float g3 = 0.044715f * gv * gv * gv;
+                    const float uu = 1.5957691216f * (gv + g3);
+                    e = exp_det(-uu);
+                } else {
+                    e = exp_det(-gv);
+                }
+                const float den = 1.0f + e;
+                const float sg = gv / den;
+                a.h[row] = u * sg;
+            }
+        }
+    } else if (tid < RT * 8) {
+        const float v = reduce8_to_lane7(acc);
+        const Item &I = a.item[item];
+        const uint32_t r = r0 + tid / 8;
+        if ((tid & 7) == 7 && r < I.rows) store_out(I, a.flag, 0, r, v);
+    }
+}
+
+template <bool Q5, int RT, int PRO, int EPI>
+hipError_t launch_fused_rt(FusedArgs a, hipStream_t s) {
+    uint32_t tiles = 0;
+    if (EPI == EPI_GLU) {
+        constexpr uint32_t half = RT / 2 > 0 ? RT / 2 : 1;
+        tiles = (a.rows + half - 1) / half;
+    } else {
+        for (uint32_t i = 0; i < a.nitems; ++i) {
+            a.item[i].tile_begin = tiles;
+            tiles += (a.item[i].rows + RT - 1) / RT;
+        }
+    }
+    if (!tiles) return hipSuccess;
+    const size_t lds = ((PRO == PRO_NORM ? 3 * ((a.n + 3) / 4 * 4) : 0) + (size_t)a.nb * (Q5 ? 17u : 9u)) * 4u;
+    static size_t allowed = 64 << 10; /* dynamic LDS beyond the 64 KiB default for wide rows */
+    if (lds > allowed) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_gemv_fused<Q5, false, RT, PRO, EPI>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        allowed = lds;
+    }
+    hipLaunchKernelGGL((k_gemv_fused<Q5, false, RT, PRO, EPI>), dim3(tiles), dim3(WG), lds, s, a);
+    return hipGetLastError();
+}
+
+template <bool Q5, int PRO, int EPI>
+hipError_t launch_fused_pe(const FusedArgs &a, int rt, hipStream_t s) {
+    if constexpr (EPI == EPI_GLU) { /* two to eight rows: a gate/up pair per slot, all slots in wave 0 */
+        switch (rt) {
+        case 1:
+        case 2: return launch_fused_rt<Q5, 2, PRO, EPI_GLU>(a, s);
+        case 4: return launch_fused_rt<Q5, 4, PRO, EPI_GLU>(a, s);
+        default: return launch_fused_rt<Q5, 8, PRO, EPI_GLU>(a, s);
+        }
+    } else {
+    switch (rt) {
+    case 1: return launch_fused_rt<Q5, 1, PRO, EPI_STORE>(a, s);
+    case 2: return launch_fused_rt<Q5, 2, PRO, EPI_STORE>(a, s);
+    case 4: return launch_fused_rt<Q5, 4, PRO, EPI_STORE>(a, s);
+    default: return launch_fused_rt<Q5, 8, PRO, EPI_STORE>(a, s);
+    }
+    }
+}
+
+template <bool Q5>
+hipError_t launch_fused_typed(const FusedArgs &a, int pro, bool glu, hipStream_t s) {
+    const int rt = gemv_rows_per_tile(a.nb, Q5, 0);
+    if (glu) /* the dense FFN's form: RMSNorm prologue */
+        return pro == PRO_NORM ? launch_fused_pe<Q5, PRO_NORM, EPI_GLU>(a, rt, s) : hipErrorInvalidValue;
+    if (pro == PRO_NORM) return launch_fused_pe<Q5, PRO_NORM, EPI_STORE>(a, rt, s);
+    if (pro == PRO_F32) return launch_fused_pe<Q5, PRO_F32, EPI_STORE>(a, rt, s);
+    return hipErrorInvalidValue; /* a given Q8 activation is smq_matmul's case */
+}
+
+}  // namespace
+
+bool fused_layout_ok(const FusedArgs &a, bool q5, int pro) {
+    if (!a.nb || a.nb > MAX_FAST_NB || (q5 && (a.nb & 1u))) return false;
+    if (a.n > a.nb * QK || a.n + QK <= a.nb * QK) return false;
+    if (pro == 1 && a.n > MAX_NORM_K) return false;
+    if (pro == 0 && (((uintptr_t)a.xq | (uintptr_t)a.xd) & 3u)) return false;
+    for (uint32_t i = 0; i < a.nitems; ++i)
+        if ((((uintptr_t)a.item[i].w) | a.item[i].row_bytes) & 3u) return false;
+    return true;
+}
+
+hipError_t launch_matmul_fused(const FusedArgs &a, bool q5, int pro, bool glu, hipStream_t s) {
+    return q5 ? launch_fused_typed<true>(a, pro, glu, s) : launch_fused_typed<false>(a, pro, glu, s);
+}
+
+}  // namespace smq

@@ -64,6 +64,33 @@ struct GroupArgs {
 bool group_layout_ok(const GroupArgs &g, bool q5);
 hipError_t launch_gemv_grouped(GroupArgs &g, bool q5, bool fast, hipStream_t s);
 
+/* Fused decode GEMV (ntok == 1): the activation formed in the launch
+ * (pro 0: Q8 given in xd/xq; 1: RMSNorm of src with norm/eps, then Q8; 2: Q8
+ * of the f32 row src; n columns), and optionally the gated product of a
+ * gate/up pair (glu: items 0 and 1, `rows` each, h = up * act(gate); act 1
+ * SwiGLU, 2 GeGLU). fused_layout_ok: 4-byte aligned rows, nb <= MAX_FAST_NB,
+ * even nb for Q5, n <= MAX_NORM_K for RMSNorm. The exact contract only (the
+ * fast one takes the unfused calls). */
+constexpr uint32_t MAX_NORM_K = 8192;
+struct FusedArgs {
+    Item item[MAX_ITEMS];
+    uint32_t nitems, nb, n;
+    const float *src, *norm;
+    float eps;
+    const float *xd;
+    const int8_t *xq;
+    float *h;
+    uint32_t rows;
+    int act;
+    int *flag;
+};
+bool fused_layout_ok(const FusedArgs &a, bool q5, int pro);
+/* Rows per decode-GEMV workgroup for nb blocks (smq_kernels.hip). */
+int gemv_rows_per_tile(uint32_t nb, bool q5, uint32_t total_rows);
+hipError_t launch_matmul_fused(const FusedArgs &a, bool q5, int pro, bool glu, hipStream_t s);
+/* h = h * act(gate) elementwise (act 1 SwiGLU, 2 GeGLU). */
+hipError_t launch_glu(float *h, const float *gate, uint32_t n, int act, hipStream_t s);
+
 /* Launchers; each returns the hipError_t of its launch. */
 hipError_t launch_quantize_q8(const float *x, uint32_t rows, uint32_t n, float *d, int8_t *q, int *flag,
                               hipStream_t s);
@@ -93,9 +120,23 @@ hipError_t launch_rope_kv(float *q, float *k, const float *v, uint32_t ntok, con
 hipError_t launch_attention(const float *q, const float *kcache, const float *vcache, float *att, uint32_t ntok,
                             const AttnShape &sh, uint32_t pos0, const int32_t *pos_dev, int *flag, float *xd,
                             int8_t *xq, hipStream_t s);
+/* One decoding token: RoPE of q and k, the cache store of k and v, and
+ * attention (+ Q8 of the row) in one launch; q/k/v are the unrotated QKV
+ * outputs. Needs attention_rows_ok (head_dim 64, 16-byte aligned q and
+ * caches) and 16-byte aligned k, v. */
+bool attention_rows_ok(const AttnShape &sh, const void *q, const void *kcache, const void *vcache);
+hipError_t launch_attention_rope(const float *q, const float *k, const float *v, const float *cs, const float *sn,
+                                 float *kcache, float *vcache, float *att, const AttnShape &sh, uint32_t pos0,
+                                 const int32_t *pos_dev, int *flag, float *xd, int8_t *xq, hipStream_t s);
 hipError_t launch_decode_advance(int32_t *pos, uint32_t *count, const uint32_t *token, uint32_t *history,
                                  uint32_t capacity, hipStream_t s);
-hipError_t launch_argmax(const float *logits, uint32_t n, const unsigned char *banned, uint32_t *out, hipStream_t s);
+/* Greedy argmax in two launches through `parts` (ARGMAX_PART_BYTES *
+ * MAX_ARGMAX_PARTS bytes of device workspace); with count != NULL also the
+ * bookkeeping of one decode step (as launch_decode_advance). */
+constexpr uint32_t MAX_ARGMAX_PARTS = 1024;
+constexpr uint32_t ARGMAX_PART_BYTES = 12;
+hipError_t launch_argmax(const float *logits, uint32_t n, const unsigned char *banned, uint32_t *out, void *parts,
+                         int32_t *pos, uint32_t *count, uint32_t *history, uint32_t capacity, hipStream_t s);
 hipError_t launch_embed(const unsigned char *w, size_t row_bytes, bool q5, uint32_t vocab, const uint32_t *tokens,
                         uint32_t ntok, uint32_t cols, float *out, int *flag, hipStream_t s);
 hipError_t launch_dequantize_row(const unsigned char *w, uint32_t cols, float *out, bool q5, hipStream_t s);

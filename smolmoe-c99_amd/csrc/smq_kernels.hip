@@ -17,82 +17,11 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "smq_device.h"
 #include "smq_internal.h"
 
 namespace smq {
 namespace {
-
-constexpr int WG = 256;
-
-typedef uint32_t u4a __attribute__((ext_vector_type(4), aligned(4)));
-typedef uint32_t u3a __attribute__((ext_vector_type(3), aligned(4)));
-
-/* Exact int32 sum of four int8 products plus c (v_dot4_i32_i8). */
-__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
-    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
-}
-
-/* IEEE binary16 bits to float, exact for every input including subnormals
- * (reference: src/f16.h:10-27): subnormal m * 2^-24 is exact in binary32. */
-__device__ __forceinline__ float half_to_float(uint32_t h) {
-    const uint32_t e = (h >> 10) & 31u, m = h & 1023u, sign = (h & 0x8000u) << 16;
-    if (e == 31u) return __uint_as_float(sign | 0x7f800000u | (m << 13));
-    if (e != 0u) return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
-    return __uint_as_float(__float_as_uint((float)m * 0x1p-24f) | sign);
-}
-
-/* One lane step of the contract: acc + d*f with two roundings, or fmaf. */
-template <bool FAST>
-__device__ __forceinline__ float lane_step(float acc, float d, int s) {
-    const float f = (float)s;
-    if (FAST) return __builtin_fmaf(d, f, acc);
-    const float p = d * f;
-    return acc + p;
-}
-
-/* The fixed lane reduction over eight consecutive threads (lane = tid & 7):
- * thread 0 ends with ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)). IEEE addition is
- * commutative, so the partner's copy of each pair sum is the same bits. */
-__device__ __forceinline__ float reduce8(float a) {
-    const float s = a + __shfl_xor(a, 4, 8);
-    const float t = s + __shfl_xor(s, 2, 8);
-    return t + __shfl_xor(t, 1, 8);
-}
-
-/* Q5 block fields (docs/FORMAT.md:124-134). */
-struct Q5Fields {
-    float scale;
-    uint32_t high;   /* bit j = bit 4 of element j */
-    uint32_t nib[4]; /* byte j: element j low nibble, element j+16 high nibble */
-};
-
-/* A pair of Q5 blocks is 44 bytes = 11 dwords: the first block's fields sit
- * at 2-byte offsets inside the dwords, the second block's are dword aligned. */
-__device__ __forceinline__ void q5_parse_pair(const uint32_t d[11], Q5Fields &b0, Q5Fields &b1) {
-    b0.scale = half_to_float(d[0] & 0xffffu);
-    b0.high = __builtin_amdgcn_alignbit(d[1], d[0], 16);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) b0.nib[k] = __builtin_amdgcn_alignbit(d[k + 2], d[k + 1], 16);
-    b1.scale = half_to_float(d[5] >> 16);
-    b1.high = d[6];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) b1.nib[k] = d[7 + k];
-}
-
-/* Lane l's four 5-bit codes q in [0, 31] as bytes: low nibble | high bit << 4.
- * The high bits 4l..4l+3 are spread to bit 0 of each byte by a multiply
- * (x * 0x204081 moves bit i to bit 8i; the partial products do not overlap). */
-__device__ __forceinline__ uint32_t q5_codes(const Q5Fields &b, int l) {
-    const uint32_t nib = l < 4 ? (b.nib[l] & 0x0f0f0f0fu) : ((b.nib[l - 4] >> 4) & 0x0f0f0f0fu);
-    const uint32_t hb = (b.high >> (4 * l)) & 15u;
-    const uint32_t spread = __umul24(hb, 0x204081u) & 0x01010101u;
-    return nib | (spread << 4);
-}
-
-/* Signed weights q - 16 as int8 bytes: (q + 112) ^ 0x80 per byte, no carries. */
-__device__ __forceinline__ uint32_t q5_signed(const Q5Fields &b, int l) {
-    return (q5_codes(b, l) + 0x70707070u) ^ 0x80808080u;
-}
 
 __device__ __forceinline__ uint32_t find_item(const MatArgs &a, uint32_t tile) {
     uint32_t it = 0;
@@ -100,97 +29,6 @@ __device__ __forceinline__ uint32_t find_item(const MatArgs &a, uint32_t tile) {
     if (a.nitems > 2 && tile >= a.item[2].tile_begin) it = 2;
     if (a.nitems > 3 && tile >= a.item[3].tile_begin) it = 3;
     return it;
-}
-
-__device__ __forceinline__ void store_out(const Item &I, int *flag, uint32_t t, uint32_t r, float v) {
-    if (I.bias) v = v + I.bias[r]; /* model.c:259-262 */
-    if (flag && !(fabsf(v) <= FLT_MAX)) *flag = 1;
-    float *cell = &I.y[(size_t)t * I.y_stride + r];
-    if (I.accumulate) v = *cell + v; /* residual: x += out (model.c:452-455) */
-    *cell = v;
-}
-
-/* DPP row shift by N lanes (row_shr:N): lane i reads lane i-N of its row of 16. */
-template <int N>
-__device__ __forceinline__ float shr_dpp(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x110 + N, 0xf, 0xf, false));
-}
-
-/* The fixed lane reduction with DPP shifts (no LDS round trip). For eight
- * consecutive threads holding lanes a0..a7, thread 4+i first holds
- * a_i + a_{4+i} = s_i; thread 6 then s0 + s2 and thread 7 s1 + s3; thread 7
- * ends with (s0+s2) + (s1+s3). Only thread 7 of each group is meaningful;
- * every add is one the reference makes, with its operands swapped at most. */
-__device__ __forceinline__ float reduce8_to_lane7(float a) {
-    const float s = a + shr_dpp<4>(a);
-    const float t = s + shr_dpp<2>(s);
-    return t + shr_dpp<1>(t);
-}
-
-/* One chain thread's step over `count` (<= 4*NQ) products in block order:
- * float4 p[q*ps] holds blocks 4q..4q+3 (fast mode: their scales in
- * d[q*dst]). Up to eight float4 are read at once before the first add
- * (clamped indices); the adds run in block order: acc = acc + p (exact) or
- * fma(d, p, acc). */
-template <bool FAST, int G>
-__device__ __forceinline__ void chain_read(float4 (&v)[G], float4 (&w)[G], const float4 *p, uint32_t ps,
-                                           const float4 *d, uint32_t dst, uint32_t q0, uint32_t nq) {
-#pragma unroll
-    for (int u = 0; u < G; ++u) {
-        const uint32_t qq = q0 + (uint32_t)u < nq ? q0 + (uint32_t)u : nq - 1;
-        v[u] = p[qq * ps];
-        if (FAST) w[u] = d[qq * dst];
-    }
-}
-template <bool FAST, int G>
-__device__ __forceinline__ void chain_add(float &acc, const float4 (&v)[G], const float4 (&w)[G], uint32_t q0,
-                                          uint32_t count) {
-#pragma unroll
-    for (int u = 0; u < G; ++u) {
-        const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-        const float f[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-            if (4 * (q0 + (uint32_t)u) + (uint32_t)c < count) acc = FAST ? __builtin_fmaf(f[c], e[c], acc) : acc + e[c];
-    }
-}
-template <bool FAST, int NQ>
-__device__ __forceinline__ void chain_sum(float &acc, const float4 *p, uint32_t ps, const float4 *d, uint32_t dst,
-                                          uint32_t count) {
-    const uint32_t nq = (count + 3) / 4;
-    if (NQ <= 8) { /* short rows: every read at once */
-        float4 x[NQ <= 8 ? NQ : 1], xw[NQ <= 8 ? NQ : 1];
-        chain_read<FAST, NQ <= 8 ? NQ : 1>(x, xw, p, ps, d, dst, 0, nq);
-        chain_add<FAST, NQ <= 8 ? NQ : 1>(acc, x, xw, 0, count);
-        return;
-    }
-    /* wide rows (a few chain threads, many blocks): whole float4 first (the
-     * compiler unrolls this loop and batches its reads), then the tail */
-    const uint32_t full = count / 4;
-    uint32_t q = 0;
-    for (; q < full; ++q) {
-        const float4 v = p[q * ps];
-        if (FAST) {
-            const float4 dv = d[q * dst];
-            acc = __builtin_fmaf(dv.x, v.x, acc);
-            acc = __builtin_fmaf(dv.y, v.y, acc);
-            acc = __builtin_fmaf(dv.z, v.z, acc);
-            acc = __builtin_fmaf(dv.w, v.w, acc);
-        } else {
-            acc = acc + v.x;
-            acc = acc + v.y;
-            acc = acc + v.z;
-            acc = acc + v.w;
-        }
-    }
-    const uint32_t rem = count - 4 * full;
-    if (rem) {
-        const float4 v = p[q * ps];
-        const float4 dv = FAST ? d[q * dst] : v;
-        acc = FAST ? __builtin_fmaf(dv.x, v.x, acc) : acc + v.x;
-        if (rem > 1) acc = FAST ? __builtin_fmaf(dv.y, v.y, acc) : acc + v.y;
-        if (rem > 2) acc = FAST ? __builtin_fmaf(dv.z, v.z, acc) : acc + v.z;
-    }
 }
 
 /* ------------------------------------------------------------------------
@@ -1125,58 +963,6 @@ __global__ __launch_bounds__(WG) void k_quantize_q8(const float *x, uint32_t row
     }
 }
 
-/* s = ((0 + a[0]) + a[1]) + ... + a[n-1] in f32, by one lane: the order of
- * the reference's sequential loops (model.c:337, kernels.c:1150). a is
- * 16-byte aligned LDS. Two register batches alternate so that the reads of
- * one batch are in flight while the other is added (the scheduling barriers
- * keep the compiler from sinking the reads below the adds). */
-__device__ __forceinline__ void add_batch(float &s, const float4 (&v)[8]) {
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-        s = s + v[b].x;
-        s = s + v[b].y;
-        s = s + v[b].z;
-        s = s + v[b].w;
-    }
-}
-__device__ __forceinline__ void read_batch(float4 (&v)[8], const float4 *p) {
-#pragma unroll
-    for (int b = 0; b < 8; ++b) v[b] = p[b];
-}
-__device__ __forceinline__ float serial_sum_lds(const float *a, uint32_t n) {
-    const float4 *a4 = (const float4 *)a;
-    const uint32_t batches = n / 32; /* 32 floats = 8 float4 per batch */
-    float s = 0.0f;
-    uint32_t c = 0;
-    if (batches) {
-        float4 x[8], y[8];
-        read_batch(x, a4);
-        for (; c + 2 <= batches; c += 2) {
-            read_batch(y, a4 + 8 * (c + 1));
-            __builtin_amdgcn_sched_barrier(0);
-            add_batch(s, x);
-            read_batch(x, a4 + 8 * (c + 2 < batches ? c + 2 : c + 1)); /* clamped re-read past the end */
-            __builtin_amdgcn_sched_barrier(0);
-            add_batch(s, y);
-        }
-        if (c < batches) {
-            add_batch(s, x);
-            ++c;
-        }
-    }
-    const uint32_t rest = n - c * 32; /* < 32: read together, then added in order */
-    if (rest) {
-        const float *t = a + c * 32;
-        float v[32];
-#pragma unroll
-        for (uint32_t u = 0; u < 32; ++u) v[u] = t[u < rest ? u : rest - 1];
-#pragma unroll
-        for (uint32_t u = 0; u < 32; ++u)
-            if (u < rest) s = s + v[u];
-    }
-    return s;
-}
-
 /* ------------------------------------------------------------------------
  * Activation producers (reference: src/model.c:334-415, src/vecmath.c:61-93).
  * One workgroup of 1024 threads per token row: optional RMSNorm (sequential
@@ -1185,40 +971,6 @@ __device__ __forceinline__ float serial_sum_lds(const float *a, uint32_t n) {
  * exp below, then the Q8 block quantization of kernels.c:912-935, written
  * straight to d/q. Element i lives in thread i % 1024, register i / 1024.
  * ---------------------------------------------------------------------- */
-/* 2^(j/32) correctly rounded to binary64, minus j << 47 (vecmath.c:44-52). */
-__constant__ uint64_t EXP2_TABLE[32] = {
-    0x3ff0000000000000u, 0x3fefd9b0d3158574u, 0x3fefb5586cf9890fu, 0x3fef9301d0125b51u,
-    0x3fef72b83c7d517bu, 0x3fef54873168b9aau, 0x3fef387a6e756238u, 0x3fef1e9df51fdee1u,
-    0x3fef06fe0a31b715u, 0x3feef1a7373aa9cbu, 0x3feedea64c123422u, 0x3feece086061892du,
-    0x3feebfdad5362a27u, 0x3feeb42b569d4f82u, 0x3feeab07dd485429u, 0x3feea47eb03a5585u,
-    0x3feea09e667f3bcdu, 0x3fee9f75e8ec5f74u, 0x3feea11473eb0187u, 0x3feea589994cce13u,
-    0x3feeace5422aa0dbu, 0x3feeb737b0cdc5e5u, 0x3feec49182a3f090u, 0x3feed503b23e255du,
-    0x3feee89f995ad3adu, 0x3feeff76f2fb5e47u, 0x3fef199bdd85529cu, 0x3fef3720dcef9069u,
-    0x3fef5818dcfba487u, 0x3fef7c97337b9b5fu, 0x3fefa4afa2a490dau, 0x3fefd0765b6e4540u,
-};
-
-/* e^x in binary64, rounded once (vecmath.c:61-76): k = round(32x/ln2) from the
- * low bits of z + 1.5*2^52, remainder r, degree-4 Taylor polynomial of
- * e^(r ln2/32) with separate multiplies and adds, times 2^(k/32). */
-__device__ __forceinline__ float exp_det(float x) {
-    const double inv_ln2_n = 0x1.71547652b82fep+5, shift = 0x1.8p+52;
-    const double ea = 0x1.62e42fefa39efp-1 / 32;
-    const double c1 = ea, c2 = ea * ea / 2, c3 = ea * ea * ea / 6, c4 = ea * ea * ea * ea / 24;
-    if (x != x) return x;
-    x = x > 89.0f ? 89.0f : (x < -104.0f ? -104.0f : x);
-    const double z = inv_ln2_n * (double)x;
-    double kd = z + shift;
-    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
-    kd = kd - shift;
-    const double r = z - kd;
-    double p = c4 * r + c3;
-    p = p * r + c2;
-    p = p * r + c1;
-    p = p * r + 1.0;
-    const double scale = __longlong_as_double((long long)(EXP2_TABLE[ki & 31u] + (ki << 47)));
-    return (float)(p * scale);
-}
-
 constexpr int RW_WG = 1024;
 constexpr int RW_EPT = 16; /* elements per thread: rows up to 16384 */
 
@@ -1321,6 +1073,26 @@ __global__ __launch_bounds__(RW_WG) void k_row_quantize(const float *src, const 
             }
         }
     }
+}
+
+/* h[i] = h[i] * (g / (1 + exp_det(-g))) with g = gate[i] (SwiGLU, act 1) or
+ * the GeGLU form (act 2), vecmath.c:78-93: the gated product alone, for
+ * callers that quantize later. */
+__global__ __launch_bounds__(WG) void k_glu(float *h, const float *gate, uint32_t n, int act) {
+    const uint32_t i = blockIdx.x * WG + threadIdx.x;
+    if (i >= n) return;
+    const float gv = gate[i];
+    float e;
+    if (act == 2) {
+        const float g3 = 0.044715f * gv * gv * gv;
+        const float u = 1.5957691216f * (gv + g3);
+        e = exp_det(-u);
+    } else {
+        e = exp_det(-gv);
+    }
+    const float den = 1.0f + e;
+    const float sg = gv / den;
+    h[i] = h[i] * sg;
 }
 
 /* ------------------------------------------------------------------------
@@ -1669,46 +1441,374 @@ __global__ __launch_bounds__(ATT_WG) void k_attend(const float *q, const float *
     }
 }
 
-/* Greedy choice (sampler.c:57-63): the first non-banned id, replaced by any
- * later id with a strictly greater logit. Equivalently: the lowest id of the
- * largest non-NaN logit, unless the first candidate itself is NaN. */
-__global__ __launch_bounds__(1024) void k_argmax(const float *logits, uint32_t n, const unsigned char *banned,
-                                                 uint32_t *out) {
-    __shared__ float bv[1024];
-    __shared__ uint32_t bi[1024], bf[1024];
+/* Attention for head_dim 64 (16-byte aligned caches): the arithmetic of
+ * k_attend, laid out so that a decode step pays one memory round trip before
+ * the two serial sums.
+ *  0. every load is issued first: the K rows of up to AR_KR positions
+ *     (coalesced: 16 threads per row, AR_KU float4 per thread held in
+ *     registers), the first AR_VP value rows of this workgroup's 32
+ *     coordinates, q and the exp table;
+ *  1. scores: the rows pass through LDS AR_KT at a time; one thread per
+ *     position forms the 8-lane dot_f32 of kernels.c:1119-1127 (lane tree,
+ *     times 1/sqrt(hd));
+ *  2. maximum (order-free) and exp_det(s - max) in parallel;
+ *  3. the total in position order by one lane, inv = 1/total;
+ *  4. the products (s_p*inv)*v_p[j] of AR_VP rows at a time to LDS, then lane
+ *     j adds its column in position order while the next rows load.
+ * ROPE (one token, decode): q and this position's k arrive unrotated, as the
+ * QKV matmul left them; the workgroup rotates q and this position's k row
+ * into LDS (model.c:442-450, 511-526), and the first workgroup of each KV
+ * head stores the rotated k and the v row into the caches. The other workgroups read the caches only below
+ * the current position, so no workgroup waits for another. */
+constexpr uint32_t AR_WG = 512;
+constexpr uint32_t AR_HD = 64;                           /* head_dim of this kernel */
+constexpr uint32_t AR_Q4 = AR_HD / 4;                    /* float4 per K row */
+constexpr uint32_t AR_KU = 32;                           /* float4 K loads per thread per round */
+constexpr uint32_t AR_KR = AR_KU * AR_WG / AR_Q4;        /* positions per round: 1024 */
+constexpr uint32_t AR_KT = 256;                          /* K rows per LDS tile */
+constexpr uint32_t AR_KTU = AR_KT * AR_Q4 / AR_WG;       /* float4 loads per thread per tile: 8 */
+constexpr uint32_t AR_KP = AR_HD + 4;                    /* K tile row pitch (floats) */
+constexpr uint32_t AR_VP = 512;                          /* value rows per pass */
+constexpr uint32_t AR_VPP = AR_VP + 4;                   /* products column pitch (floats) */
+constexpr uint32_t AR_VL = AR_VP * ATT_JW / 4 / AR_WG;   /* float4 value loads per thread per pass */
+constexpr uint32_t AR_FIXED = ATT_JW * AR_VPP > AR_KT * AR_KP ? ATT_JW * AR_VPP : AR_KT * AR_KP; /* LDS floats */
+
+struct RopeRows {
+    const float *k, *v;    /* this token's k and v rows (kv_dim each), unrotated */
+    const float *cs, *sn;  /* rotation tables, `pairs` floats per absolute position */
+};
+
+/* Rotation of float4 u of a head row (elements 4u..4u+3 = pairs 2u, 2u+1)
+ * by table row (c, s): x0' = x0*c - x1*s, x1' = x0*s + x1*c (model.c:447-448). */
+__device__ __forceinline__ float4 rope4(float4 x, uint32_t u, uint32_t pairs, const float *c, const float *s) {
+    if (2 * u < pairs) {
+        const float a = x.x, b = x.y, cc = c[2 * u], ss = s[2 * u];
+        const float ac = a * cc, bs = b * ss, as = a * ss, bc = b * cc;
+        x.x = ac - bs;
+        x.y = as + bc;
+    }
+    if (2 * u + 1 < pairs) {
+        const float a = x.z, b = x.w, cc = c[2 * u + 1], ss = s[2 * u + 1];
+        const float ac = a * cc, bs = b * ss, as = a * ss, bc = b * cc;
+        x.z = ac - bs;
+        x.w = as + bc;
+    }
+    return x;
+}
+
+/* K rows p0 + krow + u*(AR_WG/AR_Q4), float4 kcol of each, for the slabs u
+ * that start below np; rows at or past `lim` re-read row 0 (in bounds,
+ * never used). */
+__device__ __forceinline__ void att_rows_keys(f4v (&kr)[AR_KU], const float *kbase, uint32_t kvd, uint32_t p0,
+                                              uint32_t np, uint32_t lim, uint32_t krow, uint32_t kcol) {
+#pragma unroll
+    for (uint32_t u = 0; u < AR_KU; ++u) {
+        const uint32_t p = p0 + krow + u * (AR_WG / AR_Q4);
+        if (p0 + u * (AR_WG / AR_Q4) < np) /* uniform across the workgroup */
+            kr[u] = *(const f4v *)(kbase + (size_t)(p < lim ? p : 0) * kvd + 4 * kcol);
+    }
+}
+
+template <bool ROPE>
+/* 2 waves per SIMD: the round's K rows stay in registers (no spills) */
+__global__ __launch_bounds__(AR_WG) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_attend_rows(const float *q, float *kcache, float *vcache, float *att,
+                                                       AttnShape sh, uint32_t pos0, const int32_t *pos_dev, int *flag,
+                                                       float *xd, int8_t *xq, RopeRows rr) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    __shared__ __attribute__((aligned(16))) float qv[AR_HD];
+    __shared__ uint64_t etab[32];
+    __shared__ float rtab[ROPE ? AR_HD : 1]; /* ROPE: cos then sin of this position (pairs <= 32 each) */
+    __shared__ __attribute__((aligned(16))) float krot[ROPE ? AR_HD : 4]; /* ROPE: this position's rotated k */
+    __shared__ float red[AR_WG / 64];
+    __shared__ float s_inv;
+    constexpr uint32_t ngrp = AR_HD / ATT_JW;
     const uint32_t tid = threadIdx.x;
-    float best = 0.0f;
-    uint32_t besti = UINT32_MAX, first = UINT32_MAX;
-    for (uint32_t i = tid; i < n; i += 1024) {
-        if (banned && banned[i]) continue;
-        if (first == UINT32_MAX) first = i;
-        const float v = logits[i];
-        if (v != v) continue;
-        if (besti == UINT32_MAX || v > best) {
-            best = v;
-            besti = i;
+    const uint32_t g = blockIdx.x % ngrp, th = blockIdx.x / ngrp, t = th / sh.heads, h = th % sh.heads;
+    const uint32_t kh = h / (sh.heads / sh.kv_heads), kvd = sh.kv_dim, j0 = g * ATT_JW;
+    const uint32_t pos = (pos_dev ? (uint32_t)*pos_dev : pos0) + t;
+    if (pos >= sh.context) { /* the scores row holds at most context positions */
+        if (tid == 0 && flag) *flag = 1;
+        return;
+    }
+    const uint32_t start = sh.window && pos >= sh.window ? pos - sh.window + 1 : 0, np = pos - start + 1;
+    const uint32_t last = np - 1; /* ROPE: the current position, taken from rr rather than the caches */
+    float *sc = lds;
+    float *shared = lds + ((sh.context + 3) & ~3u); /* K tiles, then the products [ATT_JW][AR_VPP] */
+    float *prod = shared;
+    float *kt = shared;
+    const float *kbase = kcache + (size_t)start * kvd + (size_t)kh * AR_HD;
+    const float *vbase = vcache + (size_t)start * kvd + (size_t)kh * AR_HD + j0;
+    const float *crow = ROPE ? rtab : nullptr, *srow = ROPE ? rtab + AR_HD / 2 : nullptr;
+    const bool keeper = ROPE && g == 0 && h % (sh.heads / sh.kv_heads) == 0; /* stores this KV head's cache row */
+
+    /* 0. loads: value pass 0, the K rows of round 0, q, the exp table */
+    const uint32_t vrow = tid / (ATT_JW / 4), vcol = (tid % (ATT_JW / 4)) * 4;
+    float4 pre[AR_VL];
+    auto load_values = [&](uint32_t p0) __attribute__((always_inline)) {
+#pragma unroll
+        for (uint32_t u = 0; u < AR_VL; ++u) {
+            const uint32_t p = p0 + vrow + u * (AR_WG * 4 / ATT_JW);
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (p < np)
+                v = *(const float4 *)((ROPE && p == last) ? rr.v + (size_t)kh * AR_HD + j0 + vcol
+                                                          : vbase + (size_t)p * kvd + vcol);
+            pre[u] = v;
+        }
+    };
+    const uint32_t krow = tid / AR_Q4, kcol = tid % AR_Q4; /* load u covers rows krow + u*(AR_WG/AR_Q4) */
+    /* issue order = need order (loads complete in order): q, tables, K, V */
+    const float *qh = q + (size_t)t * sh.q_dim + (size_t)h * AR_HD;
+    float4 qx = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (tid < AR_Q4) qx = *(const float4 *)(qh + 4 * tid);
+    uint64_t ev = 0;
+    if (tid >= 64 && tid < 96) ev = EXP2_TABLE[tid - 64];
+    float rv = 0.0f;
+    const uint32_t ri = tid - 256, rhalf = ri < sh.pairs ? 0 : 1, rj = ri - rhalf * sh.pairs;
+    const bool rload = ROPE && tid >= 256 && tid < 256 + 2 * sh.pairs; /* pairs <= head_dim / 2 */
+    if (rload) rv = (rhalf ? rr.sn : rr.cs)[(size_t)pos * sh.pairs + rj];
+    float4 kx = make_float4(0.0f, 0.0f, 0.0f, 0.0f); /* ROPE: this position's k, float4 tid - 192 */
+    const bool kown = ROPE && tid >= 192 && tid < 192 + AR_Q4;
+    if (kown) kx = *(const float4 *)(rr.k + (size_t)kh * AR_HD + 4 * (tid - 192));
+    f4v kr[AR_KU];
+    att_rows_keys(kr, kbase, kvd, 0, np, ROPE ? last : np, krow, kcol);
+    load_values(0);
+    if (rload) rtab[rhalf * (AR_HD / 2) + rj] = rv;
+    if (ROPE) __syncthreads(); /* the table rows, before q and k are rotated */
+    if (kown) {
+        const uint32_t u = tid - 192;
+        kx = rope4(kx, u, sh.pairs, crow, srow);
+        *(float4 *)&krot[4 * u] = kx;
+        if (keeper) *(float4 *)(kcache + (size_t)pos * kvd + (size_t)kh * AR_HD + 4 * u) = kx;
+    }
+    if (keeper && tid >= 128 && tid < 128 + AR_HD) /* v is stored as is (model.c:520-523) */
+        vcache[(size_t)pos * kvd + (size_t)kh * AR_HD + (tid - 128)] = rr.v[(size_t)kh * AR_HD + (tid - 128)];
+    if (tid < AR_Q4) {
+        if (ROPE) qx = rope4(qx, tid, sh.pairs, crow, srow);
+        *(float4 *)&qv[4 * tid] = qx;
+    }
+    if (tid >= 64 && tid < 96) etab[tid - 64] = ev;
+
+    /* 1. scores */
+    const float factor = 1.0f / sqrtf((float)AR_HD);
+    float high = -FLT_MAX; /* NaN never wins, as in softmax_inv (kernels.c:1146-1148) */
+    for (uint32_t p0 = 0; p0 < np; p0 += AR_KR) {
+        if (p0) {
+            __syncthreads(); /* the previous round's last tile is consumed */
+            att_rows_keys(kr, kbase, kvd, p0, np, ROPE ? last : np, krow, kcol);
+        }
+#pragma unroll
+        for (uint32_t tile = 0; tile < AR_KU / AR_KTU; ++tile) {
+            const uint32_t tb = p0 + tile * AR_KT;
+            if (tb < np) { /* uniform */
+            if (tile || p0) __syncthreads(); /* the previous tile is consumed */
+#pragma unroll
+            for (uint32_t uu = 0; uu < AR_KTU; ++uu) {
+                const uint32_t r = krow + uu * (AR_WG / AR_Q4);
+                if (tb + r < np) *(f4v *)&kt[r * AR_KP + 4 * kcol] = kr[tile * AR_KTU + uu];
+            }
+            __syncthreads();
+            if (tid < AR_KT && tb + tid < np) {
+                const float4 *row = (ROPE && tb + tid == last) ? (const float4 *)krot : (const float4 *)&kt[tid * AR_KP];
+                DotAcc acc = {{0, 0, 0, 0, 0, 0, 0, 0}};
+                dot_groups(acc, row, (const float4 *)qv, 0, AR_HD / 8);
+                const float p04 = acc.a[0] + acc.a[4], p15 = acc.a[1] + acc.a[5], p26 = acc.a[2] + acc.a[6],
+                            p37 = acc.a[3] + acc.a[7];
+                const float e2 = p04 + p26, o2 = p15 + p37;
+                const float sv = (e2 + o2) * factor;
+                sc[tb + tid] = sv;
+                high = sv > high ? sv : high;
+            }
+            }
         }
     }
-    bv[tid] = best;
-    bi[tid] = besti;
-    bf[tid] = first;
+
+    /* 2. maximum, exp */
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(high, off, 64);
+        high = o > high ? o : high;
+    }
+    if ((tid & 63) == 0) red[tid >> 6] = high;
     __syncthreads();
-    for (uint32_t w = 512; w > 0; w >>= 1) {
-        if (tid < w) {
-            const uint32_t oi = bi[tid + w];
-            const float ov = bv[tid + w];
-            if (oi != UINT32_MAX &&
-                (bi[tid] == UINT32_MAX || ov > bv[tid] || (ov == bv[tid] && oi < bi[tid]))) {
-                bv[tid] = ov;
-                bi[tid] = oi;
+    high = red[0];
+#pragma unroll
+    for (uint32_t w = 1; w < AR_WG / 64; ++w) high = red[w] > high ? red[w] : high;
+    for (uint32_t p = tid; p < np; p += AR_WG) sc[p] = exp_det_tab(sc[p] - high, etab);
+    __syncthreads();
+
+    /* 3. the total in position order */
+    if (tid == 0) s_inv = 1.0f / serial_sum_lds(sc, np);
+    __syncthreads();
+    const float inv = s_inv;
+
+    /* 4. weighted values */
+    float o = 0.0f;
+    for (uint32_t p0 = 0; p0 < np; p0 += AR_VP) {
+#pragma unroll
+        for (uint32_t u = 0; u < AR_VL; ++u) { /* kernels.c:1165: w = scores[p] * inv, then w * v[j] */
+            const uint32_t r = vrow + u * (AR_WG * 4 / ATT_JW), p = p0 + r;
+            if (p < np) {
+                const float w = sc[p] * inv;
+                prod[(vcol + 0) * AR_VPP + r] = w * pre[u].x;
+                prod[(vcol + 1) * AR_VPP + r] = w * pre[u].y;
+                prod[(vcol + 2) * AR_VPP + r] = w * pre[u].z;
+                prod[(vcol + 3) * AR_VPP + r] = w * pre[u].w;
             }
-            if (bf[tid + w] < bf[tid]) bf[tid] = bf[tid + w];
+        }
+        __syncthreads();
+        if (p0 + AR_VP < np) load_values(p0 + AR_VP); /* next pass in flight during the sums */
+        if (tid < ATT_JW) {
+            const uint32_t rows = np - p0 < AR_VP ? np - p0 : AR_VP, nbat = rows / 32;
+            const float *colp = prod + tid * AR_VPP;
+            float acc = o;
+            uint32_t c = 0;
+            if (nbat) {
+                float4 x[8], y[8];
+                read_batch(x, (const float4 *)colp);
+                for (; c + 2 <= nbat; c += 2) {
+                    read_batch(y, (const float4 *)colp + 8 * (c + 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                    add_batch(acc, x);
+                    read_batch(x, (const float4 *)colp + 8 * (c + 2 < nbat ? c + 2 : c + 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                    add_batch(acc, y);
+                }
+                if (c < nbat) {
+                    add_batch(acc, x);
+                    ++c;
+                }
+            }
+            const uint32_t rest = rows - c * 32;
+            if (rest) {
+                const float *tl = colp + c * 32;
+                float v[32];
+#pragma unroll
+                for (uint32_t u = 0; u < 32; ++u) v[u] = tl[u < rest ? u : rest - 1];
+#pragma unroll
+                for (uint32_t u = 0; u < 32; ++u)
+                    if (u < rest) acc = acc + v[u];
+            }
+            o = acc;
         }
         __syncthreads();
     }
+    if (tid < ATT_JW) { /* this workgroup's 32 coordinates are one block (kernels.c:912-935) */
+        att[(size_t)t * sh.q_dim + (size_t)h * AR_HD + j0 + tid] = o;
+        if (xd) {
+            const float av = fabsf(o);
+            float mx = av;
+            int bad = !(av <= FLT_MAX);
+#pragma unroll
+            for (int off = 16; off >= 1; off >>= 1) {
+                const float ot = __shfl_xor(mx, off, 32);
+                mx = ot > mx ? ot : mx;
+                bad |= __shfl_xor(bad, off, 32);
+            }
+            const float scale = mx / 127.0f;
+            const float qinv = scale >= FLT_MIN ? 1.0f / scale : 0.0f;
+            const uint32_t nbq = sh.q_dim / QK, blk = (h * AR_HD + j0) / QK;
+            const float pq = o * qinv;
+            int qi = (int)__builtin_rintf(pq);
+            qi = qi > 127 ? 127 : (qi < -127 ? -127 : qi);
+            xq[((size_t)t * nbq + blk) * QK + tid] = (int8_t)qi;
+            if (tid == 0) {
+                xd[(size_t)t * nbq + blk] = scale;
+                if (bad && flag) *flag = 1;
+            }
+        }
+    }
+}
+
+/* Greedy choice (sampler.c:57-63): the first non-banned id, replaced by any
+ * later id with a strictly greater logit. Equivalently: the lowest id of the
+ * largest non-NaN logit, unless the first candidate itself is NaN (then that
+ * candidate: nothing compares greater than NaN). Two stages: AM_WG-thread
+ * workgroups each reduce one contiguous span of ids to (largest non-NaN
+ * logit, its lowest id, lowest non-banned id); one workgroup merges the
+ * partials in any order (the merge is order-free: max with ties to the lower
+ * id, min of first) and applies the NaN rule. */
+constexpr uint32_t AM_WG = 256, AM_LOADS = 4, AM_SPAN = AM_WG * AM_LOADS, AM_FINAL_WG = 1024;
+
+struct ArgBest {
+    float v;
+    uint32_t i, first; /* UINT32_MAX: none */
+};
+static_assert(sizeof(ArgBest) == ARGMAX_PART_BYTES, "argmax partial layout");
+
+__device__ __forceinline__ void am_merge(ArgBest &a, float ov, uint32_t oi, uint32_t of) {
+    if (oi != UINT32_MAX && (a.i == UINT32_MAX || ov > a.v || (ov == a.v && oi < a.i))) {
+        a.v = ov;
+        a.i = oi;
+    }
+    a.first = of < a.first ? of : a.first;
+}
+
+/* Workgroup-wide merge; the result is valid in thread 0. */
+template <uint32_t NT>
+__device__ __forceinline__ ArgBest am_reduce(ArgBest a, ArgBest *red) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+        am_merge(a, __shfl_xor(a.v, off, 64), __shfl_xor(a.i, off, 64), __shfl_xor(a.first, off, 64));
+    const uint32_t tid = threadIdx.x;
+    if ((tid & 63) == 0) red[tid >> 6] = a;
+    __syncthreads();
+    if (tid == 0)
+        for (uint32_t w = 1; w < NT / 64; ++w) am_merge(a, red[w].v, red[w].i, red[w].first);
+    return a;
+}
+
+/* Stage 1: workgroup w covers ids [w*span, (w+1)*span), AM_SPAN at a time,
+ * every load of a pass issued before the first compare. */
+__global__ __launch_bounds__(AM_WG) void k_argmax_part(const float *logits, uint32_t n, uint32_t span,
+                                                       const unsigned char *banned, ArgBest *part) {
+    __shared__ ArgBest red[AM_WG / 64];
+    const uint32_t tid = threadIdx.x, i0 = blockIdx.x * span, i1 = n - i0 < span ? n : i0 + span;
+    ArgBest a = {0.0f, UINT32_MAX, UINT32_MAX};
+    for (uint32_t base = i0; base < i1; base += AM_SPAN) {
+        float v[AM_LOADS];
+        unsigned char bn[AM_LOADS];
+#pragma unroll
+        for (uint32_t k = 0; k < AM_LOADS; ++k) {
+            const uint32_t i = base + tid + k * AM_WG, ii = i < i1 ? i : i1 - 1;
+            v[k] = logits[ii];
+            bn[k] = banned ? banned[ii] : 0;
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < AM_LOADS; ++k) { /* ids rise with k: the first hit is this thread's lowest */
+            const uint32_t i = base + tid + k * AM_WG;
+            if (i >= i1 || bn[k]) continue;
+            a.first = i < a.first ? i : a.first;
+            if (v[k] != v[k]) continue;
+            if (a.i == UINT32_MAX || v[k] > a.v) {
+                a.v = v[k];
+                a.i = i;
+            }
+        }
+    }
+    a = am_reduce<AM_WG>(a, red);
+    if (tid == 0) part[blockIdx.x] = a;
+}
+
+/* Stage 2: merge the partials; optionally the decode bookkeeping of one
+ * step (history[*count] = token, ++*count, ++*pos). */
+__global__ __launch_bounds__(AM_FINAL_WG) void k_argmax_final(const float *logits, const ArgBest *part, uint32_t np,
+                                                              uint32_t *out, int32_t *pos, uint32_t *count,
+                                                              uint32_t *history, uint32_t capacity) {
+    __shared__ ArgBest red[AM_FINAL_WG / 64];
+    const uint32_t tid = threadIdx.x;
+    ArgBest a = {0.0f, UINT32_MAX, UINT32_MAX};
+    for (uint32_t p = tid; p < np; p += AM_FINAL_WG) am_merge(a, part[p].v, part[p].i, part[p].first);
+    a = am_reduce<AM_FINAL_WG>(a, red);
     if (tid == 0) {
-        const uint32_t f = bf[0];
-        *out = (f != UINT32_MAX && logits[f] != logits[f]) ? f : bi[0];
+        const uint32_t f = a.first;
+        const uint32_t tok = (f != UINT32_MAX && logits[f] != logits[f]) ? f : a.i;
+        *out = tok;
+        if (count) {
+            const uint32_t c = *count;
+            if (c < capacity) history[c] = tok;
+            *count = c + 1;
+            *pos = *pos + 1;
+        }
     }
 }
 
@@ -1806,22 +1906,6 @@ hipError_t launch_gemv_stage(MatArgs a, int rt, hipStream_t s) {
     case 8: return launch_gemv_rt<Q5, FAST, 8, STAGE>(a, s);
     default: return launch_gemv_rt<Q5, FAST, 16, STAGE>(a, s);
     }
-}
-
-/* Rows per workgroup: the largest power of two (<= 8) whose chunk of 256
- * tasks covers all nb blocks, so each workgroup needs one round of loads
- * (Q5 keeps at least 2 rows: its wide rows run faster as two chunks of two
- * rows than as one chunk of one). Measured on MI355X over rotated weights:
- * 9728x896 Q8 4.7 us at 8 rows, 896x4864 Q8 4.6 us at 1 row, 1536x8960 Q5
- * 7.4 us at 2 rows (9.9 us at 1). SMQ_GEMV_RT / SMQ_GEMV_STAGE override. */
-int gemv_rows_per_tile(uint32_t nb, bool q5, uint32_t total_rows) {
-    (void)total_rows;
-    const char *env = getenv("SMQ_GEMV_RT");
-    if (env && *env) return atoi(env);
-    const uint32_t cover = (q5 ? 512u : 256u) / nb;
-    int rt = q5 ? 2 : 1;
-    while (rt < 8 && (uint32_t)(rt * 2) <= cover) rt *= 2;
-    return rt;
 }
 
 /* Single launches of many tiles (the LM head: 18992 tiles of 8 rows) run on
@@ -1980,6 +2064,22 @@ hipError_t launch_mfma_typed(MatArgs a, int32_t *sums, hipStream_t s) {
 
 }  // namespace
 
+/* Rows per workgroup: the largest power of two (<= 8) whose chunk of 256
+ * tasks covers all nb blocks, so each workgroup needs one round of loads
+ * (Q5 keeps at least 2 rows: its wide rows run faster as two chunks of two
+ * rows than as one chunk of one). Measured on MI355X over rotated weights:
+ * 9728x896 Q8 4.7 us at 8 rows, 896x4864 Q8 4.6 us at 1 row, 1536x8960 Q5
+ * 7.4 us at 2 rows (9.9 us at 1). SMQ_GEMV_RT / SMQ_GEMV_STAGE override. */
+int gemv_rows_per_tile(uint32_t nb, bool q5, uint32_t total_rows) {
+    (void)total_rows;
+    const char *env = getenv("SMQ_GEMV_RT");
+    if (env && *env) return atoi(env);
+    const uint32_t cover = (q5 ? 512u : 256u) / nb;
+    int rt = q5 ? 2 : 1;
+    while (rt < 8 && (uint32_t)(rt * 2) <= cover) rt *= 2;
+    return rt;
+}
+
 bool mfma_layout_ok(const MatArgs &a, bool q5) {
     if (a.nb == 0) return false;
     if (((uintptr_t)a.xq | (uintptr_t)a.xd) & 3u) return false;
@@ -1992,6 +2092,12 @@ bool mfma_layout_ok(const MatArgs &a, bool q5) {
 hipError_t launch_matmul_mfma(const MatArgs &a, bool q5, int32_t *sums, hipStream_t s) {
     if (sums) return q5 ? launch_mfma_typed<true, true>(a, sums, s) : launch_mfma_typed<false, true>(a, sums, s);
     return q5 ? launch_mfma_typed<true, false>(a, nullptr, s) : launch_mfma_typed<false, false>(a, nullptr, s);
+}
+
+hipError_t launch_glu(float *h, const float *gate, uint32_t n, int act, hipStream_t s) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(k_glu, dim3((n + WG - 1) / WG), dim3(WG), 0, s, h, gate, n, act);
+    return hipGetLastError();
 }
 
 hipError_t launch_matmul(const MatArgs &a, bool q5, bool fast, hipStream_t s) {
@@ -2055,6 +2161,11 @@ hipError_t launch_rope_kv(float *q, float *k, const float *v, uint32_t ntok, con
     return hipGetLastError();
 }
 
+bool attention_rows_ok(const AttnShape &sh, const void *q, const void *kcache, const void *vcache) {
+    return sh.head_dim == AR_HD && ((uintptr_t)q & 15) == 0 && ((uintptr_t)kcache & 15) == 0 &&
+           ((uintptr_t)vcache & 15) == 0;
+}
+
 hipError_t launch_attention(const float *q, const float *kcache, const float *vcache, float *att, uint32_t ntok,
                             const AttnShape &sh, uint32_t pos0, const int32_t *pos_dev, int *flag, float *xd,
                             int8_t *xq, hipStream_t s) {
@@ -2062,6 +2173,22 @@ hipError_t launch_attention(const float *q, const float *kcache, const float *vc
     if (sh.context > MAX_ATT_POSITIONS || sh.head_dim > MAX_HEAD_DIM || sh.head_dim < 1 ||
         (xd && sh.head_dim % QK))
         return hipErrorInvalidValue;
+    const uint32_t groups = (sh.head_dim + ATT_JW - 1) / ATT_JW;
+    if (attention_rows_ok(sh, q, kcache, vcache)) {
+        const size_t lds = (((size_t)sh.context + 3) / 4 * 4 + (size_t)AR_FIXED) * sizeof(float);
+        static bool raised_rows = false;
+        if (!raised_rows) { /* dynamic LDS beyond the 64 KiB default for long contexts */
+            const hipError_t e = hipFuncSetAttribute((const void *)k_attend_rows<false>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     (int)(((size_t)MAX_ATT_POSITIONS + AR_FIXED) * sizeof(float)));
+            if (e != hipSuccess) return e;
+            raised_rows = true;
+        }
+        RopeRows none = {nullptr, nullptr, nullptr, nullptr};
+        hipLaunchKernelGGL(k_attend_rows<false>, dim3(ntok * sh.heads * groups), dim3(AR_WG), lds, s, q,
+                           (float *)kcache, (float *)vcache, att, sh, pos0, pos_dev, flag, xd, xq, none);
+        return hipGetLastError();
+    }
     const size_t lds = (((size_t)sh.context + 3) / 4 * 4 + (size_t)ATT_SHARED) * sizeof(float);
     static bool raised = false;
     if (!raised) { /* dynamic LDS beyond the 64 KiB default for long contexts */
@@ -2070,14 +2197,41 @@ hipError_t launch_attention(const float *q, const float *kcache, const float *vc
         if (e != hipSuccess) return e;
         raised = true;
     }
-    const uint32_t groups = (sh.head_dim + ATT_JW - 1) / ATT_JW;
     hipLaunchKernelGGL(k_attend, dim3(ntok * sh.heads * groups), dim3(ATT_WG), lds, s, q, kcache, vcache, att, sh, pos0,
                        pos_dev, flag, xd, xq);
     return hipGetLastError();
 }
 
-hipError_t launch_argmax(const float *logits, uint32_t n, const unsigned char *banned, uint32_t *out, hipStream_t s) {
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, logits, n, banned, out);
+hipError_t launch_attention_rope(const float *q, const float *k, const float *v, const float *cs, const float *sn,
+                                 float *kcache, float *vcache, float *att, const AttnShape &sh, uint32_t pos0,
+                                 const int32_t *pos_dev, int *flag, float *xd, int8_t *xq, hipStream_t s) {
+    if (sh.context > MAX_ATT_POSITIONS || !attention_rows_ok(sh, q, kcache, vcache) ||
+        ((uintptr_t)k & 15) || ((uintptr_t)v & 15))
+        return hipErrorInvalidValue;
+    const uint32_t groups = (sh.head_dim + ATT_JW - 1) / ATT_JW;
+    const size_t lds = (((size_t)sh.context + 3) / 4 * 4 + (size_t)AR_FIXED) * sizeof(float);
+    static bool raised = false;
+    if (!raised) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_attend_rows<true>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)(((size_t)MAX_ATT_POSITIONS + AR_FIXED) * sizeof(float)));
+        if (e != hipSuccess) return e;
+        raised = true;
+    }
+    RopeRows rr = {k, v, cs, sn};
+    hipLaunchKernelGGL(k_attend_rows<true>, dim3(sh.heads * groups), dim3(AR_WG), lds, s, q, kcache, vcache, att, sh,
+                       pos0, pos_dev, flag, xd, xq, rr);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float *logits, uint32_t n, const unsigned char *banned, uint32_t *out, void *parts,
+                         int32_t *pos, uint32_t *count, uint32_t *history, uint32_t capacity, hipStream_t s) {
+    /* span: a multiple of AM_SPAN, large enough for at most MAX_ARGMAX_PARTS workgroups */
+    const uint32_t span = ((n + MAX_ARGMAX_PARTS - 1) / MAX_ARGMAX_PARTS + AM_SPAN - 1) / AM_SPAN * AM_SPAN;
+    const uint32_t np = (n + span - 1) / span;
+    hipLaunchKernelGGL(k_argmax_part, dim3(np), dim3(AM_WG), 0, s, logits, n, span, banned, (ArgBest *)parts);
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(AM_FINAL_WG), 0, s, logits, (const ArgBest *)parts, np, out, pos,
+                       count, history, capacity);
     return hipGetLastError();
 }
 

@@ -832,19 +832,45 @@ static smq_mat_item mat(const smq_qmat *w, const float *bias, float *y, int accu
     return it;
 }
 
+/* The RMSNorm activation of one token's row x (model.c:334-342), formed by
+ * the consuming matmul itself; xd/xq are the fallback's scratch. */
+static smq_act norm_act(smq_model *m, const float *x, const float *weight) {
+    smq_act a;
+    memset(&a, 0, sizeof(a));
+    a.kind = SMQ_ACT_NORM;
+    a.cols = m->c.dim;
+    a.x = x;
+    a.norm = weight;
+    a.eps = m->c.eps;
+    a.xd_scratch = m->xd;
+    a.xq_scratch = m->xq;
+    return a;
+}
+
 /* attention_block (model.c:496-542) for one layer. */
 static smq_status attention_block(smq_model *m, uint32_t l, uint32_t n, uint32_t pos0, const int32_t *pos_dev) {
     const Layer *L = &m->layers[l];
     const size_t base = (size_t)l * m->context * m->kv_dim;
     smq_mat_item qkv[3];
-    TRY(smq_norm_quantize(m->x, L->attn_norm, m->c.eps, n, m->c.dim, NULL, m->xd, m->xq));
     qkv[0] = mat(&L->q, L->q_bias, m->q, 0);
     qkv[1] = mat(&L->k, L->k_bias, m->k, 0);
     qkv[2] = mat(&L->v, L->v_bias, m->v, 0);
-    TRY(smq_matmul(qkv, 3, m->xd, m->xq, n));
-    TRY(smq_rope_kv(m->q, m->k, m->v, n, &m->shape, m->rope_cos, m->rope_sin, m->keys + base, m->values + base, pos0,
-                    pos_dev));
-    TRY(smq_attention_q8(m->q, m->keys + base, m->values + base, m->att, n, &m->shape, pos0, pos_dev, m->xd, m->xq));
+    if (n == 1) { /* decode: the RMSNorm and its Q8 blocks inside the QKV launch */
+        smq_act act = norm_act(m, m->x, L->attn_norm);
+        TRY(smq_matmul_act(qkv, 3, &act));
+    } else {
+        TRY(smq_norm_quantize(m->x, L->attn_norm, m->c.eps, n, m->c.dim, NULL, m->xd, m->xq));
+        TRY(smq_matmul(qkv, 3, m->xd, m->xq, n));
+    }
+    if (n == 1) { /* decode: rotation, cache store and attention in one launch */
+        TRY(smq_attention_rope_q8(m->q, m->k, m->v, &m->shape, m->rope_cos, m->rope_sin, m->keys + base,
+                                  m->values + base, m->att, pos0, pos_dev, m->xd, m->xq));
+    } else {
+        TRY(smq_rope_kv(m->q, m->k, m->v, n, &m->shape, m->rope_cos, m->rope_sin, m->keys + base, m->values + base,
+                        pos0, pos_dev));
+        TRY(smq_attention_q8(m->q, m->keys + base, m->values + base, m->att, n, &m->shape, pos0, pos_dev, m->xd,
+                             m->xq));
+    }
     qkv[0] = mat(&L->o, NULL, m->x, 1); /* x += o(att) */
     return smq_matmul(qkv, 1, m->xd, m->xq, n);
 }
@@ -853,6 +879,18 @@ static smq_status attention_block(smq_model *m, uint32_t l, uint32_t n, uint32_t
 static smq_status ffn_block(smq_model *m, uint32_t l, uint32_t n) {
     const Layer *L = &m->layers[l];
     smq_mat_item it[2];
+    if (n == 1) { /* decode: RMSNorm in the gate/up launch, SwiGLU in its store, Q8 of h in the down launch */
+        smq_act act = norm_act(m, m->x, L->ffn_norm);
+        TRY(smq_matmul_glu(&L->gate, &L->up, &act, 1, m->up, m->gate));
+        act.kind = SMQ_ACT_F32;
+        act.cols = m->c.hidden;
+        act.x = m->up;
+        act.norm = NULL;
+        act.xd_scratch = m->hd;
+        act.xq_scratch = m->hq;
+        it[0] = mat(&L->down, NULL, m->x, 1); /* x += down(act) */
+        return smq_matmul_act(it, 1, &act);
+    }
     TRY(smq_norm_quantize(m->x, L->ffn_norm, m->c.eps, n, m->c.dim, NULL, m->xd, m->xq));
     it[0] = mat(&L->gate, NULL, m->gate, 0);
     it[1] = mat(&L->up, NULL, m->up, 0);
@@ -933,8 +971,7 @@ smq_status smq_model_set_banned(smq_model *m, const unsigned char *banned) {
  * into *token, then history[*count++] = *token and ++*pos. */
 static smq_status enqueue_step(smq_model *m) {
     TRY(enqueue_forward(m, m->token, 1, 0, m->pos, SMQ_LOGITS_LAST));
-    TRY(smq_argmax(m->logits, m->c.vocab, m->banned, m->token));
-    return smq_decode_advance(m->pos, m->count, m->token, m->history, m->context);
+    return smq_argmax_advance(m->logits, m->c.vocab, m->banned, m->token, m->pos, m->count, m->history, m->context);
 }
 
 smq_status smq_model_generate(smq_model *m, uint32_t pos, uint32_t ntokens, uint32_t *out) {

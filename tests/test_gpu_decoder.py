@@ -138,6 +138,49 @@ def test_attention_q8(orc, heads, kv_heads, hd, window, context, ntok, pos0):
     assert np.array_equal(xq.download(np.int8).reshape(ntok, nb * 32), wq.reshape(ntok, nb * 32))
 
 
+@pytest.mark.parametrize("heads,kv_heads,hd,pairs,window,context,pos,use_pos_dev", [
+    (14, 2, 64, 32, 0, 1024, 700, True),   # Qwen2.5-0.5B decode step: one launch
+    (14, 2, 64, 32, 0, 1024, 700, False),
+    (14, 2, 64, 32, 0, 64, 0, True),       # first position: the score row is the new key alone
+    (4, 2, 64, 12, 9, 64, 30, False),      # partial rotary, sliding window
+    (2, 1, 64, 32, 0, 2048, 1500, True),   # several score rounds and value passes
+    (3, 1, 40, 20, 0, 64, 20, False),      # head_dim % 32 != 0: the two-call form
+    (4, 2, 128, 64, 0, 300, 250, True),    # head_dim 128: the two-call form
+])
+def test_attention_rope_q8(orc, heads, kv_heads, hd, pairs, window, context, pos, use_pos_dev):
+    """smq_attention_rope_q8 == smq_rope_kv then smq_attention_q8 (oracle): the
+    attention row, its Q8 blocks and both caches, bit for bit."""
+    say("attention_rope_q8", heads, kv_heads, hd, pairs, window, context, pos, use_pos_dev)
+    qd, kd = heads * hd, kv_heads * hd
+    nb = (qd + 31) // 32
+    q = synth.normal(81, qd)
+    k = synth.normal(82, kd)
+    v = synth.normal(83, kd)
+    cs = synth.normal(84, context * pairs).reshape(context, pairs)
+    sn = synth.normal(85, context * pairs).reshape(context, pairs)
+    keys0 = synth.normal(86, context * kd).reshape(context, kd)
+    values0 = synth.normal(87, context * kd).reshape(context, kd)
+    qb, kb, vb, cb, sb = dev(q), dev(k), dev(v), dev(cs), dev(sn)
+    keys, values = dev(keys0), dev(values0)
+    att = smq.DeviceBuffer(qd * 4)
+    xd, xq = smq.DeviceBuffer(nb * 4), smq.DeviceBuffer(nb * 32)
+    shape = smq.attn_shape(heads, kv_heads, hd, pairs, window, context)
+    pos_dev = dev(np.array([pos], np.int32)) if use_pos_dev else None
+    smq.attention_rope_q8(qb, kb, vb, shape, cb, sb, keys, values, att, xd, xq, 0 if use_pos_dev else pos, pos_dev)
+    smq.numeric_check()
+    want_q = orc.rope(q, heads, hd, pairs, cs[pos], sn[pos])
+    want_k = orc.rope(k, kv_heads, hd, pairs, cs[pos], sn[pos])
+    want_keys, want_values = keys0.copy(), values0.copy()
+    want_keys[pos], want_values[pos] = want_k, v
+    assert_same_f32(keys.download(np.float32).reshape(context, kd), want_keys, "keys")
+    assert_same_f32(values.download(np.float32).reshape(context, kd), want_values, "values")
+    want = attend_expect(orc, want_q.reshape(1, qd), want_keys, want_values, heads, kv_heads, hd, window, pos, 1)
+    assert_same_f32(att.download(np.float32).reshape(1, qd), want, "att")
+    _, wd, wq = orc.quantize_q8(want)
+    assert_same_f32(xd.download(np.float32).reshape(1, nb), wd.reshape(1, nb), "att scales")
+    assert np.array_equal(xq.download(np.int8).reshape(1, nb * 32), wq.reshape(1, nb * 32))
+
+
 def test_attention_position_from_device(orc):
     heads, kv_heads, hd, context = 14, 2, 64, 128
     qd, kd = heads * hd, kv_heads * hd
@@ -195,6 +238,48 @@ def test_argmax(orc):
     assert gpu_argmax(n, b0) == orc.argmax(n, b0)
     # every id banned
     assert gpu_argmax(logits[:64], np.ones(64, np.uint8)) == 0xFFFFFFFF
+
+
+def test_argmax_partials(orc):
+    """The two-stage argmax across workgroup spans: ties and the NaN rule
+    where the deciding ids sit in different spans, and vocabularies large
+    enough that each workgroup walks several passes."""
+    for vocab in (1, 1023, 1025, 151936, 3 * 1024 * 1024 + 17):
+        logits = synth.normal(43 + vocab % 97, vocab)
+        say("argmax vocab", vocab)
+        assert gpu_argmax(logits) == orc.argmax(logits)
+        if vocab < 4096:
+            continue
+        t = logits.copy()
+        top = t.max() + 1
+        t[[vocab - 1, vocab // 2, 2048 + 5]] = top  # equal maxima in three spans: the lowest id wins
+        assert gpu_argmax(t) == orc.argmax(t) == 2048 + 5
+        b = np.zeros(vocab, np.uint8)
+        b[:3000] = 1  # first candidate deep in a later span, and NaN
+        t[3000] = np.nan
+        assert gpu_argmax(t, b) == orc.argmax(t, b) == 3000
+        t[3000] = -np.inf  # a finite maximum elsewhere wins over -inf
+        assert gpu_argmax(t, b) == orc.argmax(t, b) == vocab // 2
+
+
+def test_argmax_advance(orc):
+    vocab = 151936
+    pos = dev(np.array([100], np.int32))
+    count = dev(np.array([1], np.uint32))
+    hist = dev(np.full(4, 7, np.uint32))
+    tok = smq.DeviceBuffer(4)
+    want = []
+    for i in range(5):
+        logits = synth.normal(70 + i, vocab)
+        banned = np.zeros(vocab, np.uint8)
+        banned[256] = 1
+        smq.argmax_advance(dev(logits), vocab, dev(banned), tok, pos, count, hist, 4)
+        smq.synchronize()
+        want.append(orc.argmax(logits, banned))
+        assert int(tok.download(np.uint32)[0]) == want[-1]
+    assert int(pos.download(np.int32)[0]) == 105
+    assert int(count.download(np.uint32)[0]) == 6
+    assert hist.download(np.uint32).tolist() == [7] + want[:3]  # capacity bounds the history
 
 
 @pytest.mark.parametrize("q5", [False, True])

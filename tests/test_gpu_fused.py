@@ -1,0 +1,193 @@
+"""GPU parity of the fused decode matmuls (smq_matmul_act, smq_matmul_glu):
+the activation producers of the reference's decode step (model.c:334-415,
+vecmath.c:78-93) formed inside the matmul launch, against the CPU oracle's
+row_work + mat_item composition and against the library's own unfused calls,
+bit for bit. Shapes cover the fused kernel's tile sizes (1, 2, 4 and 8 rows
+per workgroup), partial blocks, Q5 weights, bias and the residual add, the
+widest fused RMSNorm row and the fallbacks (wider rows, mixed formats)."""
+import numpy as np
+import pytest
+
+from checks import assert_same_f32, say
+from smq_pkg import smq, synth
+
+pytestmark = pytest.mark.gpu
+
+Q8, Q5 = 1, 2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    assert smq.init(0) == "gfx950"
+    smq.kernels_set_fast(False)
+    smq.kernels_select()
+    yield
+
+
+def dev(a):
+    return smq.DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+def weights(seed, rows, cols, dtype):
+    return synth.q5_weights(seed, rows, cols) if dtype == Q5 else synth.q8_weights(seed, rows, cols)
+
+
+def row_bytes(cols, dtype):
+    return (cols + 31) // 32 * (22 if dtype == Q5 else 36)
+
+
+def expect_items(orc, mats, d, q, cols):
+    """mat_item (bias, finiteness) of each (w, rows, dtype, bias, prior) on (d, q)."""
+    nb = (cols + 31) // 32
+    out = []
+    for w, rows, dtype, bias, prior in mats:
+        ok, y = orc.mat_item(w.reshape(-1), row_bytes(cols, dtype), rows, bias, d, q, 1, nb, q5=dtype == Q5)
+        assert ok
+        out.append(y if prior is None else prior + y)
+    return out
+
+
+@pytest.mark.parametrize("cols,rows,dtypes,with_bias,accumulate", [
+    (896, [896, 128, 128], [Q8, Q8, Q8], True, False),    # Qwen2.5-0.5B q/k/v: 8 rows per workgroup
+    (896, [896], [Q8], False, True),                      # an accumulating item (x += W a)
+    (200, [77, 300], [Q8, Q8], True, False),              # partial block, ragged rows
+    (1536, [1536, 256, 256], [Q8, Q8, Q8], True, False),  # 4 rows per workgroup
+    (4864, [896], [Q8], False, True),                     # 1 row per workgroup, one chunk
+    (8192, [64], [Q8], False, False),                     # the widest fused RMSNorm row (LDS past 64 KiB)
+    (8200, [40], [Q8], False, False),                     # wider: the unfused fallback
+    (896, [512, 128], [Q5, Q8], True, False),             # mixed formats: one fused launch per format
+    (1536, [300], [Q5], False, True),                     # Q5: 2 rows per workgroup
+])
+def test_matmul_act_norm(orc, cols, rows, dtypes, with_bias, accumulate):
+    say("matmul_act norm", cols, rows, dtypes, with_bias, accumulate)
+    nb = (cols + 31) // 32
+    x = synth.normal(501 + cols, cols)
+    w = synth.normal(502 + cols, cols, 0.2) + 1.0
+    eps = 1e-6
+    ok, _, d, q = orc.row_work(x, 1, cols, norm=w, eps=eps)
+    assert ok
+    mats, items = [], []
+    for i, (r, dt) in enumerate(zip(rows, dtypes)):
+        wt = weights(510 + i, r, cols, dt)
+        bias = synth.normal(520 + i, r, 0.02) if with_bias else None
+        prior = synth.normal(530 + i, r) if accumulate else None
+        y = dev(prior) if accumulate else smq.DeviceBuffer(r * 4)
+        mats.append((wt, r, dt, bias, prior))
+        items.append((smq.QMat(dev(wt), r, cols, dt), dev(bias) if with_bias else None, y, accumulate))
+    xd_s, xq_s = smq.DeviceBuffer(nb * 4), smq.DeviceBuffer(nb * 32)
+    smq.matmul_act(items, smq.act(smq.ACT_NORM, cols, x=dev(x), norm=dev(w), eps=eps, xd_scratch=xd_s,
+                                  xq_scratch=xq_s))
+    smq.numeric_check()
+    for (m, it, want) in zip(mats, items, expect_items(orc, mats, d, q, cols)):
+        assert_same_f32(it[2].download(np.float32), want, f"item rows {m[1]}")
+
+
+@pytest.mark.parametrize("cols,rows,dtype", [(4864, 896, Q8), (896, 1000, Q8), (8960, 300, Q5), (100, 50, Q8)])
+def test_matmul_act_f32(orc, cols, rows, dtype):
+    """Q8 of an f32 row inside the launch (the down projection's input)."""
+    say("matmul_act f32", cols, rows, dtype)
+    nb = (cols + 31) // 32
+    h = synth.normal(601 + cols, cols, 3.0)
+    ok, _, d, q = orc.row_work(h, 1, cols)
+    assert ok
+    wt = weights(602, rows, cols, dtype)
+    prior = synth.normal(603, rows)
+    y = dev(prior)
+    item = (smq.QMat(dev(wt), rows, cols, dtype), None, y, True)
+    smq.matmul_act([item], smq.act(smq.ACT_F32, cols, x=dev(h), xd_scratch=smq.DeviceBuffer(nb * 4),
+                                   xq_scratch=smq.DeviceBuffer(nb * 32)))
+    smq.numeric_check()
+    want = expect_items(orc, [(wt, rows, dtype, None, prior)], d, q, cols)[0]
+    assert_same_f32(y.download(np.float32), want, "x + W q8(h)")
+
+
+@pytest.mark.parametrize("cols,rows,dtype,gate_dtype", [
+    (896, 4864, Q8, Q8),    # Qwen2.5-0.5B gate/up: 4 + 4 rows per workgroup
+    (1536, 8960, Q5, Q5),   # 1.5B-shaped Q5: 1 + 1 rows per workgroup, two chunks
+    (2048, 130, Q8, Q8),    # 2 + 2 rows per workgroup, ragged last tile
+    (896, 200, Q8, Q5),     # mixed formats: the unfused fallback
+])
+def test_matmul_glu(orc, cols, rows, dtype, gate_dtype):
+    """h = up * silu(gate) of the RMSNorm activation (model.c:636-640)."""
+    say("matmul_glu", cols, rows, dtype, gate_dtype)
+    nb = (cols + 31) // 32
+    x = synth.normal(701 + cols, cols)
+    w = synth.normal(702 + cols, cols, 0.2) + 1.0
+    ok, _, d, q = orc.row_work(x, 1, cols, norm=w, eps=1e-6)
+    assert ok
+    wg = weights(703, rows, cols, gate_dtype)
+    wu = weights(704, rows, cols, dtype)
+    gate_mat = smq.QMat(dev(wg), rows, cols, gate_dtype)
+    up_mat = smq.QMat(dev(wu), rows, cols, dtype)
+    h = smq.DeviceBuffer(rows * 4)
+    smq.matmul_glu(gate_mat, up_mat, smq.act(smq.ACT_NORM, cols, x=dev(x), norm=dev(w), eps=1e-6,
+                                             xd_scratch=smq.DeviceBuffer(nb * 4), xq_scratch=smq.DeviceBuffer(nb * 32)),
+                   1, h, gate_scratch=smq.DeviceBuffer(rows * 4))
+    smq.numeric_check()
+    g, u = expect_items(orc, [(wg, rows, gate_dtype, None, None), (wu, rows, dtype, None, None)], d, q, cols)
+    assert_same_f32(h.download(np.float32), orc.act_mul(u, g), "h")
+
+
+def test_glu_chain_equals_unfused(orc):
+    """One decode FFN (RMSNorm -> gate/up -> SwiGLU -> down, x += ...) through
+    the fused calls and through the unfused ones: the same bits."""
+    cols, hidden = 896, 4864
+    nbc, nbh = cols // 32, hidden // 32
+    x0 = synth.normal(801, cols)
+    w = synth.normal(802, cols, 0.2) + 1.0
+    gate = smq.QMat(dev(synth.q8_weights(803, hidden, cols)), hidden, cols)
+    up = smq.QMat(dev(synth.q8_weights(804, hidden, cols)), hidden, cols)
+    down = smq.QMat(dev(synth.q8_weights(805, cols, hidden)), cols, hidden)
+    wb = dev(w)
+    # fused
+    xf = dev(x0)
+    h = smq.DeviceBuffer(hidden * 4)
+    smq.matmul_glu(gate, up, smq.act(smq.ACT_NORM, cols, x=xf, norm=wb, eps=1e-6), 1, h)
+    smq.matmul_act([(down, None, xf, True)], smq.act(smq.ACT_F32, hidden, x=h, xd_scratch=smq.DeviceBuffer(nbh * 4),
+                                                     xq_scratch=smq.DeviceBuffer(nbh * 32)))
+    smq.numeric_check()
+    # unfused
+    xu = dev(x0)
+    d, q = smq.DeviceBuffer(nbc * 4), smq.DeviceBuffer(nbc * 32)
+    hd, hq = smq.DeviceBuffer(nbh * 4), smq.DeviceBuffer(nbh * 32)
+    gb, ub = smq.DeviceBuffer(hidden * 4), smq.DeviceBuffer(hidden * 4)
+    smq.norm_quantize(xu, wb, 1e-6, 1, cols, None, d, q)
+    smq.matmul([(gate, None, gb), (up, None, ub)], d, q, 1)
+    smq.silu_quantize(ub, gb, 1, hidden, hd, hq)
+    smq.matmul([(down, None, xu, True)], hd, hq, 1)
+    smq.numeric_check()
+    assert_same_f32(h.download(np.float32), ub.download(np.float32), "h")
+    assert_same_f32(xf.download(np.float32), xu.download(np.float32), "x")
+
+
+def test_fused_nonfinite_flags():
+    cols, rows = 896, 64
+    wt = smq.QMat(dev(synth.q8_weights(901, rows, cols)), rows, cols)
+    for bad in (np.inf, np.nan):
+        x = synth.normal(902, cols)
+        x[333] = bad
+        y = smq.DeviceBuffer(rows * 4)
+        say("fused nonfinite", bad)
+        smq.matmul_act([(wt, None, y)], smq.act(smq.ACT_NORM, cols, x=dev(x), norm=dev(np.ones(cols, np.float32))))
+        with pytest.raises(smq.SmqError) as e:
+            smq.numeric_check()
+        assert e.value.status == smq.SM_ERR_NUMERIC
+        smq.matmul_act([(wt, None, y)], smq.act(smq.ACT_F32, cols, x=dev(x)))
+        with pytest.raises(smq.SmqError):
+            smq.numeric_check()
+
+
+def test_fused_argument_errors():
+    cols = 8200  # past the fused RMSNorm width: needs the scratch buffers
+    wt = smq.QMat(dev(synth.q8_weights(911, 8, cols)), 8, cols)
+    y = smq.DeviceBuffer(8 * 4)
+    x = dev(synth.normal(912, cols))
+    with pytest.raises(smq.SmqError) as e:
+        smq.matmul_act([(wt, None, y)], smq.act(smq.ACT_NORM, cols, x=x, norm=x))
+    assert e.value.status == smq.SM_ERR_RANGE
+    with pytest.raises(smq.SmqError):  # column count of the activation differs
+        smq.matmul_act([(wt, None, y)], smq.act(smq.ACT_F32, cols - 1, x=x))
+    g = smq.QMat(dev(synth.q8_weights(913, 8, 64)), 8, 64)
+    u = smq.QMat(dev(synth.q8_weights(914, 9, 64)), 9, 64)
+    with pytest.raises(smq.SmqError):  # gate and up differ in rows
+        smq.matmul_glu(g, u, smq.act(smq.ACT_NORM, 64, x=x, norm=x), 1, y)

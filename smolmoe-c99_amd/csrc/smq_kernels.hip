@@ -408,7 +408,7 @@ __global__ __launch_bounds__(NT) void k_gemv_stream(GroupArgs g) {
 }
 
 /* ------------------------------------------------------------------------
- * Pinned streaming GEMV (Q8, nb <= PIN_NB): each workgroup belongs to one
+ * Pinned streaming GEMV (Q8, nb <= MAX_FAST_NB): each workgroup belongs to one
  * item (the launcher gives every item a share of the resident workgroups
  * in proportion to its rows) and walks a contiguous range of that item's
  * tiles. Its activation is staged in LDS once, so a task is just the nine
@@ -416,7 +416,7 @@ __global__ __launch_bounds__(NT) void k_gemv_stream(GroupArgs g) {
  * threads), and D tasks stay in flight per thread. Products and chains as in
  * k_gemv: exact per-lane order, the fixed lane tree.
  * ---------------------------------------------------------------------- */
-constexpr uint32_t PIN_NB = 64;
+constexpr uint32_t PIN_NB = 64; /* the activation's LDS size of the narrow instantiation */
 
 struct PinTask {
     uint32_t w[9];
@@ -434,13 +434,14 @@ __device__ __forceinline__ uint32_t find_pin_item(const GroupArgs &g, uint32_t w
     return lo;
 }
 
-template <bool FAST, int RT, int NT, int D>
-__global__ __launch_bounds__(NT) void k_gemv_pin(GroupArgs g) {
+/* exact contract: at least 6 waves per SIMD (three 512-thread workgroups per CU) */
+template <bool FAST, int RT, int NT, int D, uint32_t MAXNB>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(FAST ? 4 : 6, 8))) void k_gemv_pin(GroupArgs g) {
     constexpr int TPR = NT / RT, CB = TPR, GS = RT * 32 + 4, DS = RT * 4 + 4;
     __shared__ __attribute__((aligned(16))) float prod[2][(CB / 4) * GS];
     __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? (CB / 4) * DS : 4];
-    __shared__ __attribute__((aligned(16))) uint32_t act_q[PIN_NB * 8];
-    __shared__ float act_d[PIN_NB];
+    __shared__ __attribute__((aligned(16))) uint32_t act_q[MAXNB * 8];
+    __shared__ float act_d[MAXNB];
 
     const uint32_t tid = threadIdx.x, tr = tid / TPR, ti = tid % TPR, nb = g.nb;
     const GroupItem &I = g.item[find_pin_item(g, blockIdx.x)];
@@ -502,11 +503,16 @@ __global__ __launch_bounds__(NT) void k_gemv_pin(GroupArgs g) {
                 }
                 if (FAST) db[(ti / 4) * DS + tr * 4 + (ti % 4)] = d;
             }
+            /* this task is consumed: its slot reloads now, a barrier and a chain earlier than
+             * at the end of the step (the chain threads keep its bias and prior output) */
+            const float tbias = T[j].bias, tprior = T[j].prior;
+            load(T[j], lt, lc, k + j + D < my_steps);
+            if (++lc == nchunks) { lc = 0; ++lt; }
             __syncthreads();
             if (tid < RT * 8) {
                 if (cc == 0) {
-                    bias = T[j].bias;
-                    prior = T[j].prior;
+                    bias = tbias;
+                    prior = tprior;
                 }
                 const uint32_t count = nb - cc * CB < (uint32_t)CB ? nb - cc * CB : (uint32_t)CB;
                 chain_sum<FAST, CB / 4>(acc, (const float4 *)pb + tid, GS / 4,
@@ -525,8 +531,6 @@ __global__ __launch_bounds__(NT) void k_gemv_pin(GroupArgs g) {
                 }
             }
             if (++cc == nchunks) { cc = 0; ++ct; }
-            load(T[j], lt, lc, k + j + D < my_steps);
-            if (++lc == nchunks) { lc = 0; ++lt; }
         }
     }
 }
@@ -1964,13 +1968,13 @@ hipError_t launch_gemv_stream_typed(GroupArgs &g, int rt, hipStream_t s) {
 
 /* Pinned launch: every item gets a share of the resident workgroups in
  * proportion to its tiles (at least one), each a contiguous tile range. */
-template <bool FAST>
-hipError_t launch_gemv_pin(GroupArgs &g, hipStream_t s) {
+template <bool FAST, uint32_t MAXNB>
+hipError_t launch_gemv_pin_nb(GroupArgs &g, hipStream_t s) {
     constexpr int RT = 16, NT = 512, D = 2;
     static int resident = 0;
     if (!resident) {
         int per_cu = 0, dev = 0, cus = 0;
-        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemv_pin<FAST, RT, NT, D>, NT, 0);
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemv_pin<FAST, RT, NT, D, MAXNB>, NT, 0);
         if (e == hipSuccess) e = hipGetDevice(&dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (e != hipSuccess) return e;
@@ -1988,14 +1992,19 @@ hipError_t launch_gemv_pin(GroupArgs &g, hipStream_t s) {
         g.item[i].nwg = n;
         wgs += n;
     }
-    hipLaunchKernelGGL((k_gemv_pin<FAST, RT, NT, D>), dim3(wgs), dim3(NT), 0, s, g);
+    hipLaunchKernelGGL((k_gemv_pin<FAST, RT, NT, D, MAXNB>), dim3(wgs), dim3(NT), 0, s, g);
     return hipGetLastError();
+}
+
+template <bool FAST>
+hipError_t launch_gemv_pin(GroupArgs &g, hipStream_t s) {
+    return g.nb <= PIN_NB ? launch_gemv_pin_nb<FAST, PIN_NB>(g, s) : launch_gemv_pin_nb<FAST, MAX_FAST_NB>(g, s);
 }
 
 bool gemv_pin_ok(const GroupArgs &g, bool q5) {
     const char *env = getenv("SMQ_GEMV_PIN");
     if (env && *env && atoi(env) == 0) return false;
-    return !q5 && g.nb <= PIN_NB;
+    return !q5 && g.nb <= MAX_FAST_NB;
 }
 
 template <bool Q5, bool FAST>

@@ -37,6 +37,8 @@ GROUP_CASES = [
     # q5, cols, rows of each item, fast
     (False, 896, [4864, 4864, 896, 128, 7], False),   # FFN/QKV shapes and a ragged tail tile
     (False, 4864, [896, 896, 33], False),             # wide rows: several chunks per tile
+    (False, 4864, [896, 50], True),                   # wide rows, fast contract
+    (False, 16384, [40, 7], False),                   # the widest pinned activation (512 blocks)
     (True, 1536, [8960, 1536, 5], False),             # Q5 pairs
     (False, 896, [4864, 100], True),                  # fast contract (lane FMA)
     (True, 8960, [1536, 3], True),

@@ -465,14 +465,18 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(FAST ? 4 : 6
     auto load = [&](PinTask &T, uint32_t tile, uint32_t chunk, bool real) __attribute__((always_inline)) {
         const uint32_t row0 = tile * RT, row = row0 + tr, b = chunk * CB + ti;
         T.ok = real && row < rows && b < nb;
-        const unsigned char *p = wbase + (T.ok ? (size_t)row * row_bytes + (size_t)b * Q8_BYTES : 0);
-        const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
-        T.w[0] = v0.x; T.w[1] = v0.y; T.w[2] = v0.z; T.w[3] = v0.w;
-        T.w[4] = v1.x; T.w[5] = v1.y; T.w[6] = v1.z; T.w[7] = v1.w;
-        T.w[8] = *(const uint32_t *)(p + 32);
-        const uint32_t orow = row0 + (tid < RT * 8 ? tid / 8 : 0), oc = orow < rows ? orow : 0;
-        T.bias = *(bias_p ? bias_p + oc : xd); /* unused reads when absent keep the load count uniform */
-        T.prior = *(accum ? y + oc : xd);
+        if (T.ok) { /* idle task lanes issue nothing (the load count is per wave, not per lane) */
+            const unsigned char *p = wbase + (size_t)row * row_bytes + (size_t)b * Q8_BYTES;
+            const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
+            T.w[0] = v0.x; T.w[1] = v0.y; T.w[2] = v0.z; T.w[3] = v0.w;
+            T.w[4] = v1.x; T.w[5] = v1.y; T.w[6] = v1.z; T.w[7] = v1.w;
+            T.w[8] = *(const uint32_t *)(p + 32);
+        }
+        if (tid < RT * 8) { /* the chain threads' row: its bias and prior output */
+            const uint32_t orow = row0 + tid / 8, oc = orow < rows ? orow : 0;
+            T.bias = bias_p ? bias_p[oc] : 0.0f;
+            T.prior = accum ? y[oc] : 0.0f;
+        }
     };
     PinTask T[D];
     uint32_t lt = t0, lc = 0; /* load cursor */

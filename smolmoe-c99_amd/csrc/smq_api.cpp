@@ -27,6 +27,7 @@ struct Context {
     int *qflag = nullptr;   /* per-call fault of the synchronous quantizer */
     float *scalar = nullptr;
     void *argmax_parts = nullptr; /* smq::MAX_ARGMAX_PARTS partials of the two-stage argmax */
+    float *scores = nullptr;      /* decode attention scores (heads x context), smq::SCORE_WORKSPACE_BYTES */
     hipEvent_t t0 = nullptr, t1 = nullptr;
     int fast = 0;
     int prefill_mfma = 0;
@@ -206,6 +207,7 @@ smq_status smq_init(int device) {
     if (!hip_ok(hipMemset(p, 0, 256), "hipMemset")) return t_status;
     if (!hip_ok(hipMalloc(&g.argmax_parts, (size_t)smq::MAX_ARGMAX_PARTS * smq::ARGMAX_PART_BYTES), "hipMalloc"))
         return t_status;
+    if (!hip_ok(hipMalloc((void **)&g.scores, smq::SCORE_WORKSPACE_BYTES), "hipMalloc")) return t_status;
     if (!hip_ok(hipEventCreate(&g.t0), "hipEventCreate") || !hip_ok(hipEventCreate(&g.t1), "hipEventCreate"))
         return t_status;
     g.cur = g.own;
@@ -223,6 +225,7 @@ void smq_shutdown(void) {
     (void)hipEventDestroy(g.t1);
     (void)hipFree(g.flag);
     (void)hipFree(g.argmax_parts);
+    (void)hipFree(g.scores);
     (void)hipStreamDestroy(g.own);
     g = Context();
 }
@@ -804,7 +807,7 @@ smq_status smq_attention_rope_q8(float *q, float *k, const float *v, const smq_a
     const bool aligned = !((uintptr_t)q & 15) && !((uintptr_t)k & 15) && !((uintptr_t)v & 15);
     if (aligned && smq::attention_rows_ok(sh, q, keys, values))
         return hip_ok(smq::launch_attention_rope(q, k, v, cos_table, sin_table, keys, values, att, sh, pos0, pos_dev,
-                                                 g.flag, xd, xq, g.cur),
+                                                 g.flag, xd, xq, g.scores, g.cur),
                       "attention_rope_q8")
                    ? SMQ_OK
                    : t_status;

@@ -125,9 +125,13 @@ hipError_t launch_attention(const float *q, const float *kcache, const float *vc
  * outputs. Needs attention_rows_ok (head_dim 64, 16-byte aligned q and
  * caches) and 16-byte aligned k, v. */
 bool attention_rows_ok(const AttnShape &sh, const void *q, const void *kcache, const void *vcache);
+/* scores: SCORE_WORKSPACE_BYTES of device workspace (heads x context f32) for
+ * the two-launch form; NULL (or a shape past it) takes the one-launch form. */
+constexpr size_t SCORE_WORKSPACE_BYTES = (size_t)4 << 22;
 hipError_t launch_attention_rope(const float *q, const float *k, const float *v, const float *cs, const float *sn,
                                  float *kcache, float *vcache, float *att, const AttnShape &sh, uint32_t pos0,
-                                 const int32_t *pos_dev, int *flag, float *xd, int8_t *xq, hipStream_t s);
+                                 const int32_t *pos_dev, int *flag, float *xd, int8_t *xq, float *scores,
+                                 hipStream_t s);
 hipError_t launch_decode_advance(int32_t *pos, uint32_t *count, const uint32_t *token, uint32_t *history,
                                  uint32_t capacity, hipStream_t s);
 /* Greedy argmax in two launches through `parts` (ARGMAX_PART_BYTES *

@@ -1517,6 +1517,125 @@ __device__ __forceinline__ void att_rows_keys(f4v (&kr)[AR_KU], const float *kba
     }
 }
 
+/* V rows [p0, p0 + AR_VP) of a workgroup's 32 coordinates (vrow/vcol: this
+ * thread's row and float4 column), ROPE: the current position's row from vrope. */
+template <bool ROPE>
+__device__ __forceinline__ void att_load_values(float4 (&pre)[AR_VL], const float *vbase, const float *vrope,
+                                                uint32_t kvd, uint32_t p0, uint32_t np, uint32_t last,
+                                                uint32_t vrow, uint32_t vcol) {
+#pragma unroll
+    for (uint32_t u = 0; u < AR_VL; ++u) {
+        const uint32_t p = p0 + vrow + u * (AR_WG * 4 / ATT_JW);
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (p < np)
+            v = *(const float4 *)((ROPE && p == last) ? vrope + vcol : vbase + (size_t)p * kvd + vcol);
+        pre[u] = v;
+    }
+}
+
+/* Steps 2-4 of the row attention once the scaled scores sc[0, np) are in LDS
+ * and each thread holds the maximum of its own (high): the maximum
+ * (order-free, NaN never wins as in softmax_inv, kernels.c:1146-1148),
+ * exp_det(s - max) in parallel, the total in position order by one lane,
+ * then the products (s_p*inv)*v_p[j] of AR_VP rows at a time to LDS and lane
+ * j's sum of its column in position order (kernels.c:1165), the next rows
+ * loading meanwhile. pre holds the first value rows. The 32 outputs go to
+ * out[0, 32); with xd, their Q8 block to *xd / xq[0, 32) (kernels.c:912-935). */
+template <bool ROPE>
+__device__ __forceinline__ void att_tail(float high, float *sc, float *prod, uint32_t np, uint32_t last,
+                                         float4 (&pre)[AR_VL], const float *vbase, const float *vrope,
+                                         uint32_t kvd, uint32_t vrow, uint32_t vcol, const uint64_t *etab,
+                                         float *red, float *s_inv, float *out, float *xd, int8_t *xq, int *flag) {
+    const uint32_t tid = threadIdx.x;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(high, off, 64);
+        high = o > high ? o : high;
+    }
+    if ((tid & 63) == 0) red[tid >> 6] = high;
+    __syncthreads();
+    high = red[0];
+#pragma unroll
+    for (uint32_t w = 1; w < AR_WG / 64; ++w) high = red[w] > high ? red[w] : high;
+    for (uint32_t p = tid; p < np; p += AR_WG) sc[p] = exp_det_tab(sc[p] - high, etab);
+    __syncthreads();
+
+    if (tid == 0) *s_inv = 1.0f / serial_sum_lds(sc, np);
+    __syncthreads();
+    const float inv = *s_inv;
+
+    float o = 0.0f;
+    for (uint32_t p0 = 0; p0 < np; p0 += AR_VP) {
+#pragma unroll
+        for (uint32_t u = 0; u < AR_VL; ++u) { /* kernels.c:1165: w = scores[p] * inv, then w * v[j] */
+            const uint32_t r = vrow + u * (AR_WG * 4 / ATT_JW), p = p0 + r;
+            if (p < np) {
+                const float w = sc[p] * inv;
+                prod[(vcol + 0) * AR_VPP + r] = w * pre[u].x;
+                prod[(vcol + 1) * AR_VPP + r] = w * pre[u].y;
+                prod[(vcol + 2) * AR_VPP + r] = w * pre[u].z;
+                prod[(vcol + 3) * AR_VPP + r] = w * pre[u].w;
+            }
+        }
+        __syncthreads();
+        if (p0 + AR_VP < np) /* next pass in flight during the sums */
+            att_load_values<ROPE>(pre, vbase, vrope, kvd, p0 + AR_VP, np, last, vrow, vcol);
+        if (tid < ATT_JW) {
+            const uint32_t rows = np - p0 < AR_VP ? np - p0 : AR_VP, nbat = rows / 32;
+            const float *colp = prod + tid * AR_VPP;
+            float acc = o;
+            uint32_t c = 0;
+            if (nbat) {
+                float4 x[8], y[8];
+                read_batch(x, (const float4 *)colp);
+                for (; c + 2 <= nbat; c += 2) {
+                    read_batch(y, (const float4 *)colp + 8 * (c + 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                    add_batch(acc, x);
+                    read_batch(x, (const float4 *)colp + 8 * (c + 2 < nbat ? c + 2 : c + 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                    add_batch(acc, y);
+                }
+                if (c < nbat) {
+                    add_batch(acc, x);
+                    ++c;
+                }
+            }
+            const uint32_t rest = rows - c * 32;
+            if (rest) {
+                const float *tl = colp + c * 32;
+                float v[32];
+#pragma unroll
+                for (uint32_t u = 0; u < 32; ++u) v[u] = tl[u < rest ? u : rest - 1];
+#pragma unroll
+                for (uint32_t u = 0; u < 32; ++u)
+                    if (u < rest) acc = acc + v[u];
+            }
+            o = acc;
+        }
+        __syncthreads();
+    }
+    if (tid < ATT_JW) {
+        out[tid] = o;
+        if (xd) {
+            const float av = fabsf(o);
+            int bad = !(av <= FLT_MAX);
+            const float mx = max32(av);
+            bad = __ballot(bad) != 0;
+            const float scale = mx / 127.0f;
+            const float qinv = scale >= FLT_MIN ? 1.0f / scale : 0.0f;
+            const float pq = o * qinv;
+            int qi = (int)__builtin_rintf(pq);
+            qi = qi > 127 ? 127 : (qi < -127 ? -127 : qi);
+            xq[tid] = (int8_t)qi;
+            if (tid == 0) {
+                *xd = scale;
+                if (bad && flag) *flag = 1;
+            }
+        }
+    }
+}
+
 template <bool ROPE>
 /* 2 waves per SIMD: the round's K rows stay in registers (no spills) */
 __global__ __launch_bounds__(AR_WG) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_attend_rows(const float *q, float *kcache, float *vcache, float *att,
@@ -1552,17 +1671,6 @@ __global__ __launch_bounds__(AR_WG) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     /* 0. loads: value pass 0, the K rows of round 0, q, the exp table */
     const uint32_t vrow = tid / (ATT_JW / 4), vcol = (tid % (ATT_JW / 4)) * 4;
     float4 pre[AR_VL];
-    auto load_values = [&](uint32_t p0) __attribute__((always_inline)) {
-#pragma unroll
-        for (uint32_t u = 0; u < AR_VL; ++u) {
-            const uint32_t p = p0 + vrow + u * (AR_WG * 4 / ATT_JW);
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (p < np)
-                v = *(const float4 *)((ROPE && p == last) ? rr.v + (size_t)kh * AR_HD + j0 + vcol
-                                                          : vbase + (size_t)p * kvd + vcol);
-            pre[u] = v;
-        }
-    };
     const uint32_t krow = tid / AR_Q4, kcol = tid % AR_Q4; /* load u covers rows krow + u*(AR_WG/AR_Q4) */
     /* issue order = need order (loads complete in order): q, tables, K, V */
     const float *qh = q + (size_t)t * sh.q_dim + (size_t)h * AR_HD;
@@ -1579,7 +1687,8 @@ __global__ __launch_bounds__(AR_WG) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     if (kown) kx = *(const float4 *)(rr.k + (size_t)kh * AR_HD + 4 * (tid - 192));
     f4v kr[AR_KU];
     att_rows_keys(kr, kbase, kvd, 0, np, ROPE ? last : np, krow, kcol);
-    load_values(0);
+    const float *vrope = ROPE ? rr.v + (size_t)kh * AR_HD + j0 : nullptr;
+    att_load_values<ROPE>(pre, vbase, vrope, kvd, 0, np, last, vrow, vcol);
     if (rload) rtab[rhalf * (AR_HD / 2) + rj] = rv;
     if (ROPE) __syncthreads(); /* the table rows, before q and k are rotated */
     if (kown) {
@@ -1630,101 +1739,156 @@ __global__ __launch_bounds__(AR_WG) __attribute__((amdgpu_waves_per_eu(1, 2))) v
         }
     }
 
-    /* 2. maximum, exp */
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float o = __shfl_xor(high, off, 64);
-        high = o > high ? o : high;
+    const uint32_t nbq = sh.q_dim / QK, blk = (h * AR_HD + j0) / QK;
+    att_tail<ROPE>(high, sc, prod, np, last, pre, vbase, vrope, kvd, vrow, vcol, etab, red,
+                   &s_inv, att + (size_t)t * sh.q_dim + (size_t)h * AR_HD + j0, xd ? xd + (size_t)t * nbq + blk : nullptr,
+                   xq ? xq + ((size_t)t * nbq + blk) * QK : nullptr, flag);
+}
+
+/* Decode attention in two launches (one token, head_dim 64): the K rows are
+ * spread over many workgroups instead of being fetched by one workgroup per
+ * head, the part of k_attend_rows that a single CU's load bandwidth bounds.
+ * k_attend_scores: workgroup (block of AS_SP positions, KV head) forms the
+ * scaled scores of every query head of the group (8-lane dot_f32, times
+ * 1/sqrt(64)) into scores[h][p]; with ROPE it rotates q and this position's
+ * k itself (model.c:442-450) and the workgroup holding the current position
+ * stores the rotated k and the v row into the caches (model.c:511-526).
+ * Workgroups past the current position leave at once (the grid covers the
+ * context, so a captured step replays at any position). */
+constexpr uint32_t AS_WG = 256;
+constexpr uint32_t AS_SP = 32;                 /* positions per scores workgroup */
+constexpr uint32_t AS_MAXG = 16;               /* query heads per KV head */
+constexpr uint32_t MAX_SCORE_FLOATS = 1u << 22; /* the library's scores workspace: heads x context */
+
+template <bool ROPE>
+__global__ __launch_bounds__(AS_WG) void k_attend_scores(const float *q, float *kcache, float *vcache, AttnShape sh,
+                                                         uint32_t pos0, const int32_t *pos_dev, int *flag,
+                                                         RopeRows rr, float *scores) {
+    __shared__ __attribute__((aligned(16))) float qs[AS_MAXG * AR_HD];
+    __shared__ __attribute__((aligned(16))) float kt[AS_SP * AR_KP];
+    __shared__ float rtab[ROPE ? AR_HD : 1];
+    const uint32_t tid = threadIdx.x, grp = sh.heads / sh.kv_heads, kh = blockIdx.y, kvd = sh.kv_dim;
+    const uint32_t pos = pos_dev ? (uint32_t)*pos_dev : pos0;
+    if (pos >= sh.context) {
+        if (tid == 0 && blockIdx.x == 0 && flag) *flag = 1;
+        return;
     }
-    if ((tid & 63) == 0) red[tid >> 6] = high;
-    __syncthreads();
-    high = red[0];
+    const uint32_t start = sh.window && pos >= sh.window ? pos - sh.window + 1 : 0, np = pos - start + 1;
+    const uint32_t last = np - 1, p0 = blockIdx.x * AS_SP;
+    if (p0 >= np) return; /* uniform: past the current position */
+    const uint32_t cnt = np - p0 < AS_SP ? np - p0 : AS_SP;
+    const bool holds_last = ROPE && last < p0 + cnt;
+    const float *kbase = kcache + (size_t)start * kvd + (size_t)kh * AR_HD;
+
+    /* loads: q of the group's heads, the table rows, this block's K rows (the current one from rr.k) */
+    float4 qx[AS_MAXG * AR_Q4 / AS_WG];
 #pragma unroll
-    for (uint32_t w = 1; w < AR_WG / 64; ++w) high = red[w] > high ? red[w] : high;
-    for (uint32_t p = tid; p < np; p += AR_WG) sc[p] = exp_det_tab(sc[p] - high, etab);
+    for (uint32_t u = 0; u < AS_MAXG * AR_Q4 / AS_WG; ++u) {
+        const uint32_t f = tid + u * AS_WG, hh = f / AR_Q4, c = f % AR_Q4;
+        qx[u] = hh < grp ? *(const float4 *)(q + (size_t)(kh * grp + hh) * AR_HD + 4 * c) : make_float4(0, 0, 0, 0);
+    }
+    float rv = 0.0f;
+    const uint32_t ri = tid, rhalf = ri < sh.pairs ? 0 : 1, rj = ri - rhalf * sh.pairs;
+    const bool rload = ROPE && ri < 2 * sh.pairs;
+    if (rload) rv = (rhalf ? rr.sn : rr.cs)[(size_t)pos * sh.pairs + rj];
+    float4 kx[AS_SP * AR_Q4 / AS_WG];
+#pragma unroll
+    for (uint32_t u = 0; u < AS_SP * AR_Q4 / AS_WG; ++u) {
+        const uint32_t f = tid + u * AS_WG, r = f / AR_Q4, c = f % AR_Q4, p = p0 + r;
+        const float *src = (ROPE && p == last) ? rr.k + (size_t)kh * AR_HD : kbase + (size_t)(r < cnt ? p : p0) * kvd;
+        kx[u] = *(const float4 *)(src + 4 * c);
+    }
+    if (ROPE && holds_last && tid >= 64 && tid < 64 + AR_HD) /* v is stored as is (model.c:520-523) */
+        vcache[(size_t)pos * kvd + (size_t)kh * AR_HD + (tid - 64)] = rr.v[(size_t)kh * AR_HD + (tid - 64)];
+    if (rload) rtab[rhalf * (AR_HD / 2) + rj] = rv;
+    if (ROPE) __syncthreads(); /* the table rows */
+    const float *crow = ROPE ? rtab : nullptr, *srow = ROPE ? rtab + AR_HD / 2 : nullptr;
+#pragma unroll
+    for (uint32_t u = 0; u < AS_MAXG * AR_Q4 / AS_WG; ++u) {
+        const uint32_t f = tid + u * AS_WG, hh = f / AR_Q4, c = f % AR_Q4;
+        if (hh < grp) *(float4 *)&qs[hh * AR_HD + 4 * c] = ROPE ? rope4(qx[u], c, sh.pairs, crow, srow) : qx[u];
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < AS_SP * AR_Q4 / AS_WG; ++u) {
+        const uint32_t f = tid + u * AS_WG, r = f / AR_Q4, c = f % AR_Q4, p = p0 + r;
+        if (r < cnt) {
+            float4 x = kx[u];
+            if (ROPE && p == last) {
+                x = rope4(x, c, sh.pairs, crow, srow);
+                *(float4 *)(kcache + (size_t)pos * kvd + (size_t)kh * AR_HD + 4 * c) = x;
+            }
+            *(float4 *)&kt[r * AR_KP + 4 * c] = x;
+        }
+    }
     __syncthreads();
 
-    /* 3. the total in position order */
-    if (tid == 0) s_inv = 1.0f / serial_sum_lds(sc, np);
-    __syncthreads();
-    const float inv = s_inv;
+    /* (position, head) pairs: dot_f32 of kernels.c:1119-1127, lane tree, times 1/sqrt(hd) */
+    const float factor = 1.0f / sqrtf((float)AR_HD);
+    for (uint32_t i = tid; i < cnt * grp; i += AS_WG) {
+        const uint32_t r = i % cnt, hh = i / cnt;
+        DotAcc acc = {{0, 0, 0, 0, 0, 0, 0, 0}};
+        dot_groups(acc, (const float4 *)&kt[r * AR_KP], (const float4 *)&qs[hh * AR_HD], 0, AR_HD / 8);
+        const float p04 = acc.a[0] + acc.a[4], p15 = acc.a[1] + acc.a[5], p26 = acc.a[2] + acc.a[6],
+                    p37 = acc.a[3] + acc.a[7];
+        const float e2 = p04 + p26, o2 = p15 + p37;
+        scores[(size_t)(kh * grp + hh) * sh.context + p0 + r] = (e2 + o2) * factor;
+    }
+}
 
-    /* 4. weighted values */
-    float o = 0.0f;
-    for (uint32_t p0 = 0; p0 < np; p0 += AR_VP) {
+/* k_attend_values: workgroup (head, 32 coordinates) loads its scores row and
+ * its value rows up front, then steps 2-4 of the row attention (att_tail). */
+template <bool ROPE>
+__global__ __launch_bounds__(AR_WG) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_attend_values(
+    const float *vcache, float *att, AttnShape sh, uint32_t pos0, const int32_t *pos_dev, float *xd, int8_t *xq,
+    const float *vraw, const float *scores, int *flag) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    __shared__ uint64_t etab[32];
+    __shared__ float red[AR_WG / 64];
+    __shared__ float s_inv;
+    constexpr uint32_t ngrp = AR_HD / ATT_JW;
+    const uint32_t tid = threadIdx.x, g = blockIdx.x % ngrp, h = blockIdx.x / ngrp;
+    const uint32_t kh = h / (sh.heads / sh.kv_heads), kvd = sh.kv_dim, j0 = g * ATT_JW;
+    const uint32_t pos = pos_dev ? (uint32_t)*pos_dev : pos0;
+    if (pos >= sh.context) return; /* flagged by the scores launch */
+    const uint32_t start = sh.window && pos >= sh.window ? pos - sh.window + 1 : 0, np = pos - start + 1;
+    const uint32_t last = np - 1;
+    float *sc = lds;
+    float *prod = lds + ((sh.context + 3) & ~3u);
+    const float *vbase = vcache + (size_t)start * kvd + (size_t)kh * AR_HD + j0;
+    const float *vrope = ROPE ? vraw + (size_t)kh * AR_HD + j0 : nullptr;
+    const float *srow = scores + (size_t)h * sh.context;
+    const uint32_t vrow = tid / (ATT_JW / 4), vcol = (tid % (ATT_JW / 4)) * 4;
+
+    /* issue order = need order: the table, the scores (a round of AR_WG x AS_LD), the first value rows */
+    uint64_t ev = 0;
+    if (tid < 32) ev = EXP2_TABLE[tid];
+    constexpr uint32_t AS_LD = 4;
+    float sv[AS_LD];
 #pragma unroll
-        for (uint32_t u = 0; u < AR_VL; ++u) { /* kernels.c:1165: w = scores[p] * inv, then w * v[j] */
-            const uint32_t r = vrow + u * (AR_WG * 4 / ATT_JW), p = p0 + r;
-            if (p < np) {
-                const float w = sc[p] * inv;
-                prod[(vcol + 0) * AR_VPP + r] = w * pre[u].x;
-                prod[(vcol + 1) * AR_VPP + r] = w * pre[u].y;
-                prod[(vcol + 2) * AR_VPP + r] = w * pre[u].z;
-                prod[(vcol + 3) * AR_VPP + r] = w * pre[u].w;
-            }
-        }
-        __syncthreads();
-        if (p0 + AR_VP < np) load_values(p0 + AR_VP); /* next pass in flight during the sums */
-        if (tid < ATT_JW) {
-            const uint32_t rows = np - p0 < AR_VP ? np - p0 : AR_VP, nbat = rows / 32;
-            const float *colp = prod + tid * AR_VPP;
-            float acc = o;
-            uint32_t c = 0;
-            if (nbat) {
-                float4 x[8], y[8];
-                read_batch(x, (const float4 *)colp);
-                for (; c + 2 <= nbat; c += 2) {
-                    read_batch(y, (const float4 *)colp + 8 * (c + 1));
-                    __builtin_amdgcn_sched_barrier(0);
-                    add_batch(acc, x);
-                    read_batch(x, (const float4 *)colp + 8 * (c + 2 < nbat ? c + 2 : c + 1));
-                    __builtin_amdgcn_sched_barrier(0);
-                    add_batch(acc, y);
-                }
-                if (c < nbat) {
-                    add_batch(acc, x);
-                    ++c;
-                }
-            }
-            const uint32_t rest = rows - c * 32;
-            if (rest) {
-                const float *tl = colp + c * 32;
-                float v[32];
-#pragma unroll
-                for (uint32_t u = 0; u < 32; ++u) v[u] = tl[u < rest ? u : rest - 1];
-#pragma unroll
-                for (uint32_t u = 0; u < 32; ++u)
-                    if (u < rest) acc = acc + v[u];
-            }
-            o = acc;
-        }
-        __syncthreads();
+    for (uint32_t u = 0; u < AS_LD; ++u) {
+        const uint32_t p = tid + u * AR_WG;
+        sv[u] = p < np ? srow[p] : 0.0f;
     }
-    if (tid < ATT_JW) { /* this workgroup's 32 coordinates are one block (kernels.c:912-935) */
-        att[(size_t)t * sh.q_dim + (size_t)h * AR_HD + j0 + tid] = o;
-        if (xd) {
-            const float av = fabsf(o);
-            float mx = av;
-            int bad = !(av <= FLT_MAX);
+    float4 pre[AR_VL];
+    att_load_values<ROPE>(pre, vbase, vrope, kvd, 0, np, last, vrow, vcol);
+    if (tid < 32) etab[tid] = ev;
+    float high = -FLT_MAX;
 #pragma unroll
-            for (int off = 16; off >= 1; off >>= 1) {
-                const float ot = __shfl_xor(mx, off, 32);
-                mx = ot > mx ? ot : mx;
-                bad |= __shfl_xor(bad, off, 32);
-            }
-            const float scale = mx / 127.0f;
-            const float qinv = scale >= FLT_MIN ? 1.0f / scale : 0.0f;
-            const uint32_t nbq = sh.q_dim / QK, blk = (h * AR_HD + j0) / QK;
-            const float pq = o * qinv;
-            int qi = (int)__builtin_rintf(pq);
-            qi = qi > 127 ? 127 : (qi < -127 ? -127 : qi);
-            xq[((size_t)t * nbq + blk) * QK + tid] = (int8_t)qi;
-            if (tid == 0) {
-                xd[(size_t)t * nbq + blk] = scale;
-                if (bad && flag) *flag = 1;
-            }
+    for (uint32_t u = 0; u < AS_LD; ++u) {
+        const uint32_t p = tid + u * AR_WG;
+        if (p < np) {
+            sc[p] = sv[u];
+            high = sv[u] > high ? sv[u] : high;
         }
     }
+    for (uint32_t p = tid + AS_LD * AR_WG; p < np; p += AR_WG) { /* long contexts */
+        const float v = srow[p];
+        sc[p] = v;
+        high = v > high ? v : high;
+    }
+    const uint32_t nbq = sh.q_dim / QK, blk = (h * AR_HD + j0) / QK;
+    att_tail<ROPE>(high, sc, prod, np, last, pre, vbase, vrope, kvd, vrow, vcol, etab, red, &s_inv,
+                   att + (size_t)h * AR_HD + j0, xd ? xd + blk : nullptr, xq ? xq + (size_t)blk * QK : nullptr, flag);
 }
 
 /* Greedy choice (sampler.c:57-63): the first non-banned id, replaced by any
@@ -2217,12 +2381,30 @@ hipError_t launch_attention(const float *q, const float *kcache, const float *vc
 
 hipError_t launch_attention_rope(const float *q, const float *k, const float *v, const float *cs, const float *sn,
                                  float *kcache, float *vcache, float *att, const AttnShape &sh, uint32_t pos0,
-                                 const int32_t *pos_dev, int *flag, float *xd, int8_t *xq, hipStream_t s) {
+                                 const int32_t *pos_dev, int *flag, float *xd, int8_t *xq, float *scores,
+                                 hipStream_t s) {
     if (sh.context > MAX_ATT_POSITIONS || !attention_rows_ok(sh, q, kcache, vcache) ||
         ((uintptr_t)k & 15) || ((uintptr_t)v & 15))
         return hipErrorInvalidValue;
     const uint32_t groups = (sh.head_dim + ATT_JW - 1) / ATT_JW;
     const size_t lds = (((size_t)sh.context + 3) / 4 * 4 + (size_t)AR_FIXED) * sizeof(float);
+    RopeRows rr = {k, v, cs, sn};
+    if (scores && (size_t)sh.heads * sh.context <= MAX_SCORE_FLOATS && sh.heads / sh.kv_heads <= AS_MAXG) {
+        static bool raised_v = false;
+        if (!raised_v) {
+            const hipError_t e = hipFuncSetAttribute((const void *)k_attend_values<true>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     (int)(((size_t)MAX_ATT_POSITIONS + AR_FIXED) * sizeof(float)));
+            if (e != hipSuccess) return e;
+            raised_v = true;
+        }
+        const dim3 sgrid((sh.context + AS_SP - 1) / AS_SP, sh.kv_heads);
+        hipLaunchKernelGGL(k_attend_scores<true>, sgrid, dim3(AS_WG), 0, s, q, kcache, vcache, sh, pos0, pos_dev, flag,
+                           rr, scores);
+        hipLaunchKernelGGL(k_attend_values<true>, dim3(sh.heads * groups), dim3(AR_WG), lds, s, vcache, att, sh, pos0,
+                           pos_dev, xd, xq, v, scores, flag);
+        return hipGetLastError();
+    }
     static bool raised = false;
     if (!raised) {
         const hipError_t e = hipFuncSetAttribute((const void *)k_attend_rows<true>,
@@ -2231,7 +2413,6 @@ hipError_t launch_attention_rope(const float *q, const float *k, const float *v,
         if (e != hipSuccess) return e;
         raised = true;
     }
-    RopeRows rr = {k, v, cs, sn};
     hipLaunchKernelGGL(k_attend_rows<true>, dim3(sh.heads * groups), dim3(AR_WG), lds, s, q, kcache, vcache, att, sh,
                        pos0, pos_dev, flag, xd, xq, rr);
     return hipGetLastError();

@@ -42,6 +42,10 @@ GROUP_CASES = [
     (True, 1536, [8960, 1536, 5], False),             # Q5 pairs
     (False, 896, [4864, 100], True),                  # fast contract (lane FMA)
     (True, 8960, [1536, 3], True),
+    (False, 896, [1, 4864, 31, 4864, 33, 2000], False),  # item edges inside a workgroup's tile range
+    (False, 2048, [3000, 17], True),                  # 64 blocks: the wide pinned activation
+    (True, 2560, [3000, 9], False),                   # Q5, 80 blocks
+    (False, 928, [4864, 4864], False),                # nb = 29 (odd)
 ]
 
 

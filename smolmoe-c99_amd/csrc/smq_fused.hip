@@ -22,14 +22,23 @@ namespace {
  *  EPI_GLU   items 0 and 1 are gate and up with the same rows; a workgroup
  *            owns RT/2 rows of each and stores h[r] = up[r] * (g / (1 +
  *            exp_det(-g))) (SwiGLU) or the GeGLU form (vecmath.c:78-93).
- * Every workgroup issues its first weight loads before the prologue, so the
- * prologue's loads and serial sum overlap the weight fetch. Products, chains
+ * Every workgroup issues its first weight loads during the prologue (after
+ * the RMSNorm's serial sum), and the prologue's barriers wait for LDS only,
+ * so the weight fetch overlaps the activation's quantization. Products, chains
  * and the lane tree are those of k_gemv (exact per-lane order).
  * ---------------------------------------------------------------------- */
 constexpr int PRO_NORM = 1, PRO_F32 = 2; /* SMQ_ACT_NORM, SMQ_ACT_F32 */
-constexpr uint32_t FU_BATCH = 32; /* prologue loads in flight per thread */
-static_assert(FU_BATCH * WG == MAX_NORM_K, "one batch holds the widest RMSNorm row");
+constexpr uint32_t FU_BATCH = 32; /* activation elements per thread of the widest RMSNorm row */
+static_assert(FU_BATCH * WG == MAX_NORM_K, "the widest RMSNorm row");
+constexpr uint32_t FU_SHORT = 8;  /* elements per thread loaded ahead of the weights (rows up to 2048) */
 constexpr int EPI_STORE = 0, EPI_GLU = 1;
+
+/* A workgroup barrier that orders LDS only: this thread's LDS accesses are
+ * complete, global loads may stay in flight (s_barrier without the release
+ * fence of __syncthreads, which would wait for them). */
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 __device__ __forceinline__ uint32_t find_fused_item(const FusedArgs &a, uint32_t tile) {
     uint32_t it = 0;
@@ -40,7 +49,7 @@ __device__ __forceinline__ uint32_t find_fused_item(const FusedArgs &a, uint32_t
 }
 
 template <bool Q5, bool FAST, int RT, int PRO, int EPI>
-__global__ __launch_bounds__(WG) void k_gemv_fused(FusedArgs a) {
+__global__ __launch_bounds__(WG) void k_gemv_fused(FusedArgs a, uint32_t ntiles) {
     constexpr int TB = Q5 ? 2 : 1;    /* blocks per task */
     constexpr int TPR = WG / RT;      /* tasks per row per chunk */
     constexpr int CB = TPR * TB;      /* blocks per chunk */
@@ -61,32 +70,42 @@ __global__ __launch_bounds__(WG) void k_gemv_fused(FusedArgs a) {
     float *act_d = (float *)(act_q + nb * 8);
     int *act_b = (int *)(act_d + nb); /* Q5: -16 * lane sums of x */
 
-    /* this thread's weight row */
+    /* this workgroup's tiles: a contiguous range (the grid is at most one resident wave) */
+    const uint32_t t0 = (uint32_t)((uint64_t)ntiles * blockIdx.x / gridDim.x);
+    const uint32_t t1 = (uint32_t)((uint64_t)ntiles * (blockIdx.x + 1) / gridDim.x);
+    if (t0 >= t1) return;
+    /* this thread's weight row in a tile */
     const uint32_t tr = tid / TPR, ti = tid % TPR;
-    const unsigned char *wrow;
-    size_t row_bytes;
-    bool row_ok;
-    uint32_t item = 0, r0 = 0;
-    if (EPI == EPI_GLU) {
-        constexpr uint32_t half = RT / 2 > 0 ? RT / 2 : 1;
-        const uint32_t row = blockIdx.x * half + tr % half;
-        const Item &I = a.item[tr < half ? 0 : 1];
-        row_ok = row < a.rows;
-        row_bytes = I.row_bytes;
-        wrow = I.w + (size_t)(row_ok ? row : 0) * row_bytes;
-    } else {
-        item = find_fused_item(a, blockIdx.x);
-        const Item &I = a.item[item];
-        r0 = (blockIdx.x - I.tile_begin) * RT;
-        row_ok = r0 + tr < I.rows;
-        row_bytes = I.row_bytes;
-        wrow = I.w + (size_t)(row_ok ? r0 + tr : 0) * row_bytes;
-    }
+    struct Row {
+        const unsigned char *w;
+        size_t row_bytes;
+        bool ok;
+        uint32_t item, r0;
+    };
+    auto setup = [&](uint32_t tile, Row &R) __attribute__((always_inline)) {
+        R.item = 0;
+        R.r0 = 0;
+        if (EPI == EPI_GLU) {
+            constexpr uint32_t half = RT / 2 > 0 ? RT / 2 : 1;
+            const uint32_t row = tile * half + tr % half;
+            const Item &I = a.item[tr < half ? 0 : 1];
+            R.ok = row < a.rows;
+            R.row_bytes = I.row_bytes;
+            R.w = I.w + (size_t)(R.ok ? row : 0) * R.row_bytes;
+        } else {
+            R.item = find_fused_item(a, tile);
+            const Item &I = a.item[R.item];
+            R.r0 = (tile - I.tile_begin) * RT;
+            R.ok = R.r0 + tr < I.rows;
+            R.row_bytes = I.row_bytes;
+            R.w = I.w + (size_t)(R.ok ? R.r0 + tr : 0) * R.row_bytes;
+        }
+    };
     const uint32_t nchunks = (nb + CB - 1) / CB;
     uint32_t wr[NW] = {};
-    auto load_task = [&](uint32_t b) {
-        if (row_ok && b < nb) {
-            const unsigned char *p = wrow + (size_t)b * (Q5 ? Q5_BYTES : Q8_BYTES);
+    auto load_task = [&](const Row &R, uint32_t b) __attribute__((always_inline)) {
+        if (R.ok && b < nb) {
+            const unsigned char *p = R.w + (size_t)b * (Q5 ? Q5_BYTES : Q8_BYTES);
             const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
             wr[0] = v0.x; wr[1] = v0.y; wr[2] = v0.z; wr[3] = v0.w;
             wr[4] = v1.x; wr[5] = v1.y; wr[6] = v1.z; wr[7] = v1.w;
@@ -98,52 +117,75 @@ __global__ __launch_bounds__(WG) void k_gemv_fused(FusedArgs a) {
             }
         }
     };
-    load_task(ti * TB);
+    Row cur, nxt;
+    setup(t0, cur);
 
-    /* prologue: the activation into LDS, loaded in batches of FU_BATCH
-     * elements per thread (a batch's loads all issue before any is used). The
-     * weight loads above stay in flight meanwhile. */
+    /* prologue: the activation into LDS. Rows of up to FU_SHORT elements per thread load x (and
+     * the norm weights) before the first weight loads are issued: loads complete in order, so
+     * the prologue waits for its own loads only. Wider rows load in batches of FU_SHORT per
+     * thread inside a loop. The f32 form issues the weight loads right after its x loads. */
     static_assert(PRO == PRO_NORM || PRO == PRO_F32, "a given Q8 activation takes k_gemv");
+    const uint32_t ke = (np + WG - 1) / WG; /* NORM: <= FU_BATCH (n <= MAX_NORM_K) */
+    const bool short_row = ke <= FU_SHORT;
+    float xv[FU_SHORT], wv[FU_SHORT];
+    if (short_row) {
+#pragma unroll
+        for (uint32_t k = 0; k < FU_SHORT; ++k) {
+            const uint32_t i = tid + k * WG;
+            xv[k] = k < ke && i < n ? a.src[i] : 0.0f;
+            if (PRO == PRO_NORM) wv[k] = k < ke && i < n ? a.norm[i] : 0.0f;
+        }
+    }
+    if (PRO != PRO_NORM) load_task(cur, ti * TB);
     {
-        const uint32_t ke = (np + WG - 1) / WG; /* NORM: <= FU_BATCH (n <= MAX_NORM_K) */
         int bad = 0;
         int8_t *q8 = (int8_t *)act_q;
         if (PRO == PRO_NORM) {
-            /* x, w and the squares to LDS; then the sum in order; then (x*inv)*w. (The
-             * batch loop, one trip for n <= MAX_NORM_K, keeps the batch registers'
-             * live range short: 5 workgroups per CU.) */
-            for (uint32_t k0 = 0; k0 < ke; k0 += FU_BATCH) {
-                float xv[FU_BATCH], wv[FU_BATCH];
+            /* x, w and the squares to LDS; then the sum in order; then (x*inv)*w */
+            if (short_row) {
 #pragma unroll
-                for (uint32_t k = 0; k < FU_BATCH; ++k) {
-                    const uint32_t i = tid + (k0 + k) * WG;
-                    xv[k] = i < n ? a.src[i] : 0.0f;
-                    wv[k] = i < n ? a.norm[i] : 0.0f;
-                }
-#pragma unroll
-                for (uint32_t k = 0; k < FU_BATCH; ++k) {
-                    const uint32_t i = tid + (k0 + k) * WG;
-                    if (i < n) {
+                for (uint32_t k = 0; k < FU_SHORT; ++k) {
+                    const uint32_t i = tid + k * WG;
+                    if (k < ke && i < n) {
                         sq[i] = xv[k] * xv[k];
                         xs[i] = xv[k];
                         ws[i] = wv[k];
                     }
                 }
+            } else {
+                for (uint32_t k0 = 0; k0 < ke; k0 += FU_SHORT) {
+#pragma unroll
+                    for (uint32_t k = 0; k < FU_SHORT; ++k) {
+                        const uint32_t i = tid + (k0 + k) * WG;
+                        xv[k] = i < n ? a.src[i] : 0.0f;
+                        wv[k] = i < n ? a.norm[i] : 0.0f;
+                    }
+#pragma unroll
+                    for (uint32_t k = 0; k < FU_SHORT; ++k) {
+                        const uint32_t i = tid + (k0 + k) * WG;
+                        if (i < n) {
+                            sq[i] = xv[k] * xv[k];
+                            xs[i] = xv[k];
+                            ws[i] = wv[k];
+                        }
+                    }
+                }
             }
-            __syncthreads();
+            lds_barrier();
             if (tid == 0) {
                 const float ss = serial_sum_lds(sq, n);
                 const float iv = 1.0f / sqrtf(ss / (float)n + a.eps); /* model.c:338 */
                 s_inv = iv;
                 s_bad = !(fabsf(ss) <= FLT_MAX) || !(fabsf(iv) <= FLT_MAX);
             }
-            __syncthreads();
+            lds_barrier();
+            load_task(cur, ti * TB); /* after the serial sum (measured faster than before it) */
             const float inv = s_inv;
             if (tid == 0 && s_bad && a.flag) *a.flag = 1;
-#pragma unroll
-            for (uint32_t k = 0; k < FU_BATCH; ++k) { /* uniform; a block's 32 lanes are all below np or past it */
+            /* (x*inv)*w and its Q8 blocks; uniform: a block's 32 lanes are all below np or past it */
+            auto stage = [&](uint32_t k) __attribute__((always_inline)) {
                 const uint32_t i = tid + k * WG;
-                if (k < ke && i < np) {
+                if (i < np) {
                     const bool valid = i < n;
                     float v = 0.0f;
                     if (valid) {
@@ -152,17 +194,29 @@ __global__ __launch_bounds__(WG) void k_gemv_fused(FusedArgs a) {
                     }
                     stage_q8(v, valid, i, q8, act_d, bad);
                 }
+            };
+            if (short_row) {
+#pragma unroll
+                for (uint32_t k = 0; k < FU_SHORT; ++k)
+                    if (k < ke) stage(k);
+            } else {
+                for (uint32_t k = 0; k < ke; ++k) stage(k);
+            }
+        } else if (short_row) {
+#pragma unroll
+            for (uint32_t k = 0; k < FU_SHORT; ++k) {
+                const uint32_t i = tid + k * WG;
+                if (k < ke && i < np) stage_q8(xv[k], i < n, i, q8, act_d, bad); /* uniform per block */
             }
         } else {
-            for (uint32_t k0 = 0; k0 < ke; k0 += FU_BATCH) {
-                float xv[FU_BATCH];
+            for (uint32_t k0 = 0; k0 < ke; k0 += FU_SHORT) {
 #pragma unroll
-                for (uint32_t k = 0; k < FU_BATCH; ++k) {
+                for (uint32_t k = 0; k < FU_SHORT; ++k) {
                     const uint32_t i = tid + (k0 + k) * WG;
                     xv[k] = i < n ? a.src[i] : 0.0f;
                 }
 #pragma unroll
-                for (uint32_t k = 0; k < FU_BATCH; ++k) {
+                for (uint32_t k = 0; k < FU_SHORT; ++k) {
                     const uint32_t i = tid + (k0 + k) * WG;
                     if (i < np) stage_q8(xv[k], i < n, i, q8, act_d, bad); /* uniform per block */
                 }
@@ -171,73 +225,79 @@ __global__ __launch_bounds__(WG) void k_gemv_fused(FusedArgs a) {
         if (bad && a.flag) *a.flag = 1;
     }
     if (Q5) {
-        __syncthreads();
+        lds_barrier();
         for (uint32_t i = tid; i < nb * 8; i += WG) act_b[i] = dot4(act_q[i], 0xf0f0f0f0u, 0); /* int8 0xf0 = -16 */
     }
-    __syncthreads(); /* activation staged */
+    lds_barrier(); /* activation staged */
 
-    float acc = 0.0f;
-    for (uint32_t c = 0; c < nchunks; ++c) {
-        const uint32_t bt = c * CB + ti * TB;
-        uint32_t cw[NW];
+    uint32_t step = 0; /* products buffer parity */
+    for (uint32_t tile = t0; tile < t1; ++tile) {
+        if (tile + 1 < t1) setup(tile + 1, nxt);
+        float acc = 0.0f;
+        for (uint32_t c = 0; c < nchunks; ++c, ++step) {
+            const uint32_t bt = c * CB + ti * TB;
+            uint32_t cw[NW];
 #pragma unroll
-        for (int k = 0; k < NW; ++k) cw[k] = wr[k];
-        if (c + 1 < nchunks) load_task(bt + CB);
-        float *pb = prod[c & 1];
-        if (row_ok && bt < nb) {
-            Q5Fields f[2];
-            if (Q5) q5_parse_pair(cw, f[0], f[1]);
+            for (int k = 0; k < NW; ++k) cw[k] = wr[k];
+            if (c + 1 < nchunks) load_task(cur, bt + CB); /* the next chunk, or the next tile's first, in flight */
+            else if (tile + 1 < t1) load_task(nxt, ti * TB);
+            float *pb = prod[step & 1];
+            if (cur.ok && bt < nb) {
+                Q5Fields f[2];
+                if (Q5) q5_parse_pair(cw, f[0], f[1]);
 #pragma unroll
-            for (int k = 0; k < TB; ++k) {
-                const uint32_t b = bt + k, bb = ti * TB + k;
-                const float wscale = Q5 ? f[k].scale : __uint_as_float(cw[0]);
-                const float d = wscale * act_d[b];
-                float *dst = pb + (bb / 4) * GS + tr * 32 + (bb % 4);
+                for (int k = 0; k < TB; ++k) {
+                    const uint32_t b = bt + k, bb = ti * TB + k;
+                    const float wscale = Q5 ? f[k].scale : __uint_as_float(cw[0]);
+                    const float d = wscale * act_d[b];
+                    float *dst = pb + (bb / 4) * GS + tr * 32 + (bb % 4);
 #pragma unroll
-                for (int l = 0; l < 8; ++l) {
-                    const uint32_t x = act_q[b * 8 + l];
-                    int sv;
-                    if (Q5) sv = dot4(q5_codes(f[k], l), x, act_b[b * 8 + l]);
-                    else sv = dot4(cw[1 + l], x, 0);
-                    dst[l * 4] = FAST ? (float)sv : d * (float)sv;
+                    for (int l = 0; l < 8; ++l) {
+                        const uint32_t x = act_q[b * 8 + l];
+                        int sv;
+                        if (Q5) sv = dot4(q5_codes(f[k], l), x, act_b[b * 8 + l]);
+                        else sv = dot4(cw[1 + l], x, 0);
+                        dst[l * 4] = FAST ? (float)sv : d * (float)sv;
+                    }
+                    if (FAST) dsc[step & 1][(bb / 4) * DS + tr * 4 + (bb % 4)] = d;
                 }
-                if (FAST) dsc[c & 1][(bb / 4) * DS + tr * 4 + (bb % 4)] = d;
+            }
+            __syncthreads();
+            if (tid < RT * 8) {
+                const uint32_t count = nb - c * CB < (uint32_t)CB ? nb - c * CB : (uint32_t)CB;
+                chain_sum<FAST, CB / 4>(acc, (const float4 *)pb + tid, GS / 4,
+                                        FAST ? (const float4 *)dsc[step & 1] + tid / 8 : nullptr, DS / 4, count);
             }
         }
-        __syncthreads();
-        if (tid < RT * 8) {
-            const uint32_t count = nb - c * CB < (uint32_t)CB ? nb - c * CB : (uint32_t)CB;
-            chain_sum<FAST, CB / 4>(acc, (const float4 *)pb + tid, GS / 4,
-                                    FAST ? (const float4 *)dsc[c & 1] + tid / 8 : nullptr, DS / 4, count);
-        }
-    }
 
-    if (EPI == EPI_GLU) {
-        if (tid < 64) { /* every row slot is in wave 0 */
+        if (EPI == EPI_GLU) {
+            if (tid < 64) { /* every row slot is in wave 0 */
+                const float v = reduce8_to_lane7(acc);
+                const float u = __shfl_down(v, RT * 4, 64); /* up slot tr + RT/2 */
+                const uint32_t row = tile * (RT / 2 > 0 ? RT / 2 : 1) + tid / 8;
+                if ((tid & 7) == 7 && tid < RT * 4 && row < a.rows) {
+                    const float gv = v;
+                    if (a.flag && (!(fabsf(gv) <= FLT_MAX) || !(fabsf(u) <= FLT_MAX))) *a.flag = 1; /* model.c:309 */
+                    float e;
+                    if (a.act == 2) {
+                        const float g3 = 0.044715f * gv * gv * gv;
+                        const float uu = 1.5957691216f * (gv + g3);
+                        e = exp_det(-uu);
+                    } else {
+                        e = exp_det(-gv);
+                    }
+                    const float den = 1.0f + e;
+                    const float sg = gv / den;
+                    a.h[row] = u * sg;
+                }
+            }
+        } else if (tid < RT * 8) {
             const float v = reduce8_to_lane7(acc);
-            const float u = __shfl_down(v, RT * 4, 64); /* up slot tr + RT/2 */
-            const uint32_t row = blockIdx.x * (RT / 2 > 0 ? RT / 2 : 1) + tid / 8;
-            if ((tid & 7) == 7 && tid < RT * 4 && row < a.rows) {
-                const float gv = v;
-                if (a.flag && (!(fabsf(gv) <= FLT_MAX) || !(fabsf(u) <= FLT_MAX))) *a.flag = 1; /* model.c:309 */
-                float e;
-                if (a.act == 2) {
-                    const float g3 = 0.044715f * gv * gv * gv;
-                    const float uu = 1.5957691216f * (gv + g3);
-                    e = exp_det(-uu);
-                } else {
-                    e = exp_det(-gv);
-                }
-                const float den = 1.0f + e;
-                const float sg = gv / den;
-                a.h[row] = u * sg;
-            }
+            const Item &I = a.item[cur.item];
+            const uint32_t r = cur.r0 + tid / 8;
+            if ((tid & 7) == 7 && r < I.rows) store_out(I, a.flag, 0, r, v);
         }
-    } else if (tid < RT * 8) {
-        const float v = reduce8_to_lane7(acc);
-        const Item &I = a.item[item];
-        const uint32_t r = r0 + tid / 8;
-        if ((tid & 7) == 7 && r < I.rows) store_out(I, a.flag, 0, r, v);
+        cur = nxt;
     }
 }
 
@@ -262,7 +322,22 @@ hipError_t launch_fused_rt(FusedArgs a, hipStream_t s) {
         if (e != hipSuccess) return e;
         allowed = lds;
     }
-    hipLaunchKernelGGL((k_gemv_fused<Q5, false, RT, PRO, EPI>), dim3(tiles), dim3(WG), lds, s, a);
+    /* at most one resident wave of workgroups, each taking a range of tiles: the prologue runs
+     * once per workgroup (the occupancy of this instantiation is read at the widest LDS seen) */
+    static size_t queried_lds = 0;
+    static int resident = 0;
+    if (lds > queried_lds) {
+        int per_cu = 0, dev = 0, cus = 0;
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemv_fused<Q5, false, RT, PRO, EPI>,
+                                                                    WG, lds);
+        if (e == hipSuccess) e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        resident = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+        queried_lds = lds;
+    }
+    const uint32_t grid = tiles < (uint32_t)resident ? tiles : (uint32_t)resident;
+    hipLaunchKernelGGL((k_gemv_fused<Q5, false, RT, PRO, EPI>), dim3(grid), dim3(WG), lds, s, a, tiles);
     return hipGetLastError();
 }
 

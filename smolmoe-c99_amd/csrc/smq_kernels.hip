@@ -408,18 +408,20 @@ __global__ __launch_bounds__(NT) void k_gemv_stream(GroupArgs g) {
 }
 
 /* ------------------------------------------------------------------------
- * Pinned streaming GEMV (Q8, nb <= MAX_FAST_NB): each workgroup belongs to one
- * item (the launcher gives every item a share of the resident workgroups
- * in proportion to its rows) and walks a contiguous range of that item's
- * tiles. Its activation is staged in LDS once, so a task is just the nine
- * weight dwords (plus the row's bias and prior output for the chain
- * threads), and D tasks stay in flight per thread. Products and chains as in
- * k_gemv: exact per-lane order, the fixed lane tree.
+ * Pinned streaming GEMV (Q8 nb <= MAX_FAST_NB; Q5 nb even <= PIN_NB): each
+ * workgroup belongs to one item (the launcher gives every item a share of
+ * the resident workgroups in proportion to its rows) and walks a contiguous
+ * range of that item's tiles. Its activation is staged in LDS once, so a
+ * task is just the weight dwords of one Q8 block or one Q5 pair (plus the
+ * row's bias and prior output for the chain threads), and D tasks stay in
+ * flight per thread. Products and chains as in k_gemv: exact per-lane
+ * order, the fixed lane tree.
  * ---------------------------------------------------------------------- */
 constexpr uint32_t PIN_NB = 64; /* the activation's LDS size of the narrow instantiation */
 
+template <bool Q5>
 struct PinTask {
-    uint32_t w[9];
+    uint32_t w[Q5 ? 11 : 9];
     float bias, prior;
     bool ok;
 };
@@ -434,10 +436,12 @@ __device__ __forceinline__ uint32_t find_pin_item(const GroupArgs &g, uint32_t w
     return lo;
 }
 
-/* exact contract: at least 6 waves per SIMD (three 512-thread workgroups per CU) */
-template <bool FAST, int RT, int NT, int D, uint32_t MAXNB>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(FAST ? 4 : 6, 8))) void k_gemv_pin(GroupArgs g) {
-    constexpr int TPR = NT / RT, CB = TPR, GS = RT * 32 + 4, DS = RT * 4 + 4;
+/* occupancy floor: exact Q8 6 waves per SIMD (three 512-thread workgroups per CU) */
+template <bool Q5, bool FAST, int RT, int NT, int D, uint32_t MAXNB>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FAST ? 4 : 6), 8))) void k_gemv_pin(
+    GroupArgs g) {
+    constexpr int TB = Q5 ? 2 : 1, TPR = NT / RT, CB = TPR * TB, GS = RT * 32 + 4, DS = RT * 4 + 4;
+    constexpr uint32_t BYTES = Q5 ? Q5_BYTES : Q8_BYTES;
     __shared__ __attribute__((aligned(16))) float prod[2][(CB / 4) * GS];
     __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? (CB / 4) * DS : 4];
     __shared__ __attribute__((aligned(16))) uint32_t act_q[MAXNB * 8];
@@ -462,15 +466,20 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(FAST ? 4 : 6
     for (uint32_t i = tid; i < nb; i += NT) act_d[i] = xd[i];
 
     /* step s: tile t0 + s / nchunks, chunk s % nchunks (counters, no division per step) */
-    auto load = [&](PinTask &T, uint32_t tile, uint32_t chunk, bool real) __attribute__((always_inline)) {
-        const uint32_t row0 = tile * RT, row = row0 + tr, b = chunk * CB + ti;
+    auto load = [&](PinTask<Q5> &T, uint32_t tile, uint32_t chunk, bool real) __attribute__((always_inline)) {
+        const uint32_t row0 = tile * RT, row = row0 + tr, b = chunk * CB + ti * TB;
         T.ok = real && row < rows && b < nb;
         if (T.ok) { /* idle task lanes issue nothing (the load count is per wave, not per lane) */
-            const unsigned char *p = wbase + (size_t)row * row_bytes + (size_t)b * Q8_BYTES;
+            const unsigned char *p = wbase + (size_t)row * row_bytes + (size_t)b * BYTES;
             const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
             T.w[0] = v0.x; T.w[1] = v0.y; T.w[2] = v0.z; T.w[3] = v0.w;
             T.w[4] = v1.x; T.w[5] = v1.y; T.w[6] = v1.z; T.w[7] = v1.w;
-            T.w[8] = *(const uint32_t *)(p + 32);
+            if constexpr (Q5) { /* a pair: 44 bytes */
+                const u3a v2 = *(const u3a *)(p + 32);
+                T.w[8] = v2.x; T.w[9] = v2.y; T.w[10] = v2.z;
+            } else {
+                T.w[8] = *(const uint32_t *)(p + 32);
+            }
         }
         if (tid < RT * 8) { /* the chain threads' row: its bias and prior output */
             const uint32_t orow = row0 + tid / 8, oc = orow < rows ? orow : 0;
@@ -478,7 +487,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(FAST ? 4 : 6
             T.prior = accum ? y[oc] : 0.0f;
         }
     };
-    PinTask T[D];
+    PinTask<Q5> T[D];
     uint32_t lt = t0, lc = 0; /* load cursor */
 #pragma unroll
     for (int j = 0; j < D; ++j) {
@@ -495,17 +504,25 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(FAST ? 4 : 6
             float *pb = prod[(k + j) & 1];
             float *db = dsc[FAST ? (k + j) & 1 : 0];
             if (T[j].ok) {
-                const uint32_t b = cc * CB + ti;
-                const float d = __uint_as_float(T[j].w[0]) * act_d[b];
-                float *dst = pb + (ti / 4) * GS + tr * 32 + (ti % 4);
-                const u4a xa = *(const u4a *)&act_q[b * 8], xb = *(const u4a *)&act_q[b * 8 + 4];
-                const uint32_t xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+                Q5Fields f[2];
+                if constexpr (Q5) q5_parse_pair(T[j].w, f[0], f[1]);
 #pragma unroll
-                for (int l = 0; l < 8; ++l) {
-                    const int sv = dot4(T[j].w[1 + l], xs[l], 0);
-                    dst[l * 4] = FAST ? (float)sv : d * (float)sv;
+                for (int q = 0; q < TB; ++q) {
+                    const uint32_t bb = ti * TB + q, b = cc * CB + bb;
+                    const float ws = Q5 ? f[q].scale : __uint_as_float(T[j].w[0]);
+                    const float d = ws * act_d[b];
+                    float *dst = pb + (bb / 4) * GS + tr * 32 + (bb % 4);
+                    const u4a xa = *(const u4a *)&act_q[b * 8], xb = *(const u4a *)&act_q[b * 8 + 4];
+                    const uint32_t xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) {
+                        int sv;
+                        if constexpr (Q5) sv = dot4(q5_codes(f[q], l), xs[l], dot4(xs[l], 0xf0f0f0f0u, 0));
+                        else sv = dot4(T[j].w[1 + l], xs[l], 0);
+                        dst[l * 4] = FAST ? (float)sv : d * (float)sv;
+                    }
+                    if (FAST) db[(bb / 4) * DS + tr * 4 + (bb % 4)] = d;
                 }
-                if (FAST) db[(ti / 4) * DS + tr * 4 + (ti % 4)] = d;
             }
             /* this task is consumed: its slot reloads now, a barrier and a chain earlier than
              * at the end of the step (the chain threads keep its bias and prior output) */
@@ -2135,14 +2152,17 @@ hipError_t launch_gemv_stream_typed(GroupArgs &g, int rt, hipStream_t s) {
 }
 
 /* Pinned launch: every item gets a share of the resident workgroups in
- * proportion to its tiles (at least one), each a contiguous tile range. */
-template <bool FAST, uint32_t MAXNB>
+ * proportion to its tiles (at least one), each a contiguous tile range.
+ * Q8: 16 rows x 32 blocks per 512-thread step; Q5: 8 rows x 32 pairs per
+ * 256-thread step. */
+template <bool Q5, bool FAST, uint32_t MAXNB>
 hipError_t launch_gemv_pin_nb(GroupArgs &g, hipStream_t s) {
-    constexpr int RT = 16, NT = 512, D = 2;
+    constexpr int RT = Q5 ? 8 : 16, NT = Q5 ? 256 : 512, D = 2;
     static int resident = 0;
     if (!resident) {
         int per_cu = 0, dev = 0, cus = 0;
-        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemv_pin<FAST, RT, NT, D, MAXNB>, NT, 0);
+        hipError_t e =
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemv_pin<Q5, FAST, RT, NT, D, MAXNB>, NT, 0);
         if (e == hipSuccess) e = hipGetDevice(&dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (e != hipSuccess) return e;
@@ -2160,19 +2180,21 @@ hipError_t launch_gemv_pin_nb(GroupArgs &g, hipStream_t s) {
         g.item[i].nwg = n;
         wgs += n;
     }
-    hipLaunchKernelGGL((k_gemv_pin<FAST, RT, NT, D, MAXNB>), dim3(wgs), dim3(NT), 0, s, g);
+    hipLaunchKernelGGL((k_gemv_pin<Q5, FAST, RT, NT, D, MAXNB>), dim3(wgs), dim3(NT), 0, s, g);
     return hipGetLastError();
 }
 
-template <bool FAST>
+template <bool Q5, bool FAST>
 hipError_t launch_gemv_pin(GroupArgs &g, hipStream_t s) {
-    return g.nb <= PIN_NB ? launch_gemv_pin_nb<FAST, PIN_NB>(g, s) : launch_gemv_pin_nb<FAST, MAX_FAST_NB>(g, s);
+    if (Q5 || g.nb <= PIN_NB) return launch_gemv_pin_nb<Q5, FAST, PIN_NB>(g, s);
+    return launch_gemv_pin_nb<Q5, FAST, Q5 ? PIN_NB : MAX_FAST_NB>(g, s);
 }
 
 bool gemv_pin_ok(const GroupArgs &g, bool q5) {
     const char *env = getenv("SMQ_GEMV_PIN");
     if (env && *env && atoi(env) == 0) return false;
-    return !q5 && g.nb <= MAX_FAST_NB;
+    /* Q5 pairs: narrow rows only (wide Q5 rows measure faster on the streaming kernel) */
+    return q5 ? g.nb <= PIN_NB && (g.nb & 1u) == 0 : g.nb <= MAX_FAST_NB;
 }
 
 template <bool Q5, bool FAST>
@@ -2200,7 +2222,7 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
                     it.rows = a.item[i].rows;
                     it.accumulate = a.item[i].accumulate;
                 }
-                if (gemv_pin_ok(g, Q5)) return launch_gemv_pin<FAST>(g, s);
+                if (gemv_pin_ok(g, Q5)) return launch_gemv_pin<Q5, FAST>(g, s);
                 return launch_gemv_stream_typed<Q5, FAST>(g, rt, s);
             }
             return gemv_stage(total_rows) ? launch_gemv_stage<Q5, FAST, true>(a, rt, s)
@@ -2323,7 +2345,10 @@ bool group_layout_ok(const GroupArgs &g, bool q5) {
 hipError_t launch_gemv_grouped(GroupArgs &g, bool q5, bool fast, hipStream_t s) {
     if (!g.nitems) return hipSuccess;
     if (!group_layout_ok(g, q5)) return hipErrorInvalidValue;
-    if (gemv_pin_ok(g, q5)) return fast ? launch_gemv_pin<true>(g, s) : launch_gemv_pin<false>(g, s);
+    if (gemv_pin_ok(g, q5)) {
+        if (q5) return fast ? launch_gemv_pin<true, true>(g, s) : launch_gemv_pin<true, false>(g, s);
+        return fast ? launch_gemv_pin<false, true>(g, s) : launch_gemv_pin<false, false>(g, s);
+    }
     const int rt = gemv_rows_per_tile(g.nb, q5, 0);
     if (q5) return fast ? launch_gemv_stream_typed<true, true>(g, rt, s) : launch_gemv_stream_typed<true, false>(g, rt, s);
     return fast ? launch_gemv_stream_typed<false, true>(g, rt, s) : launch_gemv_stream_typed<false, false>(g, rt, s);

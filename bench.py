@@ -28,7 +28,8 @@ ids, then 128 greedy decode steps as graph replays) with the reference's own
 model_forward on the same checkpoint as CPU rate and bit-exactness gate.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-       python bench.py --forward-only        (configs[4] alone, for profiling)
+       python bench.py --forward-only [--checkpoint PATH]   (configs[4] alone, for profiling;
+                                             PATH from python bench.py --write-checkpoint PATH)
 """
 import argparse
 import importlib
@@ -204,11 +205,21 @@ def main():
     if len(sys.argv) > 1 and sys.argv[1] == "--summarize-pmc":
         summarize_pmc(sys.argv[2], sys.argv[3])
         return
+    if len(sys.argv) > 2 and sys.argv[1] == "--write-checkpoint":
+        # the configs[4] checkpoint, written ahead of a profiled --forward-only run
+        smoe = importlib.import_module("smolmoe-c99_amd.smoe")
+        smodel = importlib.import_module("smolmoe-c99_amd.model")
+        smodel.synth_checkpoint(sys.argv[2], smoe.config_text(smoe.QWEN05), seed=4000, sigma=0.02, tied=True,
+                                threads=min(16, len(os.sched_getaffinity(0))))
+        log(f"bench: wrote {sys.argv[2]}")
+        return
     if len(sys.argv) > 1 and sys.argv[1] == "--forward-only":
-        # configs[4] alone (no CPU leg): the program the decode-step rocprofv3 summaries profile
+        # configs[4] alone (no CPU leg): the program the decode-step rocprofv3 summaries profile;
+        # --checkpoint PATH takes a file written by --write-checkpoint (and leaves it in place)
         log("bench: init", smq.init(0), smq.kernels_select())
         extra = {}
-        model_forward_extra(argparse.Namespace(no_cpu=True), extra)
+        ckpt = sys.argv[3] if len(sys.argv) > 3 and sys.argv[2] == "--checkpoint" else None
+        model_forward_extra(argparse.Namespace(no_cpu=True, checkpoint=ckpt), extra)
         print(json.dumps(extra), flush=True)
         return
     ap = argparse.ArgumentParser()
@@ -455,11 +466,13 @@ def model_forward_extra(args, extra):
     smoe = importlib.import_module("smolmoe-c99_amd.smoe")
     smodel = importlib.import_module("smolmoe-c99_amd.model")
     ncpu = len(os.sched_getaffinity(0))
-    path = os.path.join(tempfile.gettempdir(), f"smq_bench_qwen05_{os.getpid()}.smoe")
+    given = getattr(args, "checkpoint", None)
+    path = given or os.path.join(tempfile.gettempdir(), f"smq_bench_qwen05_{os.getpid()}.smoe")
     try:
         t0 = time.time()
-        smodel.synth_checkpoint(path, smoe.config_text(smoe.QWEN05), seed=4000, sigma=0.02, tied=True,
-                                threads=min(16, ncpu))
+        if not given:
+            smodel.synth_checkpoint(path, smoe.config_text(smoe.QWEN05), seed=4000, sigma=0.02, tied=True,
+                                    threads=min(16, ncpu))
         t_synth = time.time() - t0
         smq.set_checks(True)
         m = smodel.Model(path, context=1024, batch=512, logit_rows=1)
@@ -521,7 +534,7 @@ def model_forward_extra(args, extra):
     except Exception as ex:  # the model leg must not hide the matmul result
         log(f"bench: model forward leg failed: {ex!r}")
     finally:
-        if os.path.exists(path):
+        if not given and os.path.exists(path):
             os.remove(path)
 
 

@@ -54,10 +54,11 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def q8_bytes(rows, cols, ntok=1):
-    """Algorithmic bytes of one Q8 matmul: weights + int8 x + f32 x scales + f32 outputs."""
+def q8_bytes(rows, cols, ntok=1, block=36):
+    """Algorithmic bytes of one matmul (Q8 blocks of 36 B, Q5 of 22 B): weights + int8 x + f32 x scales
+    + f32 outputs."""
     nb = (cols + 31) // 32
-    return rows * nb * 36 + ntok * (nb * 32 + nb * 4) + ntok * rows * 4
+    return rows * nb * block + ntok * (nb * 32 + nb * 4) + ntok * rows * 4
 
 
 class Act:
@@ -394,6 +395,22 @@ def main():
         qx = Act(5, 1, HIDDEN)
         single("quantize_q8_4864",
                lambda i: smq.quantize_q8_rows(qx.x, 1, HIDDEN, qx.d, qx.q), HIDDEN * 4 + HIDDEN + HIDDEN // 8, 32)
+        # the single 896x896 Q8 GEMV (one launch; the 48 o-projections of the two copies in turn)
+        single("c0_gemv_896x896",
+               lambda i: smq.matmul([(copies[i // LAYERS % 2][i % LAYERS].qmat("o"), None, o_out)], ax[0].d,
+                                    ax[0].q, 1),
+               q8_bytes(DIM, Q_DIM), 2 * LAYERS, note="48 distinct 0.9 MB matrices in turn")
+        # configs[3] at batch 64 (exact GEMM; int8 MFMA)
+        hx = Act(4100, 64, DIM)
+        hout = smq.DeviceBuffer(64 * VOCAB * 4)
+        single("c3_lm_head_gemm_151936x896_b64",
+               lambda i: smq.gemm_q8(head[i % 2], 28 * 36, hx.d, hx.q, VOCAB, 64, 28, hout, VOCAB),
+               q8_bytes(VOCAB, DIM, 64), 4)
+        single("c3_lm_head_mfma_151936x896_b64",
+               lambda i: smq.gemm_q8_mfma(head[i % 2], 28 * 36, hx.d, hx.q, VOCAB, 64, 28, hout, VOCAB),
+               q8_bytes(VOCAB, DIM, 64), 4)
+        del hout
+        q5_extra(single, extra)
 
     if not args.no_extra:
         model_forward_extra(args, extra)
@@ -536,6 +553,46 @@ def model_forward_extra(args, extra):
     finally:
         if not given and os.path.exists(path):
             os.remove(path)
+
+
+def q5_extra(single, extra):
+    """Qwen2.5-1.5B-shaped Q5 matmuls 8960x1536 and 1536x8960, each as one grouped launch of 16
+    matrices with their own activations (two sets of 16 distinct 9.5 MB buffers alternated: 606 MB, past the
+    Infinity Cache; the weights are an eighth of the rows packed by the Q5 rule and repeated, which changes no
+    byte count), one matrix at batch 64 (exact GEMM, int8 MFMA); checks a grouped output against its
+    single-matrix launch bit for bit."""
+    n5 = 16
+    shapes = {"gate": (8960, 1536), "down": (1536, 8960)}
+    mats, acts, outs = {}, {}, {}
+    for k, (name, (rows, cols)) in enumerate(shapes.items()):
+        w = np.tile(synth.q5_weights(6000 + k, rows // 8, cols), (8, 1))  # an eighth of the rows, repeated
+        bufs = [smq.DeviceBuffer.from_array(w) for _ in range(2 * n5)]
+        mats[name] = [smq.QMat(b, rows, cols, smq.DTYPE_Q5) for b in bufs]
+        acts[name] = [Act(6100 + 32 * k + i, 1, cols) for i in range(n5)]
+        outs[name] = [smq.DeviceBuffer(rows * 4) for _ in range(n5)]
+    for name, (rows, cols) in shapes.items():
+        def grouped(i, name=name):
+            base = (i % 2) * n5
+            smq.gemv_grouped([(mats[name][base + j], None, outs[name][j], False, acts[name][j].d, acts[name][j].q)
+                              for j in range(n5)])
+        nbytes = n5 * q8_bytes(rows, cols, block=22)
+        single(f"c2_q5_gemv_{rows}x{cols}_group{n5}", grouped, nbytes, 8,
+               note=f"one launch of {n5} matrices with their own activations; two sets alternated (606 MB)")
+        smq.synchronize()
+        got = outs[name][3].download(np.float32)
+        one = smq.DeviceBuffer(rows * 4)
+        smq.matmul([(mats[name][3], None, one)], acts[name][3].d, acts[name][3].q, 1)
+        extra[f"c2_q5_gemv_{rows}x{cols}_group{n5}"]["bit_identical_to_single"] = bool(
+            np.array_equal(got.view(np.uint32), one.download(np.float32).view(np.uint32)))
+    bx = Act(6500, 64, 1536)
+    bout = smq.DeviceBuffer(64 * 8960 * 4)
+    nb = 1536 // 32
+    single("c2_q5_gemm_8960x1536_b64",
+           lambda i: smq.gemm_q5(mats["gate"][i % (2 * n5)].buf, nb * 22, bx.d, bx.q, 8960, 64, nb, bout, 8960),
+           q8_bytes(8960, 1536, 64, block=22), 8)
+    single("c2_q5_mfma_8960x1536_b64",
+           lambda i: smq.gemm_q5_mfma(mats["gate"][i % (2 * n5)].buf, nb * 22, bx.d, bx.q, 8960, 64, nb, bout, 8960),
+           q8_bytes(8960, 1536, 64, block=22), 8)
 
 
 def synth_q(act, cols):

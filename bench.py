@@ -28,8 +28,8 @@ ids, then 128 greedy decode steps as graph replays) with the reference's own
 model_forward on the same checkpoint as CPU rate and bit-exactness gate.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-       python bench.py --forward-only [--checkpoint PATH]   (configs[4] alone, for profiling;
-                                             PATH from python bench.py --write-checkpoint PATH)
+       python bench.py --forward-only [--checkpoint PATH] [--decode-steps N] [--profile]   (configs[4]
+                                alone, for profiling; PATH from python bench.py --write-checkpoint PATH)
 """
 import argparse
 import importlib
@@ -216,11 +216,19 @@ def main():
         return
     if len(sys.argv) > 1 and sys.argv[1] == "--forward-only":
         # configs[4] alone (no CPU leg): the program the decode-step rocprofv3 summaries profile;
-        # --checkpoint PATH takes a file written by --write-checkpoint (and leaves it in place)
+        # --checkpoint PATH takes a file written by --write-checkpoint (and leaves it in place);
+        # --decode-steps N times N greedy steps instead of 128; --profile runs the prefill and one timed
+        # decode only (the sequence the rocprofv3 kernel trace of the decode step is taken over)
+        fp = argparse.ArgumentParser()
+        fp.add_argument("--forward-only", action="store_true")
+        fp.add_argument("--checkpoint", default=None)
+        fp.add_argument("--decode-steps", type=int, default=128)
+        fp.add_argument("--profile", action="store_true")
+        fa = fp.parse_args()
         log("bench: init", smq.init(0), smq.kernels_select())
         extra = {}
-        ckpt = sys.argv[3] if len(sys.argv) > 3 and sys.argv[2] == "--checkpoint" else None
-        model_forward_extra(argparse.Namespace(no_cpu=True, checkpoint=ckpt), extra)
+        model_forward_extra(argparse.Namespace(no_cpu=True, checkpoint=fa.checkpoint, decode_steps=fa.decode_steps,
+                                               profile=fa.profile), extra)
         print(json.dumps(extra), flush=True)
         return
     ap = argparse.ArgumentParser()
@@ -484,6 +492,7 @@ def model_forward_extra(args, extra):
     smodel = importlib.import_module("smolmoe-c99_amd.model")
     ncpu = len(os.sched_getaffinity(0))
     given = getattr(args, "checkpoint", None)
+    nsteps = getattr(args, "decode_steps", 128)
     path = given or os.path.join(tempfile.gettempdir(), f"smq_bench_qwen05_{os.getpid()}.smoe")
     try:
         t0 = time.time()
@@ -500,6 +509,15 @@ def model_forward_extra(args, extra):
         m.forward(prompt, 0, smodel.LOGITS_LAST)  # warm-up: first launches, graph capture
         m.generate(512, 5)
         smq.set_checks(False)
+        if getattr(args, "profile", False):  # (a prefill between decode runs here has crashed rocprofv3 itself)
+            t0 = time.time()
+            m.generate(512, nsteps + 1)
+            dec_s = time.time() - t0
+            extra["c4_qwen05_forward"] = {"decode_tok_s": round(nsteps / dec_s, 1), "decode_steps": nsteps,
+                                          "what": "profile run: prefill 512 ids, 5 untimed and then N timed greedy "
+                                                  "decode steps"}
+            log(f"bench: qwen0.5B profile run: decode {nsteps / dec_s:.1f} tok/s")
+            return
         runs = []
         for _ in range(3):
             t0 = time.time()
@@ -507,7 +525,7 @@ def model_forward_extra(args, extra):
             t1 = time.time()
             gl = m.logits(1)
             t1b = time.time()
-            toks = m.generate(512, 129)
+            toks = m.generate(512, nsteps + 1)
             t2 = time.time()
             runs.append((t1 - t0, t2 - t1b))
         pre_s = min(r[0] for r in runs)
@@ -518,8 +536,8 @@ def model_forward_extra(args, extra):
         mfma_s = time.time() - t0
         smq.set_prefill_mfma(False)
         e = {"what": "Qwen2.5-0.5B shape (24 layers, 896/4864, GQA 14/2, vocab 151936, tied), random-init Q8, "
-                     "prefill 512 ids in one batch then 128 greedy decode steps (HIP graph per step), BOS banned",
-             "decode_tok_s": round(128 / dec_s, 1), "decode_ms_per_token": round(dec_s / 128 * 1e3, 3),
+                     f"prefill 512 ids in one batch then {nsteps} greedy decode steps (HIP graph per step), BOS banned",
+             "decode_tok_s": round(nsteps / dec_s, 1), "decode_ms_per_token": round(dec_s / nsteps * 1e3, 3),
              "prefill_tok_s": round(512 / pre_s, 1), "prefill_ms": round(pre_s * 1e3, 2),
              "prefill_mfma_tok_s": round(512 / mfma_s, 1),
              "prefill_mfma_note": "int8-MFMA prefill: exact int32 block sums, f32 block order relaxed (not bit-exact)",

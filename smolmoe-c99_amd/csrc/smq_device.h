@@ -24,13 +24,13 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-/* IEEE binary16 bits to float, exact for every input including subnormals
- * (reference: src/f16.h:10-27): subnormal m * 2^-24 is exact in binary32. */
+/* IEEE binary16 bits (the low 16 bits of h) to float: one v_cvt_f32_f16,
+ * exact for every finite input including subnormals (f16 denormals are not
+ * flushed in this build), infinities kept (reference: src/f16.h:10-27). A NaN
+ * stays a NaN, quieted as the reference's F16C path quiets it
+ * (src/kernels.c:259-261). */
 __device__ __forceinline__ float half_to_float(uint32_t h) {
-    const uint32_t e = (h >> 10) & 31u, m = h & 1023u, sign = (h & 0x8000u) << 16;
-    if (e == 31u) return __uint_as_float(sign | 0x7f800000u | (m << 13));
-    if (e != 0u) return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
-    return __uint_as_float(__float_as_uint((float)m * 0x1p-24f) | sign);
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
 /* One lane step of the contract: acc + d*f with two roundings, or fmaf. */
@@ -79,6 +79,22 @@ __device__ __forceinline__ uint32_t q5_codes(const Q5Fields &b, int l) {
     const uint32_t hb = (b.high >> (4 * l)) & 15u;
     const uint32_t spread = __umul24(hb, 0x204081u) & 0x01010101u;
     return nib | (spread << 4);
+}
+
+/* Product tile layout (pitch GS floats per four blocks): lane l of block bb
+ * sits at (bb/4)*GS + tr*32 + l*4 + bb%4, so a chain thread (row tr, lane l)
+ * reads four consecutive blocks as one float4. tile_slot is where the task
+ * starting at block bb0 writes; a Q5 pair starts at an even bb0, so its two
+ * floats of lane l are adjacent: one 8-byte write (put_lane<2>). */
+typedef float f2v __attribute__((ext_vector_type(2)));
+template <int GS>
+__device__ __forceinline__ float *tile_slot(float *pb, uint32_t tr, uint32_t bb0) {
+    return pb + (bb0 / 4) * GS + tr * 32 + (bb0 % 4);
+}
+template <int TB>
+__device__ __forceinline__ void put_lane(float *slot, int l, float v0, float v1) {
+    if constexpr (TB == 2) *(f2v *)(slot + l * 4) = f2v{v0, v1};
+    else slot[l * 4] = v0;
 }
 
 /* Signed weights q - 16 as int8 bytes: (q + 112) ^ 0x80 per byte, no carries. */

@@ -313,21 +313,26 @@ __device__ __forceinline__ void stream_products(const StreamTask<Q5> &T, float *
     if (!T.ok) return;
     Q5Fields f[2];
     if (Q5) q5_parse_pair(T.w, f[0], f[1]);
+    float d[TB];
 #pragma unroll
     for (int q = 0; q < TB; ++q) {
         const uint32_t bb = ti * TB + q;
-        const float wscale = Q5 ? f[q].scale : __uint_as_float(T.w[0]);
-        const float d = wscale * T.s[q];
-        float *dst = pb + (bb / 4) * GS + tr * 32 + (bb % 4);
+        d[q] = (Q5 ? f[q].scale : __uint_as_float(T.w[0])) * T.s[q];
+        if (FAST) db[(bb / 4) * DS + tr * 4 + (bb % 4)] = d[q];
+    }
+    float *slot = tile_slot<GS>(pb, tr, ti * TB);
 #pragma unroll
-        for (int l = 0; l < 8; ++l) {
+    for (int l = 0; l < 8; ++l) {
+        float v[TB];
+#pragma unroll
+        for (int q = 0; q < TB; ++q) {
             const uint32_t x = T.x[q * 8 + l];
             int sv;
             if (Q5) sv = dot4(q5_codes(f[q], l), x, dot4(x, 0xf0f0f0f0u, 0));
             else sv = dot4(T.w[1 + l], x, 0);
-            dst[l * 4] = FAST ? (float)sv : d * (float)sv;
+            v[q] = FAST ? (float)sv : d[q] * (float)sv;
         }
-        if (FAST) db[(bb / 4) * DS + tr * 4 + (bb % 4)] = d;
+        put_lane<TB>(slot, l, v[0], v[TB - 1]);
     }
 }
 
@@ -417,7 +422,8 @@ __global__ __launch_bounds__(NT) void k_gemv_stream(GroupArgs g) {
  * flight per thread. Products and chains as in k_gemv: exact per-lane
  * order, the fixed lane tree.
  * ---------------------------------------------------------------------- */
-constexpr uint32_t PIN_NB = 64; /* the activation's LDS size of the narrow instantiation */
+constexpr uint32_t PIN_NB = 64;  /* the activation's LDS size of the narrow instantiation */
+constexpr uint32_t PIN_NB1 = 32; /* Q8: one chunk of a 16-row tile (512 threads / 16 rows) */
 
 template <bool Q5>
 struct PinTask {
@@ -442,6 +448,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
     GroupArgs g) {
     constexpr int TB = Q5 ? 2 : 1, TPR = NT / RT, CB = TPR * TB, GS = RT * 32 + 4, DS = RT * 4 + 4;
     constexpr uint32_t BYTES = Q5 ? Q5_BYTES : Q8_BYTES;
+    constexpr bool HOIST = (uint32_t)CB >= MAXNB;
     __shared__ __attribute__((aligned(16))) float prod[2][(CB / 4) * GS];
     __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? (CB / 4) * DS : 4];
     __shared__ __attribute__((aligned(16))) uint32_t act_q[MAXNB * 8];
@@ -495,6 +502,23 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
         if (++lc == nchunks) { lc = 0; ++lt; }
     }
     __syncthreads(); /* activation staged */
+    /* one chunk covers the row (CB >= MAXNB >= nb): a thread's blocks are the
+     * same at every step, so their activation words, scales and Q5 offsets
+     * c = -16 * (sum of the four int8 of a lane) live in registers */
+    uint32_t hx_q[HOIST ? TB : 1][8], hx_c[HOIST && Q5 ? TB : 1][8];
+    float hx_d[HOIST ? TB : 1];
+    if constexpr (HOIST) {
+#pragma unroll
+        for (int q = 0; q < TB; ++q) {
+            const uint32_t b = ti * TB + q; /* < CB <= MAXNB: inside the staged arrays */
+            hx_d[q] = act_d[b];
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                hx_q[q][l] = act_q[b * 8 + l];
+                if constexpr (Q5) hx_c[q][l] = dot4(hx_q[q][l], 0xf0f0f0f0u, 0);
+            }
+        }
+    }
     uint32_t ct = t0, cc = 0; /* chain cursor */
     float acc = 0.0f, bias = 0.0f, prior = 0.0f;
     for (uint32_t k = 0; k < my_steps; k += D) {
@@ -506,22 +530,35 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
             if (T[j].ok) {
                 Q5Fields f[2];
                 if constexpr (Q5) q5_parse_pair(T[j].w, f[0], f[1]);
+                float d[TB];
+                uint32_t xs[TB][8];
 #pragma unroll
                 for (int q = 0; q < TB; ++q) {
                     const uint32_t bb = ti * TB + q, b = cc * CB + bb;
-                    const float ws = Q5 ? f[q].scale : __uint_as_float(T[j].w[0]);
-                    const float d = ws * act_d[b];
-                    float *dst = pb + (bb / 4) * GS + tr * 32 + (bb % 4);
-                    const u4a xa = *(const u4a *)&act_q[b * 8], xb = *(const u4a *)&act_q[b * 8 + 4];
-                    const uint32_t xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+                    d[q] = (Q5 ? f[q].scale : __uint_as_float(T[j].w[0])) * (HOIST ? hx_d[q] : act_d[b]);
+                    if (FAST) db[(bb / 4) * DS + tr * 4 + (bb % 4)] = d[q];
+                    if constexpr (HOIST) {
 #pragma unroll
-                    for (int l = 0; l < 8; ++l) {
-                        int sv;
-                        if constexpr (Q5) sv = dot4(q5_codes(f[q], l), xs[l], dot4(xs[l], 0xf0f0f0f0u, 0));
-                        else sv = dot4(T[j].w[1 + l], xs[l], 0);
-                        dst[l * 4] = FAST ? (float)sv : d * (float)sv;
+                        for (int l = 0; l < 8; ++l) xs[q][l] = hx_q[q][l];
+                    } else {
+                        const u4a xa = *(const u4a *)&act_q[b * 8], xb = *(const u4a *)&act_q[b * 8 + 4];
+                        xs[q][0] = xa.x; xs[q][1] = xa.y; xs[q][2] = xa.z; xs[q][3] = xa.w;
+                        xs[q][4] = xb.x; xs[q][5] = xb.y; xs[q][6] = xb.z; xs[q][7] = xb.w;
                     }
-                    if (FAST) db[(bb / 4) * DS + tr * 4 + (bb % 4)] = d;
+                }
+                float *slot = tile_slot<GS>(pb, tr, ti * TB);
+#pragma unroll
+                for (int l = 0; l < 8; ++l) {
+                    float v[TB];
+#pragma unroll
+                    for (int q = 0; q < TB; ++q) {
+                        int sv;
+                        if constexpr (Q5)
+                            sv = dot4(q5_codes(f[q], l), xs[q][l], HOIST ? hx_c[q][l] : dot4(xs[q][l], 0xf0f0f0f0u, 0));
+                        else sv = dot4(T[j].w[1 + l], xs[q][l], 0);
+                        v[q] = FAST ? (float)sv : d[q] * (float)sv;
+                    }
+                    put_lane<TB>(slot, l, v[0], v[TB - 1]);
                 }
             }
             /* this task is consumed: its slot reloads now, a barrier and a chain earlier than
@@ -2186,6 +2223,9 @@ hipError_t launch_gemv_pin_nb(GroupArgs &g, hipStream_t s) {
 
 template <bool Q5, bool FAST>
 hipError_t launch_gemv_pin(GroupArgs &g, hipStream_t s) {
+    /* Q8 rows of at most one chunk (32 blocks: K <= 1024) keep their activation in registers */
+    if constexpr (!Q5)
+        if (g.nb <= PIN_NB1) return launch_gemv_pin_nb<Q5, FAST, PIN_NB1>(g, s);
     if (Q5 || g.nb <= PIN_NB) return launch_gemv_pin_nb<Q5, FAST, PIN_NB>(g, s);
     return launch_gemv_pin_nb<Q5, FAST, Q5 ? PIN_NB : MAX_FAST_NB>(g, s);
 }

@@ -46,6 +46,12 @@ GROUP_CASES = [
     (False, 2048, [3000, 17], True),                  # 64 blocks: the wide pinned activation
     (True, 2560, [3000, 9], False),                   # Q5, 80 blocks
     (False, 928, [4864, 4864], False),                # nb = 29 (odd)
+    (False, 1024, [4864, 17], False),                 # nb = 32: the widest one-chunk (register) activation
+    (False, 1000, [300, 2], True),                    # nb = 32 with a partial last block, fast
+    (False, 1056, [500, 9], True),                    # nb = 33: the first two-chunk row
+    (False, 20, [600, 3], False),                     # nb = 1: most threads of a tile idle
+    (True, 2048, [700, 3], True),                     # Q5, 64 blocks (the widest pinned pair row), fast
+    (True, 64, [100, 1], False),                      # Q5, one pair per row
 ]
 
 

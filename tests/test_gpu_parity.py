@@ -338,6 +338,26 @@ def test_dequantize_rows(orc):
             assert_same_f32(out.download(np.float32), orc.dequantize_row(w, cols, q5=q5), "dequant")
 
 
+def test_q5_scale_every_f16(orc):
+    """Every one of the 65,536 f16 scale patterns through the Q5 row
+    dequantization (q = 17, so each value is the scale itself): the device
+    conversion against numpy's exact binary16 -> binary32 (finite values,
+    subnormals and infinities bit for bit, NaN where NaN) and the oracle."""
+    nblk = 1 << 16
+    blocks = np.zeros((nblk, 22), np.uint8)
+    blocks[:, 0:2] = np.arange(nblk, dtype=np.uint16).view(np.uint8).reshape(nblk, 2)
+    blocks[:, 2:6] = 0xFF                       # high bit set for all 32 codes
+    blocks[:, 6:22] = 0x11                      # low nibbles 1: q = 17, q - 16 = 1
+    w = blocks.reshape(-1)
+    cols = nblk * 32
+    out = smq.DeviceBuffer(cols * 4)
+    smq.dequantize_q5_row(smq.DeviceBuffer.from_array(w), cols, out)
+    got = out.download(np.float32).reshape(nblk, 32)
+    want = np.arange(nblk, dtype=np.uint16).view(np.float16).astype(np.float32)
+    assert_same_f32(got, np.repeat(want[:, None], 32, axis=1), "f16 scales")
+    assert_same_f32(got.reshape(-1), orc.dequantize_row(w, cols, q5=True), "f16 scales vs oracle")
+
+
 @pytest.mark.parametrize("rt", [1, 2, 4, 8, 16])
 @pytest.mark.parametrize("stage", [0, 1])
 def test_every_gemv_tile_variant(orc, rt, stage, monkeypatch):

@@ -19,7 +19,10 @@ typedef uint32_t u4a __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u3a __attribute__((ext_vector_type(3), aligned(4)));
 typedef float f4v __attribute__((ext_vector_type(4))); /* register-resident float4 (no struct copies) */
 
-/* Exact int32 sum of four int8 products plus c (v_dot4_i32_i8). */
+/* Exact int32 sum of four int8 products plus c (v_dot4_i32_i8). The
+ * compiler's own instruction, not inline assembly: a dot product's result
+ * needs wait states before a VALU reads it, and only the compiler's hazard
+ * pass inserts them. */
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
@@ -72,13 +75,18 @@ __device__ __forceinline__ void q5_parse_pair(const uint32_t d[11], Q5Fields &b0
 }
 
 /* Lane l's four 5-bit codes q in [0, 31] as bytes: low nibble | high bit << 4.
- * The high bits 4l..4l+3 are spread to bit 0 of each byte by a multiply
- * (x * 0x204081 moves bit i to bit 8i; the partial products do not overlap). */
+ * The lane's high bits (h bits 4l..4l+3) sit in the upper nibble of byte l/2
+ * of one of two words shared by four lanes each (even lanes (h << 4) &
+ * 0xf0f0f0f0, odd lanes h & 0xf0f0f0f0). That byte v = bits << 4 times
+ * 0x204081 puts bit i at 8i + 4: the sixteen partial products land on
+ * distinct bits (no carries) and the mask keeps the four wanted ones. */
 __device__ __forceinline__ uint32_t q5_codes(const Q5Fields &b, int l) {
+    const uint32_t src = (l & 1) ? (b.high & 0xf0f0f0f0u) : ((b.high << 4) & 0xf0f0f0f0u);
+    /* byte l/2, already shifted: the multiply needs no constant wider than 24
+     * bits, so it stays one v_mul_u32_u24 */
+    const uint32_t spread = __umul24((src >> (8 * (l >> 1))) & 0xffu, 0x204081u);
     const uint32_t nib = l < 4 ? (b.nib[l] & 0x0f0f0f0fu) : ((b.nib[l - 4] >> 4) & 0x0f0f0f0fu);
-    const uint32_t hb = (b.high >> (4 * l)) & 15u;
-    const uint32_t spread = __umul24(hb, 0x204081u) & 0x01010101u;
-    return nib | (spread << 4);
+    return (spread & 0x10101010u) | nib;
 }
 
 /* Product tile layout (pitch GS floats per four blocks): lane l of block bb

@@ -59,6 +59,7 @@ struct GroupArgs {
     GroupItem item[MAX_GROUP_ITEMS];
     uint32_t nitems, nb, total_tiles;
     int *flag;
+    uint32_t cpr, nch, rt; /* pinned launch: tasks per chunk, chunks per row, rows per tile */
 };
 /* Layout the streaming kernel needs: 4-byte aligned rows, Q5 nb even. */
 bool group_layout_ok(const GroupArgs &g, bool q5);

@@ -413,17 +413,35 @@ __global__ __launch_bounds__(NT) void k_gemv_stream(GroupArgs g) {
 }
 
 /* ------------------------------------------------------------------------
- * Pinned streaming GEMV (Q8 nb <= MAX_FAST_NB; Q5 nb even <= PIN_NB): each
- * workgroup belongs to one item (the launcher gives every item a share of
- * the resident workgroups in proportion to its rows) and walks a contiguous
- * range of that item's tiles. Its activation is staged in LDS once, so a
- * task is just the weight dwords of one Q8 block or one Q5 pair (plus the
- * row's bias and prior output for the chain threads), and D tasks stay in
- * flight per thread. Products and chains as in k_gemv: exact per-lane
- * order, the fixed lane tree.
+ * Pinned streaming GEMV (Q8 nb <= MAX_FAST_NB; Q5 nb even, <= MAX_FAST_NB):
+ * each workgroup belongs to one item (the launcher gives every item a share
+ * of the resident workgroups in proportion to its rows) and walks a
+ * contiguous range of that item's tiles. Its activation is staged in LDS
+ * once, so a task is just the weight dwords of one Q8 block or one Q5 pair
+ * (plus the row's bias and prior output for the chain threads), and D tasks
+ * stay in flight per thread. Products and chains as in k_gemv: exact
+ * per-lane order, the fixed lane tree.
+ *
+ * The tile is shaped to the row at launch: a row of ppr tasks is cut into
+ * nch chunks of cpr tasks (pin_cpr at most), and a tile is rt rows (NT / cpr,
+ * within PIN_RT and the product buffer), so rt * cpr of the NT threads hold
+ * a task (row tid / cpr, task tid % cpr): 28-block Q8 rows run 18 rows of 28
+ * threads, 24-pair Q5 rows 10 rows of 24. ONE: a single chunk per row.
  * ---------------------------------------------------------------------- */
-constexpr uint32_t PIN_NB = 64;  /* the activation's LDS size of the narrow instantiation */
-constexpr uint32_t PIN_NB1 = 32; /* Q8: one chunk of a 16-row tile (512 threads / 16 rows) */
+/* Tasks per chunk at most: a Q8 chunk stays within 32 blocks (the chain
+ * threads' short path), a Q5 chunk within 64 pairs. */
+template <bool Q5>
+constexpr uint32_t pin_cpr() { return Q5 ? 64u : 32u; }
+constexpr uint32_t PIN_RT = 32; /* rows per tile at most */
+
+/* Rows per tile for chunks of c tasks: as many as the threads allow, at most
+ * PIN_RT, and within a product buffer of pf floats (ceil(tb*c/4) groups of
+ * rt*32 + 4: eight lanes of four blocks per row and a pad). */
+__host__ __device__ constexpr uint32_t pin_rows(uint32_t nt, uint32_t tb, uint32_t c, uint32_t pf) {
+    const uint32_t groups = (tb * c + 3) / 4, by_lds = (pf / groups - 4) / 32;
+    const uint32_t r = nt / c < PIN_RT ? nt / c : PIN_RT;
+    return r < by_lds ? r : by_lds;
+}
 
 template <bool Q5>
 struct PinTask {
@@ -442,40 +460,43 @@ __device__ __forceinline__ uint32_t find_pin_item(const GroupArgs &g, uint32_t w
     return lo;
 }
 
-/* occupancy floor: exact Q8 6 waves per SIMD (three 512-thread workgroups per CU) */
-template <bool Q5, bool FAST, int RT, int NT, int D, uint32_t MAXNB>
+/* occupancy floor: exact Q8 6 waves per SIMD (three 512-thread workgroups per CU);
+ * PF: floats of one product buffer (the launcher keeps rt within it) */
+template <bool Q5, bool FAST, bool ONE, int NT, int D, uint32_t MAXNB, uint32_t PF>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FAST ? 4 : 6), 8))) void k_gemv_pin(
     GroupArgs g) {
-    constexpr int TB = Q5 ? 2 : 1, TPR = NT / RT, CB = TPR * TB, GS = RT * 32 + 4, DS = RT * 4 + 4;
+    constexpr int TB = Q5 ? 2 : 1;
+    constexpr bool HOIST = ONE && Q5;
     constexpr uint32_t BYTES = Q5 ? Q5_BYTES : Q8_BYTES;
-    constexpr bool HOIST = (uint32_t)CB >= MAXNB;
-    __shared__ __attribute__((aligned(16))) float prod[2][(CB / 4) * GS];
-    __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? (CB / 4) * DS : 4];
+    __shared__ __attribute__((aligned(16))) float prod[2][PF];
+    __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? PF / 8 + 128 : 4];
     __shared__ __attribute__((aligned(16))) uint32_t act_q[MAXNB * 8];
     __shared__ float act_d[MAXNB];
 
-    const uint32_t tid = threadIdx.x, tr = tid / TPR, ti = tid % TPR, nb = g.nb;
+    const uint32_t tid = threadIdx.x, nb = g.nb, cpr = g.cpr, nch = ONE ? 1u : g.nch, rt = g.rt;
+    const uint32_t tr = tid / cpr, ti = tid % cpr, cb = cpr * TB; /* cb: blocks per chunk */
+    const uint32_t gs = rt * 32 + 4, ds = rt * 4 + 4, chains = rt * 8;
     const GroupItem &I = g.item[find_pin_item(g, blockIdx.x)];
-    const uint32_t wg = blockIdx.x - I.wg_begin, item_tiles = (I.rows + RT - 1) / RT;
+    const uint32_t wg = blockIdx.x - I.wg_begin, item_tiles = (I.rows + rt - 1) / rt;
     const uint32_t t0 = (uint32_t)((uint64_t)item_tiles * wg / I.nwg);
     const uint32_t t1 = (uint32_t)((uint64_t)item_tiles * (wg + 1) / I.nwg);
-    const uint32_t nchunks = (nb + CB - 1) / CB, my_steps = (t1 - t0) * nchunks;
+    const uint32_t my_steps = (t1 - t0) * nch;
     const unsigned char *wbase = I.w;
     const size_t row_bytes = I.row_bytes;
     const uint32_t rows = I.rows;
     const float *bias_p = I.bias, *xd = I.xd;
     float *y = I.y;
-    const bool accum = I.accumulate != 0;
+    const bool accum = I.accumulate != 0, worker = tr < rt;
 
     /* the activation, once (kernels.c:912-935 layout: nb scales, nb*8 words) */
     const uint32_t *xq32 = (const uint32_t *)I.xq;
     for (uint32_t i = tid; i < nb * 8; i += NT) act_q[i] = xq32[i];
     for (uint32_t i = tid; i < nb; i += NT) act_d[i] = xd[i];
 
-    /* step s: tile t0 + s / nchunks, chunk s % nchunks (counters, no division per step) */
+    /* step s: tile t0 + s / nch, chunk s % nch (counters, no division per step) */
     auto load = [&](PinTask<Q5> &T, uint32_t tile, uint32_t chunk, bool real) __attribute__((always_inline)) {
-        const uint32_t row0 = tile * RT, row = row0 + tr, b = chunk * CB + ti * TB;
-        T.ok = real && row < rows && b < nb;
+        const uint32_t row0 = tile * rt, row = row0 + tr, b = chunk * cb + ti * TB;
+        T.ok = real && worker && row < rows && b < nb;
         if (T.ok) { /* idle task lanes issue nothing (the load count is per wave, not per lane) */
             const unsigned char *p = wbase + (size_t)row * row_bytes + (size_t)b * BYTES;
             const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
@@ -488,7 +509,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
                 T.w[8] = *(const uint32_t *)(p + 32);
             }
         }
-        if (tid < RT * 8) { /* the chain threads' row: its bias and prior output */
+        if (tid < chains) { /* the chain threads' row: its bias and prior output */
             const uint32_t orow = row0 + tid / 8, oc = orow < rows ? orow : 0;
             T.bias = bias_p ? bias_p[oc] : 0.0f;
             T.prior = accum ? y[oc] : 0.0f;
@@ -499,23 +520,23 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
 #pragma unroll
     for (int j = 0; j < D; ++j) {
         load(T[j], lt, lc, (uint32_t)j < my_steps);
-        if (++lc == nchunks) { lc = 0; ++lt; }
+        if (++lc == nch) { lc = 0; ++lt; }
     }
     __syncthreads(); /* activation staged */
-    /* one chunk covers the row (CB >= MAXNB >= nb): a thread's blocks are the
-     * same at every step, so their activation words, scales and Q5 offsets
-     * c = -16 * (sum of the four int8 of a lane) live in registers */
-    uint32_t hx_q[HOIST ? TB : 1][8], hx_c[HOIST && Q5 ? TB : 1][8];
+    /* Q5, one chunk: a thread's blocks are the same at every step, so their
+     * activation words, scales and offsets c = -16 * (sum of the four int8 of
+     * a lane) live in registers (idle threads read clamped, unused indices) */
+    uint32_t hx_q[HOIST ? TB : 1][8], hx_c[HOIST ? TB : 1][8];
     float hx_d[HOIST ? TB : 1];
     if constexpr (HOIST) {
 #pragma unroll
         for (int q = 0; q < TB; ++q) {
-            const uint32_t b = ti * TB + q; /* < CB <= MAXNB: inside the staged arrays */
+            const uint32_t b0 = ti * TB + q, b = b0 < nb ? b0 : nb - 1;
             hx_d[q] = act_d[b];
 #pragma unroll
             for (int l = 0; l < 8; ++l) {
                 hx_q[q][l] = act_q[b * 8 + l];
-                if constexpr (Q5) hx_c[q][l] = dot4(hx_q[q][l], 0xf0f0f0f0u, 0);
+                hx_c[q][l] = dot4(hx_q[q][l], 0xf0f0f0f0u, 0);
             }
         }
     }
@@ -534,9 +555,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
                 uint32_t xs[TB][8];
 #pragma unroll
                 for (int q = 0; q < TB; ++q) {
-                    const uint32_t bb = ti * TB + q, b = cc * CB + bb;
+                    const uint32_t bb = ti * TB + q, b = cc * cb + bb;
                     d[q] = (Q5 ? f[q].scale : __uint_as_float(T[j].w[0])) * (HOIST ? hx_d[q] : act_d[b]);
-                    if (FAST) db[(bb / 4) * DS + tr * 4 + (bb % 4)] = d[q];
+                    if (FAST) db[(bb / 4) * ds + tr * 4 + (bb % 4)] = d[q];
                     if constexpr (HOIST) {
 #pragma unroll
                         for (int l = 0; l < 8; ++l) xs[q][l] = hx_q[q][l];
@@ -546,7 +567,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
                         xs[q][4] = xb.x; xs[q][5] = xb.y; xs[q][6] = xb.z; xs[q][7] = xb.w;
                     }
                 }
-                float *slot = tile_slot<GS>(pb, tr, ti * TB);
+                const uint32_t bb0 = ti * TB;
+                float *slot = pb + (bb0 / 4) * gs + tr * 32 + (bb0 % 4);
 #pragma unroll
                 for (int l = 0; l < 8; ++l) {
                     float v[TB];
@@ -565,19 +587,20 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
              * at the end of the step (the chain threads keep its bias and prior output) */
             const float tbias = T[j].bias, tprior = T[j].prior;
             load(T[j], lt, lc, k + j + D < my_steps);
-            if (++lc == nchunks) { lc = 0; ++lt; }
+            if (++lc == nch) { lc = 0; ++lt; }
             __syncthreads();
-            if (tid < RT * 8) {
+            if (tid < chains) {
                 if (cc == 0) {
                     bias = tbias;
                     prior = tprior;
                 }
-                const uint32_t count = nb - cc * CB < (uint32_t)CB ? nb - cc * CB : (uint32_t)CB;
-                chain_sum<FAST, CB / 4>(acc, (const float4 *)pb + tid, GS / 4,
-                                        FAST ? (const float4 *)db + tid / 8 : nullptr, DS / 4, count);
-                if (cc + 1 == nchunks) {
+                const uint32_t count = nb - cc * cb < cb ? nb - cc * cb : cb;
+                const float4 *pp = (const float4 *)pb + tid, *dp = FAST ? (const float4 *)db + tid / 8 : nullptr;
+                if (!Q5 || cb <= 32) chain_sum<FAST, 8>(acc, pp, gs / 4, dp, ds / 4, count);
+                else chain_sum<FAST, 32>(acc, pp, gs / 4, dp, ds / 4, count);
+                if (cc + 1 == nch) {
                     const float v = reduce8_to_lane7(acc);
-                    const uint32_t r = ct * RT + tid / 8;
+                    const uint32_t r = ct * rt + tid / 8;
                     if ((tid & 7) == 7 && r < rows) {
                         float o = v;
                         if (bias_p) o = o + bias; /* model.c:259-262 */
@@ -588,7 +611,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
                     acc = 0.0f;
                 }
             }
-            if (++cc == nchunks) { cc = 0; ++ct; }
+            if (++cc == nch) { cc = 0; ++ct; }
         }
     }
 }
@@ -2192,49 +2215,59 @@ hipError_t launch_gemv_stream_typed(GroupArgs &g, int rt, hipStream_t s) {
  * proportion to its tiles (at least one), each a contiguous tile range.
  * Q8: 16 rows x 32 blocks per 512-thread step; Q5: 8 rows x 32 pairs per
  * 256-thread step. */
-template <bool Q5, bool FAST, uint32_t MAXNB>
-hipError_t launch_gemv_pin_nb(GroupArgs &g, hipStream_t s) {
-    constexpr int RT = Q5 ? 8 : 16, NT = Q5 ? 256 : 512, D = 2;
+/* The pinned launch: the tile shape for the row width (see k_gemv_pin), then
+ * each item's share of the resident workgroups in proportion to its tiles.
+ * LDS per workgroup (product buffers, the staged activation) is sized for
+ * three resident workgroups per CU (four for one-chunk Q5 rows). */
+template <bool Q5, bool FAST, bool ONE>
+hipError_t launch_gemv_pin_shape(GroupArgs &g, hipStream_t s) {
+    constexpr int NT = Q5 ? 256 : 512, D = 2;
+    constexpr uint32_t TB = Q5 ? 2 : 1, CPR = pin_cpr<Q5>();
+    constexpr uint32_t MAXNB = ONE ? CPR * TB : MAX_FAST_NB;
+    constexpr uint32_t PF = Q5 && ONE ? 4480 : (ONE ? 4832 : 4400); /* LDS is allocated in 512-byte units */
+    const uint32_t ppr = (g.nb + TB - 1) / TB;
+    g.nch = (ppr + CPR - 1) / CPR;
+    g.cpr = (ppr + g.nch - 1) / g.nch;
+    g.rt = pin_rows(NT, TB, g.cpr, PF);
+    if (g.nb > MAXNB || (ONE && g.nch != 1) || g.rt == 0) return hipErrorInvalidValue; /* launcher precondition */
     static int resident = 0;
     if (!resident) {
         int per_cu = 0, dev = 0, cus = 0;
-        hipError_t e =
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemv_pin<Q5, FAST, RT, NT, D, MAXNB>, NT, 0);
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, k_gemv_pin<Q5, FAST, ONE, NT, D, MAXNB, PF>, NT, 0);
         if (e == hipSuccess) e = hipGetDevice(&dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (e != hipSuccess) return e;
         resident = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
     }
     uint64_t tiles = 0;
-    for (uint32_t i = 0; i < g.nitems; ++i) tiles += (g.item[i].rows + RT - 1) / RT;
+    for (uint32_t i = 0; i < g.nitems; ++i) tiles += (g.item[i].rows + g.rt - 1) / g.rt;
     if (!tiles) return hipSuccess;
     uint32_t wgs = 0;
     for (uint32_t i = 0; i < g.nitems; ++i) {
-        const uint32_t t = (g.item[i].rows + RT - 1) / RT;
+        const uint32_t t = (g.item[i].rows + g.rt - 1) / g.rt;
         uint32_t n = (uint32_t)(((uint64_t)resident * t + tiles / 2) / tiles);
         n = n < 1 ? 1 : (n > t ? t : n);
         g.item[i].wg_begin = wgs;
         g.item[i].nwg = n;
         wgs += n;
     }
-    hipLaunchKernelGGL((k_gemv_pin<Q5, FAST, RT, NT, D, MAXNB>), dim3(wgs), dim3(NT), 0, s, g);
+    hipLaunchKernelGGL((k_gemv_pin<Q5, FAST, ONE, NT, D, MAXNB, PF>), dim3(wgs), dim3(NT), 0, s, g);
     return hipGetLastError();
 }
 
 template <bool Q5, bool FAST>
 hipError_t launch_gemv_pin(GroupArgs &g, hipStream_t s) {
-    /* Q8 rows of at most one chunk (32 blocks: K <= 1024) keep their activation in registers */
-    if constexpr (!Q5)
-        if (g.nb <= PIN_NB1) return launch_gemv_pin_nb<Q5, FAST, PIN_NB1>(g, s);
-    if (Q5 || g.nb <= PIN_NB) return launch_gemv_pin_nb<Q5, FAST, PIN_NB>(g, s);
-    return launch_gemv_pin_nb<Q5, FAST, Q5 ? PIN_NB : MAX_FAST_NB>(g, s);
+    const uint32_t ppr = Q5 ? (g.nb + 1) / 2 : g.nb;
+    if (ppr <= pin_cpr<Q5>()) return launch_gemv_pin_shape<Q5, FAST, true>(g, s);
+    return launch_gemv_pin_shape<Q5, FAST, false>(g, s);
 }
 
 bool gemv_pin_ok(const GroupArgs &g, bool q5) {
     const char *env = getenv("SMQ_GEMV_PIN");
     if (env && *env && atoi(env) == 0) return false;
-    /* Q5 pairs: narrow rows only (wide Q5 rows measure faster on the streaming kernel) */
-    return q5 ? g.nb <= PIN_NB && (g.nb & 1u) == 0 : g.nb <= MAX_FAST_NB;
+    /* Q5: whole pairs (nb even) */
+    return g.nb <= MAX_FAST_NB && (!q5 || (g.nb & 1u) == 0);
 }
 
 template <bool Q5, bool FAST>

@@ -468,7 +468,8 @@ def main():
                    "parallelism": "none (1 GPU)"},
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
         "decode_tok_s": extra.get("c4_qwen05_forward", {}).get("decode_tok_s"),
-        "roofline": {"kernel": "k_gemv_pin<exact,RT=16,NT=512,D=2> (48 gate/up GEMVs 4864x896, one launch)",
+        "roofline": {"kernel": "k_gemv_pin<exact, one chunk, NT=512, D=2>: 18-row x 28-block tiles (48 gate/up GEMVs "
+                               "4864x896, one launch)",
                      "bound": "hbm",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,

@@ -162,6 +162,44 @@ __device__ __forceinline__ void chain_add(float &acc, const float4 (&v)[G], cons
             if (4 * (q0 + (uint32_t)u) + (uint32_t)c < count) acc = FAST ? __builtin_fmaf(f[c], e[c], acc) : acc + e[c];
     }
 }
+/* One chain thread's step over nq <= NQ groups of four products (block
+ * order), where every slot of a group past the row's last block holds +0.0:
+ * adding +0.0 (or fma(0, 0, acc) in fast mode) leaves acc unchanged, since
+ * acc is never -0.0 (it starts at +0.0, and a round-to-nearest sum is -0.0
+ * only when both terms are). So the chain is NQ*4 plain dependent adds, with
+ * no per-element guard on it; every group is read at once and groups past nq
+ * read as zeros, selected off the chain. */
+template <bool FAST, int NQ>
+__device__ __forceinline__ void chain_sum_padded(float &acc, const float4 *p, uint32_t ps, const float4 *d,
+                                                 uint32_t dst, uint32_t nq) {
+    const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 x[NQ], w[NQ];
+#pragma unroll
+    for (uint32_t u = 0; u < NQ; ++u) {
+        const uint32_t gc = u < nq ? u : 0;
+        const float4 t = p[gc * ps];
+        x[u] = u < nq ? t : zero;
+        if (FAST) {
+            const float4 tw = d[gc * dst];
+            w[u] = u < nq ? tw : zero;
+        }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < NQ; ++u) {
+        if (FAST) {
+            acc = __builtin_fmaf(w[u].x, x[u].x, acc);
+            acc = __builtin_fmaf(w[u].y, x[u].y, acc);
+            acc = __builtin_fmaf(w[u].z, x[u].z, acc);
+            acc = __builtin_fmaf(w[u].w, x[u].w, acc);
+        } else {
+            acc = acc + x[u].x;
+            acc = acc + x[u].y;
+            acc = acc + x[u].z;
+            acc = acc + x[u].w;
+        }
+    }
+}
+
 template <bool FAST, int NQ>
 __device__ __forceinline__ void chain_sum(float &acc, const float4 *p, uint32_t ps, const float4 *d, uint32_t dst,
                                           uint32_t count) {

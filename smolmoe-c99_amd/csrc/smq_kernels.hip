@@ -492,6 +492,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
     const uint32_t *xq32 = (const uint32_t *)I.xq;
     for (uint32_t i = tid; i < nb * 8; i += NT) act_q[i] = xq32[i];
     for (uint32_t i = tid; i < nb; i += NT) act_d[i] = xd[i];
+    if constexpr (ONE && !Q5) { /* +0.0 in the slots past the last block, never written after (chain_sum_padded) */
+        for (uint32_t i = tid; i < 2 * PF; i += NT) (&prod[0][0])[i] = 0.0f;
+        if constexpr (FAST)
+            for (uint32_t i = tid; i < 2 * (PF / 8 + 128); i += NT) (&dsc[0][0])[i] = 0.0f;
+    }
 
     /* step s: tile t0 + s / nch, chunk s % nch (counters, no division per step) */
     auto load = [&](PinTask<Q5> &T, uint32_t tile, uint32_t chunk, bool real) __attribute__((always_inline)) {
@@ -596,7 +601,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
                 }
                 const uint32_t count = nb - cc * cb < cb ? nb - cc * cb : cb;
                 const float4 *pp = (const float4 *)pb + tid, *dp = FAST ? (const float4 *)db + tid / 8 : nullptr;
-                if (!Q5 || cb <= 32) chain_sum<FAST, 8>(acc, pp, gs / 4, dp, ds / 4, count);
+                if constexpr (ONE && !Q5) chain_sum_padded<FAST, 8>(acc, pp, gs / 4, dp, ds / 4, (nb + 3) / 4);
+                else if (!Q5 || cb <= 32) chain_sum<FAST, 8>(acc, pp, gs / 4, dp, ds / 4, count);
                 else chain_sum<FAST, 32>(acc, pp, gs / 4, dp, ds / 4, count);
                 if (cc + 1 == nch) {
                     const float v = reduce8_to_lane7(acc);

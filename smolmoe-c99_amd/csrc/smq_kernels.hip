@@ -468,8 +468,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
     constexpr int TB = Q5 ? 2 : 1;
     constexpr bool HOIST = ONE && Q5;
     constexpr uint32_t BYTES = Q5 ? Q5_BYTES : Q8_BYTES;
-    __shared__ __attribute__((aligned(16))) float prod[2][PF];
-    __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? PF / 8 + 128 : 4];
+    /* one chunk: each buffer ends in a sink for the product writes of idle task lanes */
+    __shared__ __attribute__((aligned(16))) float prod[2][PF + (ONE ? 32 : 0)];
+    __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? PF / 8 + 128 + (ONE ? 4 : 0) : 4];
     __shared__ __attribute__((aligned(16))) uint32_t act_q[MAXNB * 8];
     __shared__ float act_d[MAXNB];
 
@@ -502,8 +503,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
     auto load = [&](PinTask<Q5> &T, uint32_t tile, uint32_t chunk, bool real) __attribute__((always_inline)) {
         const uint32_t row0 = tile * rt, row = row0 + tr, b = chunk * cb + ti * TB;
         T.ok = real && worker && row < rows && b < nb;
-        if (T.ok) { /* idle task lanes issue nothing (the load count is per wave, not per lane) */
-            const unsigned char *p = wbase + (size_t)row * row_bytes + (size_t)b * BYTES;
+        auto fetch = [&](const unsigned char *p) __attribute__((always_inline)) {
             const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
             T.w[0] = v0.x; T.w[1] = v0.y; T.w[2] = v0.z; T.w[3] = v0.w;
             T.w[4] = v1.x; T.w[5] = v1.y; T.w[6] = v1.z; T.w[7] = v1.w;
@@ -513,11 +513,29 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
             } else {
                 T.w[8] = *(const uint32_t *)(p + 32);
             }
-        }
-        if (tid < chains) { /* the chain threads' row: its bias and prior output */
-            const uint32_t orow = row0 + tid / 8, oc = orow < rows ? orow : 0;
-            T.bias = bias_p ? bias_p[oc] : 0.0f;
-            T.prior = accum ? y[oc] : 0.0f;
+        };
+        if constexpr (ONE) {
+            /* every thread issues the same loads at every step, outside any
+             * branch (an idle task re-reads a block of its own or the last row:
+             * in bounds, unused), so the compiler's in-order wait counts stay
+             * exact and the next task stays in flight across the step */
+            const uint32_t rc = row < rows ? row : rows - 1, bc = b < nb ? b : 0;
+            fetch(wbase + (size_t)rc * row_bytes + (size_t)bc * BYTES);
+            /* the chain threads' row: its bias and prior output (the other threads
+             * read the tile's first row; an absent one reads the activation's
+             * first scale: unused) */
+            const uint32_t orow = row0 + (tid < chains ? tid / 8 : 0), oc = orow < rows ? orow : rows - 1;
+            T.bias = *(bias_p ? bias_p + oc : xd);
+            T.prior = *(accum ? y + oc : xd);
+        } else {
+            /* several chunks per row: idle task lanes issue nothing (measured
+             * faster here than the branch-free form) */
+            if (T.ok) fetch(wbase + (size_t)row * row_bytes + (size_t)b * BYTES);
+            if (tid < chains) {
+                const uint32_t orow = row0 + tid / 8, oc = orow < rows ? orow : 0;
+                T.bias = bias_p ? bias_p[oc] : 0.0f;
+                T.prior = accum ? y[oc] : 0.0f;
+            }
         }
     };
     PinTask<Q5> T[D];
@@ -553,16 +571,17 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
             if (k + j >= my_steps) break;
             float *pb = prod[(k + j) & 1];
             float *db = dsc[FAST ? (k + j) & 1 : 0];
-            if (T[j].ok) {
+            if (ONE || T[j].ok) { /* one chunk: every lane forms products, an idle task's go to the sink */
+                const bool ok = T[j].ok;
                 Q5Fields f[2];
                 if constexpr (Q5) q5_parse_pair(T[j].w, f[0], f[1]);
                 float d[TB];
                 uint32_t xs[TB][8];
 #pragma unroll
                 for (int q = 0; q < TB; ++q) {
-                    const uint32_t bb = ti * TB + q, b = cc * cb + bb;
+                    const uint32_t bb = ti * TB + q, b0 = cc * cb + bb, b = b0 < nb ? b0 : nb - 1;
                     d[q] = (Q5 ? f[q].scale : __uint_as_float(T[j].w[0])) * (HOIST ? hx_d[q] : act_d[b]);
-                    if (FAST) db[(bb / 4) * ds + tr * 4 + (bb % 4)] = d[q];
+                    if (FAST) db[ok ? (bb / 4) * ds + tr * 4 + (bb % 4) : PF / 8 + 128 + q] = d[q];
                     if constexpr (HOIST) {
 #pragma unroll
                         for (int l = 0; l < 8; ++l) xs[q][l] = hx_q[q][l];
@@ -573,7 +592,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
                     }
                 }
                 const uint32_t bb0 = ti * TB;
-                float *slot = pb + (bb0 / 4) * gs + tr * 32 + (bb0 % 4);
+                float *slot = ok ? pb + (bb0 / 4) * gs + tr * 32 + (bb0 % 4) : pb + PF;
 #pragma unroll
                 for (int l = 0; l < 8; ++l) {
                     float v[TB];

@@ -516,15 +516,18 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
         };
         if constexpr (ONE) {
             /* every thread issues the same loads at every step, outside any
-             * branch (an idle task re-reads a block of its own or the last row:
-             * in bounds, unused), so the compiler's in-order wait counts stay
-             * exact and the next task stays in flight across the step */
-            const uint32_t rc = row < rows ? row : rows - 1, bc = b < nb ? b : 0;
+             * branch, so the compiler's in-order wait counts stay exact and the
+             * next task stays in flight across the step. An idle task re-reads
+             * bytes this workgroup reads anyway (past its range: its last tile;
+             * a spare thread: the tile's first row; past the row: its block 0;
+             * past the matrix: the last row), so no extra HBM traffic. */
+            const uint32_t tl = real ? tile : t1 - 1, rl = tl * rt + (worker ? tr : 0);
+            const uint32_t rc = rl < rows ? rl : rows - 1, bc = b < nb ? b : 0;
             fetch(wbase + (size_t)rc * row_bytes + (size_t)bc * BYTES);
             /* the chain threads' row: its bias and prior output (the other threads
              * read the tile's first row; an absent one reads the activation's
              * first scale: unused) */
-            const uint32_t orow = row0 + (tid < chains ? tid / 8 : 0), oc = orow < rows ? orow : rows - 1;
+            const uint32_t orow = tl * rt + (tid < chains ? tid / 8 : 0), oc = orow < rows ? orow : rows - 1;
             T.bias = *(bias_p ? bias_p + oc : xd);
             T.prior = *(accum ? y + oc : xd);
         } else {

@@ -426,7 +426,8 @@ __global__ __launch_bounds__(NT) void k_gemv_stream(GroupArgs g) {
  * nch chunks of cpr tasks (pin_cpr at most), and a tile is rt rows (NT / cpr,
  * within PIN_RT and the product buffer), so rt * cpr of the NT threads hold
  * a task (row tid / cpr, task tid % cpr): 28-block Q8 rows run 18 rows of 28
- * threads, 24-pair Q5 rows 10 rows of 24. ONE: a single chunk per row.
+ * threads of 512, 24-pair Q5 rows 20 rows of 24 of 512. ONE: a single chunk
+ * per row.
  * ---------------------------------------------------------------------- */
 /* Tasks per chunk at most: a Q8 chunk stays within 32 blocks (the chain
  * threads' short path), a Q5 chunk within 64 pairs. */
@@ -2246,13 +2247,18 @@ hipError_t launch_gemv_stream_typed(GroupArgs &g, int rt, hipStream_t s) {
 /* The pinned launch: the tile shape for the row width (see k_gemv_pin), then
  * each item's share of the resident workgroups in proportion to its tiles.
  * LDS per workgroup (product buffers, the staged activation) is sized for
- * three resident workgroups per CU (four for one-chunk Q5 rows). */
+ * three resident workgroups per CU (Q8, fast Q5: four for one-chunk rows) or
+ * two (exact Q5). */
 template <bool Q5, bool FAST, bool ONE>
 hipError_t launch_gemv_pin_shape(GroupArgs &g, hipStream_t s) {
-    constexpr int NT = Q5 ? 256 : 512, D = 2;
+    /* exact Q5: 512 threads, two workgroups per CU (measured 10-16 % faster than
+     * four of 256 threads: larger tiles, fewer barriers per byte); fast Q5
+     * keeps 256 (its registers allow three waves per SIMD) */
+    constexpr int NT = Q5 && FAST ? 256 : 512, D = 2;
     constexpr uint32_t TB = Q5 ? 2 : 1, CPR = pin_cpr<Q5>();
     constexpr uint32_t MAXNB = ONE ? CPR * TB : MAX_FAST_NB;
-    constexpr uint32_t PF = Q5 && ONE ? 4480 : (ONE ? 4832 : 4400); /* LDS is allocated in 512-byte units */
+    /* floats of one product buffer; LDS is allocated in 512-byte units */
+    constexpr uint32_t PF = Q5 ? (FAST ? (ONE ? 4480 : 4400) : 7776) : (ONE ? 4832 : 4400);
     const uint32_t ppr = (g.nb + TB - 1) / TB;
     g.nch = (ppr + CPR - 1) / CPR;
     g.cpr = (ppr + g.nch - 1) / g.nch;

@@ -1997,6 +1997,151 @@ __global__ __launch_bounds__(AR_WG) __attribute__((amdgpu_waves_per_eu(1, 2))) v
                    att + (size_t)h * AR_HD + j0, xd ? xd + blk : nullptr, xq ? xq + (size_t)blk * QK : nullptr, flag);
 }
 
+/* Prefill attention (many tokens, head_dim 64): workgroup (token, KV head)
+ * serves all query heads of the group, so each K and V row is read once per
+ * group instead of once per head and column half, and a workgroup's
+ * registers and LDS are small enough for several per CU. Same arithmetic as
+ * attend_f32 (kernels.c:1154-1176) and k_attend_rows, bit for bit:
+ * 1. scores: eight threads per position, lane l accumulating q[8e+l]*k[8e+l]
+ *    over e in order (the 8-lane dot_f32), the fixed lane tree, times 1/8;
+ * 2. the maximum (order-free; NaN never wins), exp_det(s - max) in parallel;
+ * 3. each head's total in position order by one lane;
+ * 4. thread (head, j) sums (s_p * inv) * v_p[j] in position order, v rows
+ *    read a batch ahead;
+ * 5. the 64 outputs of a head, and with xd their two Q8 blocks. */
+constexpr uint32_t AG_WG = 512, AG_MAXG = 8, AG_MAXP = 1024, AG_VB = 16;
+
+__global__ __launch_bounds__(AG_WG) void k_attend_group(const float *q, const float *kcache, const float *vcache,
+                                                        float *att, AttnShape sh, uint32_t pos0,
+                                                        const int32_t *pos_dev, int *flag, float *xd, int8_t *xq) {
+    __shared__ __attribute__((aligned(16))) float sc[AG_MAXG * AG_MAXP];
+    __shared__ float qs[AG_MAXG * AR_HD];
+    __shared__ float hmax[AG_MAXG][AG_WG / 8];
+    __shared__ float hinv[AG_MAXG];
+    __shared__ uint64_t etab[32];
+    const uint32_t tid = threadIdx.x, grp = sh.heads / sh.kv_heads, kvd = sh.kv_dim;
+    const uint32_t t = blockIdx.x / sh.kv_heads, kh = blockIdx.x % sh.kv_heads;
+    const uint32_t pos = (pos_dev ? (uint32_t)*pos_dev : pos0) + t;
+    if (pos >= sh.context) { /* the scores row holds at most context positions */
+        if (tid == 0 && flag) *flag = 1;
+        return;
+    }
+    const uint32_t start = sh.window && pos >= sh.window ? pos - sh.window + 1 : 0, np = pos - start + 1;
+    const float *kbase = kcache + (size_t)start * kvd + (size_t)kh * AR_HD;
+    const float *vbase = vcache + (size_t)start * kvd + (size_t)kh * AR_HD;
+    const float *qg = q + (size_t)t * sh.q_dim + (size_t)kh * grp * AR_HD;
+    for (uint32_t i = tid; i < grp * AR_HD; i += AG_WG) qs[i] = qg[i];
+    if (tid < 32) etab[tid] = EXP2_TABLE[tid];
+    __syncthreads();
+
+    /* 1. scores */
+    const uint32_t l = tid & 7u, gi = tid >> 3;
+    float qr[AG_MAXG][8], mx[AG_MAXG];
+#pragma unroll
+    for (uint32_t hh = 0; hh < AG_MAXG; ++hh) {
+        mx[hh] = -FLT_MAX;
+#pragma unroll
+        for (uint32_t e = 0; e < 8; ++e) qr[hh][e] = hh < grp ? qs[hh * AR_HD + 8 * e + l] : 0.0f;
+    }
+    const float factor = 1.0f / sqrtf((float)AR_HD);
+    for (uint32_t p = gi; p < np; p += AG_WG / 8) { /* all eight threads of a group take the same positions */
+        const float *kr = kbase + (size_t)p * kvd + l;
+        float kv[8];
+#pragma unroll
+        for (uint32_t e = 0; e < 8; ++e) kv[e] = kr[8 * e];
+#pragma unroll
+        for (uint32_t hh = 0; hh < AG_MAXG; ++hh) {
+            if (hh < grp) { /* uniform */
+                float a = 0.0f;
+#pragma unroll
+                for (uint32_t e = 0; e < 8; ++e) {
+                    const float pr = qr[hh][e] * kv[e];
+                    a = a + pr;
+                }
+                const float sv = reduce8_to_lane7(a) * factor;
+                if (l == 7) {
+                    sc[hh * AG_MAXP + p] = sv;
+                    mx[hh] = sv > mx[hh] ? sv : mx[hh];
+                }
+            }
+        }
+    }
+    if (l == 7)
+#pragma unroll
+        for (uint32_t hh = 0; hh < AG_MAXG; ++hh) hmax[hh][gi] = mx[hh];
+    __syncthreads();
+    if (tid < grp) {
+        float m = -FLT_MAX;
+        for (uint32_t k = 0; k < AG_WG / 8; ++k) m = hmax[tid][k] > m ? hmax[tid][k] : m;
+        hmax[tid][0] = m;
+    }
+    __syncthreads();
+
+    /* 2. exp_det(s - max) */
+    for (uint32_t hh = 0; hh < grp; ++hh) {
+        const float high = hmax[hh][0];
+        for (uint32_t p = tid; p < np; p += AG_WG) sc[hh * AG_MAXP + p] = exp_det_tab(sc[hh * AG_MAXP + p] - high, etab);
+    }
+    __syncthreads();
+
+    /* 3. totals in position order */
+    if (tid < grp) hinv[tid] = 1.0f / serial_sum_lds(sc + tid * AG_MAXP, np);
+    __syncthreads();
+
+    /* 4. values: wave hh (64 threads) is head kh*grp + hh, thread j its column */
+    const uint32_t hh = tid / AR_HD, j = tid % AR_HD;
+    if (hh >= grp) return; /* whole waves */
+    const float inv = hinv[hh];
+    const float *srow = sc + hh * AG_MAXP, *vcol = vbase + j;
+    float vb[2][AG_VB];
+    auto vload = [&](float (&v)[AG_VB], uint32_t p0) __attribute__((always_inline)) {
+#pragma unroll
+        for (uint32_t u = 0; u < AG_VB; ++u) {
+            const uint32_t p = p0 + u < np ? p0 + u : np - 1; /* in bounds; unused past np */
+            v[u] = vcol[(size_t)p * kvd];
+        }
+    };
+    float acc = 0.0f;
+    vload(vb[0], 0);
+    uint32_t p0 = 0;
+    auto vadd = [&](const float (&v)[AG_VB], uint32_t b0) __attribute__((always_inline)) {
+#pragma unroll
+        for (uint32_t u = 0; u < AG_VB; ++u) {
+            const float w = srow[b0 + u < np ? b0 + u : np - 1] * inv; /* kernels.c:1165: w = scores[p] * inv */
+            const float pr = w * v[u];
+            acc = acc + (b0 + u < np ? pr : 0.0f); /* past np: +0.0, which leaves acc unchanged */
+        }
+    };
+    for (; p0 + AG_VB < np; p0 += 2 * AG_VB) {
+        vload(vb[1], p0 + AG_VB);
+        vadd(vb[0], p0);
+        if (p0 + 2 * AG_VB < np) vload(vb[0], p0 + 2 * AG_VB);
+        vadd(vb[1], p0 + AG_VB);
+    }
+    if (p0 < np) vadd(vb[0], p0);
+
+    /* 5. the outputs and their Q8 blocks (lanes 0-31 and 32-63: one block each) */
+    const uint32_t head = kh * grp + hh;
+    att[(size_t)t * sh.q_dim + (size_t)head * AR_HD + j] = acc;
+    if (xd) {
+        const float av = fabsf(acc);
+        const float mxa = max32(av);
+        const uint64_t badm = __ballot(!(av <= FLT_MAX));
+        const bool bad = ((j < 32 ? badm : badm >> 32) & 0xffffffffull) != 0;
+        const float scale = mxa / 127.0f;
+        const float qinv = scale >= FLT_MIN ? 1.0f / scale : 0.0f;
+        const float pq = acc * qinv;
+        int qi = (int)__builtin_rintf(pq);
+        qi = qi > 127 ? 127 : (qi < -127 ? -127 : qi);
+        const size_t blk = (size_t)t * (sh.q_dim / QK) + (size_t)head * (AR_HD / QK) + j / QK;
+        xq[blk * QK + j % QK] = (int8_t)qi;
+        if (j % QK == 0) {
+            xd[blk] = scale;
+            if (bad && flag) *flag = 1;
+        }
+    }
+}
+
 /* Greedy choice (sampler.c:57-63): the first non-banned id, replaced by any
  * later id with a strictly greater logit. Equivalently: the lowest id of the
  * largest non-NaN logit, unless the first candidate itself is NaN (then that
@@ -2470,6 +2615,12 @@ hipError_t launch_rope_kv(float *q, float *k, const float *v, uint32_t ntok, con
     return hipGetLastError();
 }
 
+/* SMQ_ATT_GROUP=0 sends prefill attention to k_attend_rows instead (tuning, tests) */
+bool att_group_on() {
+    const char *e = getenv("SMQ_ATT_GROUP");
+    return !(e && *e && atoi(e) == 0);
+}
+
 bool attention_rows_ok(const AttnShape &sh, const void *q, const void *kcache, const void *vcache) {
     return sh.head_dim == AR_HD && ((uintptr_t)q & 15) == 0 && ((uintptr_t)kcache & 15) == 0 &&
            ((uintptr_t)vcache & 15) == 0;
@@ -2483,6 +2634,12 @@ hipError_t launch_attention(const float *q, const float *kcache, const float *vc
         (xd && sh.head_dim % QK))
         return hipErrorInvalidValue;
     const uint32_t groups = (sh.head_dim + ATT_JW - 1) / ATT_JW;
+    if (ntok > 1 && attention_rows_ok(sh, q, kcache, vcache) && sh.context <= AG_MAXP &&
+        sh.heads % sh.kv_heads == 0 && sh.heads / sh.kv_heads <= AG_MAXG && att_group_on()) {
+        hipLaunchKernelGGL(k_attend_group, dim3(ntok * sh.kv_heads), dim3(AG_WG), 0, s, q, kcache, vcache, att, sh, pos0,
+                           pos_dev, flag, xd, xq);
+        return hipGetLastError();
+    }
     if (attention_rows_ok(sh, q, kcache, vcache)) {
         const size_t lds = (((size_t)sh.context + 3) / 4 * 4 + (size_t)AR_FIXED) * sizeof(float);
         static bool raised_rows = false;

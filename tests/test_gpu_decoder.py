@@ -94,6 +94,9 @@ ATT_CASES = [
     (2, 1, 64, 0, 8192, 1, 8000, 1.0),   # 63 value chunks through both buffers
     (4, 2, 128, 0, 2048, 2, 1500, 1.0),  # head_dim 128: 64-position chunks
     (2, 1, 256, 0, 600, 1, 590, 1.0),    # head_dim 256: four outputs per lane
+    (16, 2, 64, 0, 1024, 3, 1021, 1.0),  # grouped prefill: eight heads per KV head, up to 1024 positions
+    (6, 3, 64, 37, 200, 40, 100, 1.0),   # grouped prefill with a sliding window
+    (7, 7, 64, 0, 33, 33, 0, 1.0),       # grouped prefill: one head per group, from position 0
 ]
 
 
@@ -117,6 +120,7 @@ def test_attention(orc, heads, kv_heads, hd, window, context, ntok, pos0, scale)
     (14, 2, 64, 0, 1024, 1, 700),   # decode: one launch quantizes its head's blocks
     (4, 2, 96, 7, 300, 9, 100),     # head_dim 96: three blocks, the last lane group half used
     (3, 1, 40, 0, 64, 5, 20),       # head_dim % 32 != 0: attention, then a separate quantize
+    (14, 2, 64, 0, 600, 20, 500),   # grouped prefill: two Q8 blocks per head
 ])
 def test_attention_q8(orc, heads, kv_heads, hd, window, context, ntok, pos0):
     say("attention_q8", heads, kv_heads, hd, window, context, ntok, pos0)

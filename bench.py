@@ -214,6 +214,21 @@ def main():
                                 threads=min(16, len(os.sched_getaffinity(0))))
         log(f"bench: wrote {sys.argv[2]}")
         return
+    if len(sys.argv) > 1 and sys.argv[1] == "--q5-only":
+        # configs[2] alone (the grouped Q5 GEMVs and batch-64 GEMMs): the program the Q5 rocprofv3 summary profiles
+        log("bench: init", smq.init(0), smq.kernels_select())
+        extra = {}
+
+        def single(name, fn, nbytes, per_graph, reps=10, note=None):
+            gs = [smq.capture(lambda: [fn(i) for i in range(per_graph)] and None)]
+            timed_graph(gs, 2)
+            ms = timed_graph(gs, reps) / per_graph
+            extra[name] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                           "pct_hbm_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
+            log(f"bench: {name} {ms * 1e3:.2f} us {extra[name]['GBps']} GB/s")
+        q5_extra(single, extra)
+        print(json.dumps(extra), flush=True)
+        return
     if len(sys.argv) > 1 and sys.argv[1] == "--forward-only":
         # configs[4] alone (no CPU leg): the program the decode-step rocprofv3 summaries profile;
         # --checkpoint PATH takes a file written by --write-checkpoint (and leaves it in place);

@@ -340,7 +340,7 @@ def main():
     same_as_sequential = all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(gpu_layer0, seq_layer0))
     log(f"bench: FFN step streamed {ms_per_step * 1e3:.1f} us, {value:.0f} GB/s")
 
-    # dominant kernel: the gate/up group launch (k_gemv_pin<exact, RT=16, NT=512, D=2>, 235 MB), eight launches
+    # dominant kernel: the gate/up group launch (k_gemv_pin<exact, one chunk, NT=512, D=2>: 18-row tiles, 235 MB), eight launches
     # per graph (the two copies alternating) so that one graph launch's host overhead is spread over eight
     per_graph = 8
     gu_graphs = [smq.capture(lambda: [gateup_group(copies[i % 2]) for i in range(per_graph)] and None)]

@@ -30,6 +30,7 @@ model_forward on the same checkpoint as CPU rate and bit-exactness gate.
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
        python bench.py --forward-only [--checkpoint PATH] [--decode-steps N] [--profile]   (configs[4]
                                 alone, for profiling; PATH from python bench.py --write-checkpoint PATH)
+       python bench.py --q5-only   (configs[2] alone, for profiling)
 """
 import argparse
 import importlib

@@ -962,13 +962,17 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(MatArgs a, uint32_t tok_tiles,
             }
         };
         if (count == (uint32_t)MT_CB) {
-            /* all MFMAs of the chunk first (16 independent ones per wave), then
-             * the scale epilogue in block order */
-            v4i S[MT_CB][2];
+            /* half a chunk's MFMAs at a time (eight independent ones per wave),
+             * then their scale epilogue in block order: half the accumulation
+             * registers of a whole chunk, so three waves fit per SIMD */
 #pragma unroll
-            for (int bb = 0; bb < MT_CB; ++bb) block_sums(bb, S[bb]);
+            for (int h0 = 0; h0 < MT_CB; h0 += MT_CB / 2) {
+                v4i S[MT_CB / 2][2];
 #pragma unroll
-            for (int bb = 0; bb < MT_CB; ++bb) epilogue(bb, S[bb]);
+                for (int bb = 0; bb < MT_CB / 2; ++bb) block_sums(h0 + bb, S[bb]);
+#pragma unroll
+                for (int bb = 0; bb < MT_CB / 2; ++bb) epilogue(h0 + bb, S[bb]);
+            }
         } else {
             for (uint32_t bb = 0; bb < count; ++bb) {
                 v4i S[2];

@@ -811,18 +811,21 @@ __global__ __launch_bounds__(WG) void k_gemm_exact(MatArgs a, uint32_t tok_tiles
  * The per-block integer sums are bit-exact; the f32 result differs from the
  * eight-lane contract only in rounding (within 1e-5 relative).
  * Workgroup tile: 32 rows x 64 tokens; wave w owns rows 16*(w/2).. and tokens
- * 32*(w%2).. (two 16x16 tiles). K is staged in chunks of 8 blocks, stored in
+ * 32*(w%2).. (two 16x16 tiles). K is staged in chunks of MT_CB blocks, stored in
  * MFMA operand order so that a wave's operand read is one contiguous 512-byte
  * run: A[block][k8 chunk][row] and B[block][k8 chunk][token], 8 bytes each.
  * Operand layout (16x16x32 i8): lane l supplies A[l%16][8*(l/16)+0..7] and
  * B[8*(l/16)+0..7][l%16]; it receives D[4*(l/16)+v][l%16], v = 0..3.
  * SUMS writes the raw block sums instead (test entry point).
  * ---------------------------------------------------------------------- */
-constexpr int MT_R = 32, MT_T = 64, MT_CB = 8;
+constexpr int MT_R = 32, MT_T = 64, MT_CB = 14; /* 14 blocks: a 896-wide row in two chunks */
+constexpr int MT_WT = 32 * MT_CB / 2;           /* staging threads of the weights (two blocks each) */
+constexpr int MT_XP = 64 * MT_CB * 2 / 256;     /* 16-byte activation pieces per thread */
+constexpr int MT_XS = (64 * MT_CB + 255) / 256; /* activation scales per thread (last one partial) */
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 template <bool Q5, bool SUMS>
-__global__ __launch_bounds__(WG) void k_gemm_mfma(MatArgs a, uint32_t tok_tiles, int32_t *sums) {
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_gemm_mfma(MatArgs a, uint32_t tok_tiles, int32_t *sums) {
     __shared__ __attribute__((aligned(16))) uint2 wqa[MT_CB][4][MT_R];
     __shared__ __attribute__((aligned(16))) uint2 xqb[MT_CB][4][MT_T];
     __shared__ __attribute__((aligned(16))) float wsl[MT_CB][MT_R];
@@ -840,15 +843,15 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(MatArgs a, uint32_t tok_tiles,
      * writes 32 consecutive rows of one block. Activations: a wave stages one
      * (block, half) for 64 consecutive tokens (one contiguous LDS run). */
     const uint32_t srow = tid % 32, spair = tid / 32;
-    const bool srow_ok = tid < 128 && r0 + srow < I.rows;
+    const bool srow_ok = tid < MT_WT && r0 + srow < I.rows;
     const unsigned char *wrow = I.w + (size_t)(srow_ok ? r0 + srow : 0) * I.row_bytes;
 
     uint32_t wr[Q5 ? 11 : 18] = {};
-    u4a xr[4] = {};
-    float xs[2] = {};
+    u4a xr[MT_XP] = {};
+    float xs[MT_XS] = {};
     auto fetch = [&](uint32_t c) {
         const uint32_t b = c * MT_CB + spair * 2;
-        if (tid < 128) {
+        if (tid < MT_WT) {
             if (Q5) {
                 if (srow_ok && b < nb) {
                     const unsigned char *p = wrow + (size_t)b * Q5_BYTES;
@@ -870,23 +873,23 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(MatArgs a, uint32_t tok_tiles,
                     }
             }
         }
-        /* 64 tokens x 8 blocks x 32 bytes = 1024 pieces of 16 bytes, 4 per thread */
+        /* 64 tokens x MT_CB blocks x 32 bytes in 16-byte pieces, MT_XP per thread */
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
+        for (int h = 0; h < MT_XP; ++h) {
             const uint32_t piece = tid + WG * h, tok = piece % 64, rest = piece / 64, bb = rest / 2, half = rest % 2;
             const uint32_t t = t0 + tok, b = c * MT_CB + bb;
             if (t < a.ntok && b < nb)
                 xr[h] = *(const u4a *)(a.xq + ((size_t)t * a.xstride + b) * QK + half * 16);
         }
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < MT_XS; ++h) {
             const uint32_t e = tid + WG * h, tok = e / MT_CB, bb = e % MT_CB;
             const uint32_t t = t0 + tok, b = c * MT_CB + bb;
-            if (t < a.ntok && b < nb) xs[h] = a.xd[(size_t)t * a.xstride + b];
+            if (e < 64u * MT_CB && t < a.ntok && b < nb) xs[h] = a.xd[(size_t)t * a.xstride + b];
         }
     };
     auto stage = [&](uint32_t c) {
-        if (tid < 128) {
+        if (tid < MT_WT) {
             const uint32_t b = c * MT_CB + spair * 2;
             Q5Fields f[2];
             if (Q5) q5_parse_pair(wr, f[0], f[1]);
@@ -903,16 +906,16 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(MatArgs a, uint32_t tok_tiles,
             }
         }
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
+        for (int h = 0; h < MT_XP; ++h) {
             const uint32_t piece = tid + WG * h, tok = piece % 64, rest = piece / 64, bb = rest / 2, half = rest % 2;
             const bool ok = t0 + tok < a.ntok && c * MT_CB + bb < nb;
             xqb[bb][2 * half][tok] = ok ? make_uint2(xr[h].x, xr[h].y) : make_uint2(0u, 0u);
             xqb[bb][2 * half + 1][tok] = ok ? make_uint2(xr[h].z, xr[h].w) : make_uint2(0u, 0u);
         }
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < MT_XS; ++h) {
             const uint32_t e = tid + WG * h, tok = e / MT_CB, bb = e % MT_CB;
-            xsl[bb][tok] = (t0 + tok < a.ntok && c * MT_CB + bb < nb) ? xs[h] : 0.0f;
+            if (e < 64u * MT_CB) xsl[bb][tok] = (t0 + tok < a.ntok && c * MT_CB + bb < nb) ? xs[h] : 0.0f;
         }
     };
 
@@ -962,16 +965,19 @@ __global__ __launch_bounds__(WG) void k_gemm_mfma(MatArgs a, uint32_t tok_tiles,
             }
         };
         if (count == (uint32_t)MT_CB) {
-            /* half a chunk's MFMAs at a time (eight independent ones per wave),
-             * then their scale epilogue in block order: half the accumulation
-             * registers of a whole chunk, so three waves fit per SIMD */
+            /* four blocks' MFMAs at a time (eight independent ones per wave),
+             * then their scale epilogue in block order: few accumulation
+             * registers live, so three waves fit per SIMD */
 #pragma unroll
-            for (int h0 = 0; h0 < MT_CB; h0 += MT_CB / 2) {
-                v4i S[MT_CB / 2][2];
+            for (int h0 = 0; h0 < MT_CB; h0 += 4) {
+                constexpr int G = 4;
+                v4i S[G][2];
 #pragma unroll
-                for (int bb = 0; bb < MT_CB / 2; ++bb) block_sums(h0 + bb, S[bb]);
+                for (int bb = 0; bb < G; ++bb)
+                    if (h0 + bb < MT_CB) block_sums(h0 + bb, S[bb]);
 #pragma unroll
-                for (int bb = 0; bb < MT_CB / 2; ++bb) epilogue(h0 + bb, S[bb]);
+                for (int bb = 0; bb < G; ++bb)
+                    if (h0 + bb < MT_CB) epilogue(h0 + bb, S[bb]);
             }
         } else {
             for (uint32_t bb = 0; bb < count; ++bb) {

@@ -153,6 +153,11 @@ void smq_block_sums(int q5, const unsigned char *w, size_t row_bytes, const int8
 /* Which kernel smq_matmul uses when ntok > 1: 0 = the exact GEMM (default,
  * bit-identical to the reference), 1 = the int8-MFMA GEMM. */
 void smq_set_prefill_mfma(int on);
+/* Tuning (no reference counterpart): rows per workgroup of the
+ * one-launch decode GEMV, 1, 2, 4, 8 or 16 (every output unchanged), or 0 =
+ * chosen per width and row count (the default). Any other value is refused
+ * with SMQ_ERR_RANGE. */
+smq_status smq_set_gemv_rows(int rows);
 
 /* ---- fused matmul with bias and finiteness (src/model.c:236-310) -------- */
 /* QMat (model.h:15-19): a weight matrix in device memory. dtype 1 = Q8, 2 = Q5

@@ -521,8 +521,18 @@ class ReferenceModel:
             lib.ref_model_vocab.argtypes = [vp]
             lib.ref_model_set_banned.argtypes = [vp, vp]
             lib.ref_model_generate.argtypes = [vp, _u32, _u32, vp]
+            lib.ref_modelfile_check.argtypes = [vp, ctypes.c_uint64, _u32]
             cls._lib = lib
         return cls._lib
+
+    @classmethod
+    def check_file(cls, data, threads=2):
+        """The reference's modelfile_parse + modelfile_verify_payload over checkpoint bytes:
+        (status, message)."""
+        lib = cls._load()
+        buf = np.frombuffer(bytes(data), np.uint8).copy()
+        st = lib.ref_modelfile_check(buf.ctypes.data, buf.nbytes, threads)
+        return st, (lib.ref_last_error().decode() if st else "")
 
     def __init__(self, path, config_path=None, context=256, batch=64, logit_rows=1, threads=1, scalar=False):
         lib = self._load()

@@ -115,3 +115,27 @@ int ref_model_generate(RefModel *r, uint32_t pos, uint32_t ntokens, uint32_t *ou
     }
     return 0;
 }
+
+/* modelfile_parse, then modelfile_verify_payload on `threads` workers, as
+ * ref_model_open runs them (src/main.c:494-513), over a checkpoint already in
+ * memory. Returns the status; the message is ref_last_error's. */
+int ref_modelfile_check(const unsigned char *data, uint64_t size, uint32_t threads) {
+    Memory mem;
+    ModelFile mf;
+    Pool *pool;
+    sm_status st;
+    memset(&mem, 0, sizeof(mem));
+    mem.limit = (size_t)-1;
+    st = modelfile_parse(&mf, data, size, &mem);
+    if (st == SM_OK) {
+        pool = pool_create(threads ? threads : 1, &mem);
+        if (!pool) {
+            st = sm_last_status();
+        } else {
+            st = modelfile_verify_payload(&mf, pool);
+            pool_destroy(pool);
+        }
+    }
+    mem_release(&mem);
+    return (int)st;
+}

@@ -99,6 +99,7 @@ _SIGS = {
     "smq_gemm_q5_mfma": (None, [_vp, _sz, _vp, _vp, _u32, _u32, _u32, _vp, _sz, _vp]),
     "smq_block_sums": (None, [ctypes.c_int, _vp, _sz, _vp, _u32, _u32, _u32, _vp]),
     "smq_set_prefill_mfma": (None, [ctypes.c_int]),
+    "smq_set_gemv_rows": (ctypes.c_int, [ctypes.c_int]),
     "smq_matmul": (ctypes.c_int, [ctypes.POINTER(_MatItem), _u32, _vp, _vp, _u32]),
     "smq_numeric_check": (ctypes.c_int, []),
     "smq_matmul_act": (ctypes.c_int, [ctypes.POINTER(_MatItem), _u32, ctypes.POINTER(_Act)]),
@@ -344,6 +345,11 @@ def block_sums(q5, w, row_bytes, xq, nrows, ntok, nb, sums):
 
 def set_prefill_mfma(on):
     load().smq_set_prefill_mfma(int(bool(on)))
+
+
+def set_gemv_rows(rows):
+    """Rows per workgroup of the one-launch decode GEMV (1, 2, 4, 8, 16), or 0 for the default choice."""
+    _check(load().smq_set_gemv_rows(int(rows)))
 
 
 # ---- src/model.c:236-310

@@ -214,6 +214,8 @@ smq_status smq_init(int device) {
     g.device = device;
     const char *env = getenv("SMQ_CHECKS");
     g.checks = !(env && !strcmp(env, "0"));
+    env = getenv("SMQ_ATT_GROUP"); /* read once: 0 sends prefill attention to the per-head kernel */
+    smq::set_att_grouped(!(env && !strcmp(env, "0")));
     g.ready = true;
     return set_status(SMQ_OK, "");
 }
@@ -392,6 +394,12 @@ void smq_block_sums(int q5, const unsigned char *w, size_t row_bytes, const int8
 }
 
 void smq_set_prefill_mfma(int on) { g.prefill_mfma = on ? 1 : 0; }
+
+smq_status smq_set_gemv_rows(int rows) {
+    if (!smq::set_gemv_rows(rows))
+        return set_status(SMQ_ERR_RANGE, "set_gemv_rows: %d is not 0, 1, 2, 4, 8 or 16", rows);
+    return SMQ_OK;
+}
 
 smq_status smq_matmul(const smq_mat_item *items, uint32_t n, const float *xd, const int8_t *xq, uint32_t ntok) {
     if (!ready()) return t_status;

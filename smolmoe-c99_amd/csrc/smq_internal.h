@@ -88,6 +88,12 @@ struct FusedArgs {
 bool fused_layout_ok(const FusedArgs &a, bool q5, int pro);
 /* Rows per decode-GEMV workgroup for nb blocks (smq_kernels.hip). */
 int gemv_rows_per_tile(uint32_t nb, bool q5, uint32_t total_rows);
+/* Tuning, set from the host thread that launches: rows per tile of the
+ * one-tile-per-workgroup decode GEMV (0 = chosen per width, else 1, 2, 4, 8
+ * or 16; false for any other value), and whether prefill attention takes the
+ * grouped kernel. */
+bool set_gemv_rows(int rt);
+void set_att_grouped(bool on);
 hipError_t launch_matmul_fused(const FusedArgs &a, bool q5, int pro, bool glu, hipStream_t s);
 /* h = h * act(gate) elementwise (act 1 SwiGLU, 2 GeGLU). */
 hipError_t launch_glu(float *h, const float *gate, uint32_t n, int act, hipStream_t s);

@@ -32,22 +32,20 @@ __device__ __forceinline__ uint32_t find_item(const MatArgs &a, uint32_t tile) {
 }
 
 /* ------------------------------------------------------------------------
- * Decode GEMV (ntok == 1). Workgroup = RT rows x all K. K is walked in chunks
- * of CB blocks (the launcher sizes RT so that one chunk usually covers K). In
- * each chunk every thread owns one task (one Q8 block, or one pair of Q5
- * blocks, of one row): it loads the block straight from HBM (the next chunk's
- * task is prefetched into registers), and writes the eight lane products
- * d*float(s_l) (fast mode: float(s_l) and d) into LDS. Then the RT*8 chain
- * threads, one per (row, lane), add their CB products in block order. The
- * serial part per thread is one add per block; the loads, dot4s and
- * multiplies are spread over all 256 threads.
- * STAGE: the activation is copied to LDS once per workgroup (large row counts,
- * where it is reused by many tasks); otherwise each task reads its activation
- * block directly (L1/L2 hits) and no barrier precedes the products.
+ * Decode GEMV (ntok == 1), one tile per workgroup. Workgroup = RT rows x all
+ * K. K is walked in chunks of CB blocks (the launcher sizes RT so that one
+ * chunk usually covers K). In each chunk every thread owns one task (one Q8
+ * block, or one pair of Q5 blocks, of one row): it loads the block and its
+ * activation block straight from memory (the next chunk's task is prefetched
+ * into registers), and writes the eight lane products d*float(s_l) (fast
+ * mode: float(s_l) and d) into LDS. Then the RT*8 chain threads, one per
+ * (row, lane), add their CB products in block order. The serial part per
+ * thread is one add per block; the loads, dot4s and multiplies are spread
+ * over all 256 threads.
  * LDS products: group g of four blocks holds [thread (r*8+l)][b%4], padded by
  * four floats per group so writes from a wave fall in distinct banks.
  * ---------------------------------------------------------------------- */
-template <bool Q5, bool FAST, int RT, bool STAGE>
+template <bool Q5, bool FAST, int RT>
 __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
     constexpr int TB = Q5 ? 2 : 1;    /* blocks per task */
     constexpr int TPR = WG / RT;      /* tasks per row per chunk */
@@ -55,41 +53,13 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
     constexpr int GS = RT * 32 + 4;   /* floats per group of four blocks */
     constexpr int DS = RT * 4 + 4;    /* fast mode: scales per group */
     constexpr int NW = Q5 ? 11 : 9;   /* weight dwords per task */
-    constexpr int NX = STAGE ? 1 : TB * 8; /* activation words per task */
+    constexpr int NX = TB * 8;        /* activation words per task */
     __shared__ __attribute__((aligned(16))) float prod[2][(CB / 4) * GS];
     __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? (CB / 4) * DS : 4];
-    extern __shared__ __attribute__((aligned(16))) uint32_t act[];
 
     const uint32_t nb = a.nb, tid = threadIdx.x;
-    uint32_t *act_q = act;                  /* STAGE: nb*8 words of int8 x4 */
-    float *act_d = (float *)(act + nb * 8); /* STAGE: nb scales */
-    int *act_b = (int *)(act + nb * 9);     /* STAGE, Q5: -16 * lane sums of x */
-
     const Item &I = a.item[find_item(a, blockIdx.x)]; /* uniform index into the kernel arguments */
     const uint32_t r0 = (blockIdx.x - I.tile_begin) * RT;
-
-    /* STAGE: this thread's share of the activation is loaded first, the
-     * weights next, and the activation is written to LDS afterwards, so the
-     * wait before that write covers only the older activation loads. */
-    constexpr int SA = STAGE ? (MAX_FAST_NB * 8 + WG - 1) / WG : 1; /* staged words per thread */
-    uint32_t sav[SA];
-    float sdv[STAGE ? 2 : 1];
-    if (STAGE) {
-        /* unconditional loads from clamped (in-range) indices; only the LDS
-         * writes below are guarded */
-        const uint32_t *xq32 = (const uint32_t *)a.xq;
-        const uint32_t nw = nb * 8;
-#pragma unroll
-        for (int k = 0; k < SA; ++k) {
-            const uint32_t i = tid + k * WG;
-            if (k * WG < nw) sav[k] = xq32[i < nw ? i : nw - 1];
-        }
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const uint32_t i = tid + k * WG;
-            if (k * WG < nb) sdv[k] = a.xd[i < nb ? i : nb - 1];
-        }
-    }
 
     const uint32_t tr = tid / TPR, ti = tid % TPR;
     const bool row_ok = r0 + tr < I.rows;
@@ -104,43 +74,23 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
             const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
             wr[0] = v0.x; wr[1] = v0.y; wr[2] = v0.z; wr[3] = v0.w;
             wr[4] = v1.x; wr[5] = v1.y; wr[6] = v1.z; wr[7] = v1.w;
-            if (Q5) {
+            if constexpr (Q5) {
                 const u3a v2 = *(const u3a *)(p + 32);
                 wr[8] = v2.x; wr[9] = v2.y; wr[10] = v2.z;
             } else {
                 wr[8] = *(const uint32_t *)(p + 32);
             }
-            if (!STAGE) {
-                const unsigned char *xp = (const unsigned char *)a.xq + (size_t)b * QK;
+            const unsigned char *xp = (const unsigned char *)a.xq + (size_t)b * QK;
 #pragma unroll
-                for (int k = 0; k < TB * 2; ++k) {
-                    const u4a v = *(const u4a *)(xp + 16 * k);
-                    xr[4 * k] = v.x; xr[4 * k + 1] = v.y; xr[4 * k + 2] = v.z; xr[4 * k + 3] = v.w;
-                }
-#pragma unroll
-                for (int k = 0; k < TB; ++k) xs[k] = a.xd[b + k];
+            for (int k = 0; k < TB * 2; ++k) {
+                const u4a v = *(const u4a *)(xp + 16 * k);
+                xr[4 * k] = v.x; xr[4 * k + 1] = v.y; xr[4 * k + 2] = v.z; xr[4 * k + 3] = v.w;
             }
+#pragma unroll
+            for (int k = 0; k < TB; ++k) xs[k] = a.xd[b + k];
         }
     };
     load_task(ti * TB);
-    if (STAGE) {
-        /* keep the weight loads issued here, ahead of the barrier below */
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int k = 0; k < SA; ++k) {
-            const uint32_t i = tid + k * WG;
-            if (i < nb * 8) {
-                act_q[i] = sav[k];
-                if (Q5) act_b[i] = dot4(sav[k], 0xf0f0f0f0u, 0); /* int8 0xf0 = -16 */
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const uint32_t i = tid + k * WG;
-            if (i < nb) act_d[i] = sdv[k];
-        }
-        __syncthreads(); /* activation staged */
-    }
 
     float acc = 0.0f;
     for (uint32_t c = 0; c < nchunks; ++c) {
@@ -161,15 +111,15 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
             if (Q5) q5_parse_pair(cw, f[0], f[1]);
 #pragma unroll
             for (int k = 0; k < TB; ++k) {
-                const uint32_t b = bt + k, bb = ti * TB + k;
+                const uint32_t bb = ti * TB + k;
                 const float wscale = Q5 ? f[k].scale : __uint_as_float(cw[0]);
-                const float d = wscale * (STAGE ? act_d[b] : cs[k]);
+                const float d = wscale * cs[k];
                 float *dst = pb + (bb / 4) * GS + tr * 32 + (bb % 4);
 #pragma unroll
                 for (int l = 0; l < 8; ++l) {
-                    const uint32_t x = STAGE ? act_q[b * 8 + l] : cx[STAGE ? 0 : k * 8 + l];
+                    const uint32_t x = cx[k * 8 + l];
                     int s;
-                    if (Q5) s = dot4(q5_codes(f[k], l), x, STAGE ? act_b[b * 8 + l] : dot4(x, 0xf0f0f0f0u, 0));
+                    if (Q5) s = dot4(q5_codes(f[k], l), x, dot4(x, 0xf0f0f0f0u, 0));
                     else s = dot4(cw[1 + l], x, 0);
                     dst[l * 4] = FAST ? (float)s : d * (float)s;
                 }
@@ -189,226 +139,6 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
         const float v = reduce8_to_lane7(acc);
         const uint32_t r = r0 + tid / 8;
         if ((tid & 7) == 7 && r < I.rows) store_out(I, a.flag, 0, r, v);
-    }
-}
-
-/* ------------------------------------------------------------------------
- * Streaming decode GEMV: the same tasks, LDS products and in-order chains as
- * k_gemv, run by persistent workgroups that each walk the (tile, chunk) steps
- * of a contiguous range of tiles over the items. The next
- * step's weight and activation blocks are requested before the current
- * step's products are formed, so each workgroup keeps one step of loads in
- * flight while it computes; a launch then streams all its items' weights
- * without per-tile launch or drain gaps. Items are independent matrices with
- * the same nb, each with its own activation (a group of experts, or many
- * layers' weights in a bandwidth run).
- * ---------------------------------------------------------------------- */
-__device__ __forceinline__ uint32_t find_group_item(const GroupArgs &g, uint32_t tile) {
-    uint32_t lo = 0, hi = g.nitems; /* last item with tile_begin <= tile */
-    while (hi - lo > 1) {
-        const uint32_t mid = (lo + hi) / 2;
-        if (g.item[mid].tile_begin <= tile) lo = mid;
-        else hi = mid;
-    }
-    return lo;
-}
-
-/* One task of a streaming step: this thread's weight block(s) and
- * activation block(s), and, for the output row the thread may store, its bias
- * and prior output, all in registers. Every task issues the same loads (an
- * invalid one reads row 0, block 0 of its item and is then ignored), so the
- * in-order load counter lets a step wait for its own task only. */
-template <bool Q5>
-struct StreamTask {
-    uint32_t w[Q5 ? 11 : 9];
-    uint32_t x[Q5 ? 16 : 8];
-    float s[Q5 ? 2 : 1];
-    float bias, prior;
-    bool ok;
-};
-
-/* The item under one of a workgroup's cursors, with its fields held in
- * registers (reloaded only when the cursor crosses into the next item), and
- * the (tile, chunk) position that cursor stands at. */
-struct StreamCursor {
-    const unsigned char *w;
-    const float *bias, *xd;
-    float *y;
-    const int8_t *xq;
-    size_t row_bytes;
-    uint32_t rows, tile_begin, next_begin, idx, tile, chunk;
-    int accumulate;
-};
-__device__ __forceinline__ void cursor_load(StreamCursor &c, const GroupArgs &g) {
-    const GroupItem &I = g.item[c.idx];
-    c.w = I.w;
-    c.row_bytes = I.row_bytes;
-    c.bias = I.bias;
-    c.y = I.y;
-    c.xd = I.xd;
-    c.xq = I.xq;
-    c.rows = I.rows;
-    c.tile_begin = I.tile_begin;
-    c.accumulate = I.accumulate;
-    c.next_begin = c.idx + 1 < g.nitems ? g.item[c.idx + 1].tile_begin : 0xffffffffu;
-}
-__device__ __forceinline__ void cursor_start(StreamCursor &c, const GroupArgs &g, uint32_t tile) {
-    c.idx = find_group_item(g, tile);
-    c.tile = tile;
-    c.chunk = 0;
-    cursor_load(c, g);
-}
-/* next (tile, chunk) step; crossing items reloads the fields */
-__device__ __forceinline__ void cursor_step(StreamCursor &c, const GroupArgs &g, uint32_t nchunks) {
-    if (++c.chunk == nchunks) {
-        c.chunk = 0;
-        if (++c.tile >= c.next_begin) {
-            while (c.tile >= c.next_begin) {
-                ++c.idx;
-                c.next_begin = c.idx + 1 < g.nitems ? g.item[c.idx + 1].tile_begin : 0xffffffffu;
-            }
-            cursor_load(c, g);
-        }
-    }
-}
-
-template <bool Q5, int RT, int NT>
-__device__ __forceinline__ void stream_load(StreamTask<Q5> &T, const StreamCursor &c, uint32_t nb, bool real,
-                                            uint32_t tid, uint32_t tr, uint32_t ti) {
-    constexpr int TB = Q5 ? 2 : 1, CB = (NT / RT) * TB;
-    const uint32_t row0 = (c.tile - c.tile_begin) * RT;
-    const uint32_t row = row0 + tr, b = c.chunk * CB + ti * TB;
-    T.ok = real && row < c.rows && b < nb;
-    const unsigned char *p = c.w + (T.ok ? (size_t)row * c.row_bytes + (size_t)b * (Q5 ? Q5_BYTES : Q8_BYTES) : 0);
-    const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
-    T.w[0] = v0.x; T.w[1] = v0.y; T.w[2] = v0.z; T.w[3] = v0.w;
-    T.w[4] = v1.x; T.w[5] = v1.y; T.w[6] = v1.z; T.w[7] = v1.w;
-    if (Q5) {
-        const u3a v2 = *(const u3a *)(p + 32);
-        T.w[8] = v2.x; T.w[9] = v2.y; T.w[10] = v2.z;
-    } else {
-        T.w[8] = *(const uint32_t *)(p + 32);
-    }
-    const uint32_t bx = T.ok ? b : 0;
-    const unsigned char *xp = (const unsigned char *)c.xq + (size_t)bx * QK;
-#pragma unroll
-    for (int k = 0; k < TB * 2; ++k) {
-        const u4a v = *(const u4a *)(xp + 16 * k);
-        T.x[4 * k] = v.x; T.x[4 * k + 1] = v.y; T.x[4 * k + 2] = v.z; T.x[4 * k + 3] = v.w;
-    }
-#pragma unroll
-    for (int k = 0; k < TB; ++k) T.s[k] = c.xd[bx + k];
-    /* the chain thread's output row of this tile (used at its last chunk) */
-    const uint32_t orow = row0 + (tid < RT * 8 ? tid / 8 : 0);
-    const uint32_t oc = orow < c.rows ? orow : 0;
-    T.bias = *(c.bias ? c.bias + oc : c.xd); /* an unused read when absent keeps the load count uniform */
-    T.prior = *(c.accumulate ? c.y + oc : c.xd);
-}
-
-/* Products of one task into the LDS buffer pb (and, fast mode, its scale). */
-template <bool Q5, bool FAST, int RT>
-__device__ __forceinline__ void stream_products(const StreamTask<Q5> &T, float *pb, float *db, uint32_t tr,
-                                                uint32_t ti) {
-    constexpr int TB = Q5 ? 2 : 1, GS = RT * 32 + 4, DS = RT * 4 + 4;
-    if (!T.ok) return;
-    Q5Fields f[2];
-    if (Q5) q5_parse_pair(T.w, f[0], f[1]);
-    float d[TB];
-#pragma unroll
-    for (int q = 0; q < TB; ++q) {
-        const uint32_t bb = ti * TB + q;
-        d[q] = (Q5 ? f[q].scale : __uint_as_float(T.w[0])) * T.s[q];
-        if (FAST) db[(bb / 4) * DS + tr * 4 + (bb % 4)] = d[q];
-    }
-    float *slot = tile_slot<GS>(pb, tr, ti * TB);
-#pragma unroll
-    for (int l = 0; l < 8; ++l) {
-        float v[TB];
-#pragma unroll
-        for (int q = 0; q < TB; ++q) {
-            const uint32_t x = T.x[q * 8 + l];
-            int sv;
-            if (Q5) sv = dot4(q5_codes(f[q], l), x, dot4(x, 0xf0f0f0f0u, 0));
-            else sv = dot4(T.w[1 + l], x, 0);
-            v[q] = FAST ? (float)sv : d[q] * (float)sv;
-        }
-        put_lane<TB>(slot, l, v[0], v[TB - 1]);
-    }
-}
-
-/* Chain threads (tid < RT*8): this step's products in block order; at the
- * last chunk of a tile, the lane tree and the store (bias and prior output
- * were loaded with the tile's first chunk: no load waits here). */
-template <bool Q5, bool FAST, int RT, int NT>
-__device__ __forceinline__ void stream_chain(float &acc, float &bias, float &prior, const StreamTask<Q5> &T,
-                                             const float *pb, const float *db, const StreamCursor &c, uint32_t nb,
-                                             uint32_t nchunks, int *flag, uint32_t tid) {
-    constexpr int TB = Q5 ? 2 : 1, CB = (NT / RT) * TB, GS = RT * 32 + 4, DS = RT * 4 + 4;
-    if (c.chunk == 0) {
-        bias = T.bias;
-        prior = T.prior;
-    }
-    const uint32_t count = nb - c.chunk * CB < (uint32_t)CB ? nb - c.chunk * CB : (uint32_t)CB;
-    chain_sum<FAST, CB / 4>(acc, (const float4 *)pb + tid, GS / 4, FAST ? (const float4 *)db + tid / 8 : nullptr,
-                            DS / 4, count);
-    if (c.chunk + 1 == nchunks) {
-        const float v = reduce8_to_lane7(acc);
-        const uint32_t r = (c.tile - c.tile_begin) * RT + tid / 8;
-        if ((tid & 7) == 7 && r < c.rows) {
-            float o = v;
-            if (c.bias) o = o + bias; /* model.c:259-262 */
-            if (flag && !(fabsf(o) <= FLT_MAX)) *flag = 1;
-            if (c.accumulate) o = prior + o;
-            c.y[r] = o;
-        }
-        acc = 0.0f;
-    }
-}
-
-template <bool Q5, bool FAST, int RT, int NT>
-__global__ __launch_bounds__(NT) void k_gemv_stream(GroupArgs g) {
-    constexpr int TB = Q5 ? 2 : 1;
-    constexpr int CB = (NT / RT) * TB;
-    constexpr int GS = RT * 32 + 4;
-    constexpr int DS = RT * 4 + 4;
-    __shared__ __attribute__((aligned(16))) float prod[2][(CB / 4) * GS];
-    __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? (CB / 4) * DS : 4];
-
-    const uint32_t tid = threadIdx.x, tr = tid / (NT / RT), ti = tid % (NT / RT), nb = g.nb;
-    const uint32_t nchunks = (nb + CB - 1) / CB;
-    /* this workgroup's tiles: a contiguous range (consecutive rows, mostly one item) */
-    const uint32_t t0 = (uint32_t)((uint64_t)g.total_tiles * blockIdx.x / gridDim.x);
-    const uint32_t t1 = (uint32_t)((uint64_t)g.total_tiles * (blockIdx.x + 1) / gridDim.x);
-    const uint32_t my_steps = (t1 - t0) * nchunks;
-    if (!my_steps) return;
-
-    /* two tasks in flight: A holds even steps, B odd ones; the load cursor
-     * runs two steps ahead of the chain cursor */
-    StreamCursor cl, cc;
-    cursor_start(cl, g, t0);
-    cc = cl;
-    StreamTask<Q5> A, B;
-    stream_load<Q5, RT, NT>(A, cl, nb, true, tid, tr, ti);
-    cursor_step(cl, g, nchunks);
-    stream_load<Q5, RT, NT>(B, cl, nb, my_steps > 1, tid, tr, ti);
-    float acc = 0.0f, bias = 0.0f, prior = 0.0f;
-    for (uint32_t k = 0; k < my_steps; k += 2) {
-        /* even step k from A; then A loads step k + 2 */
-        stream_products<Q5, FAST, RT>(A, prod[0], dsc[0], tr, ti);
-        __syncthreads();
-        if (tid < RT * 8) stream_chain<Q5, FAST, RT, NT>(acc, bias, prior, A, prod[0], dsc[0], cc, nb, nchunks, g.flag, tid);
-        cursor_step(cc, g, nchunks);
-        if (k + 2 < my_steps) cursor_step(cl, g, nchunks);
-        stream_load<Q5, RT, NT>(A, cl, nb, k + 2 < my_steps, tid, tr, ti);
-        if (k + 1 >= my_steps) break;
-        /* odd step k + 1 from B; then B loads step k + 3 */
-        stream_products<Q5, FAST, RT>(B, prod[1], dsc[FAST ? 1 : 0], tr, ti);
-        __syncthreads();
-        if (tid < RT * 8)
-            stream_chain<Q5, FAST, RT, NT>(acc, bias, prior, B, prod[1], dsc[FAST ? 1 : 0], cc, nb, nchunks, g.flag, tid);
-        cursor_step(cc, g, nchunks);
-        if (k + 3 < my_steps) cursor_step(cl, g, nchunks);
-        stream_load<Q5, RT, NT>(B, cl, nb, k + 3 < my_steps, tid, tr, ti);
     }
 }
 
@@ -494,10 +224,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
     const uint32_t *xq32 = (const uint32_t *)I.xq;
     for (uint32_t i = tid; i < nb * 8; i += NT) act_q[i] = xq32[i];
     for (uint32_t i = tid; i < nb; i += NT) act_d[i] = xd[i];
-    if constexpr (ONE && !Q5) { /* +0.0 in the slots past the last block, never written after (chain_sum_padded) */
-        for (uint32_t i = tid; i < 2 * PF; i += NT) (&prod[0][0])[i] = 0.0f;
+    if constexpr (ONE && !Q5) {
+        /* +0.0 in the slots past the last block, never written after (chain_sum_padded): both
+         * buffers whole, sinks included (the launcher keeps every chain read below PF) */
+        constexpr uint32_t PROD_FLOATS = sizeof(prod) / sizeof(float), DSC_FLOATS = sizeof(dsc) / sizeof(float);
+        for (uint32_t i = tid; i < PROD_FLOATS; i += NT) (&prod[0][0])[i] = 0.0f;
         if constexpr (FAST)
-            for (uint32_t i = tid; i < 2 * (PF / 8 + 128); i += NT) (&dsc[0][0])[i] = 0.0f;
+            for (uint32_t i = tid; i < DSC_FLOATS; i += NT) (&dsc[0][0])[i] = 0.0f;
     }
 
     /* step s: tile t0 + s / nch, chunk s % nch (counters, no division per step) */
@@ -2002,7 +1735,7 @@ __global__ __launch_bounds__(AR_WG) __attribute__((amdgpu_waves_per_eu(1, 2))) v
         sc[p] = v;
         high = v > high ? v : high;
     }
-    const uint32_t nbq = sh.q_dim / QK, blk = (h * AR_HD + j0) / QK;
+    const uint32_t blk = (h * AR_HD + j0) / QK;
     att_tail<ROPE>(high, sc, prod, np, last, pre, vbase, vrope, kvd, vrow, vcol, etab, red, &s_inv,
                    att + (size_t)h * AR_HD + j0, xd ? xd + blk : nullptr, xq ? xq + (size_t)blk * QK : nullptr, flag);
 }
@@ -2317,7 +2050,7 @@ bool fast_layout(const MatArgs &a, bool q5) {
     return true;
 }
 
-template <bool Q5, bool FAST, int RT, bool STAGE>
+template <bool Q5, bool FAST, int RT>
 hipError_t launch_gemv_rt(MatArgs a, hipStream_t s) {
     uint32_t tiles = 0;
     for (uint32_t i = 0; i < a.nitems; ++i) {
@@ -2325,75 +2058,31 @@ hipError_t launch_gemv_rt(MatArgs a, hipStream_t s) {
         tiles += (a.item[i].rows + RT - 1) / RT;
     }
     if (!tiles) return hipSuccess;
-    const size_t lds = STAGE ? (size_t)a.nb * (Q5 ? 17u : 9u) * 4u : 0;
-    hipLaunchKernelGGL((k_gemv<Q5, FAST, RT, STAGE>), dim3(tiles), dim3(WG), lds, s, a);
-    return hipGetLastError();
-}
-
-template <bool Q5, bool FAST, bool STAGE>
-hipError_t launch_gemv_stage(MatArgs a, int rt, hipStream_t s) {
-    switch (rt) {
-    case 1: return launch_gemv_rt<Q5, FAST, 1, STAGE>(a, s);
-    case 2: return launch_gemv_rt<Q5, FAST, 2, STAGE>(a, s);
-    case 4: return launch_gemv_rt<Q5, FAST, 4, STAGE>(a, s);
-    case 8: return launch_gemv_rt<Q5, FAST, 8, STAGE>(a, s);
-    default: return launch_gemv_rt<Q5, FAST, 16, STAGE>(a, s);
-    }
-}
-
-/* Single launches of many tiles (the LM head: 18992 tiles of 8 rows) run on
- * the persistent streaming kernel; a few thousand tiles fit the device in one
- * wave of workgroups and keep the one-tile-per-workgroup kernel.
- * SMQ_GEMV_STREAM=0/1 forces either. */
-bool gemv_stream(uint32_t total_rows, int rt) {
-    const char *env = getenv("SMQ_GEMV_STREAM");
-    if (env && *env) return atoi(env) != 0;
-    return (total_rows + rt - 1) / rt > 4096;
-}
-
-/* Staging the activation in LDS never beat direct (L1/L2) reads on the
- * measured shapes; the staged variant stays available for tuning. */
-bool gemv_stage(uint32_t total_rows) {
-    (void)total_rows;
-    const char *env = getenv("SMQ_GEMV_STAGE");
-    return env && *env && atoi(env) != 0;
-}
-
-/* Persistent grid: as many workgroups as fit on the device at once (the
- * occupancy query runs once per kernel), never more than the tiles. */
-template <bool Q5, bool FAST, int RT, int NT>
-hipError_t launch_gemv_stream_rt(GroupArgs &g, hipStream_t s) {
-    static int resident = 0;
-    uint32_t tiles = 0;
-    for (uint32_t i = 0; i < g.nitems; ++i) {
-        g.item[i].tile_begin = tiles;
-        tiles += (g.item[i].rows + RT - 1) / RT;
-    }
-    g.total_tiles = tiles;
-    if (!tiles) return hipSuccess;
-    if (!resident) {
-        int per_cu = 0, dev = 0, cus = 0;
-        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemv_stream<Q5, FAST, RT, NT>, NT, 0);
-        if (e == hipSuccess) e = hipGetDevice(&dev);
-        if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        if (e != hipSuccess) return e;
-        resident = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
-    }
-    const uint32_t grid = tiles < (uint32_t)resident ? tiles : (uint32_t)resident;
-    hipLaunchKernelGGL((k_gemv_stream<Q5, FAST, RT, NT>), dim3(grid), dim3(NT), 0, s, g);
+    hipLaunchKernelGGL((k_gemv<Q5, FAST, RT>), dim3(tiles), dim3(WG), 0, s, a);
     return hipGetLastError();
 }
 
 template <bool Q5, bool FAST>
-hipError_t launch_gemv_stream_typed(GroupArgs &g, int rt, hipStream_t s) {
+hipError_t launch_gemv_tile(MatArgs a, int rt, hipStream_t s) {
     switch (rt) {
-    case 1: return launch_gemv_stream_rt<Q5, FAST, 1, WG>(g, s);
-    case 2: return launch_gemv_stream_rt<Q5, FAST, 2, WG>(g, s);
-    case 4: return launch_gemv_stream_rt<Q5, FAST, 4, WG>(g, s);
-    case 8: return launch_gemv_stream_rt<Q5, FAST, 8, WG>(g, s);
-    default: return launch_gemv_stream_rt<Q5, FAST, 16, WG>(g, s);
+    case 1: return launch_gemv_rt<Q5, FAST, 1>(a, s);
+    case 2: return launch_gemv_rt<Q5, FAST, 2>(a, s);
+    case 4: return launch_gemv_rt<Q5, FAST, 4>(a, s);
+    case 8: return launch_gemv_rt<Q5, FAST, 8>(a, s);
+    default: return launch_gemv_rt<Q5, FAST, 16>(a, s);
     }
 }
+
+/* Single launches of many tiles (the LM head: 18992 tiles of 8 rows) run on
+ * the pinned persistent kernel; a few thousand tiles fit the device in one
+ * wave of workgroups and keep the one-tile-per-workgroup kernel. */
+bool gemv_persistent(uint32_t total_rows, int rt) { return (total_rows + rt - 1) / rt > 4096; }
+
+/* Tile rows of the one-tile-per-workgroup decode GEMV forced by smq_set_gemv_rows
+ * (0: chosen per width). */
+int g_forced_rt = 0;
+/* set_att_grouped(false) sends prefill attention to k_attend_rows instead (tuning, tests) */
+bool g_att_grouped = true;
 
 /* Pinned launch: every item gets a share of the resident workgroups in
  * proportion to its tiles (at least one), each a contiguous tile range.
@@ -2419,6 +2108,9 @@ hipError_t launch_gemv_pin_shape(GroupArgs &g, hipStream_t s) {
     g.cpr = (ppr + g.nch - 1) / g.nch;
     g.rt = pin_rows(NT, TB, g.cpr, PF);
     if (g.nb > MAXNB || (ONE && g.nch != 1) || g.rt == 0) return hipErrorInvalidValue; /* launcher precondition */
+    /* every chain read (groups of four blocks of a chunk, rt rows each) lies below PF, clear of the
+     * sinks that idle tasks write past PF */
+    if ((uint64_t)((g.cpr * TB + 3) / 4) * (g.rt * 32 + 4) > PF) return hipErrorInvalidValue;
     static int resident = 0;
     if (!resident) {
         int per_cu = 0, dev = 0, cus = 0;
@@ -2452,12 +2144,6 @@ hipError_t launch_gemv_pin(GroupArgs &g, hipStream_t s) {
     return launch_gemv_pin_shape<Q5, FAST, false>(g, s);
 }
 
-bool gemv_pin_ok(const GroupArgs &g, bool q5) {
-    const char *env = getenv("SMQ_GEMV_PIN");
-    if (env && *env && atoi(env) == 0) return false;
-    /* Q5: whole pairs (nb even) */
-    return g.nb <= MAX_FAST_NB && (!q5 || (g.nb & 1u) == 0);
-}
 
 template <bool Q5, bool FAST>
 hipError_t launch_typed(MatArgs a, hipStream_t s) {
@@ -2467,8 +2153,8 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
     if (fast_layout(a, Q5)) {
         if (a.ntok == 1) {
             const int rt = gemv_rows_per_tile(a.nb, Q5, total_rows);
-            if (gemv_stream(total_rows, rt) && !gemv_stage(total_rows)) {
-                /* many tiles: persistent workgroups stream them (same products and order) */
+            if (!g_forced_rt && gemv_persistent(total_rows, rt)) {
+                /* many tiles: the pinned persistent kernel streams them (same products and order) */
                 GroupArgs g;
                 memset(&g, 0, sizeof(g));
                 g.nb = a.nb;
@@ -2484,11 +2170,9 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
                     it.rows = a.item[i].rows;
                     it.accumulate = a.item[i].accumulate;
                 }
-                if (gemv_pin_ok(g, Q5)) return launch_gemv_pin<Q5, FAST>(g, s);
-                return launch_gemv_stream_typed<Q5, FAST>(g, rt, s);
+                return launch_gemv_pin<Q5, FAST>(g, s);
             }
-            return gemv_stage(total_rows) ? launch_gemv_stage<Q5, FAST, true>(a, rt, s)
-                                          : launch_gemv_stage<Q5, FAST, false>(a, rt, s);
+            return launch_gemv_tile<Q5, FAST>(a, rt, s);
         }
         uint32_t tiles = 0;
         for (uint32_t i = 0; i < a.nitems; ++i) {
@@ -2530,16 +2214,23 @@ hipError_t launch_mfma_typed(MatArgs a, int32_t *sums, hipStream_t s) {
  * (Q5 keeps at least 2 rows: its wide rows run faster as two chunks of two
  * rows than as one chunk of one). Measured on MI355X over rotated weights:
  * 9728x896 Q8 4.7 us at 8 rows, 896x4864 Q8 4.6 us at 1 row, 1536x8960 Q5
- * 7.4 us at 2 rows (9.9 us at 1). SMQ_GEMV_RT / SMQ_GEMV_STAGE override. */
+ * 7.4 us at 2 rows (9.9 us at 1). set_gemv_rows overrides. */
 int gemv_rows_per_tile(uint32_t nb, bool q5, uint32_t total_rows) {
     (void)total_rows;
-    const char *env = getenv("SMQ_GEMV_RT");
-    if (env && *env) return atoi(env);
+    if (g_forced_rt) return g_forced_rt;
     const uint32_t cover = (q5 ? 512u : 256u) / nb;
     int rt = q5 ? 2 : 1;
     while (rt < 8 && (uint32_t)(rt * 2) <= cover) rt *= 2;
     return rt;
 }
+
+bool set_gemv_rows(int rt) {
+    if (rt != 0 && rt != 1 && rt != 2 && rt != 4 && rt != 8 && rt != 16) return false;
+    g_forced_rt = rt;
+    return true;
+}
+
+void set_att_grouped(bool on) { g_att_grouped = on; }
 
 bool mfma_layout_ok(const MatArgs &a, bool q5) {
     if (a.nb == 0) return false;
@@ -2607,13 +2298,8 @@ bool group_layout_ok(const GroupArgs &g, bool q5) {
 hipError_t launch_gemv_grouped(GroupArgs &g, bool q5, bool fast, hipStream_t s) {
     if (!g.nitems) return hipSuccess;
     if (!group_layout_ok(g, q5)) return hipErrorInvalidValue;
-    if (gemv_pin_ok(g, q5)) {
-        if (q5) return fast ? launch_gemv_pin<true, true>(g, s) : launch_gemv_pin<true, false>(g, s);
-        return fast ? launch_gemv_pin<false, true>(g, s) : launch_gemv_pin<false, false>(g, s);
-    }
-    const int rt = gemv_rows_per_tile(g.nb, q5, 0);
-    if (q5) return fast ? launch_gemv_stream_typed<true, true>(g, rt, s) : launch_gemv_stream_typed<true, false>(g, rt, s);
-    return fast ? launch_gemv_stream_typed<false, true>(g, rt, s) : launch_gemv_stream_typed<false, false>(g, rt, s);
+    if (q5) return fast ? launch_gemv_pin<true, true>(g, s) : launch_gemv_pin<true, false>(g, s);
+    return fast ? launch_gemv_pin<false, true>(g, s) : launch_gemv_pin<false, false>(g, s);
 }
 
 hipError_t launch_rope_kv(float *q, float *k, const float *v, uint32_t ntok, const AttnShape &sh, const float *cs,
@@ -2625,11 +2311,6 @@ hipError_t launch_rope_kv(float *q, float *k, const float *v, uint32_t ntok, con
     return hipGetLastError();
 }
 
-/* SMQ_ATT_GROUP=0 sends prefill attention to k_attend_rows instead (tuning, tests) */
-bool att_group_on() {
-    const char *e = getenv("SMQ_ATT_GROUP");
-    return !(e && *e && atoi(e) == 0);
-}
 
 bool attention_rows_ok(const AttnShape &sh, const void *q, const void *kcache, const void *vcache) {
     return sh.head_dim == AR_HD && ((uintptr_t)q & 15) == 0 && ((uintptr_t)kcache & 15) == 0 &&
@@ -2645,7 +2326,7 @@ hipError_t launch_attention(const float *q, const float *kcache, const float *vc
         return hipErrorInvalidValue;
     const uint32_t groups = (sh.head_dim + ATT_JW - 1) / ATT_JW;
     if (ntok > 1 && attention_rows_ok(sh, q, kcache, vcache) && sh.context <= AG_MAXP &&
-        sh.heads % sh.kv_heads == 0 && sh.heads / sh.kv_heads <= AG_MAXG && att_group_on()) {
+        sh.heads % sh.kv_heads == 0 && sh.heads / sh.kv_heads <= AG_MAXG && g_att_grouped) {
         hipLaunchKernelGGL(k_attend_group, dim3(ntok * sh.kv_heads), dim3(AG_WG), 0, s, q, kcache, vcache, att, sh, pos0,
                            pos_dev, flag, xd, xq);
         return hipGetLastError();

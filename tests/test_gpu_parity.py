@@ -359,25 +359,32 @@ def test_q5_scale_every_f16(orc):
 
 
 @pytest.mark.parametrize("rt", [1, 2, 4, 8, 16])
-@pytest.mark.parametrize("stage", [0, 1])
-def test_every_gemv_tile_variant(orc, rt, stage, monkeypatch):
-    """Forces each decode-GEMV variant (rows per workgroup, staged or direct
-    activation) through the launcher's tuning override, exact and fast, with
-    one- and multi-chunk widths."""
-    monkeypatch.setenv("SMQ_GEMV_RT", str(rt))
-    monkeypatch.setenv("SMQ_GEMV_STAGE", str(stage))
-    g = LcgUniform(1000 + rt * 10 + stage)
+def test_every_gemv_tile_variant(orc, rt):
+    """Forces each one-launch decode-GEMV tile shape (rows per workgroup)
+    through the tuning call, exact and fast, with one- and multi-chunk widths."""
+    g = LcgUniform(1000 + rt * 10)
     cases = [(False, 3, 37), (False, 28, 70), (False, 152, 9), (False, 300, 5), (True, 2, 41), (True, 48, 19),
              (True, 280, 6), (True, 600, 3)]
-    for q5, nb, rows in cases:
-        for fast in (False, True):
-            cols = nb * 32
-            w = weights(q5, nb * 7 + rows, rows, cols, 0.3)
-            x = g.uniform(-5, 5, cols).reshape(1, cols)
-            say("variant", rt, stage, q5, nb, rows, fast)
-            got, xd, xq = run_gemm(w, nb * (Q5B if q5 else Q8B), x, rows, 1, nb, q5, fast=fast)
-            want = orc.gemm(w, nb * (Q5B if q5 else Q8B), xd, xq, rows, 1, nb, q5=q5, fast=fast)
-            assert_same_f32(got, want, f"rt={rt} stage={stage} q5={q5} nb={nb} fast={fast}")
+    smq.set_gemv_rows(rt)
+    try:
+        for q5, nb, rows in cases:
+            for fast in (False, True):
+                cols = nb * 32
+                w = weights(q5, nb * 7 + rows, rows, cols, 0.3)
+                x = g.uniform(-5, 5, cols).reshape(1, cols)
+                say("variant", rt, q5, nb, rows, fast)
+                got, xd, xq = run_gemm(w, nb * (Q5B if q5 else Q8B), x, rows, 1, nb, q5, fast=fast)
+                want = orc.gemm(w, nb * (Q5B if q5 else Q8B), xd, xq, rows, 1, nb, q5=q5, fast=fast)
+                assert_same_f32(got, want, f"rt={rt} q5={q5} nb={nb} fast={fast}")
+    finally:
+        smq.set_gemv_rows(0)
+
+
+def test_gemv_rows_refuses_other_values():
+    for bad in (-1, 3, 5, 32):
+        with pytest.raises(smq.SmqError):
+            smq.set_gemv_rows(bad)
+    smq.set_gemv_rows(0)
 
 
 # ------------------------------------------------------------------ MFMA prefill

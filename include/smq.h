@@ -292,6 +292,17 @@ smq_status smq_decode_advance(int32_t *pos, uint32_t *count, const uint32_t *tok
 smq_status smq_argmax_advance(const float *logits, uint32_t vocab, const unsigned char *banned, uint32_t *token,
                               int32_t *pos, uint32_t *count, uint32_t *history, uint32_t capacity);
 
+/* ---- Q5 weight conversion (src/kernels.h:205, kernels.c:1064-1117) -------
+ * quantize_q5_row: cols floats x -> ceil(cols/32) Q5 blocks (22 B each) at
+ * out, byte for byte the reference's: signed extreme, the first minimum of 21
+ * f16-rounded candidate scales by binary64 squared error, codes packed as in
+ * docs/FORMAT.md:124-134. Device pointers, asynchronous. */
+void smq_quantize_q5_row(const float *x, uint32_t cols, unsigned char *out);
+/* The converter's loop over a tensor (src/quantize_main.c:107-121): `rows`
+ * rows of cols floats (row r at x + r*cols) into rows of ceil(cols/32)*22
+ * bytes (row r at out + r*ceil(cols/32)*22), one launch. */
+smq_status smq_quantize_q5_rows(const float *x, uint32_t rows, uint32_t cols, unsigned char *out);
+
 /* ---- dequantization (src/kernels.h:193-196, kernels.c:1044-1062) -------- */
 void smq_dequantize_q8_row(const unsigned char *w, uint32_t cols, float *out);
 void smq_dequantize_q5_row(const unsigned char *w, uint32_t cols, float *out);

@@ -114,6 +114,8 @@ _SIGS = {
     "smq_decode_advance": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32]),
     "smq_attention_rope_q8": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp]),
     "smq_argmax_advance": (ctypes.c_int, [_vp, _u32, _vp, _vp, _vp, _vp, _vp, _u32]),
+    "smq_quantize_q5_row": (None, [_vp, _u32, _vp]),
+    "smq_quantize_q5_rows": (ctypes.c_int, [_vp, _u32, _u32, _vp]),
     "smq_dequantize_q8_row": (None, [_vp, _u32, _vp]),
     "smq_dequantize_q5_row": (None, [_vp, _u32, _vp]),
     "smq_malloc": (_vp, [_sz]),
@@ -477,6 +479,16 @@ def numeric_check():
 
 
 # ---- src/kernels.h:193-196
+def quantize_q5_row(x, cols, out):
+    """quantize_q5_row (kernels.h:205) on device buffers."""
+    load().smq_quantize_q5_row(_p(x), cols, _p(out))
+    _check()
+
+
+def quantize_q5_rows(x, rows, cols, out):
+    _check(load().smq_quantize_q5_rows(_p(x), rows, cols, _p(out)))
+
+
 def dequantize_q8_row(w, cols, out):
     load().smq_dequantize_q8_row(_p(w), cols, _p(out))
     _check()

@@ -878,6 +878,17 @@ smq_status smq_decode_advance(int32_t *pos, uint32_t *count, const uint32_t *tok
                : t_status;
 }
 
+smq_status smq_quantize_q5_rows(const float *x, uint32_t rows, uint32_t cols, unsigned char *out) {
+    if (!ready()) return t_status;
+    if (!rows || !cols) return SMQ_OK;
+    const size_t row_out = (size_t)((cols + smq::QK - 1) / smq::QK) * smq::Q5_BYTES;
+    if (!extent_ok(x, (size_t)rows * cols * 4, "x") || !extent_ok(out, (size_t)rows * row_out, "out"))
+        return t_status;
+    return hip_ok(smq::launch_quantize_q5(x, rows, cols, out, g.cur), "quantize_q5") ? SMQ_OK : t_status;
+}
+
+void smq_quantize_q5_row(const float *x, uint32_t cols, unsigned char *out) { (void)smq_quantize_q5_rows(x, 1, cols, out); }
+
 void smq_dequantize_q8_row(const unsigned char *w, uint32_t cols, float *out) {
     if (!ready()) return;
     const uint32_t nb = (cols + smq::QK - 1) / smq::QK;

@@ -150,6 +150,9 @@ hipError_t launch_argmax(const float *logits, uint32_t n, const unsigned char *b
                          int32_t *pos, uint32_t *count, uint32_t *history, uint32_t capacity, hipStream_t s);
 hipError_t launch_embed(const unsigned char *w, size_t row_bytes, bool q5, uint32_t vocab, const uint32_t *tokens,
                         uint32_t ntok, uint32_t cols, float *out, int *flag, hipStream_t s);
+/* Q5 conversion (kernels.c:1064-1117): rows of cols floats to rows of
+ * ceil(cols/32) 22-byte blocks, row r at out + r*nb*22. */
+hipError_t launch_quantize_q5(const float *x, uint32_t rows, uint32_t cols, unsigned char *out, hipStream_t s);
 hipError_t launch_dequantize_row(const unsigned char *w, uint32_t cols, float *out, bool q5, hipStream_t s);
 
 }  // namespace smq

@@ -277,6 +277,15 @@ smq_status smq_attention_rope_q8(float *q, float *k, const float *v, const smq_a
  * non-banned id with a strictly greater logit (NaN never wins unless it is
  * the first candidate). banned may be NULL. UINT32_MAX if every id is banned. */
 smq_status smq_argmax(const float *logits, uint32_t vocab, const unsigned char *banned, uint32_t *token);
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): smq_argmax with its partial results in a static device
+ * array of the library (12 KiB per GPU, bound at smq_init) instead of the
+ * library's allocated workspace; it calls no allocation routine. Same result
+ * as smq_argmax. vocab is limited to 1,048,576 ids (SMQ_ERR_RANGE beyond).
+ * Every call on one GPU shares that array: calls that overlap on one GPU
+ * (different streams, or concurrent host threads) race. Asynchronous. */
+smq_status smq_argmax_noalloc(const float *logits, uint32_t vocab, const unsigned char *banned, uint32_t *token);
 /* model.c:669-677: x[t] = dequantized row tokens[t] of the embedding matrix
  * (embed->cols floats). Ids must be < embed->rows (checked by the caller, as
  * model.c:671-672 does; an id out of range raises the numeric flag). */

@@ -110,6 +110,7 @@ _SIGS = {
     "smq_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _u32, _vp]),
     "smq_attention_q8": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _u32, _vp, _vp, _vp]),
     "smq_argmax": (ctypes.c_int, [_vp, _u32, _vp, _vp]),
+    "smq_argmax_noalloc": (ctypes.c_int, [_vp, _u32, _vp, _vp]),
     "smq_embed": (ctypes.c_int, [ctypes.POINTER(_QMat), _vp, _u32, _vp]),
     "smq_decode_advance": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32]),
     "smq_attention_rope_q8": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp]),
@@ -457,6 +458,11 @@ def attention_rope_q8(q, k, v, shape, cos_table, sin_table, keys, values, att, x
 
 def argmax(logits, vocab, banned, token):
     _check(load().smq_argmax(_p(logits), vocab, _p(banned), _p(token)))
+
+
+def argmax_noalloc(logits, vocab, banned, token):
+    """smq_argmax_noalloc: smq_argmax with its partials in the library's static device array."""
+    _check(load().smq_argmax_noalloc(_p(logits), vocab, _p(banned), _p(token)))
 
 
 def embed(w, tokens, ntok, x):

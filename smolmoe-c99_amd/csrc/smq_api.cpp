@@ -210,6 +210,8 @@ smq_status smq_init(int device) {
     if (!hip_ok(hipMalloc((void **)&g.scores, smq::SCORE_WORKSPACE_BYTES), "hipMalloc")) return t_status;
     if (!hip_ok(hipEventCreate(&g.t0), "hipEventCreate") || !hip_ok(hipEventCreate(&g.t1), "hipEventCreate"))
         return t_status;
+    /* the allocation-free argmax's static partials: their device address, once, with the device current */
+    if (!hip_ok(smq::bind_noalloc_scratch(device), "hipGetSymbolAddress(scratch)")) return t_status;
     g.cur = g.own;
     g.device = device;
     const char *env = getenv("SMQ_CHECKS");
@@ -832,6 +834,23 @@ smq_status smq_argmax(const float *logits, uint32_t vocab, const unsigned char *
         return t_status;
     return hip_ok(smq::launch_argmax(logits, vocab, banned, token, g.argmax_parts, nullptr, nullptr, nullptr, 0, g.cur),
                   "argmax")
+               ? SMQ_OK
+               : t_status;
+}
+
+smq_status smq_argmax_noalloc(const float *logits, uint32_t vocab, const unsigned char *banned, uint32_t *token) {
+    if (!ready()) return t_status;
+    if (!vocab) return set_status(SMQ_ERR_RANGE, "argmax_noalloc: empty vocabulary");
+    if (vocab > smq::NOALLOC_MAX_VOCAB)
+        return set_status(SMQ_ERR_RANGE, "argmax_noalloc: vocabulary of %u ids exceeds its static scratch (%u ids)",
+                          vocab, smq::NOALLOC_MAX_VOCAB);
+    void *parts = smq::noalloc_scratch(g.device);
+    if (!parts) return set_status(SMQ_ERR_STATE, "argmax_noalloc: static scratch not bound on device %d", g.device);
+    if (!extent_ok(logits, (size_t)vocab * 4, "logits") || !extent_ok(banned, banned ? vocab : 0, "banned") ||
+        !extent_ok(token, 4, "token"))
+        return t_status;
+    return hip_ok(smq::launch_argmax(logits, vocab, banned, token, parts, nullptr, nullptr, nullptr, 0, g.cur),
+                  "argmax_noalloc")
                ? SMQ_OK
                : t_status;
 }

@@ -148,6 +148,14 @@ constexpr uint32_t MAX_ARGMAX_PARTS = 1024;
 constexpr uint32_t ARGMAX_PART_BYTES = 12;
 hipError_t launch_argmax(const float *logits, uint32_t n, const unsigned char *banned, uint32_t *out, void *parts,
                          int32_t *pos, uint32_t *count, uint32_t *history, uint32_t capacity, hipStream_t s);
+/* The allocation-free argmax's partials: a static device array of
+ * MAX_ARGMAX_PARTS partials. bind_noalloc_scratch (with `device` current)
+ * records its device address; noalloc_scratch returns it (NULL if unbound).
+ * With one span of AM_SPAN ids per partial it serves vocabularies up to
+ * NOALLOC_MAX_VOCAB ids. */
+constexpr uint32_t NOALLOC_MAX_VOCAB = MAX_ARGMAX_PARTS * 1024u;
+hipError_t bind_noalloc_scratch(int device);
+void *noalloc_scratch(int device);
 hipError_t launch_embed(const unsigned char *w, size_t row_bytes, bool q5, uint32_t vocab, const uint32_t *tokens,
                         uint32_t ntok, uint32_t cols, float *out, int *flag, hipStream_t s);
 /* Q5 conversion (kernels.c:1064-1117): rows of cols floats to rows of

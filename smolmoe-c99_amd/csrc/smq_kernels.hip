@@ -2398,6 +2398,30 @@ hipError_t launch_attention_rope(const float *q, const float *k, const float *v,
     return hipGetLastError();
 }
 
+/* The allocation-free argmax's partials (smq_argmax_noalloc): a file-scope
+ * device array of MAX_ARGMAX_PARTS partials (12 KiB), which every GPU the
+ * library runs on holds until the process ends. Host code never passes the
+ * symbol itself (on the host it is a stand-in, not a device address): at
+ * smq_init, with the device current, bind_noalloc_scratch takes its device
+ * address once per device, and launches use that address. */
+static __device__ __align__(256) ArgBest scratch[MAX_ARGMAX_PARTS];
+static_assert(NOALLOC_MAX_VOCAB == MAX_ARGMAX_PARTS * AM_SPAN, "one AM_SPAN of ids per partial");
+constexpr int MAX_BOUND_DEVICES = 64;
+void *g_scratch_dev[MAX_BOUND_DEVICES] = {};
+
+hipError_t bind_noalloc_scratch(int device) {
+    if (device < 0 || device >= MAX_BOUND_DEVICES) return hipErrorInvalidDevice;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_dev[device] = p;
+    return hipSuccess;
+}
+
+void *noalloc_scratch(int device) {
+    return device >= 0 && device < MAX_BOUND_DEVICES ? g_scratch_dev[device] : nullptr;
+}
+
 hipError_t launch_argmax(const float *logits, uint32_t n, const unsigned char *banned, uint32_t *out, void *parts,
                          int32_t *pos, uint32_t *count, uint32_t *history, uint32_t capacity, hipStream_t s) {
     /* span: a multiple of AM_SPAN, large enough for at most MAX_ARGMAX_PARTS workgroups */

@@ -1,0 +1,259 @@
+/* Coalesced-tile decode GEMV for Q8 rows of 36*nb bytes with nb % 4 == 0
+ * (every row a whole number of 16-byte pieces) at 16-byte aligned row
+ * starts; built for the 896-wide rows (nb 28) of the Qwen2.5-0.5B gate, up,
+ * q, k, v and o matrices and the LM head.
+ *
+ * Arithmetic (src/kernels.c:36-79): for row r, block b, lane l the exact int32
+ * sum s = w[b][4l..4l+3] . x[b][4l..4l+3] (v_dot4), the product
+ * p = (wscale_b * xscale_b) * float(s) (two roundings; fast mode one fmaf),
+ * acc_l = acc_l + p over b in increasing order, then
+ * ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)).
+ *
+ * Layout. A tile is RT consecutive rows, i.e. RT*36*nb contiguous bytes; each
+ * thread loads fixed 16-byte pieces of it (piece tid + j*CT_NT), so every
+ * load instruction of a wave reads 1 KiB of consecutive bytes, marked
+ * non-temporal (the weights are read once). A row is 9*nb dwords: dword k is
+ * field k % 9 of block k / 9 (field 0 the f32 scale, field 1 + l the four
+ * int8 of lane l). The tile shape repeats every step, so each thread knows
+ * once, for each of its dwords, the activation word it meets (the block's x
+ * scale for field 0, x's lane-l word otherwise) and where its result goes in
+ * LDS: a scale dword stores d = wscale * xscale into d[r][b], a lane dword
+ * stores float(s) into sf[r][l][b] (exact: |s| < 2^24). After one barrier,
+ * chain thread (r, l) forms p = d[r][b] * sf[r][l][b] and adds it in block
+ * order, the eight lanes of a row meet in the DPP lane tree, and lane 7
+ * stores (bias, finiteness, residual add as the other decode kernels). Two
+ * LDS buffers alternate, and the next D tiles' loads stay in flight.
+ */
+#include <float.h>
+#include <stddef.h>
+
+#include "smq_device.h"
+#include "smq_internal.h"
+
+namespace smq {
+namespace {
+
+constexpr uint32_t CT_NT = 512;
+
+__device__ __forceinline__ uint32_t find_ct_item(const GroupArgs &g, uint32_t wg) {
+    uint32_t lo = 0, hi = g.nitems; /* last item with wg_begin <= wg */
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) / 2;
+        if (g.item[mid].wg_begin <= wg) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+/* One step's LDS: lane sums sf[r][l][b] (pitch SP floats per (r, l)), block scale products
+ * d[r][b] (pitch SP per row), and a sink for the writes of pieces past the tile. */
+template <uint32_t RT, uint32_t SP>
+struct CtBuf {
+    float sf[RT * 8 * SP];
+    float d[RT * SP];
+    float sink[64];
+};
+
+template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT, uint32_t D>
+__global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gemv_ct(GroupArgs g) {
+    static_assert(NB % 4 == 0, "rows of whole 16-byte pieces");
+    constexpr uint32_t C16 = 9 * NB / 4;       /* 16-byte pieces per row */
+    constexpr uint32_t TCH = RT * C16;         /* pieces per tile */
+    /* LDS pitch: a multiple of four floats (16-byte chain reads) that is 4 mod 32, so the lane
+     * sums of one block's eight lanes (stored 8 pitches apart by one write) fall in distinct
+     * banks, and the eight chain lanes of a row read distinct 16-byte bank groups (measured: a
+     * pitch of 32 floats, where those writes collide, cost 7 %) */
+    constexpr uint32_t SP = (NB + 3) / 4 * 4 + (36 - (NB + 3) / 4 * 4 % 32) % 32;
+    static_assert(SP % 32 == 4 && SP >= NB, "pitch 4 mod 32");
+    constexpr uint32_t NQ = NB / 4;
+    static_assert(TCH <= CPT * CT_NT, "each piece of a tile has a thread slot");
+    using Buf = CtBuf<RT, SP>;
+    __shared__ __attribute__((aligned(16))) Buf buf[2];
+
+    const uint32_t tid = threadIdx.x;
+    const GroupItem &I = g.item[find_ct_item(g, blockIdx.x)];
+    const uint32_t rows = I.rows, tiles = (rows + RT - 1) / RT, wg = blockIdx.x - I.wg_begin;
+    const uint32_t t0 = (uint32_t)((uint64_t)tiles * wg / I.nwg), t1 = (uint32_t)((uint64_t)tiles * (wg + 1) / I.nwg);
+    const uint32_t my_steps = t1 - t0;
+    const unsigned char *wbase = I.w;
+    const size_t row_bytes = I.row_bytes;
+    const float *bias_p = I.bias, *xd = I.xd;
+    float *y = I.y;
+    const bool accum = I.accumulate != 0;
+
+    /* this thread's piece slots j: piece c = tid + j*CT_NT of a tile (row c / C16, 16-byte
+     * piece c % C16 of it); per dword q the activation word it meets and its LDS target */
+    uint32_t xw[CPT][4], dst[CPT][4], prow[CPT], poff[CPT], scale_mask = 0;
+    const uint32_t *xq32 = (const uint32_t *)I.xq;
+#pragma unroll
+    for (uint32_t j = 0; j < CPT; ++j) {
+        const uint32_t c = tid + j * CT_NT, cc = c < TCH ? c : 0, r = cc / C16, pc = cc % C16;
+        prow[j] = r;
+        poff[j] = 16 * pc;
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+            const uint32_t k = 4 * pc + q, b = k / 9, f = k % 9;
+            const uint32_t sw = __float_as_uint(xd[b]), lw = xq32[8 * b + (f ? f - 1 : 0)];
+            xw[j][q] = f == 0 ? sw : lw;
+            if (f == 0) scale_mask |= 1u << (4 * j + q);
+            const uint32_t at = f == 0 ? (uint32_t)(offsetof(Buf, d) / 4) + r * SP + b
+                                       : (uint32_t)(offsetof(Buf, sf) / 4) + (r * 8 + f - 1) * SP + b;
+            dst[j][q] = c < TCH ? at : (uint32_t)(offsetof(Buf, sink) / 4) + (tid & 63u);
+        }
+    }
+
+    /* a tile's bytes, coalesced and non-temporal; rows past the matrix re-read its last row (in
+     * bounds, never stored), so every thread issues the same loads at every step */
+    auto load = [&](u4a (&w)[CPT], uint32_t tile) __attribute__((always_inline)) {
+        const uint32_t tc = tile < tiles ? tile : tiles - 1;
+        const uint32_t last = (rows - tc * RT < RT ? rows - tc * RT : RT) - 1;
+        const unsigned char *base = wbase + (size_t)tc * RT * row_bytes;
+#pragma unroll
+        for (uint32_t j = 0; j < CPT; ++j) {
+            const uint32_t r = prow[j] < last ? prow[j] : last;
+            w[j] = __builtin_nontemporal_load((const u4a *)(base + (size_t)r * row_bytes + poff[j]));
+        }
+    };
+    /* chain thread (row cr, lane cl): its row's bias and prior output (BP: some item of the launch
+     * has a bias or adds into y; otherwise no such loads at all, so the only loads in flight are
+     * the tiles' and each step waits for its own tile only) */
+    const uint32_t cr = tid / 8, cl = tid % 8;
+    auto load_bp = [&](float &bias, float &prior, uint32_t tile) __attribute__((always_inline)) {
+        if constexpr (!BP) {
+            bias = 0.0f;
+            prior = 0.0f;
+            return;
+        }
+        const uint32_t orow = tile * RT + (cr < RT ? cr : 0), oc = orow < rows ? orow : rows - 1;
+        bias = *(bias_p ? bias_p + oc : xd);
+        prior = *(accum ? y + oc : xd);
+    };
+
+    u4a W[D][CPT];
+    float B[D], P[D];
+#pragma unroll
+    for (uint32_t j = 0; j < D; ++j) {
+        load(W[j], t0 + j);
+        load_bp(B[j], P[j], t0 + j);
+    }
+    /* D steps per trip with no early exit (a straight trip keeps the in-flight tiles in their
+     * registers); a step past the range computes and does not store */
+    for (uint32_t k = 0; k < my_steps; k += D) {
+#pragma unroll
+        for (uint32_t j = 0; j < D; ++j) {
+            const uint32_t step = k + j, tile = t0 + step;
+            const bool live = step < my_steps;
+            float *lb = (float *)&buf[step & 1];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (uint32_t c = 0; c < CPT; ++c) {
+                const uint32_t wv[4] = {W[j][c].x, W[j][c].y, W[j][c].z, W[j][c].w};
+#pragma unroll
+                for (uint32_t q = 0; q < 4; ++q) {
+                    const float fs = (float)dot4(wv[q], xw[c][q], 0);
+                    const float dv = __uint_as_float(wv[q]) * __uint_as_float(xw[c][q]);
+                    lb[dst[c][q]] = (scale_mask >> (4 * c + q)) & 1u ? dv : fs;
+                }
+            }
+            load(W[j], tile + D); /* consumed: the next tile for these registers */
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+            if (tid < RT * 8) {
+                const Buf &bb = buf[step & 1];
+                const float4 *sp = (const float4 *)&bb.sf[(cr * 8 + cl) * SP];
+                const float4 *dp = (const float4 *)&bb.d[cr * SP];
+                float acc = 0.0f;
+#pragma unroll 7
+                for (uint32_t qq = 0; qq < NQ; ++qq) {
+                    const float4 sv = sp[qq], dv = dp[qq];
+                    if (FAST) {
+                        acc = __builtin_fmaf(dv.x, sv.x, acc);
+                        acc = __builtin_fmaf(dv.y, sv.y, acc);
+                        acc = __builtin_fmaf(dv.z, sv.z, acc);
+                        acc = __builtin_fmaf(dv.w, sv.w, acc);
+                    } else {
+                        float p;
+                        p = dv.x * sv.x; acc = acc + p;
+                        p = dv.y * sv.y; acc = acc + p;
+                        p = dv.z * sv.z; acc = acc + p;
+                        p = dv.w * sv.w; acc = acc + p;
+                    }
+                }
+                const float v = reduce8_to_lane7(acc);
+                const uint32_t row = tile * RT + cr;
+                if (live && cl == 7 && row < rows) {
+                    float o = v;
+                    if (bias_p) o = o + B[j]; /* model.c:259-262 */
+                    if (g.flag && !(fabsf(o) <= FLT_MAX)) *g.flag = 1;
+                    if (accum) o = P[j] + o;
+                    y[row] = o;
+                }
+            }
+            load_bp(B[j], P[j], tile + D);
+        }
+    }
+}
+
+template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT, uint32_t D>
+hipError_t launch_ct_shape(GroupArgs &g, hipStream_t s) {
+    static int resident = 0;
+    if (!resident) {
+        int per_cu = 0, dev = 0, cus = 0;
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemv_ct<FAST, BP, NB, RT, CPT, D>, CT_NT, 0);
+        if (e == hipSuccess) e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        resident = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+    }
+    uint64_t tiles = 0;
+    for (uint32_t i = 0; i < g.nitems; ++i) tiles += (g.item[i].rows + RT - 1) / RT;
+    if (!tiles) return hipSuccess;
+    /* every item a share of the resident workgroups in proportion to its tiles (at least one,
+     * at most one per tile), each a contiguous tile range */
+    uint32_t wgs = 0;
+    for (uint32_t i = 0; i < g.nitems; ++i) {
+        const uint32_t t = (g.item[i].rows + RT - 1) / RT;
+        uint32_t n = (uint32_t)(((uint64_t)resident * t + tiles / 2) / tiles);
+        n = n < 1 ? 1 : (n > t ? t : n);
+        g.item[i].wg_begin = wgs;
+        g.item[i].nwg = n;
+        wgs += n;
+    }
+    hipLaunchKernelGGL((k_gemv_ct<FAST, BP, NB, RT, CPT, D>), dim3(wgs), dim3(CT_NT), 0, s, g);
+    return hipGetLastError();
+}
+
+/* 16 rows of 28 blocks per step: 1008 pieces in 1024 thread slots; one tile in flight per
+ * workgroup while the previous one is reduced (measured on the 48 gate/up GEMVs of Qwen2.5-0.5B:
+ * two in flight, or 8- and 12-row tiles, were no faster) */
+template <bool FAST, bool BP>
+hipError_t launch_ct_bp(GroupArgs &g, hipStream_t s) {
+    return g.nb == 28 ? launch_ct_shape<FAST, BP, 28, 16, 2, 1>(g, s) : hipErrorInvalidValue;
+}
+
+template <bool FAST>
+hipError_t launch_ct_fast(GroupArgs &g, hipStream_t s) {
+    bool bp = false;
+    for (uint32_t i = 0; i < g.nitems; ++i) bp = bp || g.item[i].bias || g.item[i].accumulate;
+    return bp ? launch_ct_bp<FAST, true>(g, s) : launch_ct_bp<FAST, false>(g, s);
+}
+
+}  // namespace
+
+bool gemv_ct_ok(const GroupArgs &g, bool q5) {
+    if (q5 || g.nb != 28) return false; /* 152-block rows: the pinned kernel measured faster */
+    for (uint32_t i = 0; i < g.nitems; ++i) {
+        const GroupItem &it = g.item[i];
+        if ((((uintptr_t)it.w) | it.row_bytes) & 15u) return false;
+        if (it.row_bytes != (size_t)g.nb * Q8_BYTES) return false; /* a tile is contiguous rows */
+        if (((uintptr_t)it.xq | (uintptr_t)it.xd) & 3u) return false;
+        if (!it.rows) return false;
+    }
+    return true;
+}
+
+hipError_t launch_gemv_ct(GroupArgs &g, bool fast, hipStream_t s) {
+    return fast ? launch_ct_fast<true>(g, s) : launch_ct_fast<false>(g, s);
+}
+
+}  // namespace smq

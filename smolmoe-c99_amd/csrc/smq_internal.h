@@ -61,6 +61,10 @@ struct GroupArgs {
     int *flag;
     uint32_t cpr, nch, rt; /* pinned launch: tasks per chunk, chunks per row, rows per tile */
 };
+/* Coalesced-tile Q8 GEMV (csrc/smq_gemv.hip): rows of nb = 28 or 152 blocks
+ * packed at 36*nb bytes, 16-byte aligned, 4-byte aligned activations. */
+bool gemv_ct_ok(const GroupArgs &g, bool q5);
+hipError_t launch_gemv_ct(GroupArgs &g, bool fast, hipStream_t s);
 /* Layout the streaming kernel needs: 4-byte aligned rows, Q5 nb even. */
 bool group_layout_ok(const GroupArgs &g, bool q5);
 hipError_t launch_gemv_grouped(GroupArgs &g, bool q5, bool fast, hipStream_t s);

@@ -258,12 +258,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
             const uint32_t tl = real ? tile : t1 - 1, rl = tl * rt + (worker ? tr : 0);
             const uint32_t rc = rl < rows ? rl : rows - 1, bc = b < nb ? b : 0;
             fetch(wbase + (size_t)rc * row_bytes + (size_t)bc * BYTES);
-            /* the chain threads' row: its bias and prior output (the other threads
-             * read the tile's first row; an absent one reads the activation's
-             * first scale: unused) */
-            const uint32_t orow = tl * rt + (tid < chains ? tid / 8 : 0), oc = orow < rows ? orow : rows - 1;
-            T.bias = *(bias_p ? bias_p + oc : xd);
-            T.prior = *(accum ? y + oc : xd);
         } else {
             /* several chunks per row: idle task lanes issue nothing (measured
              * faster here than the branch-free form) */
@@ -275,11 +269,22 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
             }
         }
     };
+    /* one chunk: the chain threads' row, its bias and prior output (the other threads read the
+     * tile's first row; an absent one reads the activation's first scale: unused). Requested
+     * after the previous use of the task's registers is complete (its store), so no loaded
+     * value is copied while its load is in flight */
+    auto load_bp = [&](PinTask<Q5> &T, uint32_t tile, bool real) __attribute__((always_inline)) {
+        const uint32_t tl = real ? tile : t1 - 1;
+        const uint32_t orow = tl * rt + (tid < chains ? tid / 8 : 0), oc = orow < rows ? orow : rows - 1;
+        T.bias = *(bias_p ? bias_p + oc : xd);
+        T.prior = *(accum ? y + oc : xd);
+    };
     PinTask<Q5> T[D];
     uint32_t lt = t0, lc = 0; /* load cursor */
 #pragma unroll
     for (int j = 0; j < D; ++j) {
         load(T[j], lt, lc, (uint32_t)j < my_steps);
+        if constexpr (ONE) load_bp(T[j], lt, (uint32_t)j < my_steps);
         if (++lc == nch) { lc = 0; ++lt; }
     }
     __syncthreads(); /* activation staged */
@@ -300,6 +305,80 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
             }
         }
     }
+    /* one product step of task T: its lane products into pb (an idle task's to the sink) */
+    auto products = [&](const PinTask<Q5> &Tk, float *pb, float *db, uint32_t chunk) __attribute__((always_inline)) {
+        const bool ok = Tk.ok;
+        Q5Fields f[2];
+        if constexpr (Q5) q5_parse_pair(Tk.w, f[0], f[1]);
+        float d[TB];
+        uint32_t xs[TB][8];
+#pragma unroll
+        for (int q = 0; q < TB; ++q) {
+            const uint32_t bb = ti * TB + q, b0 = chunk * cb + bb, b = b0 < nb ? b0 : nb - 1;
+            d[q] = (Q5 ? f[q].scale : __uint_as_float(Tk.w[0])) * (HOIST ? hx_d[q] : act_d[b]);
+            if (FAST) db[ok ? (bb / 4) * ds + tr * 4 + (bb % 4) : PF / 8 + 128 + q] = d[q];
+            if constexpr (HOIST) {
+#pragma unroll
+                for (int l = 0; l < 8; ++l) xs[q][l] = hx_q[q][l];
+            } else {
+                const u4a xa = *(const u4a *)&act_q[b * 8], xb = *(const u4a *)&act_q[b * 8 + 4];
+                xs[q][0] = xa.x; xs[q][1] = xa.y; xs[q][2] = xa.z; xs[q][3] = xa.w;
+                xs[q][4] = xb.x; xs[q][5] = xb.y; xs[q][6] = xb.z; xs[q][7] = xb.w;
+            }
+        }
+        const uint32_t bb0 = ti * TB;
+        float *slot = ok ? pb + (bb0 / 4) * gs + tr * 32 + (bb0 % 4) : pb + PF;
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            float v[TB];
+#pragma unroll
+            for (int q = 0; q < TB; ++q) {
+                int sv;
+                if constexpr (Q5)
+                    sv = dot4(q5_codes(f[q], l), xs[q][l], HOIST ? hx_c[q][l] : dot4(xs[q][l], 0xf0f0f0f0u, 0));
+                else sv = dot4(Tk.w[1 + l], xs[q][l], 0);
+                v[q] = FAST ? (float)sv : d[q] * (float)sv;
+            }
+            put_lane<TB>(slot, l, v[0], v[TB - 1]);
+        }
+    };
+    if constexpr (ONE) {
+        /* one chunk per row: every step is a whole tile. D steps per trip with no early exit (a
+         * straight trip keeps the in-flight tasks in their registers); a step past the range is
+         * computed (idle products, sink) and not stored */
+        for (uint32_t k = 0; k < my_steps; k += D) {
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                const uint32_t step = k + j, tile = t0 + step;
+                const bool live = step < my_steps;
+                float *pb = prod[step & 1];
+                float *db = dsc[FAST ? step & 1 : 0];
+                __builtin_amdgcn_sched_barrier(0);
+                products(T[j], pb, db, 0);
+                load(T[j], tile + D, 0, step + D < my_steps); /* consumed: the next task for these registers */
+                __builtin_amdgcn_sched_barrier(0);
+                __syncthreads();
+                if (tid < chains) {
+                    float acc = 0.0f;
+                    const float4 *pp = (const float4 *)pb + tid, *dp = FAST ? (const float4 *)db + tid / 8 : nullptr;
+                    if constexpr (!Q5) chain_sum_padded<FAST, 8>(acc, pp, gs / 4, dp, ds / 4, (nb + 3) / 4);
+                    else if (nb <= 32) chain_sum<FAST, 8>(acc, pp, gs / 4, dp, ds / 4, nb);
+                    else chain_sum<FAST, 32>(acc, pp, gs / 4, dp, ds / 4, nb);
+                    const float v = reduce8_to_lane7(acc);
+                    const uint32_t r = tile * rt + tid / 8;
+                    if (live && (tid & 7) == 7 && r < rows) {
+                        float o = v;
+                        if (bias_p) o = o + T[j].bias; /* model.c:259-262 */
+                        if (g.flag && !(fabsf(o) <= FLT_MAX)) *g.flag = 1;
+                        if (accum) o = T[j].prior + o;
+                        y[r] = o;
+                    }
+                }
+                load_bp(T[j], tile + D, step + D < my_steps);
+            }
+        }
+        return;
+    }
     uint32_t ct = t0, cc = 0; /* chain cursor */
     float acc = 0.0f, bias = 0.0f, prior = 0.0f;
     for (uint32_t k = 0; k < my_steps; k += D) {
@@ -308,42 +387,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
             if (k + j >= my_steps) break;
             float *pb = prod[(k + j) & 1];
             float *db = dsc[FAST ? (k + j) & 1 : 0];
-            if (ONE || T[j].ok) { /* one chunk: every lane forms products, an idle task's go to the sink */
-                const bool ok = T[j].ok;
-                Q5Fields f[2];
-                if constexpr (Q5) q5_parse_pair(T[j].w, f[0], f[1]);
-                float d[TB];
-                uint32_t xs[TB][8];
-#pragma unroll
-                for (int q = 0; q < TB; ++q) {
-                    const uint32_t bb = ti * TB + q, b0 = cc * cb + bb, b = b0 < nb ? b0 : nb - 1;
-                    d[q] = (Q5 ? f[q].scale : __uint_as_float(T[j].w[0])) * (HOIST ? hx_d[q] : act_d[b]);
-                    if (FAST) db[ok ? (bb / 4) * ds + tr * 4 + (bb % 4) : PF / 8 + 128 + q] = d[q];
-                    if constexpr (HOIST) {
-#pragma unroll
-                        for (int l = 0; l < 8; ++l) xs[q][l] = hx_q[q][l];
-                    } else {
-                        const u4a xa = *(const u4a *)&act_q[b * 8], xb = *(const u4a *)&act_q[b * 8 + 4];
-                        xs[q][0] = xa.x; xs[q][1] = xa.y; xs[q][2] = xa.z; xs[q][3] = xa.w;
-                        xs[q][4] = xb.x; xs[q][5] = xb.y; xs[q][6] = xb.z; xs[q][7] = xb.w;
-                    }
-                }
-                const uint32_t bb0 = ti * TB;
-                float *slot = ok ? pb + (bb0 / 4) * gs + tr * 32 + (bb0 % 4) : pb + PF;
-#pragma unroll
-                for (int l = 0; l < 8; ++l) {
-                    float v[TB];
-#pragma unroll
-                    for (int q = 0; q < TB; ++q) {
-                        int sv;
-                        if constexpr (Q5)
-                            sv = dot4(q5_codes(f[q], l), xs[q][l], HOIST ? hx_c[q][l] : dot4(xs[q][l], 0xf0f0f0f0u, 0));
-                        else sv = dot4(T[j].w[1 + l], xs[q][l], 0);
-                        v[q] = FAST ? (float)sv : d[q] * (float)sv;
-                    }
-                    put_lane<TB>(slot, l, v[0], v[TB - 1]);
-                }
-            }
+            if (T[j].ok) products(T[j], pb, db, cc);
             /* this task is consumed: its slot reloads now, a barrier and a chain earlier than
              * at the end of the step (the chain threads keep its bias and prior output) */
             const float tbias = T[j].bias, tprior = T[j].prior;
@@ -357,8 +401,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
                 }
                 const uint32_t count = nb - cc * cb < cb ? nb - cc * cb : cb;
                 const float4 *pp = (const float4 *)pb + tid, *dp = FAST ? (const float4 *)db + tid / 8 : nullptr;
-                if constexpr (ONE && !Q5) chain_sum_padded<FAST, 8>(acc, pp, gs / 4, dp, ds / 4, (nb + 3) / 4);
-                else if (!Q5 || cb <= 32) chain_sum<FAST, 8>(acc, pp, gs / 4, dp, ds / 4, count);
+                if (!Q5 || cb <= 32) chain_sum<FAST, 8>(acc, pp, gs / 4, dp, ds / 4, count);
                 else chain_sum<FAST, 32>(acc, pp, gs / 4, dp, ds / 4, count);
                 if (cc + 1 == nch) {
                     const float v = reduce8_to_lane7(acc);
@@ -2125,9 +2168,10 @@ hipError_t launch_gemv_pin_shape(GroupArgs &g, hipStream_t s) {
     for (uint32_t i = 0; i < g.nitems; ++i) tiles += (g.item[i].rows + g.rt - 1) / g.rt;
     if (!tiles) return hipSuccess;
     uint32_t wgs = 0;
+    const uint64_t target = (uint64_t)resident;
     for (uint32_t i = 0; i < g.nitems; ++i) {
         const uint32_t t = (g.item[i].rows + g.rt - 1) / g.rt;
-        uint32_t n = (uint32_t)(((uint64_t)resident * t + tiles / 2) / tiles);
+        uint32_t n = (uint32_t)((target * t + tiles / 2) / tiles);
         n = n < 1 ? 1 : (n > t ? t : n);
         g.item[i].wg_begin = wgs;
         g.item[i].nwg = n;
@@ -2139,6 +2183,7 @@ hipError_t launch_gemv_pin_shape(GroupArgs &g, hipStream_t s) {
 
 template <bool Q5, bool FAST>
 hipError_t launch_gemv_pin(GroupArgs &g, hipStream_t s) {
+    if (!Q5 && gemv_ct_ok(g, false)) return launch_gemv_ct(g, FAST, s); /* packed 28-block rows */
     const uint32_t ppr = Q5 ? (g.nb + 1) / 2 : g.nb;
     if (ppr <= pin_cpr<Q5>()) return launch_gemv_pin_shape<Q5, FAST, true>(g, s);
     return launch_gemv_pin_shape<Q5, FAST, false>(g, s);

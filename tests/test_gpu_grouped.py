@@ -57,19 +57,28 @@ GROUP_CASES = [
     (False, 544, [100000], False),
     (False, 544, [60000, 7], True),
 ]
+# items with neither bias nor residual add (the kernels then load no bias or prior output)
+PLAIN_CASES = [
+    (False, 896, [4864, 4864, 896, 7], False),
+    (False, 896, [4864, 100], True),
+    (False, 4864, [896, 896, 33], False),
+    (False, 4864, [896, 5], True),
+    (True, 1536, [8960, 5], False),
+]
 
 
-@pytest.mark.parametrize("q5,cols,rows,fast", GROUP_CASES)
-def test_grouped_gemv(orc, q5, cols, rows, fast):
-    say("grouped", q5, cols, rows, fast)
+@pytest.mark.parametrize("q5,cols,rows,fast,plain", [c + (False,) for c in GROUP_CASES] +
+                         [c + (True,) for c in PLAIN_CASES])
+def test_grouped_gemv(orc, q5, cols, rows, fast, plain):
+    say("grouped", q5, cols, rows, fast, plain)
     smq.kernels_set_fast(fast)
     nb = (cols + 31) // 32
     bb = 22 if q5 else 36
     items, want = [], []
     for i, r in enumerate(rows):
         w = (synth.q5_weights if q5 else synth.q8_weights)(100 + i, r, cols)
-        bias = synth.normal(200 + i, r, 0.02) if i % 2 == 0 else None
-        acc = i % 3 == 1
+        bias = synth.normal(200 + i, r, 0.02) if i % 2 == 0 and not plain else None
+        acc = i % 3 == 1 and not plain
         y0 = synth.normal(300 + i, r) if acc else np.zeros(r, np.float32)
         d, q, hd, hq = quantized(400 + i, cols)
         ok, prod = orc.mat_item(w, nb * bb, r, bias, hd, hq, 1, nb, q5=q5, fast=fast)

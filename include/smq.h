@@ -232,6 +232,14 @@ smq_status smq_matmul_act(const smq_mat_item *items, uint32_t n, const smq_act *
  * row if the call falls back. */
 smq_status smq_matmul_glu(const smq_qmat *gate, const smq_qmat *up, const smq_act *act, int glu, float *h,
                           float *gate_scratch);
+/* smq_matmul_glu followed by silu_quantize's quantization (model.c:409-415:
+ * quantize_q8 of h): hd (ceil(rows/32) scales) and hq (32 per block) receive
+ * h's Q8 blocks, h (may be NULL where the shape allows) the f32 values. On
+ * packed 896-wide Q8 rows the whole step is one launch; other shapes take the
+ * two-call form, which needs h. The numeric flag as smq_matmul_glu, plus a
+ * non-finite h. */
+smq_status smq_matmul_glu_q8(const smq_qmat *gate, const smq_qmat *up, const smq_act *act, int glu, float *h,
+                             float *hd, int8_t *hq, float *gate_scratch);
 smq_status smq_numeric_check(void);
 
 /* ---- decoder pieces around the matmuls ----------------------------------

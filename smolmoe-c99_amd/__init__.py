@@ -105,6 +105,8 @@ _SIGS = {
     "smq_matmul_act": (ctypes.c_int, [ctypes.POINTER(_MatItem), _u32, ctypes.POINTER(_Act)]),
     "smq_matmul_glu": (ctypes.c_int, [ctypes.POINTER(_QMat), ctypes.POINTER(_QMat), ctypes.POINTER(_Act), ctypes.c_int,
                                       _vp, _vp]),
+    "smq_matmul_glu_q8": (ctypes.c_int, [ctypes.POINTER(_QMat), ctypes.POINTER(_QMat), ctypes.POINTER(_Act),
+                                         ctypes.c_int, _vp, _vp, _vp, _vp]),
     "smq_gemv_grouped": (ctypes.c_int, [ctypes.POINTER(_GroupItem), _u32]),
     "smq_rope_kv": (ctypes.c_int, [_vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _vp, _vp, _vp, _vp, _u32, _vp]),
     "smq_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _u32, _vp]),
@@ -415,6 +417,13 @@ def matmul_glu(gate, up, activation, glu, h, gate_scratch=None):
     g, u = gate._c(), up._c()
     _check(load().smq_matmul_glu(ctypes.byref(g), ctypes.byref(u), ctypes.byref(activation), glu, _p(h),
                                  _p(gate_scratch)))
+
+
+def matmul_glu_q8(gate, up, activation, glu, h, hd, hq, gate_scratch=None):
+    """smq_matmul_glu_q8: h = up * act(gate) and h's Q8 blocks (hd, hq) of one token."""
+    g, u = gate._c(), up._c()
+    _check(load().smq_matmul_glu_q8(ctypes.byref(g), ctypes.byref(u), ctypes.byref(activation), glu, _p(h), _p(hd),
+                                    _p(hq), _p(gate_scratch)))
 
 
 def gemv_grouped(items):

@@ -622,16 +622,68 @@ smq_status smq_matmul_act(const smq_mat_item *items, uint32_t n, const smq_act *
             fused = false;
     }
     if (fused) {
-        for (int q5 = 0; q5 < 2; ++q5)
-            if (fa[q5].nitems &&
-                !hip_ok(smq::launch_matmul_fused(fa[q5], q5 == 1, act->kind, false, g.cur), "matmul_act"))
-                return t_status;
+        for (int q5 = 0; q5 < 2; ++q5) {
+            if (!fa[q5].nitems) continue;
+            const hipError_t e = smq::decode_ct_ok(fa[q5], q5 == 1, act->kind, false)
+                                     ? smq::launch_decode_ct(fa[q5], act->kind, false, g.cur)
+                                     : smq::launch_matmul_fused(fa[q5], q5 == 1, act->kind, false, g.cur);
+            if (!hip_ok(e, "matmul_act")) return t_status;
+        }
         return SMQ_OK;
     }
     const float *xd = nullptr;
     const int8_t *xq = nullptr;
     if (!act_materialize(act, &xd, &xq, "matmul_act")) return t_status;
     return smq_matmul(items, n, xd, xq, 1);
+}
+
+smq_status smq_matmul_glu_q8(const smq_qmat *gate, const smq_qmat *up, const smq_act *act, int glu, float *h,
+                             float *hd, int8_t *hq, float *gate_scratch) {
+    if (!ready()) return t_status;
+    if (!gate || !up) return set_status(SMQ_ERR_RANGE, "matmul_glu_q8: NULL matrix");
+    if (gate->rows != up->rows || gate->cols != up->cols || gate->nb != up->nb)
+        return set_status(SMQ_ERR_STATE, "matmul_glu_q8: gate %ux%u and up %ux%u differ", gate->rows, gate->cols,
+                          up->rows, up->cols);
+    if (glu != 1 && glu != 2) return set_status(SMQ_ERR_RANGE, "matmul_glu_q8: activation %d", glu);
+    const uint32_t hb = (up->rows + smq::QK - 1) / smq::QK;
+    if (!extent_ok(h, h ? (size_t)up->rows * 4 : 0, "h") || !extent_ok(hd, (size_t)hb * 4, "hd") ||
+        !extent_ok(hq, (size_t)hb * smq::QK, "hq"))
+        return t_status;
+    if (!gate->rows) return SMQ_OK;
+    if (gate->dtype == 1 && up->dtype == 1 && act && act->cols == gate->cols && !g.fast &&
+        gate->nb == (gate->cols + smq::QK - 1) / smq::QK) {
+        smq::FusedArgs f;
+        memset(&f, 0, sizeof(f));
+        f.nb = gate->nb;
+        fused_act(f, act);
+        f.nitems = 2;
+        for (int k = 0; k < 2; ++k) {
+            const smq_qmat *w = k ? up : gate;
+            f.item[k].w = w->data;
+            f.item[k].row_bytes = w->row_bytes;
+            f.item[k].rows = w->rows;
+        }
+        f.h = h;
+        f.hd = hd;
+        f.hq = hq;
+        f.rows = gate->rows;
+        f.act = glu;
+        if (smq::decode_ct_ok(f, false, act->kind, true)) {
+            for (int k = 0; k < 2; ++k) {
+                const smq_qmat *w = k ? up : gate;
+                if (!extent_ok(w->data, (size_t)(w->rows - 1) * w->row_bytes + (size_t)w->nb * smq::Q8_BYTES, "weights"))
+                    return t_status;
+            }
+            if (!act_ok(act, gate->cols, "matmul_glu_q8")) return t_status;
+            return hip_ok(smq::launch_decode_ct(f, act->kind, true, g.cur), "matmul_glu_q8") ? SMQ_OK : t_status;
+        }
+    }
+    /* the two-step form: h, then its Q8 blocks */
+    if (!h) return set_status(SMQ_ERR_RANGE, "matmul_glu_q8: this shape needs h");
+    const smq_status st = smq_matmul_glu(gate, up, act, glu, h, gate_scratch);
+    if (st != SMQ_OK) return st;
+    return hip_ok(smq::launch_quantize_q8(h, 1, up->rows, hd, hq, g.flag, g.cur), "matmul_glu_q8") ? SMQ_OK
+                                                                                                    : t_status;
 }
 
 smq_status smq_matmul_glu(const smq_qmat *gate, const smq_qmat *up, const smq_act *act, int glu, float *h,

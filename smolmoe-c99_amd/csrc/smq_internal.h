@@ -85,11 +85,18 @@ struct FusedArgs {
     const float *xd;
     const int8_t *xq;
     float *h;
+    float *hd;  /* GLU: Q8 blocks of h (rows/32 scales, rows int8), or NULL */
+    int8_t *hq;
     uint32_t rows;
     int act;
     int *flag;
 };
 bool fused_layout_ok(const FusedArgs &a, bool q5, int pro);
+/* Decode matmuls on packed 28-block Q8 rows with the activation formed in the launch and,
+ * for glu, h and its Q8 blocks formed in the store (csrc/smq_decode.hip). decode_ct_ok: Q8,
+ * nb 28, 16-byte aligned packed rows, pro 1 (RMSNorm) or 2 (f32 row), glu with hd/hq. */
+bool decode_ct_ok(const FusedArgs &a, bool q5, int pro, bool glu);
+hipError_t launch_decode_ct(const FusedArgs &a, int pro, bool glu, hipStream_t s);
 /* Rows per decode-GEMV workgroup for nb blocks (smq_kernels.hip). */
 int gemv_rows_per_tile(uint32_t nb, bool q5, uint32_t total_rows);
 /* Tuning, set from the host thread that launches: rows per tile of the

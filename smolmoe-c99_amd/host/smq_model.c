@@ -879,17 +879,11 @@ static smq_status attention_block(smq_model *m, uint32_t l, uint32_t n, uint32_t
 static smq_status ffn_block(smq_model *m, uint32_t l, uint32_t n) {
     const Layer *L = &m->layers[l];
     smq_mat_item it[2];
-    if (n == 1) { /* decode: RMSNorm in the gate/up launch, SwiGLU in its store, Q8 of h in the down launch */
+    if (n == 1) { /* decode: RMSNorm in the gate/up launch, SwiGLU and the Q8 of h in its store */
         smq_act act = norm_act(m, m->x, L->ffn_norm);
-        TRY(smq_matmul_glu(&L->gate, &L->up, &act, 1, m->up, m->gate));
-        act.kind = SMQ_ACT_F32;
-        act.cols = m->c.hidden;
-        act.x = m->up;
-        act.norm = NULL;
-        act.xd_scratch = m->hd;
-        act.xq_scratch = m->hq;
+        TRY(smq_matmul_glu_q8(&L->gate, &L->up, &act, 1, m->up, m->hd, m->hq, m->gate));
         it[0] = mat(&L->down, NULL, m->x, 1); /* x += down(act) */
-        return smq_matmul_act(it, 1, &act);
+        return smq_matmul(it, 1, m->hd, m->hq, 1);
     }
     TRY(smq_norm_quantize(m->x, L->ffn_norm, m->c.eps, n, m->c.dim, NULL, m->xd, m->xq));
     it[0] = mat(&L->gate, NULL, m->gate, 0);

@@ -128,6 +128,64 @@ def test_matmul_glu(orc, cols, rows, dtype, gate_dtype):
     assert_same_f32(h.download(np.float32), orc.act_mul(u, g), "h")
 
 
+@pytest.mark.parametrize("cols,rows,glu,prologue", [
+    (896, 4864, 1, "norm"),   # Qwen2.5-0.5B gate/up: 152 h blocks, one workgroup each
+    (896, 4864, 2, "norm"),   # GeGLU
+    (896, 200, 1, "norm"),    # a partial last h block (200 = 6*32 + 8)
+    (880, 96, 1, "f32"),      # a partial last activation block, the f32 prologue
+    (1536, 300, 1, "norm"),   # not a packed 28-block row: the unfused composition
+])
+def test_matmul_glu_q8(orc, cols, rows, glu, prologue):
+    """h = up * act(gate) of the RMSNorm (or f32) activation and h's Q8 blocks
+    (model.c:409-415, 636-640) in one call, against the oracle's row_work
+    composition and the library's unfused smq_matmul_glu + smq_quantize_q8_rows."""
+    say("matmul_glu_q8", cols, rows, glu, prologue)
+    nb, nbh = (cols + 31) // 32, (rows + 31) // 32
+    x = synth.normal(721 + cols, cols)
+    w = synth.normal(722 + cols, cols, 0.2) + 1.0
+    if prologue == "norm":
+        ok, _, d, q = orc.row_work(x, 1, cols, norm=w, eps=1e-6)
+        activation = lambda: smq.act(smq.ACT_NORM, cols, x=dev(x), norm=dev(w), eps=1e-6,  # noqa: E731
+                                     xd_scratch=smq.DeviceBuffer(nb * 4), xq_scratch=smq.DeviceBuffer(nb * 32))
+    else:
+        ok, _, d, q = orc.row_work(x, 1, cols)
+        activation = lambda: smq.act(smq.ACT_F32, cols, x=dev(x), xd_scratch=smq.DeviceBuffer(nb * 4),  # noqa: E731
+                                     xq_scratch=smq.DeviceBuffer(nb * 32))
+    assert ok
+    wg, wu = weights(723, rows, cols, Q8), weights(724, rows, cols, Q8)
+    gate_mat, up_mat = smq.QMat(dev(wg), rows, cols, Q8), smq.QMat(dev(wu), rows, cols, Q8)
+    h, hd, hq = smq.DeviceBuffer(rows * 4), smq.DeviceBuffer(nbh * 4), smq.DeviceBuffer(nbh * 32)
+    smq.matmul_glu_q8(gate_mat, up_mat, activation(), glu, h, hd, hq, gate_scratch=smq.DeviceBuffer(rows * 4))
+    smq.numeric_check()
+    g, u = expect_items(orc, [(wg, rows, Q8, None, None), (wu, rows, Q8, None, None)], d, q, cols)
+    ok, want_h, want_d, want_q = orc.row_work(u, 1, rows, gate=g, gelu=glu == 2)
+    assert ok
+    assert_same_f32(h.download(np.float32), want_h, "h")
+    assert_same_f32(hd.download(np.float32), want_d, "h scales")
+    assert np.array_equal(hq.download(np.int8), want_q), "h blocks"
+    # the unfused calls give the same bits
+    h2, hd2, hq2 = smq.DeviceBuffer(rows * 4), smq.DeviceBuffer(nbh * 4), smq.DeviceBuffer(nbh * 32)
+    smq.matmul_glu(gate_mat, up_mat, activation(), glu, h2, gate_scratch=smq.DeviceBuffer(rows * 4))
+    smq.quantize_q8_rows(h2, 1, rows, hd2, hq2)
+    smq.numeric_check()
+    assert_same_f32(h2.download(np.float32), want_h, "h unfused")
+    assert_same_f32(hd2.download(np.float32), want_d, "h scales unfused")
+    assert np.array_equal(hq2.download(np.int8), want_q), "h blocks unfused"
+
+
+def test_matmul_glu_q8_nonfinite_flag():
+    cols, rows = 896, 64
+    g = smq.QMat(dev(synth.q8_weights(931, rows, cols)), rows, cols)
+    u = smq.QMat(dev(synth.q8_weights(932, rows, cols)), rows, cols)
+    x = synth.normal(933, cols)
+    x[17] = np.inf
+    h, hd, hq = smq.DeviceBuffer(rows * 4), smq.DeviceBuffer(8), smq.DeviceBuffer(64)
+    smq.matmul_glu_q8(g, u, smq.act(smq.ACT_NORM, cols, x=dev(x), norm=dev(np.ones(cols, np.float32))), 1, h, hd, hq)
+    with pytest.raises(smq.SmqError) as e:
+        smq.numeric_check()
+    assert e.value.status == smq.SM_ERR_NUMERIC
+
+
 def test_glu_chain_equals_unfused(orc):
     """One decode FFN (RMSNorm -> gate/up -> SwiGLU -> down, x += ...) through
     the fused calls and through the unfused ones: the same bits."""

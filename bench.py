@@ -47,6 +47,9 @@ smq = importlib.import_module("smolmoe-c99_amd")
 synth = importlib.import_module("smolmoe-c99_amd.synth")
 
 HBM_PEAK_GBS = 8000.0
+FORWARD_RUNS = 10  # configs[4] runs on the GPU (median reported)
+CPU_FORWARD_RUNS = 10  # configs[4] runs of the reference's model layer on the host (median reported)
+HEAD_SAMPLES = 11  # timings of the headline graph and of the dominant kernel's graph; the median is reported
 DIM, HIDDEN, LAYERS, VOCAB = 896, 4864, 24, 151936
 Q_DIM, KV_DIM = 896, 128
 
@@ -111,6 +114,30 @@ def timed_graph(graphs, reps):
     return smq.timer_stop() / reps
 
 
+def timed_samples(graphs, reps, samples):
+    """`samples` independent timings of timed_graph(graphs, reps): (median, best, all) in ms per replay."""
+    t = [timed_graph(graphs, reps) for _ in range(samples)]
+    return float(np.median(t)), float(min(t)), t
+
+
+def physical_cores():
+    """(physical cores, logical CPUs) among the CPUs this process may run on: distinct
+    (package, core) pairs of the affinity set, from sysfs."""
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            with open(base + "physical_package_id") as f:
+                pkg = f.read().strip()
+            with open(base + "core_id") as f:
+                core = f.read().strip()
+        except OSError:
+            return None, len(cpus)
+        cores.add((pkg, core))
+    return len(cores), len(cpus)
+
+
 def cpu_baseline(model, acts_x, acts_h, threads_list, budget_s, gpu_out):
     """The reference's AVX2 gemm (oracle/_ref, compiled from its kernels.c /
     kernels_x86.c) over the same FFN step: per layer the fused gate+up rows
@@ -141,10 +168,10 @@ def cpu_baseline(model, acts_x, acts_h, threads_list, budget_s, gpu_out):
             gate = gate and np.array_equal(want.view(np.uint32), gpu_out[m].view(np.uint32))
     out = {}
     for threads in threads_list:
-        one = orc.time_gemm_pass(fn, mats, rows, nbs, xds, xqs, 1, 36, threads, 1)
-        reps = max(2, min(200, int(budget_s / max(one, 1e-4))))
-        best = orc.time_gemm_pass(fn, mats, rows, nbs, xds, xqs, 1, 36, threads, reps)
-        out[threads] = (best, reps)
+        one, _ = orc.time_gemm_pass(fn, mats, rows, nbs, xds, xqs, 1, 36, threads, 1)
+        reps = max(10, min(200, int(budget_s / max(one, 1e-4))))
+        best, med = orc.time_gemm_pass(fn, mats, rows, nbs, xds, xqs, 1, 36, threads, reps)
+        out[threads] = (best, reps, med)
     return kind, name, out, gate
 
 
@@ -332,7 +359,9 @@ def main():
         warm = smq.capture(lambda: [ffn_streamed(copies[i % 2]) for i in range(args.warmup)] and None)
         warm.launch()
     timed = smq.capture(lambda: [ffn_streamed(copies[i % 2]) for i in range(args.steps)] and None)
-    ms_per_step = timed_graph([timed], 1) / args.steps
+    # ms_per_step: the median of HEAD_SAMPLES replays of the K-step graph (best and all beside it)
+    med, best, samples = timed_samples([timed], 1, HEAD_SAMPLES)
+    ms_per_step = med / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     step_graphs = [smq.capture(lambda m=m: ffn_streamed(m)) for m in copies]
     per_graph_ms = timed_graph(step_graphs, args.steps)
@@ -341,13 +370,14 @@ def main():
     same_as_sequential = all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(gpu_layer0, seq_layer0))
     log(f"bench: FFN step streamed {ms_per_step * 1e3:.1f} us, {value:.0f} GB/s")
 
-    # dominant kernel: the gate/up group launch (k_gemv_pin<exact, one chunk, NT=512, D=2>: 18-row tiles, 235 MB), eight launches
+    # dominant kernel: the gate/up group launch (k_gemv_ct: coalesced 16-row x 28-block tiles, 236 MB), eight launches
     # per graph (the two copies alternating) so that one graph launch's host overhead is spread over eight
     per_graph = 8
     gu_graphs = [smq.capture(lambda: [gateup_group(copies[i % 2]) for i in range(per_graph)] and None)]
     timed_graph(gu_graphs, 2)
-    reps = max(4, args.steps // 4)
-    gu_ms = timed_graph(gu_graphs, reps) / per_graph
+    reps = max(2, args.steps // 10)
+    gu_med, gu_best, _ = timed_samples(gu_graphs, reps, HEAD_SAMPLES)
+    gu_ms = gu_med / per_graph
     gu_bytes = LAYERS * q8_bytes(2 * HIDDEN, DIM)
     gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
     log(f"bench: gate/up group {gu_ms * 1e3:.2f} us/launch, {gu_gbs:.0f} GB/s")
@@ -357,7 +387,14 @@ def main():
     timed_graph(seq_graphs, 4)
     seq_ms = timed_graph(seq_graphs, max(20, args.steps))
     one_ms = timed_graph([smq.capture(lambda m=m: gateup_only(m)) for m in copies], max(20, args.steps)) / LAYERS
-    extra = {"ffn_step_sequential": {
+    extra = {"headline_timing": {
+        "what": "value = the 24-layer FFN step's 72 GEMVs as two grouped launches (cross-layer grouped GEMV "
+                "bandwidth: each GEMV has its own precomputed activation, so no layer waits for another); "
+                "ms_per_step = median of the samples below, each one replay of the K-step graph",
+        "samples_us_per_step": [round(t / args.steps * 1e3, 3) for t in samples],
+        "median_us_per_step": round(med / args.steps * 1e3, 3), "best_us_per_step": round(best / args.steps * 1e3, 3),
+        "best_GBps": round(step_bytes / (best / args.steps * 1e-3) / 1e9, 1)},
+        "ffn_step_sequential": {
         "what": "the same 24-layer FFN step as 48 launches in layer order (gate+up fused, down), one graph",
         "us_per_step": round(seq_ms * 1e3, 2), "GBps": round(step_bytes / (seq_ms * 1e-3) / 1e9, 1),
         "gateup_single_launch_us": round(one_ms * 1e3, 3),
@@ -424,6 +461,44 @@ def main():
                lambda i: smq.matmul([(copies[i // LAYERS % 2][i % LAYERS].qmat("o"), None, o_out)], ax[0].d,
                                     ax[0].q, 1),
                q8_bytes(DIM, Q_DIM), 2 * LAYERS, note="48 distinct 0.9 MB matrices in turn")
+        # configs[0] streamed: one grouped launch of 48 distinct 896x896 GEMVs (each with one of the 24
+        # layer activations), 384 matrices in turn (347 MB > the 256 MB Infinity Cache), as the reference's
+        # tests/bench_matmul.c:112-117 rotates a matrix past the caches
+        n0, g0 = 384, 48
+        c0_bufs = [smq.DeviceBuffer(copies[0][0].dev["o"][0].nbytes) for _ in range(n0)]
+        for k, b in enumerate(c0_bufs):
+            b.copy_from(copies[k % 2][k // 2 % LAYERS].dev["o"][0])
+        c0_out = [smq.DeviceBuffer(DIM * 4) for _ in range(g0)]
+
+        def c0_grouped(i):
+            base = (i % (n0 // g0)) * g0
+            smq.gemv_grouped([(smq.QMat(c0_bufs[base + j], DIM, Q_DIM), None, c0_out[j], False, ax[j % LAYERS].d,
+                               ax[j % LAYERS].q) for j in range(g0)])
+        single("c0_gemv_896x896_grouped48", c0_grouped, g0 * q8_bytes(DIM, Q_DIM), n0 // g0,
+               note="one launch of 48 distinct 896x896 GEMVs, 384 matrices (347 MB) in turn")
+        smq.synchronize()
+        one = smq.DeviceBuffer(DIM * 4)
+        smq.matmul([(smq.QMat(c0_bufs[(n0 // g0 - 1) * g0 + 5], DIM, Q_DIM), None, one)], ax[5].d, ax[5].q, 1)
+        extra["c0_gemv_896x896_grouped48"]["bit_identical_to_single"] = bool(np.array_equal(
+            c0_out[5].download(np.float32).view(np.uint32), one.download(np.float32).view(np.uint32)))
+        del c0_bufs
+        # configs[1] down projection at batch 128 (exact GEMM; int8 MFMA)
+        hx128 = Act(4200, 128, HIDDEN)
+        dout = smq.DeviceBuffer(128 * DIM * 4)
+
+        def prefill_down(i):
+            layer = copies[i // LAYERS % 2][i % LAYERS]
+            smq.matmul([(layer.qmat("down"), None, dout)], hx128.d, hx128.q, 128)
+
+        single("c1_prefill_exact_gemm_896x4864_b128", prefill_down, q8_bytes(DIM, HIDDEN, 128), 8)
+        smq.set_prefill_mfma(True)
+        single("c1_prefill_mfma_gemm_896x4864_b128", prefill_down, q8_bytes(DIM, HIDDEN, 128), 24)
+        smq.set_prefill_mfma(False)
+        ops = 2 * DIM * HIDDEN * 128
+        for k in ("c1_prefill_exact_gemm_896x4864_b128", "c1_prefill_mfma_gemm_896x4864_b128"):
+            e = extra[k]
+            e["int_TOPS"] = round(ops / (e["us"] * 1e-6) / 1e12, 2)
+            e["pct_int8_peak"] = round(100 * ops / (e["us"] * 1e-6) / 5.0e15, 2)
         # configs[3] at batch 64 (exact GEMM; int8 MFMA)
         hx = Act(4100, 64, DIM)
         hout = smq.DeviceBuffer(64 * VOCAB * 4)
@@ -434,6 +509,32 @@ def main():
                lambda i: smq.gemm_q8_mfma(head[i % 2], 28 * 36, hx.d, hx.q, VOCAB, 64, 28, hout, VOCAB),
                q8_bytes(VOCAB, DIM, 64), 4)
         del hout
+        # the reference's own matmul benchmark shape (tests/bench_matmul.c:111-117): one Q8 matrix of 65536 rows x
+        # 4864 (152 blocks, 342 MiB) against 1 token (decode GEMV) and 32 tokens (prefill); two copies alternate
+        rb_rows, rb_nb = 65536, 152
+        rb_host = np.tile(synth.q8_weights(7000, rb_rows // 64, rb_nb * 32), (64, 1))
+        rb = [smq.DeviceBuffer.from_array(rb_host)]
+        rb.append(smq.DeviceBuffer(rb[0].nbytes))
+        rb[1].copy_from(rb[0])
+        del rb_host
+        rx = Act(7100, 32, rb_nb * 32)
+        rout = smq.DeviceBuffer(32 * rb_rows * 4)
+        single("refbench_gemv_65536x4864",
+               lambda i: smq.gemm_q8(rb[i % 2], rb_nb * 36, rx.d, rx.q, rb_rows, 1, rb_nb, rout, rb_rows),
+               q8_bytes(rb_rows, rb_nb * 32), 4,
+               note="tests/bench_matmul.c's matrix (weights: 1/64 of the rows packed by the q8pack rule, repeated)")
+        single("refbench_gemm_65536x4864_b32",
+               lambda i: smq.gemm_q8(rb[i % 2], rb_nb * 36, rx.d, rx.q, rb_rows, 32, rb_nb, rout, rb_rows),
+               q8_bytes(rb_rows, rb_nb * 32, 32), 4)
+        single("refbench_mfma_65536x4864_b32",
+               lambda i: smq.gemm_q8_mfma(rb[i % 2], rb_nb * 36, rx.d, rx.q, rb_rows, 32, rb_nb, rout, rb_rows),
+               q8_bytes(rb_rows, rb_nb * 32, 32), 4)
+        for k in ("refbench_gemv_65536x4864", "refbench_gemm_65536x4864_b32", "refbench_mfma_65536x4864_b32"):
+            e = extra[k]
+            ntok = 1 if "gemv" in k else 32
+            e["weight_GBps"] = round(rb_rows * rb_nb * 36 / (e["us"] * 1e-6) / 1e9, 1)
+            e["tok_s_eq_556MiB"] = round(ntok / (556 * 2 ** 20 / (rb_rows * rb_nb * 36) * e["us"] * 1e-6), 1)
+        del rb, rout
         q5_extra(single, extra)
 
     if not args.no_extra:
@@ -448,11 +549,15 @@ def main():
             threads = min(16, ncpu)
             kind, name, res, gate = cpu_baseline(copies[0], acts_x, acts_h, sorted({1, threads}), args.cpu_budget,
                                                  gpu_layer0)
-            best, nreps = res[threads]
+            best, nreps, med_s = res[threads]
+            phys, logical = physical_cores()
             cpu = {"value": round(step_bytes / best / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": kind,
+                   "threads": threads, "physical_cores_visible": phys, "logical_cpus_visible": logical,
+                   "median_value": round(step_bytes / med_s / 1e9, 2),
                    "gpu_bit_identical_layer0": gate,
                    "sample": f"{name}: {nreps} passes over the same 24-layer FFN decode step (353 MB of Q8 weights, "
-                             f"best pass {best * 1e3:.2f} ms); 1 thread: {step_bytes / res[1][0] / 1e9:.2f} GB/s; "
+                             f"best pass {best * 1e3:.2f} ms, median {med_s * 1e3:.2f} ms); 1 thread: "
+                             f"{step_bytes / res[1][0] / 1e9:.2f} GB/s; "
                              f"host {cpu_model()}, {ncpu} CPUs visible, rows split statically, caller is worker 0"}
             log(f"bench: cpu {cpu['value']} GB/s on {threads} threads ({kind})")
         except Exception as ex:  # the CPU leg must not hide the GPU result
@@ -484,8 +589,8 @@ def main():
                    "parallelism": "none (1 GPU)"},
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
         "decode_tok_s": extra.get("c4_qwen05_forward", {}).get("decode_tok_s"),
-        "roofline": {"kernel": "k_gemv_pin<exact, one chunk, NT=512, D=2>: 18-row x 28-block tiles (48 gate/up GEMVs "
-                               "4864x896, one launch)",
+        "roofline": {"kernel": "k_gemv_ct<exact, NB=28, RT=16>: coalesced 16-row x 28-block tiles (48 gate/up GEMVs "
+                               "4864x896, one launch); HIP events, median of 11 graph replays of 8 launches",
                      "bound": "hbm",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
@@ -536,7 +641,7 @@ def model_forward_extra(args, extra):
             log(f"bench: qwen0.5B profile run: decode {nsteps / dec_s:.1f} tok/s")
             return
         runs = []
-        for _ in range(3):
+        for _ in range(FORWARD_RUNS):
             t0 = time.time()
             m.forward(prompt, 0, smodel.LOGITS_LAST)
             t1 = time.time()
@@ -545,8 +650,9 @@ def model_forward_extra(args, extra):
             toks = m.generate(512, nsteps + 1)
             t2 = time.time()
             runs.append((t1 - t0, t2 - t1b))
-        pre_s = min(r[0] for r in runs)
-        dec_s = min(r[1] for r in runs)
+        pre_s = float(np.median([r[0] for r in runs]))
+        dec_s = float(np.median([r[1] for r in runs]))
+        pre_best, dec_best = min(r[0] for r in runs), min(r[1] for r in runs)
         smq.set_prefill_mfma(True)
         t0 = time.time()
         m.forward(prompt, 0, smodel.LOGITS_LAST)
@@ -556,6 +662,8 @@ def model_forward_extra(args, extra):
                      f"prefill 512 ids in one batch then {nsteps} greedy decode steps (HIP graph per step), BOS banned",
              "decode_tok_s": round(nsteps / dec_s, 1), "decode_ms_per_token": round(dec_s / nsteps * 1e3, 3),
              "prefill_tok_s": round(512 / pre_s, 1), "prefill_ms": round(pre_s * 1e3, 2),
+             "timing": f"median of {FORWARD_RUNS} runs (prefill, then the decode steps); best: decode "
+                       f"{nsteps / dec_best:.1f} tok/s, prefill {512 / pre_best:.1f} tok/s",
              "prefill_mfma_tok_s": round(512 / mfma_s, 1),
              "prefill_mfma_note": "int8-MFMA prefill: exact int32 block sums, f32 block order relaxed (not bit-exact)",
              "decode_roofline_tok_s": round(8e12 / 555.7e6, 1), "weights_bytes_per_token": 555706368,
@@ -565,19 +673,33 @@ def model_forward_extra(args, extra):
             import oracle
             if oracle.ReferenceModel.available():
                 th = min(16, ncpu)
-                r = oracle.ReferenceModel(path, context=1024, batch=512, logit_rows=1, threads=th)
+                try:  # the AVX2 kernels BASELINE names (kernels_select would pick VNNI where the host has it)
+                    r = oracle.ReferenceModel(path, context=1024, batch=512, logit_rows=1, threads=th, avx2=True)
+                except RuntimeError:
+                    r = oracle.ReferenceModel(path, context=1024, batch=512, logit_rows=1, threads=th)
                 r.set_banned(banned)
-                t0 = time.time()
-                r.prefill(prompt, 0, True)
-                t1 = time.time()
-                rl = r.logits(1)
-                rt = r.generate(512, 9)
-                t2 = time.time()
+                cpu_runs = []
+                for _ in range(CPU_FORWARD_RUNS):  # prefill 512, then 8 decode steps, each run timed
+                    t0 = time.time()
+                    r.prefill(prompt, 0, True)
+                    t1 = time.time()
+                    rl = r.logits(1)
+                    rt = r.generate(512, 9)
+                    t2 = time.time()
+                    cpu_runs.append((t1 - t0, t2 - t1))
+                cpre = [x[0] for x in cpu_runs]
+                cdec = [x[1] for x in cpu_runs]
+                phys, logical = physical_cores()
                 e["cpu_reference"] = {"kind": "reference", "backend": r.backend, "threads": th,
-                                      "prefill_tok_s": round(512 / (t1 - t0), 1),
-                                      "decode_tok_s": round(8 / (t2 - t1), 2),
+                                      "physical_cores_visible": phys, "logical_cpus_visible": logical,
+                                      "cpu": cpu_model(),
+                                      "prefill_tok_s": round(512 / float(np.median(cpre)), 1),
+                                      "decode_tok_s": round(8 / float(np.median(cdec)), 2),
+                                      "prefill_tok_s_best": round(512 / min(cpre), 1),
+                                      "decode_tok_s_best": round(8 / min(cdec), 2),
                                       "sample": "the reference's own model_forward (src/model.c built from its "
-                                                "sources) on the same checkpoint: prefill 512, 8 decode steps"}
+                                                f"sources) on the same checkpoint: {CPU_FORWARD_RUNS} runs of "
+                                                "prefill 512 + 8 decode steps; medians, best beside them"}
                 e["gpu_logits_bit_identical"] = bool(np.array_equal(gl.view(np.uint32), rl.view(np.uint32)))
                 e["gpu_tokens_identical_first9"] = toks[:9].tolist() == rt.tolist()
                 r.close()
@@ -628,6 +750,22 @@ def q5_extra(single, extra):
     single("c2_q5_mfma_8960x1536_b64",
            lambda i: smq.gemm_q5_mfma(mats["gate"][i % (2 * n5)].buf, nb * 22, bx.d, bx.q, 8960, 64, nb, bout, 8960),
            q8_bytes(8960, 1536, 64, block=22), 8)
+    hx = Act(6600, 64, 8960)
+    hout = smq.DeviceBuffer(64 * 1536 * 4)
+    nbh = 8960 // 32
+    single("c2_q5_gemm_1536x8960_b64",
+           lambda i: smq.gemm_q5(mats["down"][i % (2 * n5)].buf, nbh * 22, hx.d, hx.q, 1536, 64, nbh, hout, 1536),
+           q8_bytes(1536, 8960, 64, block=22), 8)
+    single("c2_q5_mfma_1536x8960_b64",
+           lambda i: smq.gemm_q5_mfma(mats["down"][i % (2 * n5)].buf, nbh * 22, hx.d, hx.q, 1536, 64, nbh, hout,
+                                      1536),
+           q8_bytes(1536, 8960, 64, block=22), 8)
+    ops = 2 * 8960 * 1536 * 64
+    for k in ("c2_q5_gemm_8960x1536_b64", "c2_q5_mfma_8960x1536_b64", "c2_q5_gemm_1536x8960_b64",
+              "c2_q5_mfma_1536x8960_b64"):
+        e = extra[k]
+        e["int_TOPS"] = round(ops / (e["us"] * 1e-6) / 1e12, 2)
+        e["pct_int8_peak"] = round(100 * ops / (e["us"] * 1e-6) / 5.0e15, 2)
 
 
 def synth_q(act, cols):

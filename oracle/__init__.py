@@ -112,7 +112,7 @@ class Oracle:
         lib.orc_time_gemm_pass.restype = ctypes.c_double
         lib.orc_time_gemm_pass.argtypes = [ctypes.c_void_p, ctypes.POINTER(_u8p), ctypes.POINTER(_u32),
                                            ctypes.POINTER(_u32), ctypes.POINTER(_f32p), ctypes.POINTER(_i8p), _u32,
-                                           _u32, _u32, _f32p, _u32, _u32, _sz]
+                                           _u32, _u32, _f32p, _u32, _u32, _sz, ctypes.c_void_p]
 
     # -- binary16
     def f16_to_f32(self, h):
@@ -282,8 +282,9 @@ class Oracle:
     # -- CPU baseline timing
     def time_gemm_pass(self, fn_addr, mats, rows, nbs, xds, xqs, ntok, block_bytes, threads, reps,
                        scratch_bytes=0):
-        """Best wall time (s) of one pass over `mats` with a GemmQ8-shaped
-        function at address `fn_addr`, rows split over `threads`."""
+        """(best, median) wall time (s) of one pass over `mats` with a
+        GemmQ8-shaped function at address `fn_addr`, rows split over
+        `threads`, over `reps` passes."""
         n = len(mats)
         mp = (_u8p * n)(*[_ptr(m, _u8p) for m in mats])
         rp = (_u32 * n)(*rows)
@@ -291,8 +292,10 @@ class Oracle:
         dp = (_f32p * n)(*[_ptr(d, _f32p) for d in xds])
         qp = (_i8p * n)(*[_ptr(q, _i8p) for q in xqs])
         out = np.zeros(max(rows) * ntok, np.float32)
-        return self.lib.orc_time_gemm_pass(ctypes.c_void_p(fn_addr), mp, rp, bp, dp, qp, n, ntok, block_bytes,
-                                           _ptr(out, _f32p), threads, reps, scratch_bytes)
+        times = np.zeros(max(reps, 1), np.float64)
+        best = self.lib.orc_time_gemm_pass(ctypes.c_void_p(fn_addr), mp, rp, bp, dp, qp, n, ntok, block_bytes,
+                                           _ptr(out, _f32p), threads, reps, scratch_bytes, times.ctypes.data)
+        return best, float(np.median(times[:reps])) if reps else best
 
     def gemm_fn_addr(self, q5=False):
         fn = self.lib.orc_gemm_q5_fn if q5 else self.lib.orc_gemm_q8_fn
@@ -508,6 +511,8 @@ class ReferenceModel:
             lib.ref_last_error.restype = ctypes.c_char_p
             lib.ref_backend.restype = ctypes.c_char_p
             lib.ref_backend.argtypes = [ctypes.c_int, ctypes.c_int]
+            lib.ref_backend_avx2.restype = ctypes.c_char_p
+            lib.ref_backend_avx2.argtypes = []
             lib.ref_model_open.restype = vp
             lib.ref_model_open.argtypes = [ctypes.c_char_p, ctypes.c_char_p, _u32, _u32, _u32, _u32]
             lib.ref_model_close.argtypes = [vp]
@@ -534,9 +539,18 @@ class ReferenceModel:
         st = lib.ref_modelfile_check(buf.ctypes.data, buf.nbytes, threads)
         return st, (lib.ref_last_error().decode() if st else "")
 
-    def __init__(self, path, config_path=None, context=256, batch=64, logit_rows=1, threads=1, scalar=False):
+    def __init__(self, path, config_path=None, context=256, batch=64, logit_rows=1, threads=1, scalar=False,
+                 avx2=False):
+        """avx2=True: the kernels kernels_select picks on an AVX2+F16C host without VNNI
+        (RuntimeError where this CPU has no AVX2)."""
         lib = self._load()
-        self.backend = lib.ref_backend(int(scalar), 0).decode()
+        if avx2 and not scalar:
+            b = lib.ref_backend_avx2()
+            if not b:
+                raise RuntimeError("this CPU has no AVX2+F16C")
+            self.backend = b.decode()
+        else:
+            self.backend = lib.ref_backend(int(scalar), 0).decode()
         self._h = lib.ref_model_open(path.encode(), config_path.encode() if config_path else None, context, batch,
                                      logit_rows, threads)
         if not self._h:

@@ -92,7 +92,7 @@ static void *worker_main(void *arg) {
 double orc_time_gemm_pass(orc_gemm_fn gemm, const unsigned char *const *mats, const uint32_t *rows,
                           const uint32_t *nbs, const float *const *xds, const int8_t *const *xqs, uint32_t nmats,
                           uint32_t ntok, uint32_t block_bytes, float *out, uint32_t threads, uint32_t reps,
-                          size_t scratch_bytes) {
+                          size_t scratch_bytes, double *times) {
     Pass p;
     pthread_t th[256];
     Worker wk[256];
@@ -130,6 +130,7 @@ double orc_time_gemm_pass(orc_gemm_fn gemm, const unsigned char *const *mats, co
         __atomic_add_fetch(&p.generation, 1u, __ATOMIC_ACQ_REL);
         run_pass(&p, 0, &barrier_gen);
         dt = now() - t0;
+        if (times) times[rep] = dt;
         if (dt < best) best = dt;
     }
     __atomic_store_n(&p.stop, 1u, __ATOMIC_RELEASE);

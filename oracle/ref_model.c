@@ -36,6 +36,30 @@ const char *ref_backend(int scalar, int fast) {
     return kernels_select(scalar);
 }
 
+/* kernels_select (kernels.c:721-800) on a host with AVX2+F16C but no AVX-VNNI
+ * or AVX512-VNNI: the same selection, then the integer dot kernels set to the
+ * AVX2 ones that kernels.c:796-806 picks there (exact contract). Returns
+ * "avx2", or NULL when this CPU has no AVX2+F16C. */
+const char *ref_backend_avx2(void) {
+#if defined(SM_HAVE_AVX2)
+    const char *picked;
+    kernels_set_fast(0);
+    picked = kernels_select(0);
+    if (!strncmp(picked, "scalar", 6)) return NULL;
+    dot_q8 = dot_q8_avx2;
+    dot_q8_x4 = dot_q8_avx2_x4;
+    dot_q8_r4 = dot_q8_avx2_r4;
+    dot_q5 = dot_q5_avx2;
+    dot_q5_x4 = dot_q5_avx2_x4;
+    dot_q5_r4 = dot_q5_avx2_r4;
+    gemm_q8 = gemm_q8_avx2;
+    gemm_q5 = gemm_q5_avx2;
+    return "avx2";
+#else
+    return NULL;
+#endif
+}
+
 void ref_model_close(RefModel *r) {
     if (!r) return;
     if (r->pool) pool_destroy(r->pool);

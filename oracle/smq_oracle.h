@@ -53,14 +53,15 @@ void orc_dequantize_row(int q5, const unsigned char *w, uint32_t cols, float *ou
 /* CPU baseline timing (cpu_timing.c): runs `gemm` (a GemmQ8-shaped function,
  * the reference's kernels.h:60-65 signature) over `nmats` weight matrices in
  * turn (blocks of `block_bytes`), rows split statically over `threads` threads with the caller as
- * worker 0, `reps` times; returns the best wall time of one pass in seconds. */
+ * worker 0, `reps` times; returns the best wall time of one pass in seconds
+ * (and each pass's time in times[0, reps) when times is not NULL). */
 typedef void (*orc_gemm_fn)(const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq,
                             uint32_t nrows, uint32_t ntok, uint32_t nb, float *out, size_t stride,
                             unsigned char *scratch);
 double orc_time_gemm_pass(orc_gemm_fn gemm, const unsigned char *const *mats, const uint32_t *rows,
                           const uint32_t *nbs, const float *const *xds, const int8_t *const *xqs, uint32_t nmats,
                           uint32_t ntok, uint32_t block_bytes, float *out, uint32_t threads, uint32_t reps,
-                          size_t scratch_bytes);
+                          size_t scratch_bytes, double *times);
 /* The oracle's own scalar gemm in the GemmQ8 shape (exact contract, Q8 / Q5). */
 void orc_gemm_q8_fn(const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq, uint32_t nrows,
                     uint32_t ntok, uint32_t nb, float *out, size_t stride, unsigned char *scratch);

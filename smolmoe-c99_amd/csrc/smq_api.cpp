@@ -212,6 +212,9 @@ smq_status smq_init(int device) {
         return t_status;
     /* the allocation-free argmax's static partials: their device address, once, with the device current */
     if (!hip_ok(smq::bind_noalloc_scratch(device), "hipGetSymbolAddress(scratch)")) return t_status;
+    if (!hip_ok(smq::prepare_attention_attributes(), "hipFuncSetAttribute(attention)") ||
+        !hip_ok(smq::prepare_fused_attributes(), "hipFuncSetAttribute(fused GEMV)"))
+        return t_status;
     g.cur = g.own;
     g.device = device;
     const char *env = getenv("SMQ_CHECKS");
@@ -1022,8 +1025,10 @@ smq_status smq_memset(void *dst, int value, size_t bytes) {
 smq_status smq_capture_begin(void) {
     if (!ready()) return t_status;
     if (g.cur != g.own) return set_status(SMQ_ERR_STATE, "capture needs the library stream");
-    return hip_ok(hipStreamBeginCapture(g.cur, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture") ? SMQ_OK
-                                                                                                        : t_status;
+    /* thread-local mode: a call from this thread that may not be captured (a synchronizing copy, an
+     * allocation) fails the capture instead of being recorded or run behind the graph's back */
+    return hip_ok(hipStreamBeginCapture(g.cur, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture") ? SMQ_OK
+                                                                                                            : t_status;
 }
 
 void *smq_capture_end(void) {

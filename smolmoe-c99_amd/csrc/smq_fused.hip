@@ -301,6 +301,12 @@ __global__ __launch_bounds__(WG) void k_gemv_fused(FusedArgs a, uint32_t ntiles)
     }
 }
 
+/* Dynamic LDS limit of every k_gemv_fused instance, raised once at smq_init (before any
+ * capture) to the widest row fused_layout_ok admits: 3 x MAX_NORM_K RMSNorm floats plus
+ * MAX_FAST_NB Q5 blocks of 17 floats. */
+constexpr size_t FUSED_MAX_LDS = (3 * (size_t)MAX_NORM_K + (size_t)MAX_FAST_NB * 17u) * 4u;
+static_assert(FUSED_MAX_LDS <= 160u * 1024u, "within one CU's LDS");
+
 template <bool Q5, int RT, int PRO, int EPI>
 hipError_t launch_fused_rt(FusedArgs a, hipStream_t s) {
     uint32_t tiles = 0;
@@ -315,13 +321,7 @@ hipError_t launch_fused_rt(FusedArgs a, hipStream_t s) {
     }
     if (!tiles) return hipSuccess;
     const size_t lds = ((PRO == PRO_NORM ? 3 * ((a.n + 3) / 4 * 4) : 0) + (size_t)a.nb * (Q5 ? 17u : 9u)) * 4u;
-    static size_t allowed = 64 << 10; /* dynamic LDS beyond the 64 KiB default for wide rows */
-    if (lds > allowed) {
-        const hipError_t e = hipFuncSetAttribute((const void *)k_gemv_fused<Q5, false, RT, PRO, EPI>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        allowed = lds;
-    }
+    if (lds > FUSED_MAX_LDS) return hipErrorInvalidValue; /* past the limit prepare_fused_attributes set */
     /* at most one resident wave of workgroups, each taking a range of tiles: the prologue runs
      * once per workgroup (the occupancy of this instantiation is read at the widest LDS seen) */
     static size_t queried_lds = 0;
@@ -339,6 +339,30 @@ hipError_t launch_fused_rt(FusedArgs a, hipStream_t s) {
     const uint32_t grid = tiles < (uint32_t)resident ? tiles : (uint32_t)resident;
     hipLaunchKernelGGL((k_gemv_fused<Q5, false, RT, PRO, EPI>), dim3(grid), dim3(WG), lds, s, a, tiles);
     return hipGetLastError();
+}
+
+template <bool Q5, int RT, int PRO, int EPI>
+hipError_t raise_fused_lds() { /* at most what the CU holds beside the kernel's static LDS */
+    const void *fn = (const void *)k_gemv_fused<Q5, false, RT, PRO, EPI>;
+    hipFuncAttributes at;
+    const hipError_t e = hipFuncGetAttributes(&at, fn);
+    if (e != hipSuccess) return e;
+    const size_t room = (size_t)160 * 1024 - at.sharedSizeBytes;
+    return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)(FUSED_MAX_LDS < room ? FUSED_MAX_LDS : room));
+}
+
+template <bool Q5>
+hipError_t raise_fused_lds_typed() {
+    const hipError_t es[] = {raise_fused_lds<Q5, 2, PRO_NORM, EPI_GLU>(),  raise_fused_lds<Q5, 4, PRO_NORM, EPI_GLU>(),
+                             raise_fused_lds<Q5, 8, PRO_NORM, EPI_GLU>(),  raise_fused_lds<Q5, 1, PRO_NORM, EPI_STORE>(),
+                             raise_fused_lds<Q5, 2, PRO_NORM, EPI_STORE>(), raise_fused_lds<Q5, 4, PRO_NORM, EPI_STORE>(),
+                             raise_fused_lds<Q5, 8, PRO_NORM, EPI_STORE>(), raise_fused_lds<Q5, 1, PRO_F32, EPI_STORE>(),
+                             raise_fused_lds<Q5, 2, PRO_F32, EPI_STORE>(),  raise_fused_lds<Q5, 4, PRO_F32, EPI_STORE>(),
+                             raise_fused_lds<Q5, 8, PRO_F32, EPI_STORE>()};
+    for (hipError_t e : es)
+        if (e != hipSuccess) return e;
+    return hipSuccess;
 }
 
 template <bool Q5, int PRO, int EPI>
@@ -380,6 +404,11 @@ bool fused_layout_ok(const FusedArgs &a, bool q5, int pro) {
     for (uint32_t i = 0; i < a.nitems; ++i)
         if ((((uintptr_t)a.item[i].w) | a.item[i].row_bytes) & 3u) return false;
     return true;
+}
+
+hipError_t prepare_fused_attributes() {
+    const hipError_t e = raise_fused_lds_typed<false>();
+    return e != hipSuccess ? e : raise_fused_lds_typed<true>();
 }
 
 hipError_t launch_matmul_fused(const FusedArgs &a, bool q5, int pro, bool glu, hipStream_t s) {

@@ -166,6 +166,11 @@ hipError_t launch_argmax(const float *logits, uint32_t n, const unsigned char *b
  * NOALLOC_MAX_VOCAB ids. */
 constexpr uint32_t NOALLOC_MAX_VOCAB = MAX_ARGMAX_PARTS * 1024u;
 hipError_t bind_noalloc_scratch(int device);
+
+/* Raise the dynamic-LDS limits of the attention and fused-GEMV kernels once,
+ * at smq_init (no kernel attribute changes later, inside or after a capture). */
+hipError_t prepare_attention_attributes();
+hipError_t prepare_fused_attributes();
 void *noalloc_scratch(int device);
 hipError_t launch_embed(const unsigned char *w, size_t row_bytes, bool q5, uint32_t vocab, const uint32_t *tokens,
                         uint32_t ntok, uint32_t cols, float *out, int *flag, hipStream_t s);

@@ -2378,30 +2378,31 @@ hipError_t launch_attention(const float *q, const float *kcache, const float *vc
     }
     if (attention_rows_ok(sh, q, kcache, vcache)) {
         const size_t lds = (((size_t)sh.context + 3) / 4 * 4 + (size_t)AR_FIXED) * sizeof(float);
-        static bool raised_rows = false;
-        if (!raised_rows) { /* dynamic LDS beyond the 64 KiB default for long contexts */
-            const hipError_t e = hipFuncSetAttribute((const void *)k_attend_rows<false>,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     (int)(((size_t)MAX_ATT_POSITIONS + AR_FIXED) * sizeof(float)));
-            if (e != hipSuccess) return e;
-            raised_rows = true;
-        }
         RopeRows none = {nullptr, nullptr, nullptr, nullptr};
         hipLaunchKernelGGL(k_attend_rows<false>, dim3(ntok * sh.heads * groups), dim3(AR_WG), lds, s, q,
                            (float *)kcache, (float *)vcache, att, sh, pos0, pos_dev, flag, xd, xq, none);
         return hipGetLastError();
     }
     const size_t lds = (((size_t)sh.context + 3) / 4 * 4 + (size_t)ATT_SHARED) * sizeof(float);
-    static bool raised = false;
-    if (!raised) { /* dynamic LDS beyond the 64 KiB default for long contexts */
-        const hipError_t e = hipFuncSetAttribute((const void *)k_attend, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)(((size_t)MAX_ATT_POSITIONS + ATT_SHARED) * sizeof(float)));
-        if (e != hipSuccess) return e;
-        raised = true;
-    }
     hipLaunchKernelGGL(k_attend, dim3(ntok * sh.heads * groups), dim3(ATT_WG), lds, s, q, kcache, vcache, att, sh, pos0,
                        pos_dev, flag, xd, xq);
     return hipGetLastError();
+}
+
+/* Dynamic LDS beyond the 64 KiB default (a score per position, up to
+ * MAX_ATT_POSITIONS): raised once at smq_init, before any capture, so no
+ * kernel's attributes change while a captured graph holds it. */
+hipError_t prepare_attention_attributes() {
+    const int rows = (int)(((size_t)MAX_ATT_POSITIONS + AR_FIXED) * sizeof(float));
+    const int tiled = (int)(((size_t)MAX_ATT_POSITIONS + ATT_SHARED) * sizeof(float));
+    const hipError_t es[] = {
+        hipFuncSetAttribute((const void *)k_attend_rows<false>, hipFuncAttributeMaxDynamicSharedMemorySize, rows),
+        hipFuncSetAttribute((const void *)k_attend_rows<true>, hipFuncAttributeMaxDynamicSharedMemorySize, rows),
+        hipFuncSetAttribute((const void *)k_attend_values<true>, hipFuncAttributeMaxDynamicSharedMemorySize, rows),
+        hipFuncSetAttribute((const void *)k_attend, hipFuncAttributeMaxDynamicSharedMemorySize, tiled)};
+    for (hipError_t e : es)
+        if (e != hipSuccess) return e;
+    return hipSuccess;
 }
 
 hipError_t launch_attention_rope(const float *q, const float *k, const float *v, const float *cs, const float *sn,
@@ -2415,28 +2416,12 @@ hipError_t launch_attention_rope(const float *q, const float *k, const float *v,
     const size_t lds = (((size_t)sh.context + 3) / 4 * 4 + (size_t)AR_FIXED) * sizeof(float);
     RopeRows rr = {k, v, cs, sn};
     if (scores && (size_t)sh.heads * sh.context <= MAX_SCORE_FLOATS && sh.heads / sh.kv_heads <= AS_MAXG) {
-        static bool raised_v = false;
-        if (!raised_v) {
-            const hipError_t e = hipFuncSetAttribute((const void *)k_attend_values<true>,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     (int)(((size_t)MAX_ATT_POSITIONS + AR_FIXED) * sizeof(float)));
-            if (e != hipSuccess) return e;
-            raised_v = true;
-        }
         const dim3 sgrid((sh.context + AS_SP - 1) / AS_SP, sh.kv_heads);
         hipLaunchKernelGGL(k_attend_scores<true>, sgrid, dim3(AS_WG), 0, s, q, kcache, vcache, sh, pos0, pos_dev, flag,
                            rr, scores);
         hipLaunchKernelGGL(k_attend_values<true>, dim3(sh.heads * groups), dim3(AR_WG), lds, s, vcache, att, sh, pos0,
                            pos_dev, xd, xq, v, scores, flag);
         return hipGetLastError();
-    }
-    static bool raised = false;
-    if (!raised) {
-        const hipError_t e = hipFuncSetAttribute((const void *)k_attend_rows<true>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)(((size_t)MAX_ATT_POSITIONS + AR_FIXED) * sizeof(float)));
-        if (e != hipSuccess) return e;
-        raised = true;
     }
     hipLaunchKernelGGL(k_attend_rows<true>, dim3(sh.heads * groups), dim3(AR_WG), lds, s, q, kcache, vcache, att, sh,
                        pos0, pos_dev, flag, xd, xq, rr);

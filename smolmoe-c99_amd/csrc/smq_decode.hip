@@ -113,11 +113,13 @@ __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
     if constexpr (PRO == DPRO_NORM) {
         if (xel) L.sq[tid] = xv * xv;
         __syncthreads();
-        if (tid == 0) {
+        if (tid < 64) { /* the whole first wave runs the chain (faster than one lane) */
             const float ss = serial_sum_lds(L.sq, n);
-            const float iv = 1.0f / sqrtf(ss / (float)n + a.eps); /* model.c:338 */
-            L.inv = iv;
-            L.bad = !(fabsf(ss) <= FLT_MAX) || !(fabsf(iv) <= FLT_MAX);
+            if (tid == 0) {
+                const float iv = 1.0f / sqrtf(ss / (float)n + a.eps); /* model.c:338 */
+                L.inv = iv;
+                L.bad = !(fabsf(ss) <= FLT_MAX) || !(fabsf(iv) <= FLT_MAX);
+            }
         }
         __syncthreads();
     }

@@ -172,11 +172,13 @@ __global__ __launch_bounds__(WG) void k_gemv_fused(FusedArgs a, uint32_t ntiles)
                 }
             }
             lds_barrier();
-            if (tid == 0) {
+            if (tid < 64) { /* the whole first wave runs the chain (faster than one lane) */
                 const float ss = serial_sum_lds(sq, n);
-                const float iv = 1.0f / sqrtf(ss / (float)n + a.eps); /* model.c:338 */
-                s_inv = iv;
-                s_bad = !(fabsf(ss) <= FLT_MAX) || !(fabsf(iv) <= FLT_MAX);
+                if (tid == 0) {
+                    const float iv = 1.0f / sqrtf(ss / (float)n + a.eps); /* model.c:338 */
+                    s_inv = iv;
+                    s_bad = !(fabsf(ss) <= FLT_MAX) || !(fabsf(iv) <= FLT_MAX);
+                }
             }
             lds_barrier();
             load_task(cur, ti * TB); /* after the serial sum (measured faster than before it) */

@@ -896,11 +896,13 @@ __global__ __launch_bounds__(RW_WG) void k_row_quantize(const float *src, const 
             if (i < n) sq_lds[i] = v[k] * v[k];
         }
         __syncthreads();
-        if (tid == 0) {
+        if (tid < 64) { /* the whole first wave runs the chain (faster than one lane) */
             const float sq = serial_sum_lds(sq_lds, n);
-            const float inv = 1.0f / sqrtf(sq / (float)n + eps); /* model.c:338 */
-            s_inv = inv;
-            s_bad = !(fabsf(sq) <= FLT_MAX) || !(fabsf(inv) <= FLT_MAX);
+            if (tid == 0) {
+                const float inv = 1.0f / sqrtf(sq / (float)n + eps); /* model.c:338 */
+                s_inv = inv;
+                s_bad = !(fabsf(sq) <= FLT_MAX) || !(fabsf(inv) <= FLT_MAX);
+            }
         }
         __syncthreads();
         const float inv = s_inv;
@@ -1253,7 +1255,10 @@ __global__ __launch_bounds__(ATT_WG) void k_attend(const float *q, const float *
     __syncthreads();
 
     /* 3. the total in position order */
-    if (tid == 0) s_inv = 1.0f / serial_sum_lds(sc, np);
+    if (tid < 64) { /* the whole first wave runs the chain */
+        const float tot = serial_sum_lds(sc, np);
+        if (tid == 0) s_inv = 1.0f / tot;
+    }
     __syncthreads();
     const float inv = s_inv;
 
@@ -1277,36 +1282,10 @@ __global__ __launch_bounds__(ATT_WG) void k_attend(const float *q, const float *
         if (tid < ATT_JW) {
             /* lane j adds its column's rows in order: 16-byte reads, one batch of
              * 8 reads in flight while the previous batch is added */
-            const uint32_t rows = np - p0 < ATT_CH ? np - p0 : ATT_CH, nbat = rows / 32;
+            const uint32_t rows = np - p0 < ATT_CH ? np - p0 : ATT_CH;
             const float *colp = prod + tid * ATT_CHP;
             float acc = o;
-            uint32_t c = 0;
-            if (nbat) {
-                float4 x[8], y[8];
-                read_batch(x, (const float4 *)colp);
-                for (; c + 2 <= nbat; c += 2) {
-                    read_batch(y, (const float4 *)colp + 8 * (c + 1));
-                    __builtin_amdgcn_sched_barrier(0);
-                    add_batch(acc, x);
-                    read_batch(x, (const float4 *)colp + 8 * (c + 2 < nbat ? c + 2 : c + 1));
-                    __builtin_amdgcn_sched_barrier(0);
-                    add_batch(acc, y);
-                }
-                if (c < nbat) {
-                    add_batch(acc, x);
-                    ++c;
-                }
-            }
-            const uint32_t rest = rows - c * 32;
-            if (rest) {
-                const float *tl = colp + c * 32;
-                float v[32];
-#pragma unroll
-                for (uint32_t u = 0; u < 32; ++u) v[u] = tl[u < rest ? u : rest - 1];
-#pragma unroll
-                for (uint32_t u = 0; u < 32; ++u)
-                    if (u < rest) acc = acc + v[u];
-            }
+            acc = chain_lds(acc, colp, rows); /* kernels.c:1165, position order */
             o = acc;
         }
         __syncthreads();
@@ -1452,7 +1431,10 @@ __device__ __forceinline__ void att_tail(float high, float *sc, float *prod, uin
     for (uint32_t p = tid; p < np; p += AR_WG) sc[p] = exp_det_tab(sc[p] - high, etab);
     __syncthreads();
 
-    if (tid == 0) *s_inv = 1.0f / serial_sum_lds(sc, np);
+    if (tid < 64) { /* the whole first wave runs the chain */
+        const float tot = serial_sum_lds(sc, np);
+        if (tid == 0) *s_inv = 1.0f / tot;
+    }
     __syncthreads();
     const float inv = *s_inv;
 
@@ -1473,36 +1455,10 @@ __device__ __forceinline__ void att_tail(float high, float *sc, float *prod, uin
         if (p0 + AR_VP < np) /* next pass in flight during the sums */
             att_load_values<ROPE>(pre, vbase, vrope, kvd, p0 + AR_VP, np, last, vrow, vcol);
         if (tid < ATT_JW) {
-            const uint32_t rows = np - p0 < AR_VP ? np - p0 : AR_VP, nbat = rows / 32;
+            const uint32_t rows = np - p0 < AR_VP ? np - p0 : AR_VP;
             const float *colp = prod + tid * AR_VPP;
             float acc = o;
-            uint32_t c = 0;
-            if (nbat) {
-                float4 x[8], y[8];
-                read_batch(x, (const float4 *)colp);
-                for (; c + 2 <= nbat; c += 2) {
-                    read_batch(y, (const float4 *)colp + 8 * (c + 1));
-                    __builtin_amdgcn_sched_barrier(0);
-                    add_batch(acc, x);
-                    read_batch(x, (const float4 *)colp + 8 * (c + 2 < nbat ? c + 2 : c + 1));
-                    __builtin_amdgcn_sched_barrier(0);
-                    add_batch(acc, y);
-                }
-                if (c < nbat) {
-                    add_batch(acc, x);
-                    ++c;
-                }
-            }
-            const uint32_t rest = rows - c * 32;
-            if (rest) {
-                const float *tl = colp + c * 32;
-                float v[32];
-#pragma unroll
-                for (uint32_t u = 0; u < 32; ++u) v[u] = tl[u < rest ? u : rest - 1];
-#pragma unroll
-                for (uint32_t u = 0; u < 32; ++u)
-                    if (u < rest) acc = acc + v[u];
-            }
+            acc = chain_lds(acc, colp, rows); /* kernels.c:1165, position order */
             o = acc;
         }
         __syncthreads();
@@ -1871,7 +1827,10 @@ __global__ __launch_bounds__(AG_WG) void k_attend_group(const float *q, const fl
     __syncthreads();
 
     /* 3. totals in position order */
-    if (tid < grp) hinv[tid] = 1.0f / serial_sum_lds(sc + tid * AG_MAXP, np);
+    if (tid < 64) { /* the whole first wave: lane h < grp sums head h's row, the others re-run row 0 */
+        const float tot = serial_sum_lds(sc + (tid < grp ? tid : 0) * AG_MAXP, np);
+        if (tid < grp) hinv[tid] = 1.0f / tot;
+    }
     __syncthreads();
 
     /* 4. values: wave hh (64 threads) is head kh*grp + hh, thread j its column */

@@ -31,6 +31,7 @@ usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
        python bench.py --forward-only [--checkpoint PATH] [--decode-steps N] [--profile]   (configs[4]
                                 alone, for profiling; PATH from python bench.py --write-checkpoint PATH)
        python bench.py --q5-only   (configs[2] alone, for profiling)
+       python bench.py --prefill-only   (the batched prefill GEMMs alone, for profiling)
 """
 import argparse
 import importlib
@@ -255,6 +256,14 @@ def main():
                            "pct_hbm_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
             log(f"bench: {name} {ms * 1e3:.2f} us {extra[name]['GBps']} GB/s")
         q5_extra(single, extra)
+        print(json.dumps(extra), flush=True)
+        return
+    if len(sys.argv) > 1 and sys.argv[1] == "--prefill-only":
+        # the batched prefill GEMMs alone (configs[1] at batch 128, configs[3] at batch 64; exact and int8-MFMA):
+        # the program the prefill rocprofv3 summaries profile
+        log("bench: init", smq.init(0), smq.kernels_select())
+        extra = {}
+        prefill_only(extra)
         print(json.dumps(extra), flush=True)
         return
     if len(sys.argv) > 1 and sys.argv[1] == "--forward-only":
@@ -766,6 +775,35 @@ def q5_extra(single, extra):
         e = extra[k]
         e["int_TOPS"] = round(ops / (e["us"] * 1e-6) / 1e12, 2)
         e["pct_int8_peak"] = round(100 * ops / (e["us"] * 1e-6) / 5.0e15, 2)
+
+
+def prefill_only(extra):
+    """configs[1] gate/up 9728x896 and down 896x4864 at batch 128, configs[3] 151936x896 at batch 64: each as
+    a graph of launches over two weight copies, exact GEMM and int8-MFMA GEMM."""
+    def single(name, fn, nbytes, ops, per_graph, reps=10):
+        gs = [smq.capture(lambda: [fn(i) for i in range(per_graph)] and None)]
+        timed_graph(gs, 2)
+        ms = timed_graph(gs, reps) / per_graph
+        extra[name] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                       "int_TOPS": round(ops / (ms * 1e-3) / 1e12, 2),
+                       "pct_int8_peak": round(100 * ops / (ms * 1e-3) / 5.0e15, 2)}
+        log(f"bench: {name} {ms * 1e3:.2f} us {extra[name]['int_TOPS']} TOPS")
+
+    shapes = {"gate_up": (2 * HIDDEN, DIM, 128), "down": (DIM, HIDDEN, 128), "lm_head": (VOCAB, DIM, 64)}
+    for name, (rows, cols, ntok) in shapes.items():
+        nb = cols // 32
+        w = synth.q8_weights(8000 + rows, rows if rows < 20000 else rows // 16, cols)
+        if rows >= 20000:
+            w = np.tile(w, (16, 1))
+        bufs = [smq.DeviceBuffer.from_array(w) for _ in range(2)]
+        x = Act(8100 + cols, ntok, cols)
+        out = smq.DeviceBuffer(ntok * rows * 4)
+        nbytes, ops = q8_bytes(rows, cols, ntok), 2 * rows * cols * ntok
+        single(f"{name}_exact_{rows}x{cols}_b{ntok}",
+               lambda i: smq.gemm_q8(bufs[i % 2], nb * 36, x.d, x.q, rows, ntok, nb, out, rows), nbytes, ops, 4)
+        single(f"{name}_mfma_{rows}x{cols}_b{ntok}",
+               lambda i: smq.gemm_q8_mfma(bufs[i % 2], nb * 36, x.d, x.q, rows, ntok, nb, out, rows), nbytes, ops, 8)
+        del bufs, out
 
 
 def synth_q(act, cols):

@@ -28,6 +28,7 @@ struct Context {
     float *scalar = nullptr;
     void *argmax_parts = nullptr; /* smq::MAX_ARGMAX_PARTS partials of the two-stage argmax */
     float *scores = nullptr;      /* decode attention scores (heads x context), smq::SCORE_WORKSPACE_BYTES */
+    float *mq_ws = nullptr;       /* split-K partial sums of the MFMA prefill GEMM, smq::MQ_WORKSPACE_BYTES */
     hipEvent_t t0 = nullptr, t1 = nullptr;
     int fast = 0;
     int prefill_mfma = 0;
@@ -147,6 +148,19 @@ void gemm_impl(bool q5, const unsigned char *w, size_t row_bytes, const float *x
            who);
 }
 
+/* The int8-MFMA prefill GEMM (relaxed block order) for a, if its layout allows: Q8 on the 64 x 64
+ * tile kernel (split K over the library workspace), Q5 on the block-pair kernel. Returns false when
+ * the layout does not allow it (nothing launched); a launch error sets the status. */
+bool mfma_launch(const smq::MatArgs &a, bool q5) {
+    if (!q5 && smq::mq8_wanted(a)) {
+        hip_ok(smq::launch_mq8(a, g.mq_ws, smq::MQ_WORKSPACE_BYTES, g.cur), "mfma gemm");
+        return true;
+    }
+    if (!smq::mfma_layout_ok(a, q5)) return false;
+    hip_ok(smq::launch_matmul_mfma(a, q5, nullptr, g.cur), "mfma gemm");
+    return true;
+}
+
 void gemm_mfma_impl(bool q5, const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq,
                     uint32_t nrows, uint32_t ntok, uint32_t nb, float *out, size_t stride, const char *who) {
     if (!ready()) return;
@@ -154,9 +168,8 @@ void gemm_mfma_impl(bool q5, const unsigned char *w, size_t row_bytes, const flo
     if (!check_operands(w, row_bytes, nrows, nb, q5, xd, xq, ntok, nb, out, stride, who)) return;
     const smq::MatArgs a = one_item(w, row_bytes, xd, xq, nrows, ntok, nb, nb, out, stride);
     /* rows or activations the MFMA staging cannot load take the exact GEMM */
-    hip_ok(smq::mfma_layout_ok(a, q5) ? smq::launch_matmul_mfma(a, q5, nullptr, g.cur)
-                                      : smq::launch_matmul(a, q5, g.fast != 0, g.cur),
-           who);
+    if (mfma_launch(a, q5)) return; /* a launch error has set the status */
+    hip_ok(smq::launch_matmul(a, q5, g.fast != 0, g.cur), who);
 }
 
 float dot_impl(bool q5, const unsigned char *w, const float *xd, const int8_t *xq, uint32_t nb) {
@@ -208,12 +221,14 @@ smq_status smq_init(int device) {
     if (!hip_ok(hipMalloc(&g.argmax_parts, (size_t)smq::MAX_ARGMAX_PARTS * smq::ARGMAX_PART_BYTES), "hipMalloc"))
         return t_status;
     if (!hip_ok(hipMalloc((void **)&g.scores, smq::SCORE_WORKSPACE_BYTES), "hipMalloc")) return t_status;
+    if (!hip_ok(hipMalloc((void **)&g.mq_ws, smq::MQ_WORKSPACE_BYTES), "hipMalloc")) return t_status;
     if (!hip_ok(hipEventCreate(&g.t0), "hipEventCreate") || !hip_ok(hipEventCreate(&g.t1), "hipEventCreate"))
         return t_status;
     /* the allocation-free argmax's static partials: their device address, once, with the device current */
     if (!hip_ok(smq::bind_noalloc_scratch(device), "hipGetSymbolAddress(scratch)")) return t_status;
     if (!hip_ok(smq::prepare_attention_attributes(), "hipFuncSetAttribute(attention)") ||
-        !hip_ok(smq::prepare_fused_attributes(), "hipFuncSetAttribute(fused GEMV)"))
+        !hip_ok(smq::prepare_fused_attributes(), "hipFuncSetAttribute(fused GEMV)") ||
+        !hip_ok(smq::prepare_mq8_attributes(), "hipFuncSetAttribute(MFMA GEMM)"))
         return t_status;
     g.cur = g.own;
     g.device = device;
@@ -233,6 +248,7 @@ void smq_shutdown(void) {
     (void)hipFree(g.flag);
     (void)hipFree(g.argmax_parts);
     (void)hipFree(g.scores);
+    (void)hipFree(g.mq_ws);
     (void)hipStreamDestroy(g.own);
     g = Context();
 }
@@ -446,11 +462,11 @@ smq_status smq_matmul(const smq_mat_item *items, uint32_t n, const float *xd, co
             it.accumulate = items[i].accumulate != 0;
         }
         if (!a.nitems) continue;
-        const bool mfma = ntok > 1 && g.prefill_mfma && smq::mfma_layout_ok(a, q5 == 1);
-        if (!hip_ok(mfma ? smq::launch_matmul_mfma(a, q5 == 1, nullptr, g.cur)
-                         : smq::launch_matmul(a, q5 == 1, g.fast != 0, g.cur),
-                    "matmul"))
-            return t_status;
+        if (ntok > 1 && g.prefill_mfma && mfma_launch(a, q5 == 1)) {
+            if (t_status != SMQ_OK) return t_status;
+            continue;
+        }
+        if (!hip_ok(smq::launch_matmul(a, q5 == 1, g.fast != 0, g.cur), "matmul")) return t_status;
     }
     return SMQ_OK;
 }

@@ -118,6 +118,16 @@ hipError_t launch_matmul(const MatArgs &a, bool q5, bool fast, hipStream_t s);
  * mfma_layout_ok: 4-byte aligned rows and activations, even nb for Q5. */
 bool mfma_layout_ok(const MatArgs &a, bool q5);
 hipError_t launch_matmul_mfma(const MatArgs &a, bool q5, int32_t *sums, hipStream_t s);
+/* Q8 prefill GEMM on int8 MFMA with 64 x 64 tiles and K split over slices when the tiles are few
+ * (csrc/smq_mfma.hip); ws: MQ_WORKSPACE_BYTES of device workspace for the slices' partial sums.
+ * mq8_ok: 4-byte aligned rows and activations, ntok >= 2. */
+constexpr size_t MQ_WORKSPACE_BYTES = (size_t)16 << 20;
+bool mq8_ok(const MatArgs &a);
+/* mq8_ok and few enough tiles (with a K long enough) that splitting K pays: the shapes
+ * launch_mq8 serves (the others take launch_matmul_mfma). */
+bool mq8_wanted(const MatArgs &a);
+hipError_t launch_mq8(MatArgs a, float *ws, size_t ws_bytes, hipStream_t s);
+hipError_t prepare_mq8_attributes();
 /* Activation producer rows (model.c:354-415): optional RMSNorm, optional
  * gated activation (act 1 = SwiGLU, 2 = GeGLU), optional f32 store, Q8. */
 constexpr uint32_t MAX_ROW = 16384;

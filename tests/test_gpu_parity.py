@@ -401,7 +401,11 @@ def mfma_tolerance_ok(got, want, ntok, rows):
 
 MFMA_SHAPES = [("c1-gate-b128", False, 4864, 896, 128), ("c1-down-b128", False, 896, 4864, 128),
                ("c2-up-b64", True, 8960, 1536, 64), ("c2-down-b64", True, 1536, 8960, 64),
-               ("ragged", False, 77, 416, 13), ("ragged-q5", True, 45, 64 * 5, 70), ("one-token", False, 33, 96, 1)]
+               ("ragged", False, 77, 416, 13), ("ragged-q5", True, 45, 64 * 5, 70), ("one-token", False, 33, 96, 1),
+               ("c1-gateup-b128", False, 9728, 896, 128),   # 304 tiles: one slice
+               ("split-ragged", False, 200, 4864, 70),      # K split over slices, a partial last chunk, ragged tiles
+               ("two-tokens", False, 130, 224, 2),          # one K chunk of 7 blocks, two tokens
+               ("lm-head-b64", False, 4096, 896, 64)]
 
 
 @pytest.mark.parametrize("name,q5,rows,cols,ntok", MFMA_SHAPES)
@@ -425,6 +429,34 @@ def test_mfma_block_sums_exact_and_outputs_within_tolerance(orc, name, q5, rows,
     ok, worst = mfma_tolerance_ok(out.download(np.float32), want, ntok, rows)
     say("  worst normwise relative error", worst)
     assert ok, (name, worst)
+
+
+@pytest.mark.parametrize("rows,cols,ntok", [(640, 896, 64), (300, 4864, 96)])
+def test_mfma_prefill_items_bias_accumulate(orc, rows, cols, ntok):
+    """smq_matmul on the MFMA GEMM with three items (bias, residual add; one K slice and several):
+    within 1e-5 of the exact contract, the prior added once."""
+    nb = (cols + 31) // 32
+    x = synth.activations(555 + rows, ntok, cols)
+    dbuf, qbuf, xd, xq = gpu_quantize(x)
+    items, wants = [], []
+    for i, (r, with_bias, acc) in enumerate(((rows, True, False), (rows // 2 + 3, False, True), (64, True, True))):
+        w = weights(False, 600 + i, r, cols)
+        bias = synth.normal(610 + i, r, 0.05) if with_bias else None
+        prior = synth.normal(620 + i, ntok * r, 1.0)
+        y = smq.DeviceBuffer.from_array(prior)
+        items.append((smq.QMat(smq.DeviceBuffer.from_array(w), r, cols),
+                      smq.DeviceBuffer.from_array(bias) if bias is not None else None, y, acc))
+        want = orc.mat_item(w, nb * Q8B, r, bias, xd, xq, ntok, nb)[1]
+        wants.append((want + prior if acc else want, r))
+    try:
+        smq.set_prefill_mfma(True)
+        smq.matmul(items, dbuf, qbuf, ntok)
+        smq.numeric_check()
+    finally:
+        smq.set_prefill_mfma(False)
+    for (_, _, y, _), (want, r) in zip(items, wants):
+        ok, worst = mfma_tolerance_ok(y.download(np.float32), want, ntok, r)
+        assert ok, worst
 
 
 def test_matmul_prefill_switch(orc):

@@ -263,8 +263,11 @@ bool mq8_ok(const MatArgs &a) {
 constexpr uint32_t MQ_MIN_SPLIT_TILES = 192;
 
 bool mq8_wanted(const MatArgs &a) {
+    /* counted in the 32 x 64 tiles of the block-pair kernel: where it has enough workgroups on its own
+     * (e.g. 896 x 4864 at 512 tokens: 224), splitting K (a second launch, the partials' traffic) does
+     * not pay */
     uint32_t tiles = 0;
-    for (uint32_t i = 0; i < a.nitems; ++i) tiles += (a.item[i].rows + MQ_R - 1) / MQ_R;
+    for (uint32_t i = 0; i < a.nitems; ++i) tiles += (a.item[i].rows + 31) / 32;
     return mq8_ok(a) && tiles * ((a.ntok + MQ_T - 1) / MQ_T) < MQ_MIN_SPLIT_TILES && (a.nb + MQ_KC - 1) / MQ_KC >= 4;
 }
 

@@ -209,7 +209,7 @@ def summarize_pmc(fetch_dir, write_dir):
         rows = []
         for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
             rows += [r for r in csv.DictReader(open(f)) if r["Counter_Name"] == counter]
-        gemv = [float(r["Counter_Value"]) for r in rows if "k_gemv_pin" in r["Kernel_Name"]]
+        gemv = [float(r["Counter_Value"]) for r in rows if "k_gemv_ct" in r["Kernel_Name"]]
         copy = sum(float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]
                    and float(r["Counter_Value"]) > 1e5)
         return gemv, copy
@@ -573,7 +573,7 @@ def main():
             log(f"bench: cpu baseline failed: {ex!r}")
 
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", "gemv_pin_q8_gateup_group_traffic.json")
+    tfile = os.path.join(ROOT, "profiles", "gemv_ct_q8_gateup_group_traffic.json")
     if os.path.exists(tfile):  # measured by two rocprofv3 --pmc runs of --traffic-probe (see that file)
         with open(tfile) as f:
             traffic = json.load(f).get("traffic_bytes")

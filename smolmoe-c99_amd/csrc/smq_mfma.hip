@@ -94,8 +94,9 @@ __global__ __launch_bounds__(MQ_NT, 2) void k_gemm_mq8(MqArgs q) {
     const uint32_t xstep = !wlane ? 0u : l < 56 ? 2u : 1u;
 
     /* buffer resources over this tile's rows and tokens: a load past the matrix (or past the batch)
-     * returns 0, and a lane with no dword to load passes an offset past every record, so the loads
-     * need no branch and no clamp; the per-load row step is a scalar offset */
+     * returns 0, and a lane with no dword to load passes an offset past every record (2^31 plus at
+     * most 60 rows), so the loads need no branch and no clamp; the per-load row step is part of the
+     * range-checked vector offset */
     const uint32_t rows = I.rows, ntok = a.ntok, xs = a.xstride;
     const size_t rbytes = I.row_bytes;
     const __amdgpu_buffer_rsrc_t wsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -105,7 +106,7 @@ __global__ __launch_bounds__(MQ_NT, 2) void k_gemm_mq8(MqArgs q) {
     const __amdgpu_buffer_rsrc_t dsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(a.xd + (size_t)t0 * xs), (short)0, (int)((size_t)(ntok - t0) * xs * 4), 0x00020000);
     constexpr uint32_t OOB = 0x80000000u;
-    uint32_t wv[MQ_LD], xv[MQ_LD];
+    uint32_t wv[MQ_LD], qv[MQ_LD], dv[MQ_LD];
     uint32_t wo = OOB, qo = OOB, dof = OOB;
     /* chunk c's offsets, then its loads i0..i1 */
     auto fetch_setup = [&](uint32_t c) __attribute__((always_inline)) {
@@ -117,10 +118,9 @@ __global__ __launch_bounds__(MQ_NT, 2) void k_gemm_mq8(MqArgs q) {
     auto fetch_part = [&](uint32_t i0, uint32_t i1) __attribute__((always_inline)) {
 #pragma unroll
         for (uint32_t i = i0; i < i1; ++i) {
-            wv[i] = __builtin_amdgcn_raw_buffer_load_b32(wsrc, wo, (int)(4 * i * rbytes), 0);
-            const uint32_t qv = __builtin_amdgcn_raw_buffer_load_b32(qsrc, qo, (int)(4 * i * xs * QK), 0);
-            const uint32_t dv = __builtin_amdgcn_raw_buffer_load_b32(dsrc, dof, (int)(4 * i * xs * 4), 0);
-            xv[i] = qv | dv; /* at most one of them is a record */
+            wv[i] = __builtin_amdgcn_raw_buffer_load_b32(wsrc, wo + 4 * i * (uint32_t)rbytes, 0, 0);
+            qv[i] = __builtin_amdgcn_raw_buffer_load_b32(qsrc, qo + 4 * i * xs * QK, 0, 0);
+            dv[i] = __builtin_amdgcn_raw_buffer_load_b32(dsrc, dof + 4 * i * xs * 4, 0, 0);
         }
     };
     auto stage = [&](uint32_t buf) __attribute__((always_inline)) {
@@ -129,7 +129,8 @@ __global__ __launch_bounds__(MQ_NT, 2) void k_gemm_mq8(MqArgs q) {
         for (uint32_t i = 0; i < MQ_LD; ++i) { /* no branch: lane 63 writes the sink */
             const uint32_t rr = w + 4 * i;
             B[wdst + rr * wstep] = wv[i];
-            B[xdst + rr * xstep] = xv[i];
+            B[xdst + rr * xstep] = qv[i] | dv[i]; /* at most one of them is a record; merged here, not
+                                                   * at the loads, so no wait follows the loads */
         }
     };
 
@@ -248,11 +249,14 @@ __global__ __launch_bounds__(256) void k_mq8_reduce(MqArgs q) {
 
 bool mq8_ok(const MatArgs &a) {
     if (!a.nb || a.ntok < 2 || (((uintptr_t)a.xq | (uintptr_t)a.xd) & 3u)) return false;
-    /* buffer offsets stay below 2^31 (the out-of-range offset) */
-    if ((uint64_t)a.ntok * a.xstride * QK >= (1ull << 31)) return false;
+    /* buffer offsets stay below 2^31 (the out-of-range offset), and so do 64 rows or tokens of them */
+    if ((uint64_t)a.ntok * a.xstride * QK >= (1ull << 31) || (uint64_t)MQ_T * a.xstride * QK >= (1ull << 31))
+        return false;
     for (uint32_t i = 0; i < a.nitems; ++i) {
         if ((((uintptr_t)a.item[i].w) | a.item[i].row_bytes) & 3u) return false;
-        if ((uint64_t)a.item[i].rows * a.item[i].row_bytes >= (1ull << 31)) return false;
+        if ((uint64_t)a.item[i].rows * a.item[i].row_bytes >= (1ull << 31) ||
+            (uint64_t)MQ_R * a.item[i].row_bytes >= (1ull << 31))
+            return false;
     }
     return true;
 }

@@ -148,8 +148,9 @@ void gemm_impl(bool q5, const unsigned char *w, size_t row_bytes, const float *x
            who);
 }
 
-/* The int8-MFMA prefill GEMM (relaxed block order) for a, if its layout allows: Q8 on the 64 x 64
- * tile kernel (split K over the library workspace), Q5 on the block-pair kernel. Returns false when
+/* The int8-MFMA prefill GEMM (relaxed block order) for a, if its layout allows: few-tile Q8 shapes on
+ * the 64 x 64 tile kernel, the others and every Q5 shape on the block-pair kernel (K split over the
+ * library workspace where the tiles are few). Returns false when
  * the layout does not allow it (nothing launched); a launch error sets the status. */
 bool mfma_launch(const smq::MatArgs &a, bool q5) {
     if (!q5 && smq::mq8_wanted(a)) {
@@ -157,7 +158,7 @@ bool mfma_launch(const smq::MatArgs &a, bool q5) {
         return true;
     }
     if (!smq::mfma_layout_ok(a, q5)) return false;
-    hip_ok(smq::launch_matmul_mfma(a, q5, nullptr, g.cur), "mfma gemm");
+    hip_ok(smq::launch_matmul_mfma(a, q5, nullptr, g.mq_ws, smq::MQ_WORKSPACE_BYTES, g.cur), "mfma gemm");
     return true;
 }
 
@@ -411,7 +412,7 @@ void smq_block_sums(int q5, const unsigned char *w, size_t row_bytes, const int8
         set_status(SMQ_ERR_RANGE, "block_sums: rows and activations must be 4-byte aligned (and nb even for Q5)");
         return;
     }
-    hip_ok(smq::launch_matmul_mfma(a, q5 != 0, sums, g.cur), "block_sums");
+    hip_ok(smq::launch_matmul_mfma(a, q5 != 0, sums, nullptr, 0, g.cur), "block_sums");
 }
 
 void smq_set_prefill_mfma(int on) { g.prefill_mfma = on ? 1 : 0; }

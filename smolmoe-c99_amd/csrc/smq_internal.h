@@ -115,9 +115,11 @@ hipError_t launch_quantize_q8(const float *x, uint32_t rows, uint32_t n, float *
 hipError_t launch_matmul(const MatArgs &a, bool q5, bool fast, hipStream_t s);
 /* Int8-MFMA prefill GEMM (relaxed block order). sums != NULL writes the exact
  * per-block int32 sums, sums[(t*rows + r)*nb + b], instead of the outputs.
- * mfma_layout_ok: 4-byte aligned rows and activations, even nb for Q5. */
+ * ws (ws_bytes of device workspace, may be NULL) holds the partial tiles when
+ * K is split over slices (few tiles); launches that overlap in time must not
+ * share it. mfma_layout_ok: 4-byte aligned rows and activations, even nb for Q5. */
 bool mfma_layout_ok(const MatArgs &a, bool q5);
-hipError_t launch_matmul_mfma(const MatArgs &a, bool q5, int32_t *sums, hipStream_t s);
+hipError_t launch_matmul_mfma(const MatArgs &a, bool q5, int32_t *sums, float *ws, size_t ws_bytes, hipStream_t s);
 /* Q8 prefill GEMM on int8 MFMA with 64 x 64 tiles and K split over slices when the tiles are few
  * (csrc/smq_mfma.hip); ws: MQ_WORKSPACE_BYTES of device workspace for the slices' partial sums.
  * mq8_ok: 4-byte aligned rows and activations, ntok >= 2. */

@@ -593,6 +593,11 @@ __global__ __launch_bounds__(WG) void k_gemm_exact(MatArgs a, uint32_t tok_tiles
  * Operand layout (16x16x32 i8): lane l supplies A[l%16][8*(l/16)+0..7] and
  * B[8*(l/16)+0..7][l%16]; it receives D[4*(l/16)+v][l%16], v = 0..3.
  * SUMS writes the raw block sums instead (test entry point).
+ * K split: with few tiles (e.g. 1536 x 8960 at 64 tokens: 48 workgroups of 20
+ * chunks each) the chunks are cut into `slices` ranges, one workgroup per
+ * (slice, tile); each writes its partial tile to the library workspace and
+ * k_mfma_reduce adds the slices in order, then bias, finiteness and the
+ * residual add.
  * ---------------------------------------------------------------------- */
 constexpr int MT_R = 32, MT_T = 64, MT_CB = 14; /* 14 blocks: a 896-wide row in two chunks */
 constexpr int MT_WT = 32 * MT_CB / 2;           /* staging threads of the weights (two blocks each) */
@@ -600,8 +605,15 @@ constexpr int MT_XP = 64 * MT_CB * 2 / 256;     /* 16-byte activation pieces per
 constexpr int MT_XS = (64 * MT_CB + 255) / 256; /* activation scales per thread (last one partial) */
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+struct MfmaSplit {
+    uint32_t slices, cps; /* K slices, chunks per slice */
+    uint32_t total_rows;  /* tiles x MT_R: the partials' row pitch */
+    float *part;          /* slices > 1: [slice][ntok][total_rows] partial sums */
+};
+
 template <bool Q5, bool SUMS>
-__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_gemm_mfma(MatArgs a, uint32_t tok_tiles, int32_t *sums) {
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_gemm_mfma(MatArgs a, uint32_t tok_tiles, int32_t *sums,
+                                                                                   MfmaSplit sp) {
     __shared__ __attribute__((aligned(16))) uint2 wqa[MT_CB][4][MT_R];
     __shared__ __attribute__((aligned(16))) uint2 xqb[MT_CB][4][MT_T];
     __shared__ __attribute__((aligned(16))) float wsl[MT_CB][MT_R];
@@ -611,7 +623,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(3, 8))) void
     const uint32_t G = gridDim.x, xcd = blockIdx.x % 8u, kk = blockIdx.x / 8u;
     const uint32_t per = G / 8u, extra = G % 8u;
     const uint32_t L = xcd * per + (xcd < extra ? xcd : extra) + kk;
-    const uint32_t row_tile = L / tok_tiles, tok_tile = L % tok_tiles;
+    const uint32_t tiles_all = G / sp.slices, slice = L / tiles_all, rem = L % tiles_all;
+    const uint32_t row_tile = rem / tok_tiles, tok_tile = rem % tok_tiles;
     const Item &I = a.item[find_item(a, row_tile)];
     const uint32_t r0 = (row_tile - I.tile_begin) * MT_R, t0 = tok_tile * MT_T;
 
@@ -704,11 +717,12 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(3, 8))) void
     const v4i zero = {0, 0, 0, 0};
 
     const uint32_t nchunks = (nb + MT_CB - 1) / MT_CB;
-    fetch(0);
-    for (uint32_t c = 0; c < nchunks; ++c) {
+    const uint32_t c_begin = slice * sp.cps, c_end = c_begin + sp.cps < nchunks ? c_begin + sp.cps : nchunks;
+    fetch(c_begin);
+    for (uint32_t c = c_begin; c < c_end; ++c) {
         stage(c);
         __syncthreads();
-        if (c + 1 < nchunks) fetch(c + 1);
+        if (c + 1 < c_end) fetch(c + 1);
         const uint32_t count = nb - c * MT_CB < (uint32_t)MT_CB ? nb - c * MT_CB : (uint32_t)MT_CB;
         auto block_sums = [&](uint32_t bb, v4i S[2]) {
             const uint2 av = wqa[bb][l / 16][wrow0 + l % 16];
@@ -770,9 +784,27 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(3, 8))) void
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const uint32_t r = r0 + wrow0 + 4 * (l / 16) + v, t = t0 + wtok0 + 16 * j + l % 16;
-                if (r < I.rows && t < a.ntok) store_out(I, a.flag, t, r, acc[j][v]);
+                if (r < I.rows && t < a.ntok) {
+                    if (sp.slices > 1)
+                        sp.part[((size_t)slice * a.ntok + t) * sp.total_rows + I.tile_begin * MT_R + r] = acc[j][v];
+                    else
+                        store_out(I, a.flag, t, r, acc[j][v]);
+                }
             }
     }
+}
+
+/* The slices' partial sums added in slice order, then bias, finiteness and the residual add. */
+__global__ __launch_bounds__(WG) void k_mfma_reduce(MatArgs a, MfmaSplit sp) {
+    const uint64_t gi = (uint64_t)blockIdx.x * WG + threadIdx.x;
+    if (gi >= (uint64_t)a.ntok * sp.total_rows) return;
+    const uint32_t t = (uint32_t)(gi / sp.total_rows), rr = (uint32_t)(gi % sp.total_rows);
+    const Item &I = a.item[find_item(a, rr / MT_R)]; /* tile_begin counts MT_R-row tiles */
+    const uint32_t r = rr - I.tile_begin * MT_R;
+    if (r >= I.rows) return;
+    float v = sp.part[(size_t)t * sp.total_rows + rr];
+    for (uint32_t k = 1; k < sp.slices; ++k) v = v + sp.part[((size_t)k * a.ntok + t) * sp.total_rows + rr];
+    store_out(I, a.flag, t, r, v);
 }
 
 /* ------------------------------------------------------------------------
@@ -2198,8 +2230,13 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
     return hipGetLastError();
 }
 
+/* Workgroups (tiles x token tiles) below which K is split over slices: 48 workgroups of 20 chunks
+ * (1536 x 8960 Q5 at 64 tokens) leave most CUs idle; at 192 and more the split's second launch and
+ * partial traffic do not pay (as for the Q8 split-K kernel). */
+constexpr uint32_t MFMA_MIN_SPLIT_TILES = 192;
+
 template <bool Q5, bool SUMS>
-hipError_t launch_mfma_typed(MatArgs a, int32_t *sums, hipStream_t s) {
+hipError_t launch_mfma_typed(MatArgs a, int32_t *sums, float *ws, size_t ws_bytes, hipStream_t s) {
     uint32_t tiles = 0;
     for (uint32_t i = 0; i < a.nitems; ++i) {
         a.item[i].tile_begin = tiles;
@@ -2207,7 +2244,26 @@ hipError_t launch_mfma_typed(MatArgs a, int32_t *sums, hipStream_t s) {
     }
     const uint32_t tok_tiles = (a.ntok + MT_T - 1) / MT_T;
     if (!tiles || !tok_tiles || !a.nb) return hipSuccess;
-    hipLaunchKernelGGL((k_gemm_mfma<Q5, SUMS>), dim3(tiles * tok_tiles), dim3(WG), 0, s, a, tok_tiles, sums);
+    const uint32_t grid1 = tiles * tok_tiles, nchunks = (a.nb + MT_CB - 1) / MT_CB;
+    MfmaSplit sp = {1u, nchunks, tiles * MT_R, nullptr};
+    if (!SUMS && ws && grid1 < MFMA_MIN_SPLIT_TILES && nchunks >= 4) {
+        /* about 512 workgroups, at least two chunks each, the partials within the workspace */
+        uint32_t slices = (512 + grid1 - 1) / grid1;
+        slices = slices < nchunks / 2 ? slices : nchunks / 2;
+        const size_t per = (size_t)a.ntok * sp.total_rows * sizeof(float);
+        const size_t fit = per ? ws_bytes / per : 0;
+        slices = (size_t)slices < fit ? slices : (uint32_t)fit;
+        if (slices >= 2) {
+            sp.cps = (nchunks + slices - 1) / slices;
+            sp.slices = (nchunks + sp.cps - 1) / sp.cps; /* every slice holds at least one chunk */
+            sp.part = ws;
+        }
+    }
+    hipLaunchKernelGGL((k_gemm_mfma<Q5, SUMS>), dim3(grid1 * sp.slices), dim3(WG), 0, s, a, tok_tiles, sums, sp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || sp.slices == 1) return e;
+    const uint64_t n = (uint64_t)a.ntok * sp.total_rows;
+    hipLaunchKernelGGL(k_mfma_reduce, dim3((uint32_t)((n + WG - 1) / WG)), dim3(WG), 0, s, a, sp);
     return hipGetLastError();
 }
 
@@ -2245,9 +2301,12 @@ bool mfma_layout_ok(const MatArgs &a, bool q5) {
     return true;
 }
 
-hipError_t launch_matmul_mfma(const MatArgs &a, bool q5, int32_t *sums, hipStream_t s) {
-    if (sums) return q5 ? launch_mfma_typed<true, true>(a, sums, s) : launch_mfma_typed<false, true>(a, sums, s);
-    return q5 ? launch_mfma_typed<true, false>(a, nullptr, s) : launch_mfma_typed<false, false>(a, nullptr, s);
+hipError_t launch_matmul_mfma(const MatArgs &a, bool q5, int32_t *sums, float *ws, size_t ws_bytes, hipStream_t s) {
+    if (sums)
+        return q5 ? launch_mfma_typed<true, true>(a, sums, nullptr, 0, s)
+                  : launch_mfma_typed<false, true>(a, sums, nullptr, 0, s);
+    return q5 ? launch_mfma_typed<true, false>(a, nullptr, ws, ws_bytes, s)
+              : launch_mfma_typed<false, false>(a, nullptr, ws, ws_bytes, s);
 }
 
 hipError_t launch_glu(float *h, const float *gate, uint32_t n, int act, hipStream_t s) {

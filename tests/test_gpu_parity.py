@@ -405,7 +405,9 @@ MFMA_SHAPES = [("c1-gate-b128", False, 4864, 896, 128), ("c1-down-b128", False, 
                ("c1-gateup-b128", False, 9728, 896, 128),   # 304 tiles: one slice
                ("split-ragged", False, 200, 4864, 70),      # K split over slices, a partial last chunk, ragged tiles
                ("two-tokens", False, 130, 224, 2),          # one K chunk of 7 blocks, two tokens
-               ("lm-head-b64", False, 4096, 896, 64)]
+               ("lm-head-b64", False, 4096, 896, 64),
+               ("q5-split-ragged", True, 200, 8960, 70),    # block-pair kernel, K over 10 slices, ragged tiles
+               ("q5-split-partial", True, 100, 1984, 33)]   # 2 slices of 14-block chunks, the last chunk 6 blocks
 
 
 @pytest.mark.parametrize("name,q5,rows,cols,ntok", MFMA_SHAPES)
@@ -431,22 +433,25 @@ def test_mfma_block_sums_exact_and_outputs_within_tolerance(orc, name, q5, rows,
     assert ok, (name, worst)
 
 
-@pytest.mark.parametrize("rows,cols,ntok", [(640, 896, 64), (300, 4864, 96)])
-def test_mfma_prefill_items_bias_accumulate(orc, rows, cols, ntok):
-    """smq_matmul on the MFMA GEMM with three items (bias, residual add; one K slice and several):
-    within 1e-5 of the exact contract, the prior added once."""
+@pytest.mark.parametrize("rows,cols,ntok,q5", [(640, 896, 64, False), (300, 4864, 96, False),
+                                               (300, 8960, 64, True)])
+def test_mfma_prefill_items_bias_accumulate(orc, rows, cols, ntok, q5):
+    """smq_matmul on the MFMA GEMM with three items (bias, residual add; one K slice and several, on
+    the 64x64 split-K kernel for Q8 and the block-pair kernel's K split for Q5): within 1e-5 of the
+    exact contract, the prior added once."""
     nb = (cols + 31) // 32
+    bb = Q5B if q5 else Q8B
     x = synth.activations(555 + rows, ntok, cols)
     dbuf, qbuf, xd, xq = gpu_quantize(x)
     items, wants = [], []
     for i, (r, with_bias, acc) in enumerate(((rows, True, False), (rows // 2 + 3, False, True), (64, True, True))):
-        w = weights(False, 600 + i, r, cols)
+        w = weights(q5, 600 + i, r, cols)
         bias = synth.normal(610 + i, r, 0.05) if with_bias else None
         prior = synth.normal(620 + i, ntok * r, 1.0)
         y = smq.DeviceBuffer.from_array(prior)
-        items.append((smq.QMat(smq.DeviceBuffer.from_array(w), r, cols),
+        items.append((smq.QMat(smq.DeviceBuffer.from_array(w), r, cols, smq.DTYPE_Q5 if q5 else smq.DTYPE_Q8),
                       smq.DeviceBuffer.from_array(bias) if bias is not None else None, y, acc))
-        want = orc.mat_item(w, nb * Q8B, r, bias, xd, xq, ntok, nb)[1]
+        want = orc.mat_item(w, nb * bb, r, bias, xd, xq, ntok, nb, q5=q5)[1]
         wants.append((want + prior if acc else want, r))
     try:
         smq.set_prefill_mfma(True)

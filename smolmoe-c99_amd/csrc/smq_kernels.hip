@@ -1379,7 +1379,7 @@ constexpr uint32_t AR_KR = AR_KU * AR_WG / AR_Q4;        /* positions per round:
 constexpr uint32_t AR_KT = 256;                          /* K rows per LDS tile */
 constexpr uint32_t AR_KTU = AR_KT * AR_Q4 / AR_WG;       /* float4 loads per thread per tile: 8 */
 constexpr uint32_t AR_KP = AR_HD + 4;                    /* K tile row pitch (floats) */
-constexpr uint32_t AR_VP = 512;                          /* value rows per pass */
+constexpr uint32_t AR_VP = 640;                          /* value rows per pass (a 512-token prompt and 128 steps: one) */
 constexpr uint32_t AR_VPP = AR_VP + 4;                   /* products column pitch (floats) */
 constexpr uint32_t AR_VL = AR_VP * ATT_JW / 4 / AR_WG;   /* float4 value loads per thread per pass */
 constexpr uint32_t AR_FIXED = ATT_JW * AR_VPP > AR_KT * AR_KP ? ATT_JW * AR_VPP : AR_KT * AR_KP; /* LDS floats */

@@ -13,14 +13,21 @@
  * Every result is bit-identical to the unfused calls.
  *
  * Layout: a workgroup owns RT rows (STORE: a 16-row tile of one item; GLU: 32
- * gate rows and the 32 up rows of the same outputs). It requests all its
- * weight bytes at once as 16-byte pieces (one 1 KiB non-temporal load per
- * wave instruction) right after the activation's own loads, so the weights
- * arrive while the RMSNorm's serial sum runs. Then each dword of a piece
- * meets its activation word: a block's scale dword stores d = wscale*xscale,
- * a lane dword stores float(s) of its exact dot4 sum; after one barrier chain
- * thread (row, lane) adds d*float(s) in block order, and the DPP lane tree
- * gives the row (the contract of src/kernels.c:36-79).
+ * gate rows and the 32 up rows of the same outputs). Thread t owns the
+ * 16-byte piece t % 63 of rows t / 63 + 16 j (one 1 KiB non-temporal load of
+ * consecutive bytes per wave instruction), so which block and field each of
+ * its dwords holds and where its result goes are fixed for the thread, and
+ * work out while the activation loads. The activation's Q8 blocks are kept in
+ * the rows' own 36-byte layout, so dword k of a row meets dword k of the
+ * activation: one 16-byte LDS read serves all the thread's rows. Eight
+ * threads form a block's Q8 (four elements each). The weight bytes are
+ * requested once every thread's activation
+ * element is in (so no wave's activation load queues behind other waves'
+ * weights), and arrive while the RMSNorm's serial sum runs. A block's scale
+ * dword stores d = wscale*xscale, a lane dword float(s) of its exact dot4
+ * sum; after one barrier chain thread (row, lane) adds d*float(s) in block
+ * order, and the DPP lane tree gives the row (the contract of
+ * src/kernels.c:36-79).
  */
 #include <float.h>
 #include <stddef.h>
@@ -34,17 +41,16 @@ namespace {
 constexpr uint32_t DC_NT = 1024;
 constexpr int DPRO_NORM = 1, DPRO_F32 = 2; /* SMQ_ACT_NORM, SMQ_ACT_F32 */
 
-/* One launch's LDS: lane sums sf[r][l][b], block scale products d[r][b] (pitch SP floats, 4 mod
- * 32: distinct banks for one block's eight lane sums), a sink for writes past the tile, the
- * activation's Q8 blocks, the squares of the RMSNorm and the rows' results. */
+/* One launch's LDS: per row nine fields of NB floats, f[r][0][b] = the block scale products d
+ * and f[r][1 + l][b] = lane l's sums (pitch SP floats, 4 mod 32: distinct banks for one block's
+ * eight lane sums), the activation's Q8 blocks laid out as a row (dword 9b = block b's scale,
+ * 9b + 1.. its 32 int8), the squares of the RMSNorm, exp_det's table and the rows' results. */
 template <uint32_t NB, uint32_t RT, uint32_t SP>
 struct DcLds {
-    float sf[RT * 8 * SP];
-    float d[RT * SP];
-    float sink[64];
-    uint32_t act_q[NB * 8];
-    float act_d[NB];
-    float sq[DC_NT];
+    float f[RT * 9 * SP];
+    uint32_t act[NB * 9];
+    float sq[NB * 32];
+    uint64_t etab[32];
     float res[RT];
     float inv;
     int bad;
@@ -60,13 +66,16 @@ __device__ __forceinline__ uint32_t find_dec_item(const FusedArgs &a, uint32_t t
 
 template <bool GLU, int PRO, uint32_t NB, uint32_t RT, uint32_t CPT>
 __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
-    static_assert(NB % 4 == 0 && NB * 32 <= DC_NT, "packed rows of whole 16-byte pieces; one element per thread");
-    constexpr uint32_t C16 = 9 * NB / 4;
-    constexpr uint32_t TCH = RT * C16;
+    static_assert(NB % 4 == 0 && NB * 8 <= DC_NT, "packed rows of whole 16-byte pieces; four elements per thread");
+    constexpr uint32_t NQ = NB * 8;        /* threads holding four activation elements */
+    constexpr uint32_t C16 = 9 * NB / 4;   /* pieces per row */
+    constexpr uint32_t RG = DC_NT / C16;   /* rows per slab of the tile */
     constexpr uint32_t SP = (NB + 3) / 4 * 4 + (36 - (NB + 3) / 4 * 4 % 32) % 32;
+    constexpr uint32_t SLAB = RG * 9 * SP; /* LDS floats between a thread's rows */
     static_assert(SP % 32 == 4 && SP >= NB, "pitch 4 mod 32");
-    static_assert(TCH <= CPT * DC_NT, "each piece of the tile has a thread slot");
-    static_assert(!GLU || RT == 64, "GLU: 32 gate and 32 up rows");
+    static_assert((RT * 9 * SP) % 4 == 0, "the activation row starts 16-byte aligned");
+    static_assert(RT == CPT * RG, "the tile is CPT slabs of RG rows");
+    static_assert(!GLU || (RT == 64 && 32 % RG == 0), "GLU: 32 gate and 32 up rows, a slab in one of them");
     using Lds = DcLds<NB, RT, SP>;
     __shared__ __attribute__((aligned(16))) Lds L;
 
@@ -78,22 +87,42 @@ __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
         r0 = (blockIdx.x - a.item[item].tile_begin) * RT;
     }
 
-    /* 1. the activation's own loads first (loads complete in order) */
-    const bool xel = tid < n;
-    const float xv = xel ? a.src[tid] : 0.0f;
-    const float wv = PRO == DPRO_NORM && xel ? a.norm[tid] : 0.0f;
+    /* 1. the activation's own loads first: thread t < NQ holds elements 4t..4t+3 (n % 4 == 0 and
+     * 16-byte aligned rows: one in-bounds 16-byte load each, zeros past n) */
+    float xv[4], wv[4];
+    {
+        const bool ok = 4 * tid < n;
+        const uint32_t e = ok ? 4 * tid : 0;
+        const float4 xl = *(const float4 *)(a.src + e);
+        xv[0] = ok ? xl.x : 0.0f;
+        xv[1] = ok ? xl.y : 0.0f;
+        xv[2] = ok ? xl.z : 0.0f;
+        xv[3] = ok ? xl.w : 0.0f;
+        if constexpr (PRO == DPRO_NORM) {
+            const float4 wl = *(const float4 *)(a.norm + e);
+            wv[0] = ok ? wl.x : 0.0f;
+            wv[1] = ok ? wl.y : 0.0f;
+            wv[2] = ok ? wl.z : 0.0f;
+            wv[3] = ok ? wl.w : 0.0f;
+        } else {
+            wv[0] = wv[1] = wv[2] = wv[3] = 0.0f;
+        }
+    }
 
-    /* 2. all the workgroup's weight bytes: piece c = tid + j*DC_NT (row c / C16, 16-byte piece
-     * c % C16); rows past a matrix re-read its last row (in bounds, never stored) */
-    u4a W[CPT];
+    /* 2. the thread's weight pieces: piece pc of rows rg + RG*j (threads past the RG slab rows,
+     * and rows past a matrix, re-read an in-bounds row that is never stored); dword k = 4*pc + q
+     * of a row is field k % 9 of block k / 9, and its result goes to at[q] + j*SLAB */
+    const uint32_t pc = tid % C16, rg = tid / C16;
+    const bool owner = rg < RG;
+    const u4a *wp[CPT];
 #pragma unroll
     for (uint32_t j = 0; j < CPT; ++j) {
-        const uint32_t c = tid + j * DC_NT, cc = c < TCH ? c : 0, rr = cc / C16, pc = cc % C16;
+        const uint32_t rr = (owner ? rg : 0) + RG * j;
         const unsigned char *w;
         size_t rb;
         uint32_t row, rows;
         if constexpr (GLU) {
-            const Item &I = a.item[rr < 32 ? 0 : 1];
+            const Item &I = a.item[j < 32 / RG ? 0 : 1]; /* slabs of the gate rows, then the up rows */
             w = I.w;
             rb = I.row_bytes;
             rows = a.rows;
@@ -106,13 +135,39 @@ __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
             row = r0 + rr;
         }
         row = row < rows ? row : rows - 1;
-        W[j] = __builtin_nontemporal_load((const u4a *)(w + (size_t)row * rb + 16 * pc));
+        wp[j] = (const u4a *)(w + (size_t)row * rb + 16 * pc);
     }
+    uint32_t at[4];
+    bool isd[4];
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+        const uint32_t k = 4 * pc + q, b = k / 9, f = k % 9;
+        isd[q] = f == 0;
+        at[q] = (rg * 9 + f) * SP + b;
+    }
+    /* the epilogue's own loads: exp_det's table (GLU), or the bias and accumulated cell of the
+     * thread's output row (STORE), so the stores wait on no memory round trip */
+    const uint32_t cr = tid / 8, cl = tid % 8;
+    uint64_t ev = 0;
+    OutPre pre = {0.0f, 0.0f};
+    if constexpr (GLU) {
+        if (tid < 32) ev = EXP2_TABLE[tid];
+    } else {
+        const Item &I = a.item[item];
+        if (tid < RT * 8 && cl == 7 && r0 + cr < I.rows) pre = load_out(I, 0, r0 + cr);
+    }
+    u4a W[CPT];
+    auto fetch = [&]() {
+#pragma unroll
+        for (uint32_t j = 0; j < CPT; ++j) W[j] = __builtin_nontemporal_load(wp[j]);
+    };
+    if constexpr (PRO != DPRO_NORM) fetch(); /* no serial sum to hide them behind */
 
-    /* 3. the activation's Q8 blocks into LDS (RMSNorm first) */
+    /* 3. the activation's Q8 blocks into LDS in the rows' own layout (RMSNorm first) */
     if constexpr (PRO == DPRO_NORM) {
-        if (xel) L.sq[tid] = xv * xv;
-        __syncthreads();
+        if (tid < NQ) *(float4 *)&L.sq[4 * tid] = make_float4(xv[0] * xv[0], xv[1] * xv[1], xv[2] * xv[2], xv[3] * xv[3]);
+        __syncthreads(); /* every activation element is in */
+        fetch();
         if (tid < 64) { /* the whole first wave runs the chain (faster than one lane) */
             const float ss = serial_sum_lds(L.sq, n);
             if (tid == 0) {
@@ -124,46 +179,72 @@ __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
         __syncthreads();
     }
     int bad = 0;
-    if (tid < NB * 32) { /* whole half-waves: a block's 32 lanes */
-        float v = xv;
-        if constexpr (PRO == DPRO_NORM) {
-            const float t = xv * L.inv;
-            v = t * wv; /* model.c:340 */
+    if (tid < NQ) { /* eight threads per block, four elements each (kernels.c:912-935) */
+        float v[4], m = 0.0f;
+        const float inv = PRO == DPRO_NORM ? L.inv : 1.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            const bool valid = 4 * tid + i < n;
+            v[i] = xv[i];
+            if constexpr (PRO == DPRO_NORM) {
+                const float t = xv[i] * inv;
+                v[i] = t * wv[i]; /* model.c:340 */
+            }
+            const float av = fabsf(v[i]);
+            bad |= valid && !(av <= FLT_MAX);
+            const float am = valid ? av : 0.0f;
+            m = am > m ? am : m;
         }
-        stage_q8(v, xel, tid, (int8_t *)L.act_q, L.act_d, bad);
+        float o = dpp_f<0xB1>(m); /* the block's other seven threads: lane^1, lane^2, the other quad */
+        m = o > m ? o : m;
+        o = dpp_f<0x4E>(m);
+        m = o > m ? o : m;
+        o = dpp_f<0x141>(m);
+        m = o > m ? o : m;
+        const float scale = m / 127.0f;
+        const float qinv = scale >= FLT_MIN ? 1.0f / scale : 0.0f;
+        uint32_t word = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            int qv = 0;
+            if (4 * tid + i < n) {
+                const float pq = v[i] * qinv;
+                qv = (int)__builtin_rintf(pq);
+                qv = qv > 127 ? 127 : (qv < -127 ? -127 : qv);
+            }
+            word |= ((uint32_t)qv & 0xffu) << (8 * i);
+        }
+        L.act[9 * (tid / 8) + 1 + tid % 8] = word;
+        if (tid % 8 == 0) L.act[9 * (tid / 8)] = __float_as_uint(scale);
     }
     if (bad && a.flag) *a.flag = 1;
     if (PRO == DPRO_NORM && tid == 0 && L.bad && a.flag) *a.flag = 1;
+    if (GLU && tid < 32) L.etab[tid] = ev;
     __syncthreads();
 
-    /* 4. every dword of the tile: its lane sum as float, or for a scale d = wscale * xscale */
+    /* 4. every dword of the thread's pieces meets the activation dword of the same index: a
+     * scale dword gives d = wscale * xscale, a lane dword float(s) of its dot4 */
+    if (owner) {
+        const u4a A = *(const u4a *)&L.act[4 * pc];
+        const uint32_t aw[4] = {A.x, A.y, A.z, A.w};
 #pragma unroll
-    for (uint32_t j = 0; j < CPT; ++j) {
-        const uint32_t c = tid + j * DC_NT, cc = c < TCH ? c : 0, rr = cc / C16, pc = cc % C16;
-        const uint32_t wd[4] = {W[j].x, W[j].y, W[j].z, W[j].w};
+        for (uint32_t j = 0; j < CPT; ++j) {
+            const uint32_t wd[4] = {W[j].x, W[j].y, W[j].z, W[j].w};
 #pragma unroll
-        for (uint32_t q = 0; q < 4; ++q) {
-            const uint32_t k = 4 * pc + q, b = k / 9, f = k % 9;
-            float v;
-            uint32_t at;
-            if (f == 0) {
-                v = __uint_as_float(wd[q]) * L.act_d[b];
-                at = (uint32_t)(offsetof(Lds, d) / 4) + rr * SP + b;
-            } else {
-                v = (float)dot4(wd[q], L.act_q[8 * b + f - 1], 0);
-                at = (uint32_t)(offsetof(Lds, sf) / 4) + (rr * 8 + f - 1) * SP + b;
+            for (uint32_t q = 0; q < 4; ++q) {
+                const float pd = __uint_as_float(wd[q]) * __uint_as_float(aw[q]);
+                const float ps = (float)dot4(wd[q], aw[q], 0);
+                L.f[at[q] + j * SLAB] = isd[q] ? pd : ps;
             }
-            ((float *)&L)[c < TCH ? at : (uint32_t)(offsetof(Lds, sink) / 4) + (tid & 63u)] = v;
         }
     }
     __syncthreads();
 
     /* 5. chains: thread (row r, lane l) adds d*float(s) in block order; the lane tree */
-    const uint32_t cr = tid / 8, cl = tid % 8;
     float v = 0.0f;
     if (tid < RT * 8) {
-        const float4 *sp = (const float4 *)&L.sf[(cr * 8 + cl) * SP];
-        const float4 *dp = (const float4 *)&L.d[cr * SP];
+        const float4 *sp = (const float4 *)&L.f[(cr * 9 + 1 + cl) * SP];
+        const float4 *dp = (const float4 *)&L.f[cr * 9 * SP];
         float acc = 0.0f;
 #pragma unroll
         for (uint32_t qq = 0; qq < NB / 4; ++qq) {
@@ -180,7 +261,7 @@ __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
     if constexpr (!GLU) {
         const Item &I = a.item[item];
         const uint32_t row = r0 + cr;
-        if (tid < RT * 8 && cl == 7 && row < I.rows) store_out(I, a.flag, 0, row, v);
+        if (tid < RT * 8 && cl == 7 && row < I.rows) store_out_pre(I, a.flag, 0, row, v, pre);
         return;
     } else {
         /* 6. h = up * act(gate) for the 32 outputs, then their Q8 block (vecmath.c:78-93, model.c:409-415) */
@@ -197,9 +278,9 @@ __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
                 if (a.act == 2) {
                     const float g3 = 0.044715f * gv * gv * gv;
                     const float uu = 1.5957691216f * (gv + g3);
-                    e = exp_det(-uu);
+                    e = exp_det_tab(-uu, L.etab);
                 } else {
-                    e = exp_det(-gv);
+                    e = exp_det_tab(-gv, L.etab);
                 }
                 const float den = 1.0f + e;
                 const float sg = gv / den;
@@ -227,7 +308,7 @@ __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
 template <bool GLU, int PRO>
 hipError_t launch_dec(FusedArgs a, hipStream_t s) {
     constexpr uint32_t RT = GLU ? 64 : 16;
-    constexpr uint32_t CPT = (RT * 63 + DC_NT - 1) / DC_NT;
+    constexpr uint32_t CPT = RT / (DC_NT / 63); /* slabs of 16 rows (63 pieces each) */
     uint32_t blocks = 0;
     if (GLU) {
         blocks = (a.rows + 31) / 32;
@@ -246,6 +327,7 @@ hipError_t launch_dec(FusedArgs a, hipStream_t s) {
 
 bool decode_ct_ok(const FusedArgs &a, bool q5, int pro, bool glu) {
     if (q5 || a.nb != 28 || a.n > 28 * QK || a.n + QK <= 28 * QK || (pro != DPRO_NORM && pro != DPRO_F32)) return false;
+    if (a.n % 4 || ((uintptr_t)a.src & 15u) || (pro == DPRO_NORM && ((uintptr_t)a.norm & 15u))) return false;
     if (glu && (!a.hd || !a.hq || a.nitems != 2 || ((uintptr_t)a.hd & 3u))) return false;
     for (uint32_t i = 0; i < a.nitems; ++i) {
         const Item &it = a.item[i];

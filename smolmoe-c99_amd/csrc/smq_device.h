@@ -118,6 +118,26 @@ __device__ __forceinline__ void store_out(const Item &I, int *flag, uint32_t t, 
     *cell = v;
 }
 
+/* store_out with its two reads issued early (load_out at kernel entry): the
+ * bias and, for an accumulating item, the cell's old value. The cell is
+ * written only by its own thread, at the end, so the early read sees what the
+ * late one would. */
+struct OutPre {
+    float bias, cell;
+};
+__device__ __forceinline__ OutPre load_out(const Item &I, uint32_t t, uint32_t r) {
+    OutPre p = {0.0f, 0.0f};
+    if (I.bias) p.bias = I.bias[r];
+    if (I.accumulate) p.cell = I.y[(size_t)t * I.y_stride + r];
+    return p;
+}
+__device__ __forceinline__ void store_out_pre(const Item &I, int *flag, uint32_t t, uint32_t r, float v, OutPre p) {
+    if (I.bias) v = v + p.bias; /* model.c:259-262 */
+    if (flag && !(fabsf(v) <= FLT_MAX)) *flag = 1;
+    if (I.accumulate) v = p.cell + v; /* residual: x += out (model.c:452-455) */
+    I.y[(size_t)t * I.y_stride + r] = v;
+}
+
 /* DPP row shift by N lanes (row_shr:N): lane i reads lane i-N of its row of 16. */
 template <int N>
 __device__ __forceinline__ float shr_dpp(float v) {

@@ -91,6 +91,8 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
         }
     };
     load_task(ti * TB);
+    OutPre pre = {0.0f, 0.0f}; /* the store's own reads, issued now */
+    if (tid < RT * 8 && (tid & 7) == 7 && r0 + tid / 8 < I.rows) pre = load_out(I, 0, r0 + tid / 8);
 
     float acc = 0.0f;
     for (uint32_t c = 0; c < nchunks; ++c) {
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
     if (tid < RT * 8) {
         const float v = reduce8_to_lane7(acc);
         const uint32_t r = r0 + tid / 8;
-        if ((tid & 7) == 7 && r < I.rows) store_out(I, a.flag, 0, r, v);
+        if ((tid & 7) == 7 && r < I.rows) store_out_pre(I, a.flag, 0, r, v, pre);
     }
 }
 

@@ -288,8 +288,9 @@ __device__ __forceinline__ void lgkm_wait8() {
 
 /* s + a[0] + a[1] + ... + a[n-1] in f32, added one at a time in that order
  * (the order of the reference's sequential loops, model.c:337,
- * kernels.c:1150, 1165). a is 16-byte aligned LDS, each lane may pass its own
- * row, n is uniform across the wave. Batches of 32 floats (eight 16-byte
+ * kernels.c:1150, 1165). a is 16-byte aligned LDS with room for
+ * 4*ceil(n/4) floats, each lane may pass its own row, n is uniform across the
+ * wave. Batches of 32 floats (eight 16-byte
  * reads) alternate: the next batch's reads are issued, then one wait for the
  * older batch, then its 32 adds, so the chain issues little beyond its adds
  * (measured on MI355X: 6.6-7.0 cycles per add run by a whole wave, against
@@ -318,15 +319,23 @@ __device__ __forceinline__ float chain_lds(float s, const float *a, uint32_t n) 
             ++c;
         }
     }
-    const uint32_t rest = n - c * 32; /* < 32: read together, then added in order */
+    const uint32_t rest = n - c * 32; /* < 32: one more batch of 16-byte reads up to the float4 holding
+                                         a[n-1], terms past n-1 replaced by -0.0f (s + -0.0f == s, bit for bit) */
     if (rest) {
-        const float *t = a + c * 32;
-        float v[32];
+        const float4 *t4 = a4 + 8 * c;
+        const uint32_t last = (rest - 1) / 4;
+        float4 v[8];
 #pragma unroll
-        for (uint32_t u = 0; u < 32; ++u) v[u] = t[u < rest ? u : rest - 1];
+        for (uint32_t k = 0; k < 8; ++k) v[k] = t4[k < last ? k : last];
 #pragma unroll
-        for (uint32_t u = 0; u < 32; ++u)
-            if (u < rest) s = s + v[u];
+        for (uint32_t k = 0; k < 8; ++k) {
+            if (4 * k < rest) { /* uniform */
+                s = s + (4 * k + 0 < rest ? v[k].x : -0.0f);
+                s = s + (4 * k + 1 < rest ? v[k].y : -0.0f);
+                s = s + (4 * k + 2 < rest ? v[k].z : -0.0f);
+                s = s + (4 * k + 3 < rest ? v[k].w : -0.0f);
+            }
+        }
     }
     return s;
 }

@@ -912,7 +912,7 @@ template <bool NORM, int ACT>
 __global__ __launch_bounds__(RW_WG) void k_row_quantize(const float *src, const float *norm, float eps,
                                                        const float *gate, uint32_t n, float *yout, float *d,
                                                        int8_t *q, int *flag) {
-    extern __shared__ __attribute__((aligned(16))) float sq_lds[]; /* NORM: the n squares */
+    extern __shared__ __attribute__((aligned(16))) float sq_lds[]; /* NORM: the n squares (4*ceil(n/4) floats) */
     __shared__ float s_inv;
     __shared__ int s_bad;
     const uint32_t tid = threadIdx.x, row = blockIdx.x, nb = (n + QK - 1) / QK, np = nb * QK;
@@ -1383,8 +1383,17 @@ constexpr uint32_t AR_KTU = AR_KT * AR_Q4 / AR_WG;       /* float4 loads per thr
 constexpr uint32_t AR_KP = AR_HD + 4;                    /* K tile row pitch (floats) */
 constexpr uint32_t AR_VP = 640;                          /* value rows per pass (a 512-token prompt and 128 steps: one) */
 constexpr uint32_t AR_VPP = AR_VP + 4;                   /* products column pitch (floats) */
+constexpr uint32_t AR_PF = ATT_JW * AR_VPP + ATT_JW / 4 * 8; /* products floats (see att_col) */
 constexpr uint32_t AR_VL = AR_VP * ATT_JW / 4 / AR_WG;   /* float4 value loads per thread per pass */
-constexpr uint32_t AR_FIXED = ATT_JW * AR_VPP > AR_KT * AR_KP ? ATT_JW * AR_VPP : AR_KT * AR_KP; /* LDS floats */
+constexpr uint32_t AR_FIXED = AR_PF > AR_KT * AR_KP ? AR_PF : AR_KT * AR_KP; /* LDS floats */
+
+/* Start of product column j: pitch AR_VPP (4 mod 32) plus 8 floats per group of
+ * four columns, so one wave's writes (8 rows x 8 groups of four columns) put
+ * two lanes on a bank instead of four. 16-byte aligned for the chains' reads. */
+__device__ __forceinline__ uint32_t att_col(uint32_t j) {
+    static_assert(AR_VPP % 32 == 4, "bank pattern");
+    return j * AR_VPP + j / 4 * 8;
+}
 
 struct RopeRows {
     const float *k, *v;    /* this token's k and v rows (kv_dim each), unrotated */
@@ -1479,10 +1488,10 @@ __device__ __forceinline__ void att_tail(float high, float *sc, float *prod, uin
             const uint32_t r = vrow + u * (AR_WG * 4 / ATT_JW), p = p0 + r;
             if (p < np) {
                 const float w = sc[p] * inv;
-                prod[(vcol + 0) * AR_VPP + r] = w * pre[u].x;
-                prod[(vcol + 1) * AR_VPP + r] = w * pre[u].y;
-                prod[(vcol + 2) * AR_VPP + r] = w * pre[u].z;
-                prod[(vcol + 3) * AR_VPP + r] = w * pre[u].w;
+                prod[att_col(vcol + 0) + r] = w * pre[u].x;
+                prod[att_col(vcol + 1) + r] = w * pre[u].y;
+                prod[att_col(vcol + 2) + r] = w * pre[u].z;
+                prod[att_col(vcol + 3) + r] = w * pre[u].w;
             }
         }
         __syncthreads();
@@ -1490,7 +1499,7 @@ __device__ __forceinline__ void att_tail(float high, float *sc, float *prod, uin
             att_load_values<ROPE>(pre, vbase, vrope, kvd, p0 + AR_VP, np, last, vrow, vcol);
         if (tid < ATT_JW) {
             const uint32_t rows = np - p0 < AR_VP ? np - p0 : AR_VP;
-            const float *colp = prod + tid * AR_VPP;
+            const float *colp = prod + att_col(tid);
             float acc = o;
             acc = chain_lds(acc, colp, rows); /* kernels.c:1165, position order */
             o = acc;
@@ -1542,7 +1551,7 @@ __global__ __launch_bounds__(AR_WG) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     const uint32_t start = sh.window && pos >= sh.window ? pos - sh.window + 1 : 0, np = pos - start + 1;
     const uint32_t last = np - 1; /* ROPE: the current position, taken from rr rather than the caches */
     float *sc = lds;
-    float *shared = lds + ((sh.context + 3) & ~3u); /* K tiles, then the products [ATT_JW][AR_VPP] */
+    float *shared = lds + ((sh.context + 3) & ~3u); /* K tiles, then the products (att_col) */
     float *prod = shared;
     float *kt = shared;
     const float *kbase = kcache + (size_t)start * kvd + (size_t)kh * AR_HD;
@@ -2336,7 +2345,7 @@ hipError_t launch_row_quantize(const float *src, const float *norm, float eps, c
                                uint32_t rows, uint32_t n, float *y, float *d, int8_t *q, int *flag, hipStream_t s) {
     if (!rows || !n) return hipSuccess;
     if (n > (uint32_t)(RW_WG * RW_EPT)) return hipErrorInvalidValue;
-    const size_t lds = norm ? (size_t)n * sizeof(float) : 0;
+    const size_t lds = norm ? (size_t)((n + 3) & ~3u) * sizeof(float) : 0; /* the squares' whole float4s */
     const dim3 grid(rows), block(RW_WG);
 #define SMQ_RQ(NORM, ACT) \
     hipLaunchKernelGGL((k_row_quantize<NORM, ACT>), grid, block, lds, s, src, norm, eps, gate, n, y, d, q, flag)

@@ -118,6 +118,36 @@ __device__ __forceinline__ void store_out(const Item &I, int *flag, uint32_t t, 
     *cell = v;
 }
 
+/* The item holding tile `tile` of a fused launch, as a value: every item's
+ * fields are read at constant offsets of the kernel arguments and selected, so
+ * they arrive in one scalar round trip at entry instead of a second load that
+ * waits for the chosen index. */
+template <class Args>
+__device__ __forceinline__ Item pick_item(const Args &a, uint32_t tile) {
+    Item I = a.item[0];
+#pragma unroll
+    for (uint32_t k = 1; k < MAX_ITEMS; ++k) {
+        const Item c = a.item[k];
+        const bool take = k < a.nitems && tile >= c.tile_begin;
+        I.w = take ? c.w : I.w;
+        I.row_bytes = take ? c.row_bytes : I.row_bytes;
+        I.bias = take ? c.bias : I.bias;
+        I.y = take ? c.y : I.y;
+        I.y_stride = take ? c.y_stride : I.y_stride;
+        I.rows = take ? c.rows : I.rows;
+        I.tile_begin = take ? c.tile_begin : I.tile_begin;
+        I.accumulate = take ? c.accumulate : I.accumulate;
+    }
+    return I;
+}
+
+/* A uniform value made ready here: its kernel-argument load is issued with
+ * the entry's others instead of inside a later branch. */
+template <class T>
+__device__ __forceinline__ void sgpr_now(T v) {
+    asm volatile("" : : "s"(v));
+}
+
 /* store_out with its two reads issued early (load_out at kernel entry): the
  * bias and, for an accumulating item, the cell's old value. The cell is
  * written only by its own thread, at the end, so the early read sees what the
@@ -220,6 +250,8 @@ __device__ __forceinline__ void chain_sum_padded(float &acc, const float4 *p, ui
     }
 }
 
+__device__ __forceinline__ float chain_lds_strided(float s, const float4 *a4, uint32_t st, uint32_t n);
+
 template <bool FAST, int NQ>
 __device__ __forceinline__ void chain_sum(float &acc, const float4 *p, uint32_t ps, const float4 *d, uint32_t dst,
                                           uint32_t count) {
@@ -230,8 +262,12 @@ __device__ __forceinline__ void chain_sum(float &acc, const float4 *p, uint32_t 
         chain_add<FAST, NQ <= 8 ? NQ : 1>(acc, x, xw, 0, count);
         return;
     }
-    /* wide rows (a few chain threads, many blocks): whole float4 first (the
-     * compiler unrolls this loop and batches its reads), then the tail */
+    if (!FAST) { /* wide rows (a few chain threads, many blocks): batched reads */
+        acc = chain_lds_strided(acc, p, ps, count);
+        return;
+    }
+    /* fast contract, wide rows: whole float4 first (the compiler unrolls this loop and batches
+     * its reads), then the tail */
     const uint32_t full = count / 4;
     uint32_t q = 0;
     for (; q < full; ++q) {
@@ -273,9 +309,9 @@ __device__ __forceinline__ void add_batch(float &s, const float4 (&v)[8]) {
         s = s + v[b].w;
     }
 }
-__device__ __forceinline__ void read_batch(float4 (&v)[8], const float4 *p) {
+__device__ __forceinline__ void read_batch(float4 (&v)[8], const float4 *p, uint32_t stride = 1) {
 #pragma unroll
-    for (int b = 0; b < 8; ++b) v[b] = p[b];
+    for (int b = 0; b < 8; ++b) v[b] = p[b * stride];
 }
 /* lgkmcnt(8) (vmcnt and expcnt at their maxima): at most eight LDS/scalar
  * operations outstanding. LDS reads return in issue order, so after two
@@ -296,20 +332,20 @@ __device__ __forceinline__ void lgkm_wait8() {
  * (measured on MI355X: 6.6-7.0 cycles per add run by a whole wave, against
  * about 10 with a wait before every four adds in one lane). Faster run by a
  * whole wave than by one lane: callers pass every lane of the wave, each
- * with a valid pointer. */
-__device__ __forceinline__ float chain_lds(float s, const float *a, uint32_t n) {
-    const float4 *a4 = (const float4 *)a;
+ * with a valid pointer. chain_lds_strided: element 4q + i is component i of
+ * a4[q * st]. */
+__device__ __forceinline__ float chain_lds_strided(float s, const float4 *a4, uint32_t st, uint32_t n) {
     const uint32_t batches = n / 32; /* 32 floats = 8 float4 per batch */
     uint32_t c = 0;
     if (batches) {
         float4 x[8], y[8];
-        read_batch(x, a4);
+        read_batch(x, a4, st);
         for (; c + 2 <= batches; c += 2) {
-            read_batch(y, a4 + 8 * (c + 1));
+            read_batch(y, a4 + 8 * (c + 1) * st, st);
             lgkm_wait8(); /* x is in */
             add_batch(s, x);
             __builtin_amdgcn_sched_barrier(0);
-            read_batch(x, a4 + 8 * (c + 2 < batches ? c + 2 : c + 1)); /* clamped re-read past the end */
+            read_batch(x, a4 + 8 * (c + 2 < batches ? c + 2 : c + 1) * st, st); /* clamped re-read past the end */
             lgkm_wait8(); /* y is in */
             add_batch(s, y);
             __builtin_amdgcn_sched_barrier(0);
@@ -320,13 +356,13 @@ __device__ __forceinline__ float chain_lds(float s, const float *a, uint32_t n) 
         }
     }
     const uint32_t rest = n - c * 32; /* < 32: one more batch of 16-byte reads up to the float4 holding
-                                         a[n-1], terms past n-1 replaced by -0.0f (s + -0.0f == s, bit for bit) */
+                                         element n-1, terms past it replaced by -0.0f (s + -0.0f == s, bit for bit) */
     if (rest) {
-        const float4 *t4 = a4 + 8 * c;
+        const float4 *t4 = a4 + 8 * c * st;
         const uint32_t last = (rest - 1) / 4;
         float4 v[8];
 #pragma unroll
-        for (uint32_t k = 0; k < 8; ++k) v[k] = t4[k < last ? k : last];
+        for (uint32_t k = 0; k < 8; ++k) v[k] = t4[(k < last ? k : last) * st];
 #pragma unroll
         for (uint32_t k = 0; k < 8; ++k) {
             if (4 * k < rest) { /* uniform */
@@ -338,6 +374,10 @@ __device__ __forceinline__ float chain_lds(float s, const float *a, uint32_t n) 
         }
     }
     return s;
+}
+
+__device__ __forceinline__ float chain_lds(float s, const float *a, uint32_t n) {
+    return chain_lds_strided(s, (const float4 *)a, 1, n);
 }
 
 __device__ __forceinline__ float serial_sum_lds(const float *a, uint32_t n) { return chain_lds(0.0f, a, n); }

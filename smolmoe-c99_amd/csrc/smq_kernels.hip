@@ -58,8 +58,10 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
     __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? (CB / 4) * DS : 4];
 
     const uint32_t nb = a.nb, tid = threadIdx.x;
-    const Item &I = a.item[find_item(a, blockIdx.x)]; /* uniform index into the kernel arguments */
+    const Item I = pick_item(a, blockIdx.x);
     const uint32_t r0 = (blockIdx.x - I.tile_begin) * RT;
+    sgpr_now(a.xq);
+    sgpr_now(a.xd);
 
     const uint32_t tr = tid / TPR, ti = tid % TPR;
     const bool row_ok = r0 + tr < I.rows;

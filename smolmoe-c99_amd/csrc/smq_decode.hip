@@ -56,14 +56,6 @@ struct DcLds {
     int bad;
 };
 
-__device__ __forceinline__ uint32_t find_dec_item(const FusedArgs &a, uint32_t tile) {
-    uint32_t it = 0;
-    if (a.nitems > 1 && tile >= a.item[1].tile_begin) it = 1;
-    if (a.nitems > 2 && tile >= a.item[2].tile_begin) it = 2;
-    if (a.nitems > 3 && tile >= a.item[3].tile_begin) it = 3;
-    return it;
-}
-
 template <bool GLU, int PRO, uint32_t NB, uint32_t RT, uint32_t CPT>
 __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
     static_assert(NB % 4 == 0 && NB * 8 <= DC_NT, "packed rows of whole 16-byte pieces; four elements per thread");
@@ -81,11 +73,8 @@ __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
 
     const uint32_t tid = threadIdx.x, n = a.n;
     /* this workgroup's rows: STORE a tile of one item, GLU the 32 outputs of h block blockIdx.x */
-    uint32_t item = 0, r0 = 0;
-    if constexpr (!GLU) {
-        item = find_dec_item(a, blockIdx.x);
-        r0 = (blockIdx.x - a.item[item].tile_begin) * RT;
-    }
+    const Item It = GLU ? a.item[0] : pick_item(a, blockIdx.x); /* STORE: this tile's item */
+    const uint32_t r0 = GLU ? 0u : (blockIdx.x - It.tile_begin) * RT;
 
     /* 1. the activation's own loads first: thread t < NQ holds elements 4t..4t+3 (n % 4 == 0 and
      * 16-byte aligned rows: one in-bounds 16-byte load each, zeros past n) */
@@ -128,10 +117,9 @@ __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
             rows = a.rows;
             row = blockIdx.x * 32 + (rr & 31u);
         } else {
-            const Item &I = a.item[item];
-            w = I.w;
-            rb = I.row_bytes;
-            rows = I.rows;
+            w = It.w;
+            rb = It.row_bytes;
+            rows = It.rows;
             row = r0 + rr;
         }
         row = row < rows ? row : rows - 1;
@@ -153,8 +141,7 @@ __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
     if constexpr (GLU) {
         if (tid < 32) ev = EXP2_TABLE[tid];
     } else {
-        const Item &I = a.item[item];
-        if (tid < RT * 8 && cl == 7 && r0 + cr < I.rows) pre = load_out(I, 0, r0 + cr);
+        if (tid < RT * 8 && cl == 7 && r0 + cr < It.rows) pre = load_out(It, 0, r0 + cr);
     }
     u4a W[CPT];
     auto fetch = [&]() {
@@ -259,9 +246,8 @@ __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
     }
 
     if constexpr (!GLU) {
-        const Item &I = a.item[item];
         const uint32_t row = r0 + cr;
-        if (tid < RT * 8 && cl == 7 && row < I.rows) store_out_pre(I, a.flag, 0, row, v, pre);
+        if (tid < RT * 8 && cl == 7 && row < It.rows) store_out_pre(It, a.flag, 0, row, v, pre);
         return;
     } else {
         /* 6. h = up * act(gate) for the 32 outputs, then their Q8 block (vecmath.c:78-93, model.c:409-415) */

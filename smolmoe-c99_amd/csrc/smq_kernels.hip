@@ -2292,6 +2292,10 @@ int gemv_rows_per_tile(uint32_t nb, bool q5, uint32_t total_rows) {
     (void)total_rows;
     if (g_forced_rt) return g_forced_rt;
     const uint32_t cover = (q5 ? 512u : 256u) / nb;
+    /* Q8 rows of 129-256 blocks: 4 rows of chunks of 64 blocks, not 1 row in one chunk (the Qwen2.5-0.5B
+     * down projection, nb 152, in the decode step: fewer, fuller workgroups whose lane chains share no SIMD
+     * with other workgroups' products; 1,161 -> 1,170 tok/s, measured) */
+    if (!q5 && cover == 1) return 4;
     int rt = q5 ? 2 : 1;
     while (rt < 8 && (uint32_t)(rt * 2) <= cover) rt *= 2;
     return rt;

@@ -203,33 +203,198 @@ __global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     trip(k, std::false_type{}); /* my_steps >= 1: the last trip */
 }
 
-template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT, uint32_t D>
-hipError_t launch_ct_shape(GroupArgs &g, hipStream_t s) {
-    static int resident = 0;
+/* Wide rows (nb > CK_KC, 152 blocks = the 4864-wide down projection): the same coalesced pieces
+ * over K chunks of CK_KC blocks. A step is RT rows x one chunk (RT*9*CK_KC/4 contiguous-per-row
+ * pieces); the chain thread (row, lane) keeps its sum in a register across the chunks of a tile,
+ * so every lane chain still adds its row's blocks 0..nb-1 in order, and the lane tree and store
+ * follow the last chunk. The item's activation is staged once in LDS in the rows' own layout
+ * (dword 9b = block b's scale, 9b + 1.. its 32 int8), so the four dwords of a piece meet the four
+ * activation words of one 16-byte LDS read. */
+constexpr uint32_t CK_KC = 32;
+
+template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT>
+__global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gemv_ck(GroupArgs g) {
+    constexpr uint32_t KC = CK_KC;
+    constexpr uint32_t NCH = (NB + KC - 1) / KC;    /* chunks per row */
+    constexpr uint32_t KL = NB - (NCH - 1) * KC;    /* blocks of the last chunk */
+    static_assert(NB % 4 == 0 && NB > KC && KL % 4 == 0, "whole 16-byte pieces in every chunk");
+    constexpr uint32_t P = 9 * KC / 4, PL = 9 * KL / 4; /* pieces per row of a chunk, of the last */
+    constexpr uint32_t TCH = RT * P;
+    constexpr uint32_t SP = KC + (36 - KC % 32) % 32;
+    static_assert(SP % 32 == 4 && SP >= KC, "pitch 4 mod 32");
+    static_assert(TCH <= CPT * CT_NT, "each piece of a step has a thread slot");
+    using Buf = CtBuf<RT, SP>;
+    __shared__ __attribute__((aligned(16))) Buf buf[2];
+    __shared__ __attribute__((aligned(16))) uint32_t act[NB * 9];
+
+    const uint32_t tid = threadIdx.x;
+    const GroupItem &I = g.item[find_ct_item(g, blockIdx.x)];
+    const uint32_t rows = I.rows, tiles = (rows + RT - 1) / RT, wg = blockIdx.x - I.wg_begin;
+    const uint32_t t0 = (uint32_t)((uint64_t)tiles * wg / I.nwg), t1 = (uint32_t)((uint64_t)tiles * (wg + 1) / I.nwg);
+    const uint32_t my_steps = (t1 - t0) * NCH;
+    const unsigned char *wbase = I.w;
+    const size_t row_bytes = I.row_bytes;
+    const float *bias_p = I.bias, *xd = I.xd;
+    float *y = I.y;
+    const bool accum = I.accumulate != 0;
+
+    /* slot j: piece c = tid + j*CT_NT of a step (row c / P, piece c % P of the row's chunk);
+     * its dwords' LDS targets in a full chunk and in the last one (pieces past it go to the sink) */
+    uint32_t prow[CPT], ppc[CPT], dst[CPT][4], dstl[CPT][4], scale_mask = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < CPT; ++j) {
+        const uint32_t c = tid + j * CT_NT, cc = c < TCH ? c : 0, r = cc / P, pc = cc % P;
+        prow[j] = r;
+        ppc[j] = pc;
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+            const uint32_t k = 4 * pc + q, b = k / 9, f = k % 9;
+            if (f == 0) scale_mask |= 1u << (4 * j + q);
+            const uint32_t at = f == 0 ? (uint32_t)(offsetof(Buf, d) / 4) + r * SP + b
+                                       : (uint32_t)(offsetof(Buf, sf) / 4) + (r * 8 + f - 1) * SP + b;
+            const uint32_t sink = (uint32_t)(offsetof(Buf, sink) / 4) + (tid & 63u);
+            dst[j][q] = c < TCH ? at : sink;
+            dstl[j][q] = c < TCH && pc < PL ? at : sink;
+        }
+    }
+
+    /* step s = (tile t0 + s / NCH, chunk s % NCH); rows past the matrix re-read its last row and
+     * pieces past the last chunk its last piece (in bounds, never stored) */
+    auto load = [&](u4a (&w)[CPT], uint32_t step) __attribute__((always_inline)) {
+        const uint32_t tile = t0 + step / NCH, ch = step % NCH;
+        const uint32_t last = (rows - tile * RT < RT ? rows - tile * RT : RT) - 1;
+        const unsigned char *base = wbase + (size_t)tile * RT * row_bytes + (size_t)ch * KC * Q8_BYTES;
+#pragma unroll
+        for (uint32_t j = 0; j < CPT; ++j) {
+            const uint32_t r = prow[j] < last ? prow[j] : last;
+            const uint32_t pc = ch == NCH - 1 && ppc[j] >= PL ? PL - 1 : ppc[j];
+            w[j] = __builtin_nontemporal_load((const u4a *)(base + (size_t)r * row_bytes + 16 * pc));
+        }
+    };
+    const uint32_t cr = tid / 8, cl = tid % 8;
+    auto load_bp = [&](float &bias, float &prior, uint32_t tile) __attribute__((always_inline)) {
+        if constexpr (BP) {
+            const uint32_t orow = tile * RT + (cr < RT ? cr : 0), oc = orow < rows ? orow : rows - 1;
+            bias = *(bias_p ? bias_p + oc : xd);
+            prior = *(accum ? y + oc : xd);
+        }
+    };
+
+    float B = 0.0f, Pr = 0.0f;
+    load_bp(B, Pr, t0);
+    u4a W[CPT];
+    load(W, 0);
+    {
+        const uint32_t *xq32 = (const uint32_t *)I.xq;
+        for (uint32_t i = tid; i < NB * 9; i += CT_NT) {
+            const uint32_t b = i / 9, f = i % 9;
+            act[i] = f == 0 ? __float_as_uint(xd[b]) : xq32[8 * b + f - 1];
+        }
+    }
+    __syncthreads();
+
+    float acc = 0.0f;
+    for (uint32_t s = 0; s < my_steps; ++s) {
+        const uint32_t ch = s % NCH, tile = t0 + s / NCH;
+        const bool lastc = ch == NCH - 1;
+        float *lb = (float *)&buf[s & 1];
+#pragma unroll
+        for (uint32_t j = 0; j < CPT; ++j) {
+            const uint32_t pc = lastc && ppc[j] >= PL ? PL - 1 : ppc[j];
+            const u4a A = *(const u4a *)&act[ch * 9 * KC + 4 * pc];
+            const uint32_t wv[4] = {W[j].x, W[j].y, W[j].z, W[j].w}, av[4] = {A.x, A.y, A.z, A.w};
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q) {
+                const float fs = (float)dot4(wv[q], av[q], 0);
+                const float dv = __uint_as_float(wv[q]) * __uint_as_float(av[q]);
+                lb[lastc ? dstl[j][q] : dst[j][q]] = (scale_mask >> (4 * j + q)) & 1u ? dv : fs;
+            }
+        }
+        /* the next tile's bias and prior (older than the next weights, so no extra wait), then the
+         * next step's weights into the registers just consumed */
+        float Bn = B, Pn = Pr;
+        if (lastc && tid < RT * 8 && s + 1 < my_steps) load_bp(Bn, Pn, tile + 1);
+        if (s + 1 < my_steps) load(W, s + 1);
+        __syncthreads();
+        if (tid < RT * 8) {
+            const Buf &bb = buf[s & 1];
+            const float4 *sp = (const float4 *)&bb.sf[(cr * 8 + cl) * SP];
+            const float4 *dp = (const float4 *)&bb.d[cr * SP];
+            const uint32_t nq = (lastc ? KL : KC) / 4;
+#pragma unroll
+            for (uint32_t qq = 0; qq < KC / 4; ++qq) {
+                if (qq < nq) { /* uniform */
+                    const float4 sv = sp[qq], dv = dp[qq];
+                    if (FAST) {
+                        acc = __builtin_fmaf(dv.x, sv.x, acc);
+                        acc = __builtin_fmaf(dv.y, sv.y, acc);
+                        acc = __builtin_fmaf(dv.z, sv.z, acc);
+                        acc = __builtin_fmaf(dv.w, sv.w, acc);
+                    } else {
+                        float p;
+                        p = dv.x * sv.x; acc = acc + p;
+                        p = dv.y * sv.y; acc = acc + p;
+                        p = dv.z * sv.z; acc = acc + p;
+                        p = dv.w * sv.w; acc = acc + p;
+                    }
+                }
+            }
+            if (lastc) {
+                const float v = reduce8_to_lane7(acc);
+                const uint32_t row = tile * RT + cr;
+                if (cl == 7 && row < rows) {
+                    float o = v;
+                    if (bias_p) o = o + B; /* model.c:259-262 */
+                    if (g.flag && !(fabsf(o) <= FLT_MAX)) *g.flag = 1;
+                    if (accum) o = Pr + o;
+                    y[row] = o;
+                }
+                acc = 0.0f;
+            }
+        }
+        B = Bn;
+        Pr = Pn;
+    }
+}
+
+/* every item a share of the resident workgroups of kernel k in proportion to its tiles of rt rows
+ * (at least one, at most one per tile), each a contiguous tile range */
+hipError_t launch_tiles(const void *k, int &resident, uint32_t rt, GroupArgs &g, hipStream_t s) {
     if (!resident) {
         int per_cu = 0, dev = 0, cus = 0;
-        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemv_ct<FAST, BP, NB, RT, CPT, D>, CT_NT, 0);
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, CT_NT, 0);
         if (e == hipSuccess) e = hipGetDevice(&dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (e != hipSuccess) return e;
         resident = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
     }
     uint64_t tiles = 0;
-    for (uint32_t i = 0; i < g.nitems; ++i) tiles += (g.item[i].rows + RT - 1) / RT;
+    for (uint32_t i = 0; i < g.nitems; ++i) tiles += (g.item[i].rows + rt - 1) / rt;
     if (!tiles) return hipSuccess;
-    /* every item a share of the resident workgroups in proportion to its tiles (at least one,
-     * at most one per tile), each a contiguous tile range */
     uint32_t wgs = 0;
     for (uint32_t i = 0; i < g.nitems; ++i) {
-        const uint32_t t = (g.item[i].rows + RT - 1) / RT;
+        const uint32_t t = (g.item[i].rows + rt - 1) / rt;
         uint32_t n = (uint32_t)(((uint64_t)resident * t + tiles / 2) / tiles);
         n = n < 1 ? 1 : (n > t ? t : n);
         g.item[i].wg_begin = wgs;
         g.item[i].nwg = n;
         wgs += n;
     }
-    hipLaunchKernelGGL((k_gemv_ct<FAST, BP, NB, RT, CPT, D>), dim3(wgs), dim3(CT_NT), 0, s, g);
-    return hipGetLastError();
+    void *args[] = {&g};
+    const hipError_t e = hipLaunchKernel(k, dim3(wgs), dim3(CT_NT), args, 0, s);
+    return e != hipSuccess ? e : hipGetLastError();
+}
+
+template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT, uint32_t D>
+hipError_t launch_ct_shape(GroupArgs &g, hipStream_t s) {
+    static int resident = 0;
+    return launch_tiles((const void *)k_gemv_ct<FAST, BP, NB, RT, CPT, D>, resident, RT, g, s);
+}
+
+template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT>
+hipError_t launch_ck_shape(GroupArgs &g, hipStream_t s) {
+    static int resident = 0;
+    return launch_tiles((const void *)k_gemv_ck<FAST, BP, NB, RT, CPT>, resident, RT, g, s);
 }
 
 /* 16 rows of 28 blocks per step: 1008 pieces in 1024 thread slots; one tile in flight per
@@ -237,7 +402,9 @@ hipError_t launch_ct_shape(GroupArgs &g, hipStream_t s) {
  * two in flight, or 8- and 12-row tiles, were no faster) */
 template <bool FAST, bool BP>
 hipError_t launch_ct_bp(GroupArgs &g, hipStream_t s) {
-    return g.nb == 28 ? launch_ct_shape<FAST, BP, 28, 16, 2, 1>(g, s) : hipErrorInvalidValue;
+    if (g.nb == 28) return launch_ct_shape<FAST, BP, 28, 16, 2, 1>(g, s);
+    if (g.nb == 152) return launch_ck_shape<FAST, BP, 152, 14, 2>(g, s); /* 14 rows x 32-block chunks: 1008 pieces */
+    return hipErrorInvalidValue;
 }
 
 template <bool FAST>
@@ -250,7 +417,7 @@ hipError_t launch_ct_fast(GroupArgs &g, hipStream_t s) {
 }  // namespace
 
 bool gemv_ct_ok(const GroupArgs &g, bool q5) {
-    if (q5 || g.nb != 28) return false; /* 152-block rows: the pinned kernel measured faster */
+    if (q5 || (g.nb != 28 && g.nb != 152)) return false;
     for (uint32_t i = 0; i < g.nitems; ++i) {
         const GroupItem &it = g.item[i];
         if ((((uintptr_t)it.w) | it.row_bytes) & 15u) return false;

@@ -1648,7 +1648,7 @@ __global__ __launch_bounds__(AR_WG) __attribute__((amdgpu_waves_per_eu(1, 2))) v
  * stores the rotated k and the v row into the caches (model.c:511-526).
  * Workgroups past the current position leave at once (the grid covers the
  * context, so a captured step replays at any position). */
-constexpr uint32_t AS_WG = 256;
+constexpr uint32_t AS_WG = 512;
 constexpr uint32_t AS_SP = 32;                 /* positions per scores workgroup */
 constexpr uint32_t AS_MAXG = 16;               /* query heads per KV head */
 constexpr uint32_t MAX_SCORE_FLOATS = 1u << 22; /* the library's scores workspace: heads x context */
@@ -1674,9 +1674,11 @@ __global__ __launch_bounds__(AS_WG) void k_attend_scores(const float *q, float *
     const float *kbase = kcache + (size_t)start * kvd + (size_t)kh * AR_HD;
 
     /* loads: q of the group's heads, the table rows, this block's K rows (the current one from rr.k) */
-    float4 qx[AS_MAXG * AR_Q4 / AS_WG];
+    constexpr uint32_t QL = (AS_MAXG * AR_Q4 + AS_WG - 1) / AS_WG, KL = AS_SP * AR_Q4 / AS_WG;
+    static_assert(KL * AS_WG == AS_SP * AR_Q4, "whole K rows per load round");
+    float4 qx[QL];
 #pragma unroll
-    for (uint32_t u = 0; u < AS_MAXG * AR_Q4 / AS_WG; ++u) {
+    for (uint32_t u = 0; u < QL; ++u) {
         const uint32_t f = tid + u * AS_WG, hh = f / AR_Q4, c = f % AR_Q4;
         qx[u] = hh < grp ? *(const float4 *)(q + (size_t)(kh * grp + hh) * AR_HD + 4 * c) : make_float4(0, 0, 0, 0);
     }
@@ -1684,9 +1686,9 @@ __global__ __launch_bounds__(AS_WG) void k_attend_scores(const float *q, float *
     const uint32_t ri = tid, rhalf = ri < sh.pairs ? 0 : 1, rj = ri - rhalf * sh.pairs;
     const bool rload = ROPE && ri < 2 * sh.pairs;
     if (rload) rv = (rhalf ? rr.sn : rr.cs)[(size_t)pos * sh.pairs + rj];
-    float4 kx[AS_SP * AR_Q4 / AS_WG];
+    float4 kx[KL];
 #pragma unroll
-    for (uint32_t u = 0; u < AS_SP * AR_Q4 / AS_WG; ++u) {
+    for (uint32_t u = 0; u < KL; ++u) {
         const uint32_t f = tid + u * AS_WG, r = f / AR_Q4, c = f % AR_Q4, p = p0 + r;
         const float *src = (ROPE && p == last) ? rr.k + (size_t)kh * AR_HD : kbase + (size_t)(r < cnt ? p : p0) * kvd;
         kx[u] = *(const float4 *)(src + 4 * c);
@@ -1697,12 +1699,12 @@ __global__ __launch_bounds__(AS_WG) void k_attend_scores(const float *q, float *
     if (ROPE) __syncthreads(); /* the table rows */
     const float *crow = ROPE ? rtab : nullptr, *srow = ROPE ? rtab + AR_HD / 2 : nullptr;
 #pragma unroll
-    for (uint32_t u = 0; u < AS_MAXG * AR_Q4 / AS_WG; ++u) {
+    for (uint32_t u = 0; u < QL; ++u) {
         const uint32_t f = tid + u * AS_WG, hh = f / AR_Q4, c = f % AR_Q4;
         if (hh < grp) *(float4 *)&qs[hh * AR_HD + 4 * c] = ROPE ? rope4(qx[u], c, sh.pairs, crow, srow) : qx[u];
     }
 #pragma unroll
-    for (uint32_t u = 0; u < AS_SP * AR_Q4 / AS_WG; ++u) {
+    for (uint32_t u = 0; u < KL; ++u) {
         const uint32_t f = tid + u * AS_WG, r = f / AR_Q4, c = f % AR_Q4, p = p0 + r;
         if (r < cnt) {
             float4 x = kx[u];
@@ -1715,16 +1717,31 @@ __global__ __launch_bounds__(AS_WG) void k_attend_scores(const float *q, float *
     }
     __syncthreads();
 
-    /* (position, head) pairs: dot_f32 of kernels.c:1119-1127, lane tree, times 1/sqrt(hd) */
+    /* (position, head) pairs: dot_f32 of kernels.c:1119-1127, lane tree, times 1/sqrt(hd). Two
+     * adjacent threads per pair: thread half h keeps lanes 4h..4h+3 (element 8e + l added over e in
+     * order, one 16-byte read of k and of q per e), then the even thread takes the odd one's four
+     * lanes and forms the tree */
     const float factor = 1.0f / sqrtf((float)AR_HD);
-    for (uint32_t i = tid; i < cnt * grp; i += AS_WG) {
-        const uint32_t r = i % cnt, hh = i / cnt;
-        DotAcc acc = {{0, 0, 0, 0, 0, 0, 0, 0}};
-        dot_groups(acc, (const float4 *)&kt[r * AR_KP], (const float4 *)&qs[hh * AR_HD], 0, AR_HD / 8);
-        const float p04 = acc.a[0] + acc.a[4], p15 = acc.a[1] + acc.a[5], p26 = acc.a[2] + acc.a[6],
-                    p37 = acc.a[3] + acc.a[7];
-        const float e2 = p04 + p26, o2 = p15 + p37;
-        scores[(size_t)(kh * grp + hh) * sh.context + p0 + r] = (e2 + o2) * factor;
+    for (uint32_t i = tid; i < 2 * cnt * grp; i += AS_WG) { /* pairs of lanes stay together */
+        const uint32_t d = i / 2, half = i & 1u, r = d % cnt, hh = d / cnt;
+        const float4 *kr = (const float4 *)&kt[r * AR_KP], *q4 = (const float4 *)&qs[hh * AR_HD];
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+        for (uint32_t e = 0; e < AR_HD / 8; ++e) {
+            const float4 kv = kr[2 * e + half], qv = q4[2 * e + half];
+            float p;
+            p = qv.x * kv.x; a0 = a0 + p;
+            p = qv.y * kv.y; a1 = a1 + p;
+            p = qv.z * kv.z; a2 = a2 + p;
+            p = qv.w * kv.w; a3 = a3 + p;
+        }
+        const float b0 = __shfl_xor(a0, 1, 64), b1 = __shfl_xor(a1, 1, 64), b2 = __shfl_xor(a2, 1, 64),
+                    b3 = __shfl_xor(a3, 1, 64);
+        if (!half) {
+            const float p04 = a0 + b0, p15 = a1 + b1, p26 = a2 + b2, p37 = a3 + b3;
+            const float e2 = p04 + p26, o2 = p15 + p37;
+            scores[(size_t)(kh * grp + hh) * sh.context + p0 + r] = (e2 + o2) * factor;
+        }
     }
 }
 

@@ -281,6 +281,18 @@ smq_status smq_attention_q8(const float *q, const float *keys, const float *valu
 smq_status smq_attention_rope_q8(float *q, float *k, const float *v, const smq_attn_shape *shape,
                                  const float *cos_table, const float *sin_table, float *keys, float *values,
                                  float *att, uint32_t pos0, const int32_t *pos_dev, float *xd, int8_t *xq);
+/* The q, k, v matmuls of one decoding token (items[0..2], rows q_dim, kv_dim,
+ * kv_dim, no accumulate) with the activation `act`, followed by RoPE and the
+ * cache store (model.c:496-526): the same results as smq_matmul_act then
+ * smq_rope_kv(items[0].y, items[1].y, items[2].y, 1, ...), i.e. q and k rotated
+ * by the position's table rows (model.c:442-450) in their outputs, and the
+ * rotated k and the v row written into keys/values at the position (pos_dev if
+ * not NULL, else pos0). Q8 rows of 28 blocks with an RMSNorm activation do it in
+ * one launch. No reference counterpart of its own: it fuses the two calls above,
+ * each of which has one. */
+smq_status smq_matmul_act_rope(const smq_mat_item *items, const smq_act *act, const smq_attn_shape *shape,
+                               const float *cos_table, const float *sin_table, float *keys, float *values,
+                               uint32_t pos0, const int32_t *pos_dev);
 /* sampler.c:57-63: *token = first non-banned id, replaced by any later
  * non-banned id with a strictly greater logit (NaN never wins unless it is
  * the first candidate). banned may be NULL. UINT32_MAX if every id is banned. */

@@ -103,6 +103,8 @@ _SIGS = {
     "smq_matmul": (ctypes.c_int, [ctypes.POINTER(_MatItem), _u32, _vp, _vp, _u32]),
     "smq_numeric_check": (ctypes.c_int, []),
     "smq_matmul_act": (ctypes.c_int, [ctypes.POINTER(_MatItem), _u32, ctypes.POINTER(_Act)]),
+    "smq_matmul_act_rope": (ctypes.c_int, [ctypes.POINTER(_MatItem), ctypes.POINTER(_Act), ctypes.POINTER(_AttnShape),
+                                           _vp, _vp, _vp, _vp, _u32, _vp]),
     "smq_matmul_glu": (ctypes.c_int, [ctypes.POINTER(_QMat), ctypes.POINTER(_QMat), ctypes.POINTER(_Act), ctypes.c_int,
                                       _vp, _vp]),
     "smq_matmul_glu_q8": (ctypes.c_int, [ctypes.POINTER(_QMat), ctypes.POINTER(_QMat), ctypes.POINTER(_Act),
@@ -410,6 +412,13 @@ def matmul_act(items, activation):
     """smq_matmul_act: one token, the activation formed in the matmul's launch."""
     arr, _keep = _items(items)
     _check(load().smq_matmul_act(arr, len(items), ctypes.byref(activation)))
+
+
+def matmul_act_rope(items, activation, shape, cos_table, sin_table, keys, values, pos0=0, pos_dev=None):
+    """smq_matmul_act_rope: the q, k, v matmuls of one token, then RoPE and the cache store."""
+    arr, _keep = _items(items)
+    _check(load().smq_matmul_act_rope(arr, ctypes.byref(activation), ctypes.byref(shape), _p(cos_table),
+                                      _p(sin_table), _p(keys), _p(values), pos0, _p(pos_dev)))
 
 
 def matmul_glu(gate, up, activation, glu, h, gate_scratch=None):

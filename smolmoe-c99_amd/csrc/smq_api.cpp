@@ -836,7 +836,8 @@ smq_status smq_attention(const float *q, const float *keys, const float *values,
         !extent_ok(keys, cache, "keys") || !extent_ok(values, cache, "values") ||
         !extent_ok(pos_dev, pos_dev ? 4 : 0, "pos"))
         return t_status;
-    return hip_ok(smq::launch_attention(q, keys, values, att, ntok, sh, pos0, pos_dev, g.flag, nullptr, nullptr, g.cur),
+    return hip_ok(smq::launch_attention(q, keys, values, att, ntok, sh, pos0, pos_dev, g.flag, nullptr, nullptr, g.cur,
+                                        g.scores),
                   "attention")
                ? SMQ_OK
                : t_status;
@@ -858,12 +859,13 @@ smq_status smq_attention_q8(const float *q, const float *keys, const float *valu
         !extent_ok(xq, ntok * nbq * smq::QK, "xq"))
         return t_status;
     if (sh.head_dim % smq::QK == 0) /* each head owns whole blocks: quantized in the same kernel */
-        return hip_ok(smq::launch_attention(q, keys, values, att, ntok, sh, pos0, pos_dev, g.flag, xd, xq, g.cur),
+        return hip_ok(smq::launch_attention(q, keys, values, att, ntok, sh, pos0, pos_dev, g.flag, xd, xq, g.cur,
+                                            g.scores),
                       "attention_q8")
                    ? SMQ_OK
                    : t_status;
     return hip_ok(smq::launch_attention(q, keys, values, att, ntok, sh, pos0, pos_dev, g.flag, nullptr, nullptr,
-                                        g.cur),
+                                        g.cur, g.scores),
                   "attention_q8") &&
                    hip_ok(smq::launch_quantize_q8(att, ntok, sh.q_dim, xd, xq, g.flag, g.cur), "attention_q8")
                ? SMQ_OK
@@ -896,6 +898,67 @@ smq_status smq_attention_rope_q8(float *q, float *k, const float *v, const smq_a
     /* other shapes: the two-step form (q and k are left rotated) */
     if (smq_rope_kv(q, k, v, 1, shape, cos_table, sin_table, keys, values, pos0, pos_dev) != SMQ_OK) return t_status;
     return smq_attention_q8(q, keys, values, att, 1, shape, pos0, pos_dev, xd, xq);
+}
+
+smq_status smq_matmul_act_rope(const smq_mat_item *items, const smq_act *act, const smq_attn_shape *shape,
+                               const float *cos_table, const float *sin_table, float *keys, float *values,
+                               uint32_t pos0, const int32_t *pos_dev) {
+    if (!ready()) return t_status;
+    smq::AttnShape sh;
+    if (!attn_shape(shape, &sh, "matmul_act_rope")) return t_status;
+    if (!items || !items[0].w || !items[1].w || !items[2].w)
+        return set_status(SMQ_ERR_RANGE, "matmul_act_rope: items q, k and v need matrices");
+    if (items[0].w->rows != sh.q_dim || items[1].w->rows != sh.kv_dim || items[2].w->rows != sh.kv_dim)
+        return set_status(SMQ_ERR_RANGE, "matmul_act_rope: q, k, v rows %u, %u, %u against q_dim %u, kv_dim %u",
+                          items[0].w->rows, items[1].w->rows, items[2].w->rows, sh.q_dim, sh.kv_dim);
+    if (items[0].accumulate || items[1].accumulate || items[2].accumulate)
+        return set_status(SMQ_ERR_RANGE, "matmul_act_rope: q, k and v do not accumulate");
+    if (!pos_dev && pos0 >= sh.context) return set_status(SMQ_ERR_RANGE, "token batch exceeds context");
+    const size_t table = (size_t)sh.context * sh.pairs * 4, cache = (size_t)sh.context * sh.kv_dim * 4;
+    if (!extent_ok(cos_table, table, "cos table") || !extent_ok(sin_table, table, "sin table") ||
+        !extent_ok(keys, cache, "keys") || !extent_ok(values, cache, "values") ||
+        !extent_ok(pos_dev, pos_dev ? 4 : 0, "pos"))
+        return t_status;
+    const smq_qmat *w0 = items[0].w;
+    bool fused = !g.fast && act && act->kind == SMQ_ACT_NORM && act_ok(act, w0->cols, "matmul_act_rope");
+    for (uint32_t i = 0; i < 3 && fused; ++i) {
+        const smq_qmat *w = items[i].w;
+        fused = w->dtype == 1 && w->nb == w0->nb && w->cols == w0->cols && w->nb == (w->cols + smq::QK - 1) / smq::QK &&
+                extent_ok(w->data, (size_t)(w->rows - 1) * w->row_bytes + (size_t)w->nb * smq::Q8_BYTES, "weights") &&
+                extent_ok(items[i].y, (size_t)w->rows * 4, "output") &&
+                extent_ok(items[i].bias, items[i].bias ? (size_t)w->rows * 4 : 0, "bias");
+    }
+    if (fused) {
+        smq::FusedArgs f;
+        memset(&f, 0, sizeof(f));
+        f.nb = w0->nb;
+        fused_act(f, act);
+        for (uint32_t i = 0; i < 3; ++i) {
+            smq::Item &it = f.item[f.nitems++];
+            it.w = items[i].w->data;
+            it.row_bytes = items[i].w->row_bytes;
+            it.bias = items[i].bias;
+            it.y = items[i].y;
+            it.y_stride = items[i].w->rows;
+            it.rows = items[i].w->rows;
+        }
+        f.rope.cs = cos_table;
+        f.rope.sn = sin_table;
+        f.rope.kcache = keys;
+        f.rope.vcache = values;
+        f.rope.pos_dev = pos_dev;
+        f.rope.pos0 = pos0;
+        f.rope.head_dim = sh.head_dim;
+        f.rope.pairs = sh.pairs;
+        f.rope.kv_dim = sh.kv_dim;
+        f.rope.context = sh.context;
+        if (smq::decode_ct_ok(f, false, act->kind, false))
+            return hip_ok(smq::launch_decode_ct(f, act->kind, false, g.cur), "matmul_act_rope") ? SMQ_OK : t_status;
+    }
+    /* other layouts: the matmuls, then RoPE and the cache store (the same results) */
+    if (smq_matmul_act(items, 3, act) != SMQ_OK) return t_status;
+    return smq_rope_kv(items[0].y, items[1].y, items[2].y, 1, shape, cos_table, sin_table, keys, values, pos0,
+                       pos_dev);
 }
 
 smq_status smq_argmax(const float *logits, uint32_t vocab, const unsigned char *banned, uint32_t *token) {

@@ -9,7 +9,12 @@
  *  PRO_F32   the Q8 blocks of the f32 row x;
  *  EPI_STORE each item's rows + bias, finiteness, y or y += result;
  *  EPI_GLU   gate and up rows of 32 outputs h = up*act(gate) (SwiGLU or
- *            GeGLU), their finiteness, and h's Q8 block (silu_quantize).
+ *            GeGLU), their finiteness, and h's Q8 block (silu_quantize);
+ *  ROPE      (STORE, items q, k, v of one token) after bias and finiteness,
+ *            q and k rows rotated by the position's table row (model.c:442-450;
+ *            a row meets its pair partner, the next chain group's row, by a
+ *            lane exchange), and k and v also stored into the caches at the
+ *            position (model.c:511-526).
  * Every result is bit-identical to the unfused calls.
  *
  * Layout: a workgroup owns RT rows (STORE: a 16-row tile of one item; GLU: 32
@@ -56,7 +61,7 @@ struct DcLds {
     int bad;
 };
 
-template <bool GLU, int PRO, uint32_t NB, uint32_t RT, uint32_t CPT>
+template <bool GLU, int PRO, uint32_t NB, uint32_t RT, uint32_t CPT, bool ROPE = false>
 __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
     static_assert(NB % 4 == 0 && NB * 8 <= DC_NT, "packed rows of whole 16-byte pieces; four elements per thread");
     constexpr uint32_t NQ = NB * 8;        /* threads holding four activation elements */
@@ -68,6 +73,7 @@ __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
     static_assert((RT * 9 * SP) % 4 == 0, "the activation row starts 16-byte aligned");
     static_assert(RT == CPT * RG, "the tile is CPT slabs of RG rows");
     static_assert(!GLU || (RT == 64 && 32 % RG == 0), "GLU: 32 gate and 32 up rows, a slab in one of them");
+    static_assert(!(ROPE && GLU) && RT % 2 == 0, "ROPE: a STORE tile holds whole pairs of rows");
     using Lds = DcLds<NB, RT, SP>;
     __shared__ __attribute__((aligned(16))) Lds L;
 
@@ -142,6 +148,21 @@ __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
         if (tid < 32) ev = EXP2_TABLE[tid];
     } else {
         if (tid < RT * 8 && cl == 7 && r0 + cr < It.rows) pre = load_out(It, 0, r0 + cr);
+    }
+    /* ROPE: the item's role (0 q, 1 k, 2 v), the position, this row's table entries */
+    uint32_t role = 0, rpos = 0;
+    bool rok = false;
+    float rc = 0.0f, rs = 0.0f;
+    if constexpr (ROPE) {
+        role = blockIdx.x >= a.item[2].tile_begin ? 2u : (blockIdx.x >= a.item[1].tile_begin ? 1u : 0u);
+        rpos = a.rope.pos_dev ? (uint32_t)*a.rope.pos_dev : a.rope.pos0;
+        rok = rpos < a.rope.context;
+        const uint32_t pr = ((r0 + cr) % a.rope.head_dim) / 2;
+        if (role < 2 && tid < RT * 8 && cl == 7 && pr < a.rope.pairs) {
+            const size_t at = (size_t)(rok ? rpos : 0) * a.rope.pairs + pr;
+            rc = a.rope.cs[at];
+            rs = a.rope.sn[at];
+        }
     }
     u4a W[CPT];
     auto fetch = [&]() {
@@ -247,6 +268,30 @@ __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
 
     if constexpr (!GLU) {
         const uint32_t row = r0 + cr;
+        if constexpr (ROPE) {
+            const bool mine = tid < RT * 8 && cl == 7 && row < It.rows;
+            float x = v;
+            if (It.bias) x = x + pre.bias; /* model.c:259-262 */
+            if (mine && a.flag && !(fabsf(x) <= FLT_MAX)) *a.flag = 1;
+            const float xp = __shfl_xor(x, 8, 64); /* the pair partner's row (row ^ 1), every lane */
+            if (mine) {
+                const uint32_t j = row % a.rope.head_dim;
+                float o = x;
+                if (role < 2 && rok && j / 2 < a.rope.pairs) { /* rope4's ac - bs and as + bc */
+                    if (j & 1u) {
+                        const float as = xp * rs, bc = x * rc;
+                        o = as + bc;
+                    } else {
+                        const float ac = x * rc, bs = xp * rs;
+                        o = ac - bs;
+                    }
+                }
+                It.y[row] = o;
+                if (role > 0 && rok) (role == 1 ? a.rope.kcache : a.rope.vcache)[(size_t)rpos * a.rope.kv_dim + row] = o;
+            }
+            if (!rok && tid == 0 && a.flag) *a.flag = 1; /* the position is past the context */
+            return;
+        }
         if (tid < RT * 8 && cl == 7 && row < It.rows) store_out_pre(It, a.flag, 0, row, v, pre);
         return;
     } else {
@@ -291,7 +336,7 @@ __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
     }
 }
 
-template <bool GLU, int PRO>
+template <bool GLU, int PRO, bool ROPE = false>
 hipError_t launch_dec(FusedArgs a, hipStream_t s) {
     constexpr uint32_t RT = GLU ? 64 : 16;
     constexpr uint32_t CPT = RT / (DC_NT / 63); /* slabs of 16 rows (63 pieces each) */
@@ -305,13 +350,22 @@ hipError_t launch_dec(FusedArgs a, hipStream_t s) {
         }
     }
     if (!blocks) return hipSuccess;
-    hipLaunchKernelGGL((k_decode_ct<GLU, PRO, 28, RT, CPT>), dim3(blocks), dim3(DC_NT), 0, s, a);
+    hipLaunchKernelGGL((k_decode_ct<GLU, PRO, 28, RT, CPT, ROPE>), dim3(blocks), dim3(DC_NT), 0, s, a);
     return hipGetLastError();
 }
 
 }  // namespace
 
 bool decode_ct_ok(const FusedArgs &a, bool q5, int pro, bool glu) {
+    if (a.rope.kcache) { /* items q, k, v; whole heads of an even width; every row's pair in its tile */
+        const RopeStore &r = a.rope;
+        if (glu || pro != DPRO_NORM || a.nitems != 3 || !r.head_dim || r.head_dim % 2 || 2 * r.pairs > r.head_dim ||
+            a.item[1].rows != r.kv_dim || a.item[2].rows != r.kv_dim || r.kv_dim % r.head_dim ||
+            a.item[0].rows % r.head_dim)
+            return false;
+        for (uint32_t i = 0; i < 3; ++i)
+            if (a.item[i].accumulate) return false;
+    }
     if (q5 || a.nb != 28 || a.n > 28 * QK || a.n + QK <= 28 * QK || (pro != DPRO_NORM && pro != DPRO_F32)) return false;
     if (a.n % 4 || ((uintptr_t)a.src & 15u) || (pro == DPRO_NORM && ((uintptr_t)a.norm & 15u))) return false;
     if (glu && (!a.hd || !a.hq || a.nitems != 2 || ((uintptr_t)a.hd & 3u))) return false;
@@ -323,6 +377,8 @@ bool decode_ct_ok(const FusedArgs &a, bool q5, int pro, bool glu) {
 }
 
 hipError_t launch_decode_ct(const FusedArgs &a, int pro, bool glu, hipStream_t s) {
+    if (a.rope.kcache) /* decode_ct_ok admitted: pro RMSNorm, no glu */
+        return pro == DPRO_NORM && !glu ? launch_dec<false, DPRO_NORM, true>(a, s) : hipErrorInvalidValue;
     if (glu) return pro == DPRO_NORM ? launch_dec<true, DPRO_NORM>(a, s) : launch_dec<true, DPRO_F32>(a, s);
     return pro == DPRO_NORM ? launch_dec<false, DPRO_NORM>(a, s) : launch_dec<false, DPRO_F32>(a, s);
 }

@@ -77,6 +77,14 @@ hipError_t launch_gemv_grouped(GroupArgs &g, bool q5, bool fast, hipStream_t s);
  * even nb for Q5, n <= MAX_NORM_K for RMSNorm. The exact contract only (the
  * fast one takes the unfused calls). */
 constexpr uint32_t MAX_NORM_K = 8192;
+/* Decode QKV store with RoPE (items q, k, v of one token): q and k rows rotated by the position's
+ * table row, q, k and v stored to their items and k and v also into the caches at the position. */
+struct RopeStore {
+    const float *cs, *sn;   /* [context][pairs] */
+    float *kcache, *vcache; /* [context][kv_dim] */
+    const int32_t *pos_dev; /* the position, else pos0 */
+    uint32_t pos0, head_dim, pairs, kv_dim, context;
+};
 struct FusedArgs {
     Item item[MAX_ITEMS];
     uint32_t nitems, nb, n;
@@ -90,6 +98,7 @@ struct FusedArgs {
     uint32_t rows;
     int act;
     int *flag;
+    RopeStore rope; /* rope.kcache set: the decode QKV store with RoPE */
 };
 bool fused_layout_ok(const FusedArgs &a, bool q5, int pro);
 /* Decode matmuls on packed 28-block Q8 rows with the activation formed in the launch and,
@@ -149,7 +158,8 @@ hipError_t launch_rope_kv(float *q, float *k, const float *v, uint32_t ntok, con
                           int *flag, hipStream_t s);
 hipError_t launch_attention(const float *q, const float *kcache, const float *vcache, float *att, uint32_t ntok,
                             const AttnShape &sh, uint32_t pos0, const int32_t *pos_dev, int *flag, float *xd,
-                            int8_t *xq, hipStream_t s);
+                            int8_t *xq, hipStream_t s,
+                            float *scores = nullptr);
 /* One decoding token: RoPE of q and k, the cache store of k and v, and
  * attention (+ Q8 of the row) in one launch; q/k/v are the unrotated QKV
  * outputs. Needs attention_rows_ok (head_dim 64, 16-byte aligned q and

@@ -2416,12 +2416,25 @@ bool attention_rows_ok(const AttnShape &sh, const void *q, const void *kcache, c
 
 hipError_t launch_attention(const float *q, const float *kcache, const float *vcache, float *att, uint32_t ntok,
                             const AttnShape &sh, uint32_t pos0, const int32_t *pos_dev, int *flag, float *xd,
-                            int8_t *xq, hipStream_t s) {
+                            int8_t *xq, hipStream_t s, float *scores) {
     if (!ntok) return hipSuccess;
     if (sh.context > MAX_ATT_POSITIONS || sh.head_dim > MAX_HEAD_DIM || sh.head_dim < 1 ||
         (xd && sh.head_dim % QK))
         return hipErrorInvalidValue;
     const uint32_t groups = (sh.head_dim + ATT_JW - 1) / ATT_JW;
+    if (ntok == 1 && scores && attention_rows_ok(sh, q, kcache, vcache) &&
+        (size_t)sh.heads * sh.context <= MAX_SCORE_FLOATS && sh.heads / sh.kv_heads <= AS_MAXG) {
+        /* one decoding token whose q is rotated and whose k and v rows are in the caches already:
+         * the scores spread over workgroups of positions, then the values */
+        const size_t lds = (((size_t)sh.context + 3) / 4 * 4 + (size_t)AR_FIXED) * sizeof(float);
+        const RopeRows none = {nullptr, nullptr, nullptr, nullptr};
+        const dim3 sgrid((sh.context + AS_SP - 1) / AS_SP, sh.kv_heads);
+        hipLaunchKernelGGL(k_attend_scores<false>, sgrid, dim3(AS_WG), 0, s, q, (float *)kcache, (float *)vcache, sh,
+                           pos0, pos_dev, flag, none, scores);
+        hipLaunchKernelGGL(k_attend_values<false>, dim3(sh.heads * groups), dim3(AR_WG), lds, s, vcache, att, sh, pos0,
+                           pos_dev, xd, xq, nullptr, scores, flag);
+        return hipGetLastError();
+    }
     if (ntok > 1 && attention_rows_ok(sh, q, kcache, vcache) && sh.context <= AG_MAXP &&
         sh.heads % sh.kv_heads == 0 && sh.heads / sh.kv_heads <= AG_MAXG && g_att_grouped) {
         hipLaunchKernelGGL(k_attend_group, dim3(ntok * sh.kv_heads), dim3(AG_WG), 0, s, q, kcache, vcache, att, sh, pos0,
@@ -2451,6 +2464,7 @@ hipError_t prepare_attention_attributes() {
         hipFuncSetAttribute((const void *)k_attend_rows<false>, hipFuncAttributeMaxDynamicSharedMemorySize, rows),
         hipFuncSetAttribute((const void *)k_attend_rows<true>, hipFuncAttributeMaxDynamicSharedMemorySize, rows),
         hipFuncSetAttribute((const void *)k_attend_values<true>, hipFuncAttributeMaxDynamicSharedMemorySize, rows),
+        hipFuncSetAttribute((const void *)k_attend_values<false>, hipFuncAttributeMaxDynamicSharedMemorySize, rows),
         hipFuncSetAttribute((const void *)k_attend, hipFuncAttributeMaxDynamicSharedMemorySize, tiled)};
     for (hipError_t e : es)
         if (e != hipSuccess) return e;

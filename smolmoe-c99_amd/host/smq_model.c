@@ -855,17 +855,16 @@ static smq_status attention_block(smq_model *m, uint32_t l, uint32_t n, uint32_t
     qkv[0] = mat(&L->q, L->q_bias, m->q, 0);
     qkv[1] = mat(&L->k, L->k_bias, m->k, 0);
     qkv[2] = mat(&L->v, L->v_bias, m->v, 0);
-    if (n == 1) { /* decode: the RMSNorm and its Q8 blocks inside the QKV launch */
+    if (n == 1) { /* decode: the RMSNorm and its Q8 blocks inside the QKV launch, RoPE and the cache store in
+                   * its store, then attention over the caches */
         smq_act act = norm_act(m, m->x, L->attn_norm);
-        TRY(smq_matmul_act(qkv, 3, &act));
+        TRY(smq_matmul_act_rope(qkv, &act, &m->shape, m->rope_cos, m->rope_sin, m->keys + base, m->values + base,
+                                pos0, pos_dev));
+        TRY(smq_attention_q8(m->q, m->keys + base, m->values + base, m->att, 1, &m->shape, pos0, pos_dev, m->xd,
+                             m->xq));
     } else {
         TRY(smq_norm_quantize(m->x, L->attn_norm, m->c.eps, n, m->c.dim, NULL, m->xd, m->xq));
         TRY(smq_matmul(qkv, 3, m->xd, m->xq, n));
-    }
-    if (n == 1) { /* decode: rotation, cache store and attention in one launch */
-        TRY(smq_attention_rope_q8(m->q, m->k, m->v, &m->shape, m->rope_cos, m->rope_sin, m->keys + base,
-                                  m->values + base, m->att, pos0, pos_dev, m->xd, m->xq));
-    } else {
         TRY(smq_rope_kv(m->q, m->k, m->v, n, &m->shape, m->rope_cos, m->rope_sin, m->keys + base, m->values + base,
                         pos0, pos_dev));
         TRY(smq_attention_q8(m->q, m->keys + base, m->values + base, m->att, n, &m->shape, pos0, pos_dev, m->xd,

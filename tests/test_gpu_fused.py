@@ -249,3 +249,70 @@ def test_fused_argument_errors():
     u = smq.QMat(dev(synth.q8_weights(914, 9, 64)), 9, 64)
     with pytest.raises(smq.SmqError):  # gate and up differ in rows
         smq.matmul_glu(g, u, smq.act(smq.ACT_NORM, 64, x=x, norm=x), 1, y)
+
+
+@pytest.mark.parametrize("cols,heads,kv_heads,hd,pairs,dtype,context,pos,use_pos_dev", [
+    (896, 14, 2, 64, 32, Q8, 64, 37, True),     # Qwen2.5-0.5B q/k/v: one fused launch, position on the device
+    (896, 14, 2, 64, 32, Q8, 64, 63, False),    # the last cache slot, position by value
+    (896, 4, 2, 64, 12, Q8, 40, 5, True),       # partial rotary: the tail of each head passes through
+    (100, 2, 1, 32, 16, Q8, 16, 9, False),      # 4-block rows: the matmul, then RoPE and the store
+    (896, 2, 1, 64, 32, Q5, 16, 3, True),       # Q5 weights: the same two calls
+])
+def test_matmul_act_rope(orc, cols, heads, kv_heads, hd, pairs, dtype, context, pos, use_pos_dev):
+    """smq_matmul_act_rope == RMSNorm + Q8 (row_work), q/k/v mat_item with bias,
+    then rope (model.c:442-450) and the cache store of k and v at the position
+    (oracle), bit for bit; the other cache rows untouched."""
+    say("matmul_act_rope", cols, heads, kv_heads, hd, pairs, dtype, context, pos, use_pos_dev)
+    qd, kd = heads * hd, kv_heads * hd
+    x = synth.normal(951 + cols, cols)
+    nw = synth.normal(952 + cols, cols, 0.2) + 1.0
+    ok, _, d, q = orc.row_work(x, 1, cols, norm=nw, eps=1e-6)
+    assert ok
+    mats, items = [], []
+    for i, r in enumerate((qd, kd, kd)):
+        wt = weights(953 + i, r, cols, dtype)
+        bias = synth.normal(956 + i, r, 0.02)
+        mats.append((wt, r, dtype, bias, None))
+        items.append((smq.QMat(dev(wt), r, cols, dtype), dev(bias), smq.DeviceBuffer(r * 4), False))
+    cs = synth.normal(960, context * pairs).reshape(context, pairs)
+    sn = synth.normal(961, context * pairs).reshape(context, pairs)
+    keys0 = synth.normal(962, context * kd).reshape(context, kd)
+    values0 = synth.normal(963, context * kd).reshape(context, kd)
+    keys, values = dev(keys0), dev(values0)
+    shape = smq.attn_shape(heads, kv_heads, hd, pairs, 0, context)
+    pos_dev = dev(np.array([pos], np.int32)) if use_pos_dev else None
+    smq.matmul_act_rope(items, smq.act(smq.ACT_NORM, cols, x=dev(x), norm=dev(nw), eps=1e-6,
+                                       xd_scratch=smq.DeviceBuffer((cols + 31) // 32 * 4),
+                                       xq_scratch=smq.DeviceBuffer((cols + 31) // 32 * 32)),
+                        shape, dev(cs), dev(sn), keys, values, 0 if use_pos_dev else pos, pos_dev)
+    smq.numeric_check()
+    wq, wk, wv = expect_items(orc, mats, d, q, cols)
+    wq = orc.rope(wq, heads, hd, pairs, cs[pos], sn[pos])
+    wk = orc.rope(wk, kv_heads, hd, pairs, cs[pos], sn[pos])
+    want_keys, want_values = keys0.copy(), values0.copy()
+    want_keys[pos], want_values[pos] = wk, wv
+    assert_same_f32(items[0][2].download(np.float32), wq, "q")
+    assert_same_f32(items[1][2].download(np.float32), wk, "k")
+    assert_same_f32(items[2][2].download(np.float32), wv, "v")
+    assert_same_f32(keys.download(np.float32).reshape(context, kd), want_keys, "keys")
+    assert_same_f32(values.download(np.float32).reshape(context, kd), want_values, "values")
+
+
+def test_matmul_act_rope_position_past_context():
+    """A device position at the context: the numeric flag, and no cache row written."""
+    cols, heads, kv_heads, hd, context = 896, 14, 2, 64, 8
+    qd, kd = heads * hd, kv_heads * hd
+    items = [(smq.QMat(dev(synth.q8_weights(970 + i, r, cols)), r, cols), None, smq.DeviceBuffer(r * 4), False)
+             for i, r in enumerate((qd, kd, kd))]
+    keys0 = synth.normal(975, context * kd)
+    keys, values = dev(keys0), dev(keys0)
+    table = dev(synth.normal(976, context * 32))
+    x = dev(synth.normal(977, cols))
+    smq.matmul_act_rope(items, smq.act(smq.ACT_NORM, cols, x=x, norm=x), smq.attn_shape(heads, kv_heads, hd, 32, 0,
+                                                                                        context),
+                        table, table, keys, values, 0, dev(np.array([context], np.int32)))
+    with pytest.raises(smq.SmqError) as e:
+        smq.numeric_check()
+    assert e.value.status == smq.SM_ERR_NUMERIC
+    assert_same_f32(keys.download(np.float32), keys0, "keys")
+    assert_same_f32(values.download(np.float32), keys0, "values")

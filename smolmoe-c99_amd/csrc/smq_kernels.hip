@@ -134,8 +134,11 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
 
         if (tid < RT * 8) {
             const uint32_t count = nb - c * CB < (uint32_t)CB ? nb - c * CB : (uint32_t)CB;
-            chain_sum<FAST, CB / 4>(acc, (const float4 *)pb + tid, GS / 4,
-                                    FAST ? (const float4 *)dsc[c & 1] + tid / 8 : nullptr, DS / 4, count);
+            const float4 *pp = (const float4 *)pb + tid, *dp = FAST ? (const float4 *)dsc[c & 1] + tid / 8 : nullptr;
+            if (CB <= 32 && count % 4 == 0) /* whole groups: plain adds, the groups past count added as zeros */
+                chain_sum_padded<FAST, CB / 4 <= 8 ? CB / 4 : 8>(acc, pp, GS / 4, dp, DS / 4, count / 4);
+            else
+                chain_sum<FAST, CB / 4>(acc, pp, GS / 4, dp, DS / 4, count);
         }
     }
 

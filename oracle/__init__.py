@@ -83,6 +83,7 @@ class Oracle:
         lib.orc_dot_r4.argtypes = [ctypes.c_int, ctypes.c_int, _u8p, _sz, _f32p, _i8p, _u32, _f32p]
         lib.orc_gemm.argtypes = [ctypes.c_int, ctypes.c_int, _u8p, _sz, _f32p, _i8p, _u32, _u32, _u32, _f32p, _sz]
         lib.orc_block_sums.argtypes = [ctypes.c_int, _u8p, _sz, _i8p, _u32, _u32, _u32, _i32p]
+        lib.orc_gemm_blockwise.argtypes = [ctypes.c_int, _u8p, _sz, _f32p, _i8p, _u32, _u32, _u32, _f32p, _sz]
         lib.orc_split_range.argtypes = [_u32, _u32, _u32, ctypes.POINTER(_u32), ctypes.POINTER(_u32)]
         lib.orc_mat_item.restype = ctypes.c_int
         lib.orc_mat_item.argtypes = [ctypes.c_int, ctypes.c_int, _u8p, _sz, _u32, _f32p, _f32p, _i8p, _u32, _u32,
@@ -157,6 +158,17 @@ class Oracle:
         out = np.zeros(max(1, ntok * stride), np.float32)
         self.lib.orc_gemm(int(q5), int(fast), _ptr(w, _u8p), row_bytes, _ptr(xd, _f32p), _ptr(xq, _i8p), nrows,
                           ntok, nb, _ptr(out, _f32p), stride)
+        return out[:ntok * stride]
+
+    def gemm_blockwise(self, w, row_bytes, xd, xq, nrows, ntok, nb, stride=None, q5=False):
+        """The relaxed-order (MFMA) contract: blocks in order, acc = fmaf(ws * xs, S, acc)."""
+        stride = nrows if stride is None else stride
+        w = np.ascontiguousarray(w, np.uint8)
+        xd = np.ascontiguousarray(xd, np.float32)
+        xq = np.ascontiguousarray(xq, np.int8)
+        out = np.zeros(max(1, ntok * stride), np.float32)
+        self.lib.orc_gemm_blockwise(int(q5), _ptr(w, _u8p), row_bytes, _ptr(xd, _f32p), _ptr(xq, _i8p), nrows,
+                                    ntok, nb, _ptr(out, _f32p), stride)
         return out[:ntok * stride]
 
     def block_sums(self, w, row_bytes, xq, nrows, ntok, nb, q5=False):

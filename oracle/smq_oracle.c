@@ -21,6 +21,8 @@
  *   orc_q8_weight_rows : SHA-256 goldens tests/goldens/convert-q8.json.
  *   orc_quantize_q5_row : brute-force minimum search on tiny blocks, and the
  *       compiled reference.
+ *   orc_gemm_blockwise : exact equality with a float64 evaluation where every
+ *       step is exact (power-of-two scales), and 1e-5 normwise of orc_gemm.
  */
 #include <float.h>
 #include <math.h>
@@ -260,6 +262,32 @@ void orc_block_sums(int q5, const unsigned char *w, size_t row_bytes, const int8
                 for (j = 0; j < 32u; ++j) s += (int32_t)wq[j] * (int32_t)xb[j];
                 sums[((size_t)t * nrows + r) * nb + b] = s;
             }
+}
+
+/* The relaxed-order prefill contract as the GPU's MFMA kernels evaluate it:
+ * per output, the blocks in order of acc = fmaf(wscale * xscale, S, acc),
+ * S the exact integer block sum (orc_block_sums). The reference has no such
+ * order (its GEMM keeps eight lane sums); the GPU GEMMs that do not split K
+ * must equal this bit for bit. */
+void orc_gemm_blockwise(int q5, const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq,
+                        uint32_t nrows, uint32_t ntok, uint32_t nb, float *out, size_t stride) {
+    uint32_t r, t, b, j;
+    int8_t wq[32];
+    for (t = 0; t < ntok; ++t)
+        for (r = 0; r < nrows; ++r) {
+            float acc = 0.0f;
+            for (b = 0; b < nb; ++b) {
+                const unsigned char *blk = w + (size_t)r * row_bytes + (size_t)b * (q5 ? ORC_Q5_BLOCK : ORC_Q8_BLOCK);
+                const int8_t *xb = xq + ((size_t)t * nb + b) * 32u;
+                const float ws = q5 ? orc_f16_to_f32(le_u16(blk)) : le_f32(blk);
+                int32_t sum = 0;
+                if (q5) orc_unpack_q5(blk, wq);
+                else memcpy(wq, blk + 4, 32);
+                for (j = 0; j < 32u; ++j) sum += (int32_t)wq[j] * (int32_t)xb[j];
+                acc = fmaf(ws * xd[(size_t)t * nb + b], (float)sum, acc);
+            }
+            out[(size_t)t * stride + r] = acc;
+        }
 }
 
 /* ---- caller glue (src/model.c:252-310) -------------------------------- */

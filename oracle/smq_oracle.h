@@ -27,6 +27,8 @@ void orc_gemm(int q5, int fast, const unsigned char *w, size_t row_bytes, const 
               uint32_t nrows, uint32_t ntok, uint32_t nb, float *out, size_t stride);
 void orc_block_sums(int q5, const unsigned char *w, size_t row_bytes, const int8_t *xq, uint32_t nrows,
                     uint32_t ntok, uint32_t nb, int32_t *sums);
+void orc_gemm_blockwise(int q5, const unsigned char *w, size_t row_bytes, const float *xd, const int8_t *xq,
+                        uint32_t nrows, uint32_t ntok, uint32_t nb, float *out, size_t stride);
 
 void orc_split_range(uint32_t total, uint32_t index, uint32_t count, uint32_t *begin, uint32_t *end);
 int orc_mat_item(int q5, int fast, const unsigned char *w, size_t row_bytes, uint32_t rows, const float *bias,

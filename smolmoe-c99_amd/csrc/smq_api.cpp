@@ -153,6 +153,10 @@ void gemm_impl(bool q5, const unsigned char *w, size_t row_bytes, const float *x
  * library workspace where the tiles are few). Returns false when
  * the layout does not allow it (nothing launched); a launch error sets the status. */
 bool mfma_launch(const smq::MatArgs &a, bool q5) {
+    if (!q5 && smq::mh_wanted(a)) {
+        hip_ok(smq::launch_mh(a, g.cur), "mfma gemm");
+        return true;
+    }
     if (!q5 && smq::mq8_wanted(a)) {
         hip_ok(smq::launch_mq8(a, g.mq_ws, smq::MQ_WORKSPACE_BYTES, g.cur), "mfma gemm");
         return true;
@@ -237,6 +241,8 @@ smq_status smq_init(int device) {
     g.checks = !(env && !strcmp(env, "0"));
     env = getenv("SMQ_ATT_GROUP"); /* read once: 0 sends prefill attention to the per-head kernel */
     smq::set_att_grouped(!(env && !strcmp(env, "0")));
+    env = getenv("SMQ_MFMA_MH"); /* read once: 0 sends 28-block Q8 prefill GEMMs to the int8 MFMA kernels */
+    smq::set_mh_enabled(!(env && !strcmp(env, "0")));
     g.ready = true;
     return set_status(SMQ_OK, "");
 }

@@ -139,6 +139,13 @@ bool mq8_ok(const MatArgs &a);
 bool mq8_wanted(const MatArgs &a);
 hipError_t launch_mq8(MatArgs a, float *ws, size_t ws_bytes, hipStream_t s);
 hipError_t prepare_mq8_attributes();
+/* The f16-MFMA prefill GEMM with the activation in registers (csrc/smq_mfma.hip): Q8 rows of 28
+ * blocks, at least two tokens, 8-byte aligned quants, 16-byte aligned activation scale rows. Same results as the int8 kernels bit for
+ * bit. set_mh_enabled(false) (SMQ_MFMA_MH=0 at init) sends those shapes back to the int8 kernels. */
+bool mh_wanted(const MatArgs &a);
+hipError_t launch_mh(MatArgs a, hipStream_t s);
+void set_mh_enabled(bool on);
+bool mh_enabled();
 /* Activation producer rows (model.c:354-415): optional RMSNorm, optional
  * gated activation (act 1 = SwiGLU, 2 = GeGLU), optional f32 store, Q8. */
 constexpr uint32_t MAX_ROW = 16384;

@@ -245,7 +245,304 @@ __global__ __launch_bounds__(256) void k_mq8_reduce(MqArgs q) {
     store_out(I, a.flag, t, r, s);
 }
 
+/* ------------------------------------------------------------------------
+ * Prefill GEMM on f16 MFMA with the activation held in registers (Q8 rows of
+ * MH_NB blocks: the 896-wide projections and the LM head). Same contract as
+ * the int8 kernels: out[t][r] = the blocks in order of
+ * acc = fma(wscale * xscale, S, acc), S the exact block sum. The quants are
+ * exact in f16, and v_mfma_f32_16x16x32_f16 adds 32 products of at most
+ * 127^2 in f32: every partial sum is an integer below 2^24, so S is exact
+ * whatever the order of the additions, and the outputs equal the int8
+ * kernel's bit for bit with no convert in the epilogue (a multiply and a
+ * fused add per output and block).
+ *
+ * Layout. Wave w holds the B operands of 16 tokens (t0 + 16w + l%16, K group
+ * l/16) for every block, converted to f16 once (MH_NB x 4 registers), and
+ * their scales. The tokens arrive by 16-byte loads of whole rows (14 per
+ * lane) and pass through the wave's own LDS rows to reach operand order; the
+ * weight buffers later take the same bytes. The weights stream through LDS in 16-row subtiles: thread
+ * (row, block) loads its 36-byte block (consecutive threads take consecutive
+ * blocks of a row, one coalesced run) and writes the scale to Wb[block][row]
+ * and the quants as f16 into the operand planes Ab[block][k group][row] (a
+ * lane's A operand is one 16-byte read; the planes are padded by 16 bytes so
+ * the staging writes spread over the banks). Persistent workgroups: each
+ * takes one token tile and a contiguous range of subtiles; while subtile i is
+ * computed, subtile i+1's loads have landed in registers and i+2's are in
+ * flight (two LDS buffers, one barrier per subtile). The reads of the
+ * outputs' bias and prior travel with the subtile's weight loads.
+ * ---------------------------------------------------------------------- */
+constexpr uint32_t MH_NB = 28;             /* blocks per row (896 columns) */
+constexpr uint32_t MH_R = 16;              /* rows per subtile */
+constexpr uint32_t MH_PLANE = 4 * MH_R + 1; /* 16-byte operand entries per block, one of them padding */
+constexpr uint32_t MH_WP = 20;             /* scale plane pitch (floats) */
+constexpr uint32_t MH_TP = MH_NB * QK + 16; /* a staged token's pitch in bytes (padded: the operand reads spread) */
+constexpr uint32_t MH_BUF_BYTES = 2 * MH_NB * (MH_PLANE * 16 + MH_WP * 4); /* the two weight buffers */
+/* dynamic LDS: the weight buffers, or (before them, in the same bytes) the waves' token staging */
+constexpr size_t mh_lds_bytes(uint32_t nw) {
+    return (size_t)nw * 16 * MH_TP > MH_BUF_BYTES ? (size_t)nw * 16 * MH_TP : (size_t)MH_BUF_BYTES;
+}
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+/* Four int8 (one dword) as four exact f16 (two dwords): byte b becomes the half
+ * 0x6400 | (b ^ 0x80) = 1024 + (b + 128), then 1152 is taken off. */
+__device__ __forceinline__ uint2 i8x4_f16(uint32_t q) {
+    const uint32_t u = q ^ 0x80808080u;
+    const h2v m = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const h2v lo = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - m;
+    const h2v hi = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - m;
+    return make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+}
+
+struct MhArgs {
+    MatArgs m;
+    uint32_t subtiles, tok_tiles, per; /* per: workgroups per token tile */
+};
+
+template <uint32_t NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_mh(MhArgs q) {
+    constexpr uint32_t NB = MH_NB, T = 64 * NW, TASKS = MH_R * NB, TPT = (TASKS + T - 1) / T;
+    constexpr uint32_t RB = NB * Q8_BYTES, OOB = 0x80000000u;
+    constexpr uint32_t MH_AHEAD = NW == 8 ? 4 : 2; /* operand reads ahead in the product loop (within the registers) */
+    extern __shared__ __attribute__((aligned(16))) uint4 mh_lds[];
+    uint4 *const Ab = mh_lds;                                  /* [2][NB * MH_PLANE] */
+    float *const Wb = (float *)(mh_lds + 2 * NB * MH_PLANE);  /* [2][NB * MH_WP] */
+    const MatArgs &a = q.m;
+    const uint32_t tid = threadIdx.x, l = tid % 64, w = tid / 64, g = l / 16, c16 = l % 16;
+
+    /* workgroup -> (token tile, range of subtiles): an XCD's workgroups take neighbouring ranges */
+    const uint32_t G = gridDim.x, xcd = blockIdx.x % 8u, kk = blockIdx.x / 8u;
+    const uint32_t per8 = G / 8u, extra = G % 8u;
+    const uint32_t L = xcd * per8 + (xcd < extra ? xcd : extra) + kk;
+    const uint32_t tt = L % q.tok_tiles, p = L / q.tok_tiles;
+    const uint32_t s_begin = (uint32_t)((uint64_t)q.subtiles * p / q.per);
+    const uint32_t n = (uint32_t)((uint64_t)q.subtiles * (p + 1) / q.per) - s_begin;
+    const uint32_t ntok = a.ntok, t0 = tt * 16 * NW, tok = t0 + 16 * w + c16;
+    const bool live = t0 + 16 * w < ntok; /* this wave holds at least one token (uniform) */
+
+    /* staging role: (row, block) tasks of a subtile, blocks of a row on consecutive threads */
+    uint32_t trow[TPT], tblk[TPT];
+    bool tuse[TPT];
+#pragma unroll
+    for (uint32_t j = 0; j < TPT; ++j) {
+        const uint32_t k = tid + T * j;
+        tuse[j] = k < TASKS;
+        trow[j] = k / NB;
+        tblk[j] = k % NB;
+    }
+
+    u4a wa[2][TPT], wb[2][TPT];
+    uint32_t wc[2][TPT];
+    OutPre pre[2][4], cur[4];
+    /* subtile s's weight loads into slot P (rows past the item read 0: the range ends at its last
+     * row), with the reads of its outputs' bias and prior */
+    auto issue = [&](uint32_t s, u4a (&xa)[TPT], u4a (&xb)[TPT], uint32_t (&xc)[TPT], OutPre (&o)[4])
+        __attribute__((always_inline)) {
+        const Item I = pick_item(a, s);
+        const uint32_t r_sub = (s - I.tile_begin) * MH_R;
+        const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(I.w + (size_t)r_sub * RB), (short)0, (int)((I.rows - r_sub) * RB), 0x00020000);
+#pragma unroll
+        for (uint32_t j = 0; j < TPT; ++j) {
+            const uint32_t off = tuse[j] ? trow[j] * RB + tblk[j] * Q8_BYTES : OOB;
+            xa[j] = __builtin_amdgcn_raw_buffer_load_b128(src, off, 0, 0);
+            xb[j] = __builtin_amdgcn_raw_buffer_load_b128(src, off + 16, 0, 0);
+            xc[j] = __builtin_amdgcn_raw_buffer_load_b32(src, off + 32, 0, 0);
+        }
+#pragma unroll
+        for (uint32_t v = 0; v < 4; ++v) {
+            const uint32_t r = r_sub + 4 * g + v;
+            o[v] = OutPre{0.0f, 0.0f};
+            if (live && tok < ntok && r < I.rows) o[v] = load_out(I, tok, r);
+        }
+    };
+    /* slot -> LDS buffer: the scale, and the quants as f16 in operand order */
+    auto stage = [&](const u4a (&xa)[TPT], const u4a (&xb)[TPT], const uint32_t (&xc)[TPT], uint32_t buf)
+        __attribute__((always_inline)) {
+#pragma unroll
+        for (uint32_t j = 0; j < TPT; ++j)
+            if (tuse[j]) {
+                Wb[buf * NB * MH_WP + tblk[j] * MH_WP + trow[j]] = __uint_as_float(xa[j].x);
+                const uint32_t qd[8] = {xa[j].y, xa[j].z, xa[j].w, xb[j].x, xb[j].y, xb[j].z, xb[j].w, xc[j]};
+                uint4 *e = &Ab[buf * NB * MH_PLANE + tblk[j] * MH_PLANE + trow[j]];
+#pragma unroll
+                for (uint32_t gi = 0; gi < 4; ++gi) {
+                    const uint2 lo = i8x4_f16(qd[2 * gi]), hi = i8x4_f16(qd[2 * gi + 1]);
+                    e[gi * MH_R] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                }
+            }
+    };
+
+    const uint32_t n_ = n; /* subtiles of this workgroup */
+    if (n_ > 0) issue(s_begin, wa[0], wb[0], wc[0], pre[0]);
+
+    /* this wave's tokens: K group g of token `tok` for every block, as f16, and their scales (a token
+     * past the batch reads 0) */
+    h8v Bq[NB];
+    float xsc[NB];
+    {
+        const uint32_t xs = a.xstride;
+        const __amdgpu_buffer_rsrc_t qsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)a.xq, (short)0, (int)((size_t)ntok * xs * QK), 0x00020000);
+        const __amdgpu_buffer_rsrc_t dsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)a.xd, (short)0, (int)((size_t)ntok * xs * 4), 0x00020000);
+        const uint32_t dof = tok < ntok ? tok * xs * 4 : OOB;
+        /* the wave's 16 token rows in 16-byte pieces, consecutive lanes on consecutive pieces */
+        constexpr uint32_t PR = NB * QK / 16, NPC = 16 * PR / 64; /* pieces per row, per lane */
+        static_assert(16 * PR % 64 == 0, "whole pieces per lane");
+        u4a pc[NPC];
+#pragma unroll
+        for (uint32_t j = 0; j < NPC; ++j) {
+            const uint32_t P = 64 * j + l, tp = P / PR, t = t0 + 16 * w + tp;
+            pc[j] = __builtin_amdgcn_raw_buffer_load_b128(qsrc, t < ntok ? t * xs * QK + 16 * (P % PR) : OOB, 0, 0);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < NB / 4; ++j) { /* the token's scales, four a load (rows 16-byte aligned) */
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(dsrc, dof + 16 * j, 0, 0);
+            xsc[4 * j] = __uint_as_float(v[0]);
+            xsc[4 * j + 1] = __uint_as_float(v[1]);
+            xsc[4 * j + 2] = __uint_as_float(v[2]);
+            xsc[4 * j + 3] = __uint_as_float(v[3]);
+        }
+        unsigned char *const stg = (unsigned char *)mh_lds + w * 16 * MH_TP; /* this wave's rows */
+#pragma unroll
+        for (uint32_t j = 0; j < NPC; ++j) {
+            const uint32_t P = 64 * j + l;
+            *(u4a *)(stg + (P / PR) * MH_TP + 16 * (P % PR)) = pc[j];
+        }
+        /* the wave's own rows: its writes are complete before its reads */
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (uint32_t b = 0; b < NB; ++b) {
+            const uint2 v = *(const uint2 *)(stg + c16 * MH_TP + b * QK + 8 * g);
+            const uint2 lo = i8x4_f16(v.x), hi = i8x4_f16(v.y);
+            Bq[b] = __builtin_bit_cast(h8v, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        }
+    }
+    if (n_ > 1) issue(s_begin + 1, wa[1], wb[1], wc[1], pre[1]); /* (here: the rows' registers are free) */
+    __syncthreads(); /* every wave is done with its rows before the weights take those bytes */
+    if (n_ > 0) {
+        stage(wa[0], wb[0], wc[0], 0);
+#pragma unroll
+        for (uint32_t v = 0; v < 4; ++v) cur[v] = pre[0][v];
+        if (n_ > 2) issue(s_begin + 2, wa[0], wb[0], wc[0], pre[0]);
+    }
+    __syncthreads();
+
+    /* subtile i from buffer P; then subtile i+1 (slot P^1) staged into the other buffer, and i+3's loads
+     * into the slot it leaves */
+    auto step = [&](uint32_t i, uint32_t P) __attribute__((always_inline)) {
+        if (live) {
+            const Item I = pick_item(a, s_begin + i);
+            const uint32_t r_sub = (s_begin + i - I.tile_begin) * MH_R;
+            const uint4 *A = Ab + P * NB * MH_PLANE;
+            const float *W = Wb + P * NB * MH_WP;
+            const f4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            /* operand reads MH_AHEAD blocks ahead; the empty asm after each block keeps the products
+             * and their scale chain in block order (left free, the compiler issues every block's
+             * product first and holds all the sums: the registers spill) */
+            h8v av[MH_AHEAD];
+            float4 wv[MH_AHEAD];
+#pragma unroll
+            for (uint32_t b = 0; b < MH_AHEAD; ++b) {
+                av[b] = __builtin_bit_cast(h8v, A[b * MH_PLANE + g * MH_R + c16]);
+                wv[b] = *(const float4 *)&W[b * MH_WP + 4 * g];
+            }
+            /* block b+1's product is issued before block b's scale chain reads its sums */
+            f4v S = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[0], Bq[0], zero, 0, 0, 0);
+#pragma unroll
+            for (uint32_t b = 0; b < NB; ++b) {
+                const uint32_t k = b % MH_AHEAD;
+                f4v Sn = zero;
+                if (b + 1 < NB) Sn = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[(b + 1) % MH_AHEAD], Bq[b + 1], zero, 0, 0, 0);
+                acc[0] = __builtin_fmaf(wv[k].x * xsc[b], S[0], acc[0]);
+                acc[1] = __builtin_fmaf(wv[k].y * xsc[b], S[1], acc[1]);
+                acc[2] = __builtin_fmaf(wv[k].z * xsc[b], S[2], acc[2]);
+                acc[3] = __builtin_fmaf(wv[k].w * xsc[b], S[3], acc[3]);
+                S = Sn;
+                asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]) : : "memory");
+                if (b + MH_AHEAD < NB) {
+                    av[k] = __builtin_bit_cast(h8v, A[(b + MH_AHEAD) * MH_PLANE + g * MH_R + c16]);
+                    wv[k] = *(const float4 *)&W[(b + MH_AHEAD) * MH_WP + 4 * g];
+                }
+            }
+#pragma unroll
+            for (uint32_t v = 0; v < 4; ++v) {
+                const uint32_t r = r_sub + 4 * g + v;
+                if (tok < ntok && r < I.rows) store_out_pre(I, a.flag, tok, r, acc[v], cur[v]);
+            }
+        }
+        if (i + 1 < n_) {
+            const uint32_t Q = P ^ 1u;
+            stage(wa[Q], wb[Q], wc[Q], Q);
+#pragma unroll
+            for (uint32_t v = 0; v < 4; ++v) cur[v] = pre[Q][v];
+            if (i + 3 < n_) issue(s_begin + i + 3, wa[Q], wb[Q], wc[Q], pre[Q]);
+        }
+        __syncthreads();
+    };
+    for (uint32_t i = 0; i < n_; i += 2) {
+        step(i, 0);
+        if (i + 1 < n_) step(i + 1, 1);
+    }
+}
+
 }  // namespace
+
+namespace {
+bool g_mh_on = true;
+}  // namespace
+
+void set_mh_enabled(bool on) { g_mh_on = on; }
+bool mh_enabled() { return g_mh_on; }
+
+bool mh_wanted(const MatArgs &a) {
+    if (a.nb != MH_NB || a.ntok < 2 || !mh_enabled() || (((uintptr_t)a.xq) & 7u) || (((uintptr_t)a.xd) & 15u) ||
+        a.xstride % 4u)
+        return false;
+    if ((uint64_t)a.ntok * a.xstride * QK >= (1ull << 31)) return false;
+    for (uint32_t i = 0; i < a.nitems; ++i) {
+        const Item &I = a.item[i];
+        if (I.row_bytes != (size_t)MH_NB * Q8_BYTES || (((uintptr_t)I.w) & 3u)) return false;
+        if ((uint64_t)I.rows * I.row_bytes >= (1ull << 31)) return false;
+    }
+    return true;
+}
+
+hipError_t launch_mh(MatArgs a, hipStream_t s) {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+            v = 256;
+        cus = v;
+    }
+    MhArgs q;
+    uint32_t subtiles = 0;
+    for (uint32_t i = 0; i < a.nitems; ++i) {
+        a.item[i].tile_begin = subtiles;
+        subtiles += (a.item[i].rows + MH_R - 1) / MH_R;
+    }
+    if (!subtiles || !a.ntok) return hipSuccess;
+    const bool wide = a.ntok > 64; /* eight waves of 16 tokens, else four */
+    const uint32_t nw = wide ? 8u : 4u, resident = (uint32_t)cus * (wide ? 1u : 2u);
+    q.m = a;
+    q.subtiles = subtiles;
+    q.tok_tiles = (a.ntok + 16 * nw - 1) / (16 * nw);
+    uint32_t per = resident / q.tok_tiles;
+    per = per < subtiles ? per : subtiles;
+    q.per = per ? per : 1u;
+    const dim3 grid(q.per * q.tok_tiles);
+    if (wide) hipLaunchKernelGGL(k_gemm_mh<8>, grid, dim3(512), mh_lds_bytes(8), s, q);
+    else hipLaunchKernelGGL(k_gemm_mh<4>, grid, dim3(256), mh_lds_bytes(4), s, q);
+    return hipGetLastError();
+}
 
 bool mq8_ok(const MatArgs &a) {
     if (!a.nb || a.ntok < 2 || (((uintptr_t)a.xq | (uintptr_t)a.xd) & 3u)) return false;
@@ -276,7 +573,15 @@ bool mq8_wanted(const MatArgs &a) {
 }
 
 hipError_t prepare_mq8_attributes() {
-    return hipFuncSetAttribute((const void *)k_gemm_mq8, hipFuncAttributeMaxDynamicSharedMemorySize, (int)MQ_LDS_BYTES);
+    hipError_t e = hipFuncSetAttribute((const void *)k_gemm_mq8, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)MQ_LDS_BYTES);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute((const void *)k_gemm_mh<8>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)mh_lds_bytes(8));
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute((const void *)k_gemm_mh<4>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)mh_lds_bytes(4));
+    return e;
 }
 
 hipError_t launch_mq8(MatArgs a, float *ws, size_t ws_bytes, hipStream_t s) {

@@ -433,8 +433,38 @@ def test_mfma_block_sums_exact_and_outputs_within_tolerance(orc, name, q5, rows,
     assert ok, (name, worst)
 
 
-@pytest.mark.parametrize("rows,cols,ntok,q5", [(640, 896, 64, False), (300, 4864, 96, False),
-                                               (300, 8960, 64, True)])
+MFMA_WHOLE_K = [("f16-c1-gateup-b128", False, 9728, 896, 128),  # eight waves, one token tile
+                ("f16-ragged-b70", False, 200, 896, 70),        # 13 subtiles, the last half full; 3 idle waves
+                ("f16-b13", False, 77, 896, 13),                # four waves, one partial
+                ("f16-b200", False, 300, 896, 200),             # two token tiles
+                ("f16-b2", False, 33, 896, 2),
+                ("f16-lm-b64", False, 4096, 896, 64),
+                ("pair-q5-b64", True, 8960, 1536, 64),          # int8 block-pair kernel, K whole
+                ("pair-q8-nb13", False, 4864, 416, 64)]
+
+
+@pytest.mark.parametrize("name,q5,rows,cols,ntok", MFMA_WHOLE_K)
+def test_mfma_whole_k_equals_blockwise_order(orc, name, q5, rows, cols, ntok):
+    """The MFMA GEMMs that keep K whole (the f16 kernel with the activation in registers on 28-block
+    Q8 rows, the int8 block-pair kernel otherwise) apply the blocks in order, acc = fma(ws * xs, S,
+    acc): equal bit for bit to orc_gemm_blockwise, and within 1e-5 of the eight-lane contract."""
+    say("mfma whole K", name)
+    nb = (cols + 31) // 32
+    bb = Q5B if q5 else Q8B
+    w = weights(q5, 5000 + rows, rows, cols)
+    x = synth.activations(5100 + cols + ntok, ntok, cols)
+    dbuf, qbuf, xd, xq = gpu_quantize(x)
+    wb = smq.DeviceBuffer.from_array(w)
+    out = smq.DeviceBuffer(ntok * rows * 4)
+    (smq.gemm_q5_mfma if q5 else smq.gemm_q8_mfma)(wb, nb * bb, dbuf, qbuf, rows, ntok, nb, out, rows)
+    got = out.download(np.float32)
+    assert_same_f32(got, orc.gemm_blockwise(w, nb * bb, xd, xq, rows, ntok, nb, q5=q5), name)
+    ok, worst = mfma_tolerance_ok(got, orc.gemm(w, nb * bb, xd, xq, rows, ntok, nb, q5=q5), ntok, rows)
+    assert ok, (name, worst)
+
+
+@pytest.mark.parametrize("rows,cols,ntok,q5", [(640, 896, 64, False), (200, 896, 100, False),
+                                               (300, 4864, 96, False), (300, 8960, 64, True)])
 def test_mfma_prefill_items_bias_accumulate(orc, rows, cols, ntok, q5):
     """smq_matmul on the MFMA GEMM with three items (bias, residual add; one K slice and several, on
     the 64x64 split-K kernel for Q8 and the block-pair kernel's K split for Q5): within 1e-5 of the

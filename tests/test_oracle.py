@@ -308,6 +308,38 @@ def test_block_sums_brute_force(orc):
                     assert sums[t, r, b] == int((wq * xq[t, b * 32:(b + 1) * 32].astype(np.int64)).sum())
 
 
+def test_gemm_blockwise_exact_and_close(orc):
+    """orc_gemm_blockwise (the MFMA kernels' order): with power-of-two scales every product and sum
+    is exact, so it equals the float64 sum; with random scales it stays within 1e-5 (normwise, per
+    token) of the eight-lane contract orc_gemm."""
+    g = LcgUniform(11)
+    nb, nrows, ntok = 6, 7, 3
+    # exact case: scales 2^-k and 2^-m (k < 3, m < 2), |S| < 2^16: every partial sum fits 24 bits
+    w = random_q8_weights(g, nb * nrows, True)
+    blocks = w.reshape(nb * nrows, Q8B)
+    exps = (np.arange(nb * nrows) % 3).astype(np.float32)
+    blocks[:, :4] = np.ascontiguousarray((2.0 ** -exps).astype("<f4")).view(np.uint8).reshape(-1, 4)
+    xq = (np.arange(ntok * nb * 32) % 23 - 11).astype(np.int8)
+    xd = (2.0 ** -(np.arange(ntok * nb) % 2)).astype(np.float32)
+    got = orc.gemm_blockwise(w, nb * Q8B, xd, xq, nrows, ntok, nb)
+    ws = blocks[:, :4].copy().view("<f4").reshape(nrows, nb).astype(np.float64)
+    wq = blocks[:, 4:].view(np.int8).reshape(nrows, nb, 32).astype(np.int64)
+    xqb = xq.reshape(ntok, nb, 32).astype(np.int64)
+    S = np.einsum("rbk,tbk->trb", wq, xqb).astype(np.float64)
+    want = (S * ws[None] * xd.reshape(ntok, 1, nb).astype(np.float64)).sum(axis=2)
+    assert np.array_equal(got.reshape(ntok, nrows).astype(np.float64), want)
+    # random scales: close to the exact contract
+    nb, nrows, ntok = 28, 40, 5
+    for q5 in (False, True):
+        w = random_q5_weights(orc, g, nb * nrows, 2.0) if q5 else random_q8_weights(g, nb * nrows, False)
+        _, xd, xq = orc.quantize_q8(g.uniform(-3, 3, ntok * nb * 32).reshape(ntok, -1))
+        rb = nb * (Q5B if q5 else Q8B)
+        got = orc.gemm_blockwise(w, rb, xd, xq, nrows, ntok, nb, q5=q5).reshape(ntok, nrows).astype(np.float64)
+        want = orc.gemm(w, rb, xd, xq, nrows, ntok, nb, q5=q5).reshape(ntok, nrows).astype(np.float64)
+        err = np.abs(got - want).max(axis=1)
+        assert np.all(err <= 1e-5 * np.abs(want).max(axis=1)), err
+
+
 # ---------------------------------------------------------------- offline weight rules
 
 def test_q8_weight_rule_goldens(orc):

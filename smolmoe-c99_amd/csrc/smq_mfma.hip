@@ -296,12 +296,19 @@ __device__ __forceinline__ uint2 i8x4_f16(uint32_t q) {
     return make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
 }
 
+/* Lane V of each quad of lanes, to every lane of the quad (DPP quad_perm [V,V,V,V]). */
+template <int V>
+__device__ __forceinline__ float quad_lane(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), V * 0x55, 0xf, 0xf, false));
+}
+
 struct MhArgs {
     MatArgs m;
     uint32_t subtiles, tok_tiles, per; /* per: workgroups per token tile */
 };
 
-template <uint32_t NW>
+/* PRE: some item has a bias or adds to its output (their reads travel with the weight loads) */
+template <uint32_t NW, bool PRE>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_mh(MhArgs q) {
     constexpr uint32_t NB = MH_NB, T = 64 * NW, TASKS = MH_R * NB, TPT = (TASKS + T - 1) / T;
     constexpr uint32_t RB = NB * Q8_BYTES, OOB = 0x80000000u;
@@ -333,17 +340,24 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_mh(MhArgs q) {
         tblk[j] = k % NB;
     }
 
+    /* Every step issues the same vector memory operations whatever the data (loads of a subtile past
+     * the range and of rows past an item read 0 from an empty or ending range; stores past the batch
+     * or the rows are dropped by the range check): the compiler's waits for a slot's loads then count
+     * only what was issued after them, and the next subtiles' loads stay in flight. */
     u4a wa[2][TPT], wb[2][TPT];
     uint32_t wc[2][TPT];
-    OutPre pre[2][4], cur[4];
-    /* subtile s's weight loads into slot P (rows past the item read 0: the range ends at its last
-     * row), with the reads of its outputs' bias and prior */
-    auto issue = [&](uint32_t s, u4a (&xa)[TPT], u4a (&xb)[TPT], uint32_t (&xc)[TPT], OutPre (&o)[4])
+    OutPre cur[4];
+    const uint32_t s_end = s_begin + n;
+    /* subtile s's weight loads into a slot (rows past the item read 0: the range ends at its last
+     * row) */
+    auto issue = [&](uint32_t s, u4a (&xa)[TPT], u4a (&xb)[TPT], uint32_t (&xc)[TPT])
         __attribute__((always_inline)) {
-        const Item I = pick_item(a, s);
-        const uint32_t r_sub = (s - I.tile_begin) * MH_R;
+        const bool has = s < s_end; /* uniform */
+        const uint32_t sv = has ? s : s_begin;
+        const Item I = pick_item(a, sv);
+        const uint32_t r_sub = (sv - I.tile_begin) * MH_R;
         const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
-            (void *)(I.w + (size_t)r_sub * RB), (short)0, (int)((I.rows - r_sub) * RB), 0x00020000);
+            (void *)(I.w + (size_t)r_sub * RB), (short)0, has ? (int)((I.rows - r_sub) * RB) : 0, 0x00020000);
 #pragma unroll
         for (uint32_t j = 0; j < TPT; ++j) {
             const uint32_t off = tuse[j] ? trow[j] * RB + tblk[j] * Q8_BYTES : OOB;
@@ -351,11 +365,26 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_mh(MhArgs q) {
             xb[j] = __builtin_amdgcn_raw_buffer_load_b128(src, off + 16, 0, 0);
             xc[j] = __builtin_amdgcn_raw_buffer_load_b32(src, off + 32, 0, 0);
         }
+    };
+    /* the bias and prior of subtile s's outputs, one step before they are stored */
+    auto load_pre = [&](uint32_t s, OutPre (&o)[4]) __attribute__((always_inline)) {
+        if constexpr (PRE) {
+            const bool has = s < s_end; /* uniform */
+            const uint32_t sv = has ? s : s_begin;
+            const Item I = pick_item(a, sv);
+            const uint32_t r_sub = (sv - I.tile_begin) * MH_R;
+            const __amdgpu_buffer_rsrc_t bsrc = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)I.bias, (short)0, I.bias ? (int)(I.rows * 4) : 0, 0x00020000);
+            const __amdgpu_buffer_rsrc_t ysrc = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)I.y, (short)0, I.accumulate ? (int)((size_t)ntok * I.y_stride * 4) : 0, 0x00020000);
 #pragma unroll
-        for (uint32_t v = 0; v < 4; ++v) {
-            const uint32_t r = r_sub + 4 * g + v;
-            o[v] = OutPre{0.0f, 0.0f};
-            if (live && tok < ntok && r < I.rows) o[v] = load_out(I, tok, r);
+            for (uint32_t v = 0; v < 4; ++v) {
+                const uint32_t r = r_sub + 4 * g + v;
+                const bool ok = has && tok < ntok && r < I.rows;
+                o[v].bias = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(bsrc, ok ? r * 4 : OOB, 0, 0));
+                o[v].cell = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                    ysrc, ok ? (uint32_t)((tok * I.y_stride + r) * 4) : OOB, 0, 0));
+            }
         }
     };
     /* slot -> LDS buffer: the scale, and the quants as f16 in operand order */
@@ -376,7 +405,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_mh(MhArgs q) {
     };
 
     const uint32_t n_ = n; /* subtiles of this workgroup */
-    if (n_ > 0) issue(s_begin, wa[0], wb[0], wc[0], pre[0]);
+    issue(s_begin, wa[0], wb[0], wc[0]);
 
     /* this wave's tokens: K group g of token `tok` for every block, as f16, and their scales (a token
      * past the batch reads 0) */
@@ -423,35 +452,43 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_mh(MhArgs q) {
             Bq[b] = __builtin_bit_cast(h8v, make_uint4(lo.x, lo.y, hi.x, hi.y));
         }
     }
-    if (n_ > 1) issue(s_begin + 1, wa[1], wb[1], wc[1], pre[1]); /* (here: the rows' registers are free) */
-    __syncthreads(); /* every wave is done with its rows before the weights take those bytes */
-    if (n_ > 0) {
-        stage(wa[0], wb[0], wc[0], 0);
+    /* the scales in hand here, so no wait inside the subtile loop is for them */
 #pragma unroll
-        for (uint32_t v = 0; v < 4; ++v) cur[v] = pre[0][v];
-        if (n_ > 2) issue(s_begin + 2, wa[0], wb[0], wc[0], pre[0]);
+    for (uint32_t b = 0; b < NB; ++b) asm volatile("" : : "v"(xsc[b]));
+    issue(s_begin + 1, wa[1], wb[1], wc[1]); /* (here: the rows' registers are free) */
+    __syncthreads(); /* every wave is done with its rows before the weights take those bytes */
+    if (n_ > 0) stage(wa[0], wb[0], wc[0], 0);
+    load_pre(s_begin, cur);
+    {   /* four stores that the range check drops, where a step stores its outputs: the loop is entered
+         * with the operations in flight that each of its steps leaves (so its waits are the steady ones) */
+        const __amdgpu_buffer_rsrc_t none = __builtin_amdgcn_make_buffer_rsrc((void *)a.item[0].y, (short)0, 0, 0x00020000);
+#pragma unroll
+        for (uint32_t v = 0; v < 4; ++v) __builtin_amdgcn_raw_buffer_store_b32(0u, none, OOB, 0, 0);
     }
+    issue(s_begin + 2, wa[0], wb[0], wc[0]);
     __syncthreads();
+    bool bad = false; /* a non-finite output of this lane */
 
     /* subtile i from buffer P; then subtile i+1 (slot P^1) staged into the other buffer, and i+3's loads
      * into the slot it leaves */
     auto step = [&](uint32_t i, uint32_t P) __attribute__((always_inline)) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (live) {
-            const Item I = pick_item(a, s_begin + i);
-            const uint32_t r_sub = (s_begin + i - I.tile_begin) * MH_R;
             const uint4 *A = Ab + P * NB * MH_PLANE;
             const float *W = Wb + P * NB * MH_WP;
             const f4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
-            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
             /* operand reads MH_AHEAD blocks ahead; the empty asm after each block keeps the products
              * and their scale chain in block order (left free, the compiler issues every block's
              * product first and holds all the sums: the registers spill) */
+            /* a lane reads one row scale, row 4g + c16 % 4: each quad of lanes holds its four rows'
+             * scales, and the multiplies take them by a quad broadcast of their first operand */
             h8v av[MH_AHEAD];
-            float4 wv[MH_AHEAD];
+            float wv[MH_AHEAD];
+            const uint32_t wrow = 4 * g + (c16 & 3u);
 #pragma unroll
             for (uint32_t b = 0; b < MH_AHEAD; ++b) {
                 av[b] = __builtin_bit_cast(h8v, A[b * MH_PLANE + g * MH_R + c16]);
-                wv[b] = *(const float4 *)&W[b * MH_WP + 4 * g];
+                wv[b] = W[b * MH_WP + wrow];
             }
             /* block b+1's product is issued before block b's scale chain reads its sums */
             f4v S = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[0], Bq[0], zero, 0, 0, 0);
@@ -460,36 +497,50 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_mh(MhArgs q) {
                 const uint32_t k = b % MH_AHEAD;
                 f4v Sn = zero;
                 if (b + 1 < NB) Sn = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[(b + 1) % MH_AHEAD], Bq[b + 1], zero, 0, 0, 0);
-                acc[0] = __builtin_fmaf(wv[k].x * xsc[b], S[0], acc[0]);
-                acc[1] = __builtin_fmaf(wv[k].y * xsc[b], S[1], acc[1]);
-                acc[2] = __builtin_fmaf(wv[k].z * xsc[b], S[2], acc[2]);
-                acc[3] = __builtin_fmaf(wv[k].w * xsc[b], S[3], acc[3]);
+                acc[0] = __builtin_fmaf(quad_lane<0>(wv[k]) * xsc[b], S[0], acc[0]);
+                acc[1] = __builtin_fmaf(quad_lane<1>(wv[k]) * xsc[b], S[1], acc[1]);
+                acc[2] = __builtin_fmaf(quad_lane<2>(wv[k]) * xsc[b], S[2], acc[2]);
+                acc[3] = __builtin_fmaf(quad_lane<3>(wv[k]) * xsc[b], S[3], acc[3]);
                 S = Sn;
                 asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]) : : "memory");
                 if (b + MH_AHEAD < NB) {
                     av[k] = __builtin_bit_cast(h8v, A[(b + MH_AHEAD) * MH_PLANE + g * MH_R + c16]);
-                    wv[k] = *(const float4 *)&W[(b + MH_AHEAD) * MH_WP + 4 * g];
+                    wv[k] = W[(b + MH_AHEAD) * MH_WP + wrow];
                 }
             }
+        }
+        {   /* the outputs (model.c:259-262 bias, then the finiteness check, then the residual add of
+             * model.c:452-455), stored by every lane: one past the batch or the rows is dropped */
+            const Item I = pick_item(a, s_begin + i);
+            const uint32_t r_sub = (s_begin + i - I.tile_begin) * MH_R;
+            const __amdgpu_buffer_rsrc_t ydst = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)I.y, (short)0, (int)((size_t)ntok * I.y_stride * 4), 0x00020000);
 #pragma unroll
             for (uint32_t v = 0; v < 4; ++v) {
                 const uint32_t r = r_sub + 4 * g + v;
-                if (tok < ntok && r < I.rows) store_out_pre(I, a.flag, tok, r, acc[v], cur[v]);
+                const bool ok = tok < ntok && r < I.rows;
+                float val = acc[v];
+                if (PRE && I.bias) val = val + cur[v].bias;
+                bad = bad || (ok && !(fabsf(val) <= FLT_MAX));
+                if (PRE && I.accumulate) val = cur[v].cell + val;
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), ydst,
+                                                      ok ? (uint32_t)((tok * I.y_stride + r) * 4) : OOB, 0, 0);
             }
         }
-        if (i + 1 < n_) {
-            const uint32_t Q = P ^ 1u;
-            stage(wa[Q], wb[Q], wc[Q], Q);
-#pragma unroll
-            for (uint32_t v = 0; v < 4; ++v) cur[v] = pre[Q][v];
-            if (i + 3 < n_) issue(s_begin + i + 3, wa[Q], wb[Q], wc[Q], pre[Q]);
-        }
+        const uint32_t Q = P ^ 1u;
+        if (i + 1 < n_) stage(wa[Q], wb[Q], wc[Q], Q);
+        load_pre(s_begin + i + 1, cur);
+        issue(s_begin + i + 3, wa[Q], wb[Q], wc[Q]);
         __syncthreads();
     };
-    for (uint32_t i = 0; i < n_; i += 2) {
+    /* pairs of steps, then an odd last one: every way round the loop issues the same operations */
+    uint32_t i = 0;
+    for (; i + 1 < n_; i += 2) {
         step(i, 0);
-        if (i + 1 < n_) step(i + 1, 1);
+        step(i + 1, 1);
     }
+    if (i < n_) step(i, 0);
+    if (a.flag && __ballot(bad) && l == 0) *a.flag = 1;
 }
 
 }  // namespace
@@ -510,6 +561,8 @@ bool mh_wanted(const MatArgs &a) {
         const Item &I = a.item[i];
         if (I.row_bytes != (size_t)MH_NB * Q8_BYTES || (((uintptr_t)I.w) & 3u)) return false;
         if ((uint64_t)I.rows * I.row_bytes >= (1ull << 31)) return false;
+        /* buffer offsets of the outputs below 2^31 */
+        if ((uint64_t)a.ntok * I.y_stride * 4 >= (1ull << 31) || I.rows * 4ull >= (1ull << 31)) return false;
     }
     return true;
 }
@@ -539,8 +592,12 @@ hipError_t launch_mh(MatArgs a, hipStream_t s) {
     per = per < subtiles ? per : subtiles;
     q.per = per ? per : 1u;
     const dim3 grid(q.per * q.tok_tiles);
-    if (wide) hipLaunchKernelGGL(k_gemm_mh<8>, grid, dim3(512), mh_lds_bytes(8), s, q);
-    else hipLaunchKernelGGL(k_gemm_mh<4>, grid, dim3(256), mh_lds_bytes(4), s, q);
+    bool pre = false;
+    for (uint32_t i = 0; i < a.nitems; ++i) pre = pre || a.item[i].bias || a.item[i].accumulate;
+    if (wide && pre) hipLaunchKernelGGL((k_gemm_mh<8, true>), grid, dim3(512), mh_lds_bytes(8), s, q);
+    else if (wide) hipLaunchKernelGGL((k_gemm_mh<8, false>), grid, dim3(512), mh_lds_bytes(8), s, q);
+    else if (pre) hipLaunchKernelGGL((k_gemm_mh<4, true>), grid, dim3(256), mh_lds_bytes(4), s, q);
+    else hipLaunchKernelGGL((k_gemm_mh<4, false>), grid, dim3(256), mh_lds_bytes(4), s, q);
     return hipGetLastError();
 }
 
@@ -575,12 +632,10 @@ bool mq8_wanted(const MatArgs &a) {
 hipError_t prepare_mq8_attributes() {
     hipError_t e = hipFuncSetAttribute((const void *)k_gemm_mq8, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)MQ_LDS_BYTES);
-    if (e == hipSuccess)
-        e = hipFuncSetAttribute((const void *)k_gemm_mh<8>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)mh_lds_bytes(8));
-    if (e == hipSuccess)
-        e = hipFuncSetAttribute((const void *)k_gemm_mh<4>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)mh_lds_bytes(4));
+    const void *mh[4] = {(const void *)k_gemm_mh<8, false>, (const void *)k_gemm_mh<8, true>,
+                         (const void *)k_gemm_mh<4, false>, (const void *)k_gemm_mh<4, true>};
+    for (int i = 0; i < 4 && e == hipSuccess; ++i)
+        e = hipFuncSetAttribute(mh[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)mh_lds_bytes(i < 2 ? 8 : 4));
     return e;
 }
 

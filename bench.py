@@ -444,7 +444,7 @@ def main():
                lambda i: smq.matmul([(copies[i // LAYERS % 2][i % LAYERS].qmat("down"), None, y_out[0])], ah[0].d,
                                     ah[0].q, 1),
                q8_bytes(DIM, HIDDEN), 2 * LAYERS, note="48 distinct 4.9 MB matrices in turn (235 MB)")
-        # prefill: exact GEMM and int8-MFMA GEMM at batch 128 on the fused gate+up shape
+        # prefill: exact GEMM and MFMA GEMM (f16 MFMA, activation in registers) at batch 128 on the fused gate+up shape
         px = Act(4000, 128, DIM)
         pout = smq.DeviceBuffer(128 * 2 * HIDDEN * 4)
 
@@ -677,7 +677,7 @@ def model_forward_extra(args, extra):
              "timing": f"median of {FORWARD_RUNS} runs (prefill, then the decode steps); best: decode "
                        f"{nsteps / dec_best:.1f} tok/s, prefill {512 / pre_best:.1f} tok/s",
              "prefill_mfma_tok_s": round(512 / mfma_s, 1),
-             "prefill_mfma_note": "int8-MFMA prefill: exact int32 block sums, f32 block order relaxed (not bit-exact)",
+             "prefill_mfma_note": "MFMA prefill (f16 MFMA on the 896-wide Q8 rows, int8 MFMA on the others): exact block sums applied in block order (the relaxed contract, within 1e-5; not bit-exact to the eight-lane one)",
              "decode_roofline_tok_s": round(8e12 / 555.7e6, 1), "weights_bytes_per_token": 555706368,
              "synth_s": round(t_synth, 2), "first_tokens": toks[:8].tolist()}
         del m

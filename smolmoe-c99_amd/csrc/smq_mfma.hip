@@ -312,7 +312,7 @@ template <uint32_t NW, bool PRE>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_mh(MhArgs q) {
     constexpr uint32_t NB = MH_NB, T = 64 * NW, TASKS = MH_R * NB, TPT = (TASKS + T - 1) / T;
     constexpr uint32_t RB = NB * Q8_BYTES, OOB = 0x80000000u;
-    constexpr uint32_t MH_AHEAD = NW == 8 ? 4 : 2; /* operand reads ahead in the product loop (within the registers) */
+    constexpr uint32_t MH_AHEAD = NW == 8 ? 8 : 4; /* operand reads ahead in the product loop (within the registers) */
     extern __shared__ __attribute__((aligned(16))) uint4 mh_lds[];
     uint4 *const Ab = mh_lds;                                  /* [2][NB * MH_PLANE] */
     float *const Wb = (float *)(mh_lds + 2 * NB * MH_PLANE);  /* [2][NB * MH_WP] */

@@ -494,6 +494,41 @@ def test_mfma_prefill_items_bias_accumulate(orc, rows, cols, ntok, q5):
         assert ok, worst
 
 
+@pytest.mark.parametrize("ntok,with_bias", [(70, False), (40, True)])
+def test_mfma_f16_small_items_and_nonfinite_flag(orc, ntok, with_bias):
+    """The f16-MFMA GEMM (28-block Q8 rows) on items of fewer rows than a subtile and across a subtile
+    edge (within 1e-5 of the exact contract), and its finiteness flag: clear for finite outputs, raised
+    by an infinite weight scale (model.c:309's check), cleared by reading it."""
+    cols, nb = 896, 28
+    x = synth.activations(31 + ntok, ntok, cols)
+    dbuf, qbuf, xd, xq = gpu_quantize(x)
+    items, wants = [], []
+    for i, rows in enumerate((5, 37)):
+        w = weights(False, 70 + i, rows, cols)
+        bias = synth.normal(80 + i, rows, 0.05) if with_bias else None
+        items.append((smq.QMat(smq.DeviceBuffer.from_array(w), rows, cols),
+                      smq.DeviceBuffer.from_array(bias) if bias is not None else None,
+                      smq.DeviceBuffer(ntok * rows * 4)))
+        wants.append((orc.mat_item(w, nb * Q8B, rows, bias, xd, xq, ntok, nb)[1], rows))
+    try:
+        smq.set_prefill_mfma(True)
+        smq.matmul(items, dbuf, qbuf, ntok)
+        smq.numeric_check()
+        for (_, _, y), (want, r) in zip(items, wants):
+            ok, worst = mfma_tolerance_ok(y.download(np.float32), want, ntok, r)
+            assert ok, worst
+        w = weights(False, 90, 20, cols)
+        w[Q8B * 3:Q8B * 3 + 4] = np.array([np.inf], np.float32).view(np.uint8)  # row 0, block 3: scale inf
+        yb = smq.DeviceBuffer(ntok * 20 * 4)
+        smq.matmul([(smq.QMat(smq.DeviceBuffer.from_array(w), 20, cols), None, yb)], dbuf, qbuf, ntok)
+        with pytest.raises(smq.SmqError) as e:
+            smq.numeric_check()
+        assert e.value.status == smq.SM_ERR_NUMERIC
+        smq.numeric_check()  # cleared
+    finally:
+        smq.set_prefill_mfma(False)
+
+
 def test_matmul_prefill_switch(orc):
     """smq_matmul with ntok > 1 takes the MFMA GEMM when selected (bias and
     finiteness still applied), the exact GEMM otherwise."""

@@ -258,9 +258,9 @@ __global__ __launch_bounds__(256) void k_mq8_reduce(MqArgs q) {
  *
  * Layout. Wave w holds the B operands of 16 tokens (t0 + 16w + l%16, K group
  * l/16) for every block, converted to f16 once (MH_NB x 4 registers), and
- * their scales. The tokens arrive by 16-byte loads of whole rows (14 per
- * lane) and pass through the wave's own LDS rows to reach operand order; the
- * weight buffers later take the same bytes. The weights stream through LDS in 16-row subtiles: thread
+ * their scales. The tokens and their scales arrive by 16-byte loads of
+ * whole rows (14 + 2 per lane) and pass through the wave's own LDS rows to
+ * reach operand order; the weight buffers later take the same bytes. The weights stream through LDS in 16-row subtiles: thread
  * (row, block) loads its 36-byte block (consecutive threads take consecutive
  * blocks of a row, one coalesced run) and writes the scale to Wb[block][row]
  * and the quants as f16 into the operand planes Ab[block][k group][row] (a
@@ -278,8 +278,9 @@ constexpr uint32_t MH_WP = 20;             /* scale plane pitch (floats) */
 constexpr uint32_t MH_TP = MH_NB * QK + 16; /* a staged token's pitch in bytes (padded: the operand reads spread) */
 constexpr uint32_t MH_BUF_BYTES = 2 * MH_NB * (MH_PLANE * 16 + MH_WP * 4); /* the two weight buffers */
 /* dynamic LDS: the weight buffers, or (before them, in the same bytes) the waves' token staging */
+constexpr uint32_t MH_WAVE_STAGE = 16 * MH_TP + 16 * MH_NB * 4; /* a wave's token rows, then their scales */
 constexpr size_t mh_lds_bytes(uint32_t nw) {
-    return (size_t)nw * 16 * MH_TP > MH_BUF_BYTES ? (size_t)nw * 16 * MH_TP : (size_t)MH_BUF_BYTES;
+    return (size_t)nw * MH_WAVE_STAGE > MH_BUF_BYTES ? (size_t)nw * MH_WAVE_STAGE : (size_t)MH_BUF_BYTES;
 }
 
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
@@ -417,7 +418,6 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_mh(MhArgs q) {
             (void *)a.xq, (short)0, (int)((size_t)ntok * xs * QK), 0x00020000);
         const __amdgpu_buffer_rsrc_t dsrc = __builtin_amdgcn_make_buffer_rsrc(
             (void *)a.xd, (short)0, (int)((size_t)ntok * xs * 4), 0x00020000);
-        const uint32_t dof = tok < ntok ? tok * xs * 4 : OOB;
         /* the wave's 16 token rows in 16-byte pieces, consecutive lanes on consecutive pieces */
         constexpr uint32_t PR = NB * QK / 16, NPC = 16 * PR / 64; /* pieces per row, per lane */
         static_assert(16 * PR % 64 == 0, "whole pieces per lane");
@@ -427,19 +427,26 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_mh(MhArgs q) {
             const uint32_t P = 64 * j + l, tp = P / PR, t = t0 + 16 * w + tp;
             pc[j] = __builtin_amdgcn_raw_buffer_load_b128(qsrc, t < ntok ? t * xs * QK + 16 * (P % PR) : OOB, 0, 0);
         }
+        /* the 16 tokens' scales in 16-byte pieces too (rows of NB floats, 16-byte aligned) */
+        constexpr uint32_t SPR = NB / 4, NSP = (16 * SPR + 63) / 64; /* scale pieces per row, per lane */
+        u4a sp[NSP];
 #pragma unroll
-        for (uint32_t j = 0; j < NB / 4; ++j) { /* the token's scales, four a load (rows 16-byte aligned) */
-            const auto v = __builtin_amdgcn_raw_buffer_load_b128(dsrc, dof + 16 * j, 0, 0);
-            xsc[4 * j] = __uint_as_float(v[0]);
-            xsc[4 * j + 1] = __uint_as_float(v[1]);
-            xsc[4 * j + 2] = __uint_as_float(v[2]);
-            xsc[4 * j + 3] = __uint_as_float(v[3]);
+        for (uint32_t j = 0; j < NSP; ++j) {
+            const uint32_t P = 64 * j + l, t = t0 + 16 * w + P / SPR;
+            sp[j] = __builtin_amdgcn_raw_buffer_load_b128(
+                dsrc, P < 16 * SPR && t < ntok ? (t * xs + 4 * (P % SPR)) * 4 : OOB, 0, 0);
         }
-        unsigned char *const stg = (unsigned char *)mh_lds + w * 16 * MH_TP; /* this wave's rows */
+        unsigned char *const stg = (unsigned char *)mh_lds + w * MH_WAVE_STAGE; /* this wave's rows */
+        float *const stg_d = (float *)(stg + 16 * MH_TP);                      /* and their scales */
 #pragma unroll
         for (uint32_t j = 0; j < NPC; ++j) {
             const uint32_t P = 64 * j + l;
             *(u4a *)(stg + (P / PR) * MH_TP + 16 * (P % PR)) = pc[j];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < NSP; ++j) {
+            const uint32_t P = 64 * j + l;
+            if (P < 16 * SPR) *(u4a *)(stg_d + 4 * P) = sp[j];
         }
         /* the wave's own rows: its writes are complete before its reads */
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -450,6 +457,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_mh(MhArgs q) {
             const uint2 v = *(const uint2 *)(stg + c16 * MH_TP + b * QK + 8 * g);
             const uint2 lo = i8x4_f16(v.x), hi = i8x4_f16(v.y);
             Bq[b] = __builtin_bit_cast(h8v, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < NB / 4; ++j) {
+            const float4 v = *(const float4 *)(stg_d + c16 * NB + 4 * j);
+            xsc[4 * j] = v.x;
+            xsc[4 * j + 1] = v.y;
+            xsc[4 * j + 2] = v.z;
+            xsc[4 * j + 3] = v.w;
         }
     }
     /* the scales in hand here, so no wait inside the subtile loop is for them */

@@ -2,13 +2,14 @@
  * quantize_q5_row, as src/quantize_main.c:107-121 runs it row by row).
  *
  * Per 32-element block: the signed extreme (the first element of largest
- * magnitude), then 21 candidate scales d_k = f16(extreme / -(14.5 + 0.1k))
- * (f32 arithmetic, binary16 rounding to nearest even, k = 0..20; a zero or
- * non-finite d_k is skipped); each candidate's squared error
- * sum_j (x_j - clamp(rint(x_j * (1/d_k)), -16, 15) * d_k)^2 is formed in
- * binary64 in element order; the first minimum wins; codes q + 16 are packed
- * as 16 nibble bytes (element j low, j + 16 high) after the f16 scale and the
- * 32-bit plane of fifth bits (docs/FORMAT.md:124-134).
+ * magnitude; a NaN element is never chosen), then 21 candidate scales
+ * d_k = f16(extreme / -(14.5 + 0.1k)) (f32 arithmetic, binary16 rounding to
+ * nearest even, k = 0..20; a zero or non-finite d_k is skipped); each
+ * candidate's squared error sum_j (x_j - clamp(rint(x_j * (1/d_k)), -16, 15) * d_k)^2
+ * is formed in binary64 in element order; the first minimum wins (with a NaN
+ * element every sum is NaN and the first kept candidate stays); codes q + 16
+ * are packed as 16 nibble bytes (element j low, j + 16 high) after the f16
+ * scale and the 32-bit plane of fifth bits (docs/FORMAT.md:124-134).
  *
  * Mapping: half a wave per block. Lane j holds element j (the extreme is a
  * 32-lane reduction over (|x|, -j), so ties keep the first element); lane k < 21
@@ -28,11 +29,13 @@ namespace {
 constexpr uint32_t CV_WG = 256;                 /* eight blocks per workgroup */
 constexpr uint32_t CV_BLOCKS = CV_WG / 32;
 
-/* lrintf(v * inv) clamped to the 5-bit range (kernels.c:1064-1067). */
+/* lrintf(v * inv) clamped to the 5-bit range (kernels.c:1064-1067). A NaN product takes
+ * -16: x86-64's lrintf returns LONG_MIN for it (cvtss2si's "integer indefinite"), which the
+ * clamp turns into -16 on the host the reference and the oracle run on. */
 __device__ __forceinline__ int q5_level(float v, float inv) {
     const float p = v * inv;
     const float r = __builtin_rintf(p);
-    return r < -16.0f ? -16 : (r > 15.0f ? 15 : (int)r);
+    return !(r >= -16.0f) ? -16 : (r > 15.0f ? 15 : (int)r);
 }
 
 /* binary32 -> binary16 bits, round to nearest even, overflow to infinity,
@@ -55,8 +58,9 @@ __global__ __launch_bounds__(CV_WG) void k_quantize_q5(const float *x, uint32_t 
     const float v = valid ? x[(size_t)row * cols + (size_t)b * 32 + j] : 0.0f;
     xs[slot][j] = v;
 
-    /* the signed extreme: largest |x|, first on ties (kernels.c:1092-1093) */
-    float best_a = fabsf(v);
+    /* the signed extreme: largest |x|, first on ties (kernels.c:1090-1091); a NaN never wins
+     * (fabsf(NaN) > m is false there), so it enters as -1 and an all-NaN block keeps extreme 0 */
+    float best_a = v == v ? fabsf(v) : -1.0f;
     uint32_t best_j = j;
 #pragma unroll
     for (int off = 16; off >= 1; off >>= 1) {
@@ -68,10 +72,11 @@ __global__ __launch_bounds__(CV_WG) void k_quantize_q5(const float *x, uint32_t 
         }
     }
     __syncthreads(); /* xs */
-    const float extreme = xs[slot][best_j];
+    const float extreme = best_a > 0.0f ? xs[slot][best_j] : 0.0f;
 
-    /* candidate k = lane j < 21: its scale and its error sum in element order */
-    double err = -1.0; /* skipped */
+    /* candidate k = lane j < 21: its scale and its error sum in element order (a NaN element
+     * makes every kept candidate's sum NaN) */
+    double err = -1.0; /* skipped: no sum of squares is -1 */
     float d = 0.0f;
     uint32_t h = 0;
     if (extreme != 0.0f && j <= 20) {
@@ -95,12 +100,13 @@ __global__ __launch_bounds__(CV_WG) void k_quantize_q5(const float *x, uint32_t 
     }
     errs[slot][j] = err;
     __syncthreads();
-    /* first minimum: the lowest k whose error is below every earlier kept one */
+    /* first minimum over the kept candidates, as `best < 0 || err < best` (kernels.c:1099): the
+     * first kept one is taken whatever its error, so NaN sums leave the first kept candidate */
     uint32_t win = 32;
     double best = -1.0;
     for (uint32_t k = 0; k <= 20; ++k) {
         const double e = errs[slot][k];
-        if (e >= 0.0 && (best < 0.0 || e < best)) {
+        if (e != -1.0 && (best < 0.0 || e < best)) {
             best = e;
             win = k;
         }

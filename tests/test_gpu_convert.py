@@ -64,6 +64,14 @@ def edge_rows():
     r = synth.normal(8, 96, 1.0); r[::3] *= 40; rows.append(r)  # clipping at -16 / 15
     r = np.full(96, 65504.0 * 14.5, np.float32); rows.append(r)
     r = np.full(96, -0.0, np.float32); rows.append(r)       # negative zeros
+    base = np.linspace(-1, 1, 96).astype(np.float32)
+    r = base.copy(); r[3] = np.nan; rows.append(r)          # NaN: never the extreme, first candidate kept
+    r = base.copy(); r[0] = np.nan; r[40] = np.nan; rows.append(r)
+    r = np.full(96, np.nan, np.float32); rows.append(r)     # all NaN: zero blocks
+    r = np.zeros(96, np.float32); r[9] = np.nan; rows.append(r)
+    r = base.copy(); r[5] = np.inf; rows.append(r)          # infinite element: scale 0, codes 16
+    r = base.copy(); r[33] = -np.inf; r[34] = np.nan; rows.append(r)
+    r = base.copy(); r[31] = np.nan; r[30] = -3.0; rows.append(r)
     return np.stack(rows)
 
 

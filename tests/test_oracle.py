@@ -406,6 +406,55 @@ def test_q5_rule_is_first_minimum_of_candidates(orc):
             assert np.array_equal(back, (d * lv).astype(np.float32))
 
 
+def q5_nonfinite_rows():
+    """Blocks with NaN and infinite elements (the public Q5 converter takes any floats)."""
+    rows = []
+    base = np.linspace(-1, 1, 64).astype(np.float32)
+    r = base.copy(); r[3] = np.nan; rows.append(r)                     # one NaN, finite extreme
+    r = base.copy(); r[0] = np.nan; r[40] = np.nan; rows.append(r)     # NaN first in its block
+    r = np.full(64, np.nan, np.float32); rows.append(r)                # all NaN: extreme 0, zero block
+    r = np.zeros(64, np.float32); r[9] = np.nan; rows.append(r)        # NaN among zeros
+    r = base.copy(); r[5] = np.inf; rows.append(r)                     # +inf: non-finite candidates
+    r = base.copy(); r[33] = -np.inf; r[34] = np.nan; rows.append(r)   # -inf and NaN in one block
+    r = base.copy(); r[31] = np.nan; r[31 - 1] = -3.0; rows.append(r)  # NaN next to the extreme
+    return np.stack(rows)
+
+
+def test_q5_rule_nonfinite_closed_form(orc):
+    """A NaN is never the extreme (fabsf(NaN) > m is false, kernels.c:1090-1091); with a NaN in the
+    block every candidate's error is NaN, so the first kept candidate (k = 0 here) stays
+    (kernels.c:1099), and the NaN element's code is 0 (x86-64 lrintf gives LONG_MIN, clamped to -16);
+    an infinite element makes every candidate non-finite: scale 0, every code 16."""
+    x = q5_nonfinite_rows()
+    out = orc.quantize_q5_rows(x).reshape(x.shape[0], 2, Q5B)
+    for r in range(x.shape[0]):
+        for b in range(2):
+            xb = x[r, b * 32:(b + 1) * 32]
+            blk = out[r, b]
+            h = int(blk[0]) | (int(blk[1]) << 8)
+            codes = [((blk[6 + (j % 16)] >> (4 * (j // 16))) & 15) | (((int.from_bytes(bytes(blk[2:6]), "little") >> j)
+                                                                     & 1) << 4) for j in range(32)]
+            if np.any(np.isinf(xb)) or not np.any(np.abs(np.nan_to_num(xb, nan=0.0)) > 0):
+                assert h == 0 and codes == [16] * 32, (r, b)
+                continue
+            finite = np.where(np.isnan(xb), 0.0, xb)
+            ext = xb[int(np.argmax(np.abs(finite)))]
+            if np.any(np.isnan(xb)):
+                want_h = int(np.float32(ext / -np.float32(14.5)).astype(np.float16).view(np.uint16))
+                assert h == want_h, (r, b)
+                d = np.uint16(h).view(np.float16).astype(np.float32)
+                inv = np.float32(1) / d
+                for j in range(32):
+                    want = 0 if np.isnan(xb[j]) else int(np.clip(np.rint(np.float32(xb[j] * inv)), -16, 15)) + 16
+                    assert codes[j] == want, (r, b, j)
+
+
+def test_q5_rule_nonfinite_matches_reference(orc, ref):
+    x = q5_nonfinite_rows()
+    for r in range(x.shape[0]):
+        assert np.array_equal(orc.quantize_q5_rows(x[r:r + 1]), ref.quantize_q5_row(x[r])), r
+
+
 def test_q5_round_trip_bound(orc):
     # tests/test_kernels.c:71-87
     g = LcgUniform(12345)

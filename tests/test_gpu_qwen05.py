@@ -6,7 +6,11 @@ model_forward, src/sampler.c:57-63, compiled from its sources into
 oracle/_ref) on the same file. Compared bit for bit: the prompt's last logits,
 the KV cache of every layer, teacher-forced logits at eight further positions,
 and the greedy tokens of the decode loop (HIP-graph replays) with the caches
-they leave behind."""
+they leave behind: 128 steps after the teacher-forced positions (to position
+647, past the 640 value rows the decode attention takes in one pass), and
+BASELINE's own sequence, a fresh 512-token prefill and then 128 greedy steps
+(src/main.c:571-600, src/sampler.c:57-63), whose decode step is captured again
+after that prefill."""
 import os
 
 import numpy as np
@@ -18,7 +22,7 @@ from smq_pkg import smodel, smoe, smq
 
 pytestmark = pytest.mark.gpu
 
-PROMPT, EXTRA, DECODE, CONTEXT = 512, 8, 24, 1024
+PROMPT, EXTRA, DECODE, CONTEXT = 512, 8, 128, 1024
 
 
 @pytest.fixture(scope="module")
@@ -79,3 +83,27 @@ def test_qwen05_prefill_decode_bit_exact(qwen05):
     for layer in range(layers):
         assert_same_f32(m.kv(layer, False, n), ref.kv(layer, False, n, kv_dim), f"keys after decode {layer}")
         assert_same_f32(m.kv(layer, True, n), ref.kv(layer, True, n, kv_dim), f"values after decode {layer}")
+
+
+def test_qwen05_baseline_sequence_bit_exact(qwen05):
+    """configs[4] as BASELINE states it: prefill 512 random ids, then 128 greedy decode steps from
+    position 512; tokens and every layer's caches (positions 0..638) against the reference."""
+    m, ref = qwen05
+    vocab, layers, kv_dim = 151936, 24, 128
+    prompt = np.random.default_rng(3001).integers(0, vocab, PROMPT).astype(np.uint32)
+    banned = np.zeros(vocab, np.uint8)
+    banned[256] = 1
+    m.set_banned(banned)
+    ref.set_banned(banned)
+    say("qwen05 baseline: prefill 512")
+    m.forward(prompt, 0, smodel.LOGITS_LAST)
+    ref.prefill(prompt, 0, True)
+    assert_same_f32(m.logits(1), ref.logits(1), "prompt logits")
+    say("qwen05 baseline: 128 greedy decode steps")
+    got = m.generate(PROMPT, 128)
+    want = ref.generate(PROMPT, 128)
+    assert got.tolist() == want.tolist()
+    n = PROMPT + 128 - 1
+    for layer in range(layers):
+        assert_same_f32(m.kv(layer, False, n), ref.kv(layer, False, n, kv_dim), f"keys {layer}")
+        assert_same_f32(m.kv(layer, True, n), ref.kv(layer, True, n, kv_dim), f"values {layer}")

@@ -28,8 +28,9 @@ ids, then 128 greedy decode steps as graph replays) with the reference's own
 model_forward on the same checkpoint as CPU rate and bit-exactness gate.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-       python bench.py --forward-only [--checkpoint PATH] [--decode-steps N] [--profile]   (configs[4]
+       python bench.py --forward-only [--checkpoint PATH] [--decode-steps N] [--runs R]   (configs[4]
                                 alone, for profiling; PATH from python bench.py --write-checkpoint PATH)
+       python bench.py --anchor   (the HBM read/copy anchor alone)
        python bench.py --q5-only   (configs[2] alone, for profiling)
        python bench.py --prefill-only   (the batched prefill GEMMs alone, for profiling)
 """
@@ -113,6 +114,25 @@ def timed_graph(graphs, reps):
     for i in range(reps):
         graphs[i % len(graphs)].launch()
     return smq.timer_stop() / reps
+
+
+SINGLE_SAMPLES = 11  # samples per single() shape: median reported, best beside it
+
+
+def single_timing(extra, name, fn, nbytes, per_graph, reps=2, note=None):
+    """Per-launch time of fn(i), i = 0..per_graph-1 captured in one graph (fn picks distinct weight
+    buffers by i): SINGLE_SAMPLES timings of `reps` replays each; `us` is the median, `best_us` the best."""
+    gs = [smq.capture(lambda: [fn(i) for i in range(per_graph)] and None)]
+    timed_graph(gs, 2)
+    med, best, _ = timed_samples(gs, reps, SINGLE_SAMPLES)
+    ms, bms = med / per_graph, best / per_graph
+    extra[name] = {"us": round(ms * 1e3, 2), "best_us": round(bms * 1e3, 2),
+                   "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                   "pct_hbm_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),
+                   "timing": f"median of {SINGLE_SAMPLES} samples of {reps} graph replays x {per_graph} launches"}
+    if note:
+        extra[name]["note"] = note
+    log(f"bench: {name} {ms * 1e3:.2f} us (best {bms * 1e3:.2f}) {extra[name]['GBps']} GB/s")
 
 
 def timed_samples(graphs, reps, samples):
@@ -248,14 +268,16 @@ def main():
         log("bench: init", smq.init(0), smq.kernels_select())
         extra = {}
 
-        def single(name, fn, nbytes, per_graph, reps=10, note=None):
-            gs = [smq.capture(lambda: [fn(i) for i in range(per_graph)] and None)]
-            timed_graph(gs, 2)
-            ms = timed_graph(gs, reps) / per_graph
-            extra[name] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                           "pct_hbm_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
-            log(f"bench: {name} {ms * 1e3:.2f} us {extra[name]['GBps']} GB/s")
+        def single(name, fn, nbytes, per_graph, reps=2, note=None):
+            single_timing(extra, name, fn, nbytes, per_graph, reps, note)
         q5_extra(single, extra)
+        print(json.dumps(extra), flush=True)
+        return
+    if len(sys.argv) > 1 and sys.argv[1] == "--anchor":
+        # the HBM bandwidth anchor alone (the program its rocprofv3 summary profiles)
+        log("bench: init", smq.init(0), smq.kernels_select())
+        extra = {}
+        hbm_anchor(extra)
         print(json.dumps(extra), flush=True)
         return
     if len(sys.argv) > 1 and sys.argv[1] == "--prefill-only":
@@ -269,18 +291,17 @@ def main():
     if len(sys.argv) > 1 and sys.argv[1] == "--forward-only":
         # configs[4] alone (no CPU leg): the program the decode-step rocprofv3 summaries profile;
         # --checkpoint PATH takes a file written by --write-checkpoint (and leaves it in place);
-        # --decode-steps N times N greedy steps instead of 128; --profile runs the prefill and one timed
-        # decode only (the sequence the rocprofv3 kernel trace of the decode step is taken over)
+        # --decode-steps N times N greedy steps instead of 128; --runs R timed prefill + decode runs
         fp = argparse.ArgumentParser()
         fp.add_argument("--forward-only", action="store_true")
         fp.add_argument("--checkpoint", default=None)
         fp.add_argument("--decode-steps", type=int, default=128)
-        fp.add_argument("--profile", action="store_true")
+        fp.add_argument("--runs", type=int, default=FORWARD_RUNS)
         fa = fp.parse_args()
         log("bench: init", smq.init(0), smq.kernels_select())
         extra = {}
         model_forward_extra(argparse.Namespace(no_cpu=True, checkpoint=fa.checkpoint, decode_steps=fa.decode_steps,
-                                               profile=fa.profile), extra)
+                                               runs=fa.runs), extra)
         print(json.dumps(extra), flush=True)
         return
     ap = argparse.ArgumentParser()
@@ -304,8 +325,9 @@ def main():
     head = [smq.DeviceBuffer.from_array(head_host)]
     log(f"bench: generated and uploaded 24 layers + LM head in {time.time() - t0:.1f}s")
     copies = [model, [layer.copy() for layer in model]]
-    head.append(smq.DeviceBuffer(head[0].nbytes))
-    head[1].copy_from(head[0])
+    for _ in range(3):  # four LM-head copies in turn: 613 MB, past twice the 256 MB Infinity Cache
+        head.append(smq.DeviceBuffer(head[0].nbytes))
+        head[-1].copy_from(head[0])
 
     # activations per layer: x (attention/FFN input, 896) and h (FFN hidden, 4864)
     ax = [Act(2000 + l, 1, DIM) for l in range(LAYERS)]
@@ -425,21 +447,12 @@ def main():
             "GBps": round(dec_bytes / (dec_ms * 1e-3) / 1e9, 1)}
         log(f"bench: decode matmuls {dec_ms * 1e3:.1f} us/token = {1000 / dec_ms:.0f} tok/s")
 
-        def single(name, fn, nbytes, per_graph, reps=10, note=None):
-            """Per-launch time of fn(i), i = 0..per_graph-1 captured in one graph
-            (fn picks distinct weight buffers by i), timed over `reps` replays."""
-            gs = [smq.capture(lambda: [fn(i) for i in range(per_graph)] and None)]
-            timed_graph(gs, 2)
-            ms = timed_graph(gs, reps) / per_graph
-            extra[name] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                           "pct_hbm_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
-            if note:
-                extra[name]["note"] = note
-            log(f"bench: {name} {ms * 1e3:.2f} us {extra[name]['GBps']} GB/s")
+        def single(name, fn, nbytes, per_graph, reps=2, note=None):
+            single_timing(extra, name, fn, nbytes, per_graph, reps, note)
 
         single("c3_lm_head_gemv_151936x896",
-               lambda i: smq.gemm_q8(head[i % 2], 28 * 36, ax[0].d, ax[0].q, VOCAB, 1, 28, logits, VOCAB),
-               q8_bytes(VOCAB, DIM), 16, note="2 copies of 153 MB alternated (306 MB > 256 MB Infinity Cache)")
+               lambda i: smq.gemm_q8(head[i % 4], 28 * 36, ax[0].d, ax[0].q, VOCAB, 1, 28, logits, VOCAB),
+               q8_bytes(VOCAB, DIM), 16, note="4 copies of 153 MB in turn (613 MB > 2 x 256 MB Infinity Cache)")
         single("c1_down_gemv_896x4864",
                lambda i: smq.matmul([(copies[i // LAYERS % 2][i % LAYERS].qmat("down"), None, y_out[0])], ah[0].d,
                                     ah[0].q, 1),
@@ -471,9 +484,9 @@ def main():
                                     ax[0].q, 1),
                q8_bytes(DIM, Q_DIM), 2 * LAYERS, note="48 distinct 0.9 MB matrices in turn")
         # configs[0] streamed: one grouped launch of 48 distinct 896x896 GEMVs (each with one of the 24
-        # layer activations), 384 matrices in turn (347 MB > the 256 MB Infinity Cache), as the reference's
-        # tests/bench_matmul.c:112-117 rotates a matrix past the caches
-        n0, g0 = 384, 48
+        # layer activations), 576 matrices in turn (520 MB > twice the 256 MB Infinity Cache), as the
+        # reference's tests/bench_matmul.c:112-117 rotates a matrix past the caches
+        n0, g0 = 576, 48
         c0_bufs = [smq.DeviceBuffer(copies[0][0].dev["o"][0].nbytes) for _ in range(n0)]
         for k, b in enumerate(c0_bufs):
             b.copy_from(copies[k % 2][k // 2 % LAYERS].dev["o"][0])
@@ -484,7 +497,7 @@ def main():
             smq.gemv_grouped([(smq.QMat(c0_bufs[base + j], DIM, Q_DIM), None, c0_out[j], False, ax[j % LAYERS].d,
                                ax[j % LAYERS].q) for j in range(g0)])
         single("c0_gemv_896x896_grouped48", c0_grouped, g0 * q8_bytes(DIM, Q_DIM), n0 // g0,
-               note="one launch of 48 distinct 896x896 GEMVs, 384 matrices (347 MB) in turn")
+               note="one launch of 48 distinct 896x896 GEMVs, 576 matrices (520 MB) in turn")
         smq.synchronize()
         one = smq.DeviceBuffer(DIM * 4)
         smq.matmul([(smq.QMat(c0_bufs[(n0 // g0 - 1) * g0 + 5], DIM, Q_DIM), None, one)], ax[5].d, ax[5].q, 1)
@@ -512,11 +525,11 @@ def main():
         hx = Act(4100, 64, DIM)
         hout = smq.DeviceBuffer(64 * VOCAB * 4)
         single("c3_lm_head_gemm_151936x896_b64",
-               lambda i: smq.gemm_q8(head[i % 2], 28 * 36, hx.d, hx.q, VOCAB, 64, 28, hout, VOCAB),
+               lambda i: smq.gemm_q8(head[i % 4], 28 * 36, hx.d, hx.q, VOCAB, 64, 28, hout, VOCAB),
                q8_bytes(VOCAB, DIM, 64), 4)
         single("c3_lm_head_mfma_151936x896_b64",
-               lambda i: smq.gemm_q8_mfma(head[i % 2], 28 * 36, hx.d, hx.q, VOCAB, 64, 28, hout, VOCAB),
-               q8_bytes(VOCAB, DIM, 64), 4)
+               lambda i: smq.gemm_q8_mfma(head[i % 4], 28 * 36, hx.d, hx.q, VOCAB, 64, 28, hout, VOCAB),
+               q8_bytes(VOCAB, DIM, 64), 8)
         del hout
         # the reference's own matmul benchmark shape (tests/bench_matmul.c:111-117): one Q8 matrix of 65536 rows x
         # 4864 (152 blocks, 342 MiB) against 1 token (decode GEMV) and 32 tokens (prefill); two copies alternate
@@ -545,6 +558,7 @@ def main():
             e["tok_s_eq_556MiB"] = round(ntok / (556 * 2 ** 20 / (rb_rows * rb_nb * 36) * e["us"] * 1e-6), 1)
         del rb, rout
         q5_extra(single, extra)
+        hbm_anchor(extra)
 
     if not args.no_extra:
         model_forward_extra(args, extra)
@@ -640,24 +654,16 @@ def model_forward_extra(args, extra):
         m.forward(prompt, 0, smodel.LOGITS_LAST)  # warm-up: first launches, graph capture
         m.generate(512, 5)
         smq.set_checks(False)
-        # --profile: one prefill, then decode only. Under rocprofv3's kernel trace, replaying the decode graph
-        # after a second eager prefill has died inside hipGraphLaunch; without the profiler the full sequence
-        # below runs every time.
-        if getattr(args, "profile", False):
-            t0 = time.time()
-            m.generate(512, nsteps + 1)
-            dec_s = time.time() - t0
-            extra["c4_qwen05_forward"] = {"decode_tok_s": round(nsteps / dec_s, 1), "decode_steps": nsteps,
-                                          "what": "profile run: prefill 512 ids, 5 untimed and then N timed greedy "
-                                                  "decode steps"}
-            log(f"bench: qwen0.5B profile run: decode {nsteps / dec_s:.1f} tok/s")
-            return
+        # each run: the prefill (which drops the captured decode step), the decode step captured again
+        # (untimed), then the greedy steps as graph replays
+        nruns = getattr(args, "runs", FORWARD_RUNS)
         runs = []
-        for _ in range(FORWARD_RUNS):
+        for _ in range(nruns):
             t0 = time.time()
             m.forward(prompt, 0, smodel.LOGITS_LAST)
             t1 = time.time()
             gl = m.logits(1)
+            m.prepare_decode()
             t1b = time.time()
             toks = m.generate(512, nsteps + 1)
             t2 = time.time()
@@ -674,7 +680,7 @@ def model_forward_extra(args, extra):
                      f"prefill 512 ids in one batch then {nsteps} greedy decode steps (HIP graph per step), BOS banned",
              "decode_tok_s": round(nsteps / dec_s, 1), "decode_ms_per_token": round(dec_s / nsteps * 1e3, 3),
              "prefill_tok_s": round(512 / pre_s, 1), "prefill_ms": round(pre_s * 1e3, 2),
-             "timing": f"median of {FORWARD_RUNS} runs (prefill, then the decode steps); best: decode "
+             "timing": f"median of {nruns} runs (prefill, then the decode steps); best: decode "
                        f"{nsteps / dec_best:.1f} tok/s, prefill {512 / pre_best:.1f} tok/s",
              "prefill_mfma_tok_s": round(512 / mfma_s, 1),
              "prefill_mfma_note": "MFMA prefill (f16 MFMA on the 896-wide Q8 rows, int8 MFMA on the others): exact block sums applied in block order (the relaxed contract, within 1e-5; not bit-exact to the eight-lane one)",
@@ -780,17 +786,58 @@ def q5_extra(single, extra):
         e["pct_int8_peak"] = round(100 * ops / (e["us"] * 1e-6) / 5.0e15, 2)
 
 
+def hbm_anchor(extra, gib=2):
+    """What this device's HBM delivers to plain kernels (smq_stream_read / smq_stream_copy: coalesced
+    16-byte pieces, grid-stride, eight in flight per thread) over a `gib` GiB buffer, swept over launch
+    shapes; each shape is a graph of 4 launches timed 5 times (median of the samples), the best
+    shape reported with the whole sweep beside it."""
+    nbytes = gib << 30
+    src = smq.DeviceBuffer(nbytes)
+    src.fill(1)
+    dst = smq.DeviceBuffer(nbytes // 2)
+    sink = smq.DeviceBuffer(4)
+    smq.synchronize()
+    sweep = {}
+    for nt in (True, False):
+        for threads in (256, 512, 1024):
+            for wgs in (256, 512, 1024, 2048, 4096):
+                if wgs * threads > 4096 * 512:
+                    continue
+                g = [smq.capture(lambda: [smq.stream_read(src, nbytes, wgs, threads, nt, sink) for _ in range(4)]
+                                 and None)]
+                timed_graph(g, 1)
+                med, best, _ = timed_samples(g, 1, 5)
+                sweep[f"read_{'nt' if nt else 'plain'}_{wgs}x{threads}"] = round(nbytes * 4 / (med * 1e-3) / 1e9, 1)
+    copy = {}
+    half = nbytes // 2
+    for nt in (True, False):
+        for threads, wgs in ((256, 1024), (512, 1024), (512, 2048), (1024, 1024)):
+            g = [smq.capture(lambda: [smq.stream_copy(dst, src, half, wgs, threads, nt) for _ in range(4)] and None)]
+            timed_graph(g, 1)
+            med, best, _ = timed_samples(g, 1, 5)
+            copy[f"copy_{'nt' if nt else 'plain'}_{wgs}x{threads}"] = round(2 * half * 4 / (med * 1e-3) / 1e9, 1)
+    del src, dst
+    best_read = max(sweep, key=sweep.get)
+    best_copy = max(copy, key=copy.get)
+    extra["hbm_anchor"] = {
+        "what": f"plain coalesced 16-byte streaming kernels over {gib} GiB (read: nothing written; copy: bytes read "
+                "+ bytes written), medians of 5 samples of 4 graph-captured launches, per launch shape "
+                "(workgroups x threads)",
+        "read_GBps": sweep[best_read], "read_shape": best_read,
+        "read_pct_hbm_peak": round(100 * sweep[best_read] / HBM_PEAK_GBS, 1),
+        "copy_GBps": copy[best_copy], "copy_shape": best_copy,
+        "read_sweep": sweep, "copy_sweep": copy}
+    log(f"bench: HBM anchor read {sweep[best_read]} GB/s ({best_read}), copy {copy[best_copy]} GB/s ({best_copy})")
+
+
 def prefill_only(extra):
     """configs[1] gate/up 9728x896 and down 896x4864 at batch 128, configs[3] 151936x896 at batch 64: each as
     a graph of launches over two weight copies, exact GEMM and int8-MFMA GEMM."""
-    def single(name, fn, nbytes, ops, per_graph, reps=10):
-        gs = [smq.capture(lambda: [fn(i) for i in range(per_graph)] and None)]
-        timed_graph(gs, 2)
-        ms = timed_graph(gs, reps) / per_graph
-        extra[name] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                       "int_TOPS": round(ops / (ms * 1e-3) / 1e12, 2),
-                       "pct_int8_peak": round(100 * ops / (ms * 1e-3) / 5.0e15, 2)}
-        log(f"bench: {name} {ms * 1e3:.2f} us {extra[name]['int_TOPS']} TOPS")
+    def single(name, fn, nbytes, ops, per_graph, reps=2):
+        single_timing(extra, name, fn, nbytes, per_graph, reps)
+        us = extra[name]["us"]
+        extra[name]["int_TOPS"] = round(ops / (us * 1e-6) / 1e12, 2)
+        extra[name]["pct_int8_peak"] = round(100 * ops / (us * 1e-6) / 5.0e15, 2)
 
     shapes = {"gate_up": (2 * HIDDEN, DIM, 128), "down": (DIM, HIDDEN, 128), "lm_head": (VOCAB, DIM, 64)}
     for name, (rows, cols, ntok) in shapes.items():

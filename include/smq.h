@@ -84,7 +84,10 @@ int smq_kernels_fast(void);          /* kernels.h:78 */
 size_t smq_gemm_scratch_bytes(uint32_t nb);
 /* Host-side bounds checks of every operand range against its device
  * allocation before a launch (no reference counterpart). On by default, or
- * off when the environment sets SMQ_CHECKS=0. */
+ * off when the environment sets SMQ_CHECKS=0. Ranges inside smq_malloc
+ * allocations are checked against the library's own record; other device
+ * memory through the runtime, except during a capture, where such ranges are
+ * taken as given (no runtime call runs inside a capture). */
 void smq_set_checks(int on);
 
 /* ---- activation quantizer (src/kernels.h:183-187, kernels.c:912-935) ---- */
@@ -357,6 +360,19 @@ smq_status smq_memset(void *dst, int value, size_t bytes);
 smq_status smq_timer_start(void);
 /* Records a stop event, waits for it, returns milliseconds since start (<0 on error). */
 double smq_timer_stop(void);
+
+/* ---- HBM bandwidth anchors (no reference counterpart: measurement) ------
+ * Plain kernels that read (smq_stream_read) or copy (smq_stream_copy) `bytes`
+ * (a multiple of 16, 16-byte aligned) with coalesced 16-byte loads, so a
+ * GEMV's GB/s can be read against what the device's HBM delivers. A grid of
+ * `workgroups` x `threads` (64..1024, a multiple of 64) threads; nontemporal
+ * selects non-temporal loads and stores. The read writes nothing (`sink`, a
+ * device word, is written only for one improbable data pattern).
+ * Asynchronous, capturable. */
+smq_status smq_stream_read(const void *p, size_t bytes, uint32_t workgroups, uint32_t threads, int nontemporal,
+                           uint32_t *sink);
+smq_status smq_stream_copy(void *dst, const void *src, size_t bytes, uint32_t workgroups, uint32_t threads,
+                           int nontemporal);
 
 #ifdef __cplusplus
 }

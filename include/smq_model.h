@@ -113,7 +113,9 @@ size_t smq_model_device_bytes(const smq_model *m);
  * pos0..pos0+n-1; LOGITS_LAST leaves the last token's logits in row 0,
  * LOGITS_ALL n rows. Synchronizes; SMQ_ERR_NUMERIC on a non-finite
  * activation, SMQ_ERR_RANGE on an id outside the vocabulary or a batch
- * past the context. */
+ * past the context. A batch (n > 1) drops the captured decode step, so no
+ * decode graph is replayed after launches made since its capture; the next
+ * smq_model_generate (or smq_model_prepare_decode) captures it again. */
 smq_status smq_model_forward(smq_model *m, const uint32_t *tokens, uint32_t n, uint32_t pos0, int mode);
 /* model_prefill (model.c:703-714): n tokens in batch-sized chunks. */
 smq_status smq_model_prefill(smq_model *m, const uint32_t *tokens, uint32_t n, uint32_t pos0, int last_logits);
@@ -135,6 +137,10 @@ smq_status smq_model_set_banned(smq_model *m, const unsigned char *banned);
  * waits once at the end. It does not stop at EOS: a caller stops where the
  * reference would (the tokens up to EOS are the same). */
 smq_status smq_model_generate(smq_model *m, uint32_t pos, uint32_t ntokens, uint32_t *out);
+/* No reference counterpart: captures the decode step now if none is held
+ * (smq_model_generate otherwise does it on its first call after a batch
+ * forward), so a timed generate holds replays only. Synchronizes. */
+smq_status smq_model_prepare_decode(smq_model *m);
 
 /* No reference counterpart (the reference's fixtures are built the same way by
  * tests/support/fixture.ts and its Q8 writer tools/q8pack.c:38-44): writes a

@@ -135,6 +135,8 @@ _SIGS = {
     "smq_graph_destroy": (None, [_vp]),
     "smq_timer_start": (ctypes.c_int, []),
     "smq_timer_stop": (ctypes.c_double, []),
+    "smq_stream_read": (ctypes.c_int, [_vp, _sz, _u32, _u32, ctypes.c_int, _vp]),
+    "smq_stream_copy": (ctypes.c_int, [_vp, _vp, _sz, _u32, _u32, ctypes.c_int]),
 }
 
 _lib = None
@@ -567,3 +569,13 @@ def timer_stop():
     ms = load().smq_timer_stop()
     _check()
     return ms
+
+
+def stream_read(buf, nbytes, workgroups, threads, nontemporal, sink):
+    """smq_stream_read: the HBM read anchor (coalesced 16-byte loads, nothing written)."""
+    _check(load().smq_stream_read(_p(buf), nbytes, workgroups, threads, int(bool(nontemporal)), _p(sink)))
+
+
+def stream_copy(dst, src, nbytes, workgroups, threads, nontemporal):
+    """smq_stream_copy: the HBM copy anchor."""
+    _check(load().smq_stream_copy(_p(dst), _p(src), nbytes, workgroups, threads, int(bool(nontemporal))))

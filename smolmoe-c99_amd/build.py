@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libsmq_gfx950.so")
 SOURCES = [os.path.join(HERE, "csrc", f) for f in ("smq_kernels.hip", "smq_gemv.hip", "smq_decode.hip", "smq_mfma.hip", "smq_fused.hip", "smq_convert.hip",
-                                                     "smq_api.cpp")]
+                                                     "smq_anchor.hip", "smq_api.cpp")]
 HEADERS = [os.path.join(HERE, "csrc", "smq_internal.h"), os.path.join(HERE, "csrc", "smq_device.h"),
            os.path.join(ROOT, "include", "smq.h")]
 OBJ_DIR = os.path.join(HERE, "_build")

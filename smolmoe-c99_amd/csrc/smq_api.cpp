@@ -12,6 +12,8 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
 
 #include "smq.h"
 #include "smq_internal.h"
@@ -40,6 +42,25 @@ struct Context {
 Context g;
 thread_local smq_status t_status = SMQ_OK;
 thread_local char t_message[1024];
+/* set between smq_capture_begin and smq_capture_end on the capturing thread */
+thread_local bool t_capturing = false;
+
+/* The library's own allocations (smq_malloc), base -> size: extent checks look here first, so a
+ * check needs no runtime call for them, and none at all runs inside a stream capture. */
+std::mutex g_alloc_mu;
+std::map<uintptr_t, size_t> g_allocs;
+
+/* 1: inside a registered allocation, 0: outside it, -1: not a registered allocation. */
+int registry_extent(uintptr_t q, size_t bytes, uintptr_t &base, size_t &size) {
+    std::lock_guard<std::mutex> lock(g_alloc_mu);
+    auto it = g_allocs.upper_bound(q);
+    if (it == g_allocs.begin()) return -1;
+    --it;
+    base = it->first;
+    size = it->second;
+    if (q - base >= size) return -1;
+    return bytes <= size - (q - base) ? 1 : 0;
+}
 
 smq_status set_status(smq_status s, const char *fmt, ...) {
     t_status = s;
@@ -74,6 +95,19 @@ bool extent_ok(const void *p, size_t bytes, const char *what) {
         return false;
     }
     if (!g.checks) return true;
+    const uintptr_t q = (uintptr_t)p;
+    uintptr_t rb = 0;
+    size_t rsize = 0;
+    const int known = registry_extent(q, bytes, rb, rsize);
+    if (known == 1) return true;
+    if (known == 0) {
+        set_status(SMQ_ERR_RANGE, "%s: %zu bytes at offset %zu exceed its allocation of %zu bytes", what, bytes,
+                   (size_t)(q - rb), rsize);
+        return false;
+    }
+    /* memory from another allocator: the runtime's lookup, never while this thread captures (the
+     * captured launches then rest on the caller's own extents) */
+    if (t_capturing) return true;
     hipDeviceptr_t base = nullptr;
     size_t size = 0;
     if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p) != hipSuccess) {
@@ -81,7 +115,7 @@ bool extent_ok(const void *p, size_t bytes, const char *what) {
         set_status(SMQ_ERR_RANGE, "%s is not a device allocation", what);
         return false;
     }
-    const uintptr_t b = (uintptr_t)base, q = (uintptr_t)p;
+    const uintptr_t b = (uintptr_t)base;
     if (q < b || q - b > size || bytes > size - (q - b)) {
         set_status(SMQ_ERR_RANGE, "%s: %zu bytes at offset %zu exceed its allocation of %zu bytes", what, bytes,
                    (size_t)(q - b), size);
@@ -1067,11 +1101,18 @@ void *smq_malloc(size_t bytes) {
     if (!ready()) return nullptr;
     void *p = nullptr;
     if (!hip_ok(hipMalloc(&p, bytes ? bytes : 1), "hipMalloc")) return nullptr;
+    std::lock_guard<std::mutex> lock(g_alloc_mu);
+    g_allocs[(uintptr_t)p] = bytes ? bytes : 1;
     return p;
 }
 
 void smq_free(void *p) {
-    if (p) (void)hipFree(p);
+    if (!p) return;
+    {
+        std::lock_guard<std::mutex> lock(g_alloc_mu);
+        g_allocs.erase((uintptr_t)p);
+    }
+    (void)hipFree(p);
 }
 
 smq_status smq_memcpy_htod(void *dst, const void *src, size_t bytes) {
@@ -1113,14 +1154,17 @@ smq_status smq_capture_begin(void) {
     if (g.cur != g.own) return set_status(SMQ_ERR_STATE, "capture needs the library stream");
     /* thread-local mode: a call from this thread that may not be captured (a synchronizing copy, an
      * allocation) fails the capture instead of being recorded or run behind the graph's back */
-    return hip_ok(hipStreamBeginCapture(g.cur, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture") ? SMQ_OK
-                                                                                                            : t_status;
+    if (!hip_ok(hipStreamBeginCapture(g.cur, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture"))
+        return t_status;
+    t_capturing = true;
+    return SMQ_OK;
 }
 
 void *smq_capture_end(void) {
     if (!ready()) return nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    t_capturing = false;
     if (!hip_ok(hipStreamEndCapture(g.cur, &graph), "hipStreamEndCapture")) return nullptr;
     const bool ok = hip_ok(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
     (void)hipGraphDestroy(graph);
@@ -1135,6 +1179,40 @@ smq_status smq_graph_launch(void *graph) {
 
 void smq_graph_destroy(void *graph) {
     if (graph) (void)hipGraphExecDestroy((hipGraphExec_t)graph);
+}
+
+static bool anchor_shape_ok(const void *a, const void *b, size_t bytes, uint32_t wgs, uint32_t threads) {
+    if (((uintptr_t)a | (uintptr_t)b | bytes) & 15u) {
+        set_status(SMQ_ERR_RANGE, "stream: buffers and size must be 16-byte aligned");
+        return false;
+    }
+    if (!wgs || threads < 64 || threads > 1024 || threads % 64) {
+        set_status(SMQ_ERR_RANGE, "stream: grid %u x %u", wgs, threads);
+        return false;
+    }
+    return true;
+}
+
+smq_status smq_stream_read(const void *p, size_t bytes, uint32_t workgroups, uint32_t threads, int nontemporal,
+                           uint32_t *sink) {
+    if (!ready()) return t_status;
+    if (!anchor_shape_ok(p, nullptr, bytes, workgroups, threads)) return t_status;
+    if (!extent_ok(p, bytes, "stream source") || !extent_ok(sink, 4, "sink")) return t_status;
+    return hip_ok(smq::launch_stream_read(p, bytes, workgroups, threads, nontemporal != 0, sink, g.cur),
+                  "stream_read")
+               ? SMQ_OK
+               : t_status;
+}
+
+smq_status smq_stream_copy(void *dst, const void *src, size_t bytes, uint32_t workgroups, uint32_t threads,
+                           int nontemporal) {
+    if (!ready()) return t_status;
+    if (!anchor_shape_ok(dst, src, bytes, workgroups, threads)) return t_status;
+    if (!extent_ok(src, bytes, "stream source") || !extent_ok(dst, bytes, "stream destination")) return t_status;
+    return hip_ok(smq::launch_stream_copy(dst, src, bytes, workgroups, threads, nontemporal != 0, g.cur),
+                  "stream_copy")
+               ? SMQ_OK
+               : t_status;
 }
 
 smq_status smq_timer_start(void) {

@@ -22,9 +22,13 @@ typedef float f4v __attribute__((ext_vector_type(4))); /* register-resident floa
 /* Exact int32 sum of four int8 products plus c (v_dot4_i32_i8). The
  * compiler's own instruction, not inline assembly: a dot product's result
  * needs wait states before a VALU reads it, and only the compiler's hazard
- * pass inserts them. */
+ * pass inserts them. The clamp bit selects the three-operand VOP3P form
+ * (the two-operand v_dot4c has no clamp): without it the compiler emits
+ * v_dot4c, which accumulates into its destination, and copies c (or a zero)
+ * there first, one v_mov per product. Clamping saturates only past the int32
+ * range; every sum here is below 2^24 in magnitude, so the value is the same. */
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
-    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, true);
 }
 
 /* IEEE binary16 bits (the low 16 bits of h) to float: one v_cvt_f32_f16,

@@ -37,7 +37,8 @@ namespace {
 
 constexpr uint32_t CT_NT = 512;
 
-__device__ __forceinline__ uint32_t find_ct_item(const GroupArgs &g, uint32_t wg) {
+template <class GA>
+__device__ __forceinline__ uint32_t find_ct_item(const GA &g, uint32_t wg) {
     uint32_t lo = 0, hi = g.nitems; /* last item with wg_begin <= wg */
     while (hi - lo > 1) {
         const uint32_t mid = (lo + hi) / 2;
@@ -56,8 +57,8 @@ struct CtBuf {
     float sink[64];
 };
 
-template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT, uint32_t D>
-__global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gemv_ct(GroupArgs g) {
+template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT, uint32_t D, class GA>
+__global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gemv_ct(GA g) {
     static_assert(NB % 4 == 0, "rows of whole 16-byte pieces");
     constexpr uint32_t C16 = 9 * NB / 4;       /* 16-byte pieces per row */
     constexpr uint32_t TCH = RT * C16;         /* pieces per tile */
@@ -212,8 +213,8 @@ __global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) v
  * activation words of one 16-byte LDS read. */
 constexpr uint32_t CK_KC = 32;
 
-template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT>
-__global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gemv_ck(GroupArgs g) {
+template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT, class GA>
+__global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gemv_ck(GA g) {
     constexpr uint32_t KC = CK_KC;
     constexpr uint32_t NCH = (NB + KC - 1) / KC;    /* chunks per row */
     constexpr uint32_t KL = NB - (NCH - 1) * KC;    /* blocks of the last chunk */
@@ -359,7 +360,8 @@ __global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) v
 
 /* every item a share of the resident workgroups of kernel k in proportion to its tiles of rt rows
  * (at least one, at most one per tile), each a contiguous tile range */
-hipError_t launch_tiles(const void *k, int &resident, uint32_t rt, GroupArgs &g, hipStream_t s) {
+template <class GA>
+hipError_t launch_tiles(const void *k, int &resident, uint32_t rt, GA &g, hipStream_t s) {
     if (!resident) {
         int per_cu = 0, dev = 0, cus = 0;
         hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, CT_NT, 0);
@@ -385,16 +387,27 @@ hipError_t launch_tiles(const void *k, int &resident, uint32_t rt, GroupArgs &g,
     return e != hipSuccess ? e : hipGetLastError();
 }
 
+/* a launch of few items takes the kernel built for the small argument struct */
 template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT, uint32_t D>
 hipError_t launch_ct_shape(GroupArgs &g, hipStream_t s) {
+    if (g.nitems <= FEW_GROUP_ITEMS) {
+        static int resident = 0;
+        GroupArgsFew f = group_args_few(g);
+        return launch_tiles((const void *)k_gemv_ct<FAST, BP, NB, RT, CPT, D, GroupArgsFew>, resident, RT, f, s);
+    }
     static int resident = 0;
-    return launch_tiles((const void *)k_gemv_ct<FAST, BP, NB, RT, CPT, D>, resident, RT, g, s);
+    return launch_tiles((const void *)k_gemv_ct<FAST, BP, NB, RT, CPT, D, GroupArgs>, resident, RT, g, s);
 }
 
 template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT>
 hipError_t launch_ck_shape(GroupArgs &g, hipStream_t s) {
+    if (g.nitems <= FEW_GROUP_ITEMS) {
+        static int resident = 0;
+        GroupArgsFew f = group_args_few(g);
+        return launch_tiles((const void *)k_gemv_ck<FAST, BP, NB, RT, CPT, GroupArgsFew>, resident, RT, f, s);
+    }
     static int resident = 0;
-    return launch_tiles((const void *)k_gemv_ck<FAST, BP, NB, RT, CPT>, resident, RT, g, s);
+    return launch_tiles((const void *)k_gemv_ck<FAST, BP, NB, RT, CPT, GroupArgs>, resident, RT, g, s);
 }
 
 /* 16 rows of 28 blocks per step: 1008 pieces in 1024 thread slots; one tile in flight per

@@ -55,12 +55,30 @@ struct GroupItem {
     int accumulate;
     uint32_t wg_begin, nwg; /* pinned launch: this item's workgroups */
 };
-struct GroupArgs {
-    GroupItem item[MAX_GROUP_ITEMS];
+template <uint32_t N>
+struct GroupArgsN {
+    GroupItem item[N];
     uint32_t nitems, nb, total_tiles;
     int *flag;
     uint32_t cpr, nch, rt; /* pinned launch: tasks per chunk, chunks per row, rows per tile */
 };
+using GroupArgs = GroupArgsN<MAX_GROUP_ITEMS>;
+/* A launch of at most FEW_GROUP_ITEMS items (a single matmul, the decode LM head) passes this
+ * copy by value: about 0.3 KB of kernel arguments instead of 3.5 KB. */
+constexpr uint32_t FEW_GROUP_ITEMS = 4;
+using GroupArgsFew = GroupArgsN<FEW_GROUP_ITEMS>;
+inline GroupArgsFew group_args_few(const GroupArgs &g) {
+    GroupArgsFew f;
+    for (uint32_t i = 0; i < FEW_GROUP_ITEMS; ++i) f.item[i] = g.item[i];
+    f.nitems = g.nitems;
+    f.nb = g.nb;
+    f.total_tiles = g.total_tiles;
+    f.flag = g.flag;
+    f.cpr = g.cpr;
+    f.nch = g.nch;
+    f.rt = g.rt;
+    return f;
+}
 /* Coalesced-tile Q8 GEMV (csrc/smq_gemv.hip): rows of nb = 28 or 152 blocks
  * packed at 36*nb bytes, 16-byte aligned, 4-byte aligned activations. */
 bool gemv_ct_ok(const GroupArgs &g, bool q5);
@@ -207,6 +225,12 @@ hipError_t launch_embed(const unsigned char *w, size_t row_bytes, bool q5, uint3
  * ceil(cols/32) 22-byte blocks, row r at out + r*nb*22. */
 hipError_t launch_quantize_q5(const float *x, uint32_t rows, uint32_t cols, unsigned char *out, hipStream_t s);
 hipError_t launch_dequantize_row(const unsigned char *w, uint32_t cols, float *out, bool q5, hipStream_t s);
+
+/* HBM bandwidth anchors (csrc/smq_anchor.hip): bytes / 16 pieces of 16 bytes over wgs x threads. */
+hipError_t launch_stream_read(const void *p, size_t bytes, uint32_t wgs, uint32_t threads, bool nt, uint32_t *sink,
+                              hipStream_t s);
+hipError_t launch_stream_copy(void *dst, const void *src, size_t bytes, uint32_t wgs, uint32_t threads, bool nt,
+                              hipStream_t s);
 
 }  // namespace smq
 

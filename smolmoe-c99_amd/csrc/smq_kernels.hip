@@ -167,8 +167,10 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
  * per row.
  * ---------------------------------------------------------------------- */
 /* Tasks per chunk at most: a Q8 chunk stays within 32 blocks (the chain
- * threads' short path), a Q5 chunk within 64 pairs. */
-template <bool Q5>
+ * threads' short path), a Q5 chunk within 64 pairs (measured: the 280-block
+ * rows as one chunk of 140 pairs, 3 rows per step, took 64 us per grouped
+ * launch against 48 us in three chunks, their 280-add chains serialised). */
+template <bool Q5, bool FAST>
 constexpr uint32_t pin_cpr() { return Q5 ? 64u : 32u; }
 constexpr uint32_t PIN_RT = 32; /* rows per tile at most */
 
@@ -188,7 +190,8 @@ struct PinTask {
     bool ok;
 };
 
-__device__ __forceinline__ uint32_t find_pin_item(const GroupArgs &g, uint32_t wg) {
+template <class GA>
+__device__ __forceinline__ uint32_t find_pin_item(const GA &g, uint32_t wg) {
     uint32_t lo = 0, hi = g.nitems; /* last item with wg_begin <= wg */
     while (hi - lo > 1) {
         const uint32_t mid = (lo + hi) / 2;
@@ -200,17 +203,19 @@ __device__ __forceinline__ uint32_t find_pin_item(const GroupArgs &g, uint32_t w
 
 /* occupancy floor: exact Q8 6 waves per SIMD (three 512-thread workgroups per CU);
  * PF: floats of one product buffer (the launcher keeps rt within it) */
-template <bool Q5, bool FAST, bool ONE, int NT, int D, uint32_t MAXNB, uint32_t PF>
+template <bool Q5, bool FAST, bool ONE, int NT, int D, uint32_t MAXNB, uint32_t PF, class GA>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FAST ? 4 : 6), 8))) void k_gemv_pin(
-    GroupArgs g) {
+    GA g) {
     constexpr int TB = Q5 ? 2 : 1;
     constexpr bool HOIST = ONE && Q5;
     constexpr uint32_t BYTES = Q5 ? Q5_BYTES : Q8_BYTES;
     /* one chunk: each buffer ends in a sink for the product writes of idle task lanes */
     __shared__ __attribute__((aligned(16))) float prod[2][PF + (ONE ? 32 : 0)];
     __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? PF / 8 + 128 + (ONE ? 4 : 0) : 4];
-    __shared__ __attribute__((aligned(16))) uint32_t act_q[MAXNB * 8];
-    __shared__ float act_d[MAXNB];
+    /* the staged activation (a hoisting launch reads its words straight into registers) */
+    constexpr uint32_t ACT_NB = HOIST ? 1 : MAXNB;
+    __shared__ __attribute__((aligned(16))) uint32_t act_q[ACT_NB * 8];
+    __shared__ float act_d[ACT_NB];
 
     const uint32_t tid = threadIdx.x, nb = g.nb, cpr = g.cpr, nch = ONE ? 1u : g.nch, rt = g.rt;
     const uint32_t tr = tid / cpr, ti = tid % cpr, cb = cpr * TB; /* cb: blocks per chunk */
@@ -229,8 +234,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
 
     /* the activation, once (kernels.c:912-935 layout: nb scales, nb*8 words) */
     const uint32_t *xq32 = (const uint32_t *)I.xq;
-    for (uint32_t i = tid; i < nb * 8; i += NT) act_q[i] = xq32[i];
-    for (uint32_t i = tid; i < nb; i += NT) act_d[i] = xd[i];
+    if constexpr (!HOIST) {
+        for (uint32_t i = tid; i < nb * 8; i += NT) act_q[i] = xq32[i];
+        for (uint32_t i = tid; i < nb; i += NT) act_d[i] = xd[i];
+    }
     if constexpr (ONE && !Q5) {
         /* +0.0 in the slots past the last block, never written after (chain_sum_padded): both
          * buffers whole, sinks included (the launcher keeps every chain read below PF) */
@@ -304,12 +311,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
 #pragma unroll
         for (int q = 0; q < TB; ++q) {
             const uint32_t b0 = ti * TB + q, b = b0 < nb ? b0 : nb - 1;
-            hx_d[q] = act_d[b];
+            hx_d[q] = xd[b];
+            const u4a xa = *(const u4a *)&xq32[b * 8], xb = *(const u4a *)&xq32[b * 8 + 4];
+            hx_q[q][0] = xa.x; hx_q[q][1] = xa.y; hx_q[q][2] = xa.z; hx_q[q][3] = xa.w;
+            hx_q[q][4] = xb.x; hx_q[q][5] = xb.y; hx_q[q][6] = xb.z; hx_q[q][7] = xb.w;
 #pragma unroll
-            for (int l = 0; l < 8; ++l) {
-                hx_q[q][l] = act_q[b * 8 + l];
-                hx_c[q][l] = dot4(hx_q[q][l], 0xf0f0f0f0u, 0);
-            }
+            for (int l = 0; l < 8; ++l) hx_c[q][l] = dot4(hx_q[q][l], 0xf0f0f0f0u, 0);
         }
     }
     /* one product step of task T: its lane products into pb (an idle task's to the sink) */
@@ -2151,22 +2158,49 @@ int g_forced_rt = 0;
 /* set_att_grouped(false) sends prefill attention to k_attend_rows instead (tuning, tests) */
 bool g_att_grouped = true;
 
-/* Pinned launch: every item gets a share of the resident workgroups in
- * proportion to its tiles (at least one), each a contiguous tile range.
- * Q8: 16 rows x 32 blocks per 512-thread step; Q5: 8 rows x 32 pairs per
- * 256-thread step. */
+/* Workgroups of kernel k resident on the device (computed once per kernel by the caller's static). */
+inline hipError_t resident_wgs(const void *k, int nt, int &resident) {
+    if (resident) return hipSuccess;
+    int per_cu = 0, dev = 0, cus = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, nt, 0);
+    if (e == hipSuccess) e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    resident = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+    return hipSuccess;
+}
+
+/* Each item's share of `resident` workgroups in proportion to its tiles of rt rows (at least one,
+ * at most one per tile), each a contiguous tile range; returns the grid size (0: no tiles). */
+template <class GA>
+uint32_t pin_split(GA &g, uint32_t rt, uint64_t resident) {
+    uint64_t tiles = 0;
+    for (uint32_t i = 0; i < g.nitems; ++i) tiles += (g.item[i].rows + rt - 1) / rt;
+    if (!tiles) return 0;
+    uint32_t wgs = 0;
+    for (uint32_t i = 0; i < g.nitems; ++i) {
+        const uint32_t t = (g.item[i].rows + rt - 1) / rt;
+        uint32_t n = (uint32_t)((resident * t + tiles / 2) / tiles);
+        n = n < 1 ? 1 : (n > t ? t : n);
+        g.item[i].wg_begin = wgs;
+        g.item[i].nwg = n;
+        wgs += n;
+    }
+    return wgs;
+}
+
 /* The pinned launch: the tile shape for the row width (see k_gemv_pin), then
  * each item's share of the resident workgroups in proportion to its tiles.
  * LDS per workgroup (product buffers, the staged activation) is sized for
  * three resident workgroups per CU (Q8, fast Q5: four for one-chunk rows) or
- * two (exact Q5). */
+ * two (exact Q5). A launch of few items passes the small argument struct. */
 template <bool Q5, bool FAST, bool ONE>
 hipError_t launch_gemv_pin_shape(GroupArgs &g, hipStream_t s) {
     /* exact Q5: 512 threads, two workgroups per CU (measured 10-16 % faster than
      * four of 256 threads: larger tiles, fewer barriers per byte); fast Q5
      * keeps 256 (its registers allow three waves per SIMD) */
     constexpr int NT = Q5 && FAST ? 256 : 512, D = 2;
-    constexpr uint32_t TB = Q5 ? 2 : 1, CPR = pin_cpr<Q5>();
+    constexpr uint32_t TB = Q5 ? 2 : 1, CPR = pin_cpr<Q5, FAST>();
     constexpr uint32_t MAXNB = ONE ? CPR * TB : MAX_FAST_NB;
     /* floats of one product buffer; LDS is allocated in 512-byte units */
     constexpr uint32_t PF = Q5 ? (FAST ? (ONE ? 4480 : 4400) : 7776) : (ONE ? 4832 : 4400);
@@ -2176,32 +2210,29 @@ hipError_t launch_gemv_pin_shape(GroupArgs &g, hipStream_t s) {
     g.rt = pin_rows(NT, TB, g.cpr, PF);
     if (g.nb > MAXNB || (ONE && g.nch != 1) || g.rt == 0) return hipErrorInvalidValue; /* launcher precondition */
     /* every chain read (groups of four blocks of a chunk, rt rows each) lies below PF, clear of the
-     * sinks that idle tasks write past PF */
-    if ((uint64_t)((g.cpr * TB + 3) / 4) * (g.rt * 32 + 4) > PF) return hipErrorInvalidValue;
-    static int resident = 0;
-    if (!resident) {
-        int per_cu = 0, dev = 0, cus = 0;
-        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, k_gemv_pin<Q5, FAST, ONE, NT, D, MAXNB, PF>, NT, 0);
-        if (e == hipSuccess) e = hipGetDevice(&dev);
-        if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+     * sinks that idle tasks write past PF; in fast mode the scale products (groups of rt * 4 + 4)
+     * below the scale buffer's sink at PF / 8 + 128 */
+    const uint64_t groups = (g.cpr * TB + 3) / 4;
+    if (groups * (g.rt * 32 + 4) > PF) return hipErrorInvalidValue;
+    if (FAST && groups * (g.rt * 4 + 4) > PF / 8 + 128) return hipErrorInvalidValue;
+    if (g.nitems <= FEW_GROUP_ITEMS) {
+        static int resident = 0;
+        const auto k = k_gemv_pin<Q5, FAST, ONE, NT, D, MAXNB, PF, GroupArgsFew>;
+        const hipError_t e = resident_wgs((const void *)k, NT, resident);
         if (e != hipSuccess) return e;
-        resident = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+        GroupArgsFew f = group_args_few(g);
+        const uint32_t wgs = pin_split(f, g.rt, (uint64_t)resident);
+        if (!wgs) return hipSuccess;
+        hipLaunchKernelGGL(k, dim3(wgs), dim3(NT), 0, s, f);
+        return hipGetLastError();
     }
-    uint64_t tiles = 0;
-    for (uint32_t i = 0; i < g.nitems; ++i) tiles += (g.item[i].rows + g.rt - 1) / g.rt;
-    if (!tiles) return hipSuccess;
-    uint32_t wgs = 0;
-    const uint64_t target = (uint64_t)resident;
-    for (uint32_t i = 0; i < g.nitems; ++i) {
-        const uint32_t t = (g.item[i].rows + g.rt - 1) / g.rt;
-        uint32_t n = (uint32_t)((target * t + tiles / 2) / tiles);
-        n = n < 1 ? 1 : (n > t ? t : n);
-        g.item[i].wg_begin = wgs;
-        g.item[i].nwg = n;
-        wgs += n;
-    }
-    hipLaunchKernelGGL((k_gemv_pin<Q5, FAST, ONE, NT, D, MAXNB, PF>), dim3(wgs), dim3(NT), 0, s, g);
+    static int resident = 0;
+    const auto k = k_gemv_pin<Q5, FAST, ONE, NT, D, MAXNB, PF, GroupArgs>;
+    const hipError_t e = resident_wgs((const void *)k, NT, resident);
+    if (e != hipSuccess) return e;
+    const uint32_t wgs = pin_split(g, g.rt, (uint64_t)resident);
+    if (!wgs) return hipSuccess;
+    hipLaunchKernelGGL(k, dim3(wgs), dim3(NT), 0, s, g);
     return hipGetLastError();
 }
 
@@ -2209,7 +2240,7 @@ template <bool Q5, bool FAST>
 hipError_t launch_gemv_pin(GroupArgs &g, hipStream_t s) {
     if (!Q5 && gemv_ct_ok(g, false)) return launch_gemv_ct(g, FAST, s); /* packed 28-block rows */
     const uint32_t ppr = Q5 ? (g.nb + 1) / 2 : g.nb;
-    if (ppr <= pin_cpr<Q5>()) return launch_gemv_pin_shape<Q5, FAST, true>(g, s);
+    if (ppr <= pin_cpr<Q5, FAST>()) return launch_gemv_pin_shape<Q5, FAST, true>(g, s);
     return launch_gemv_pin_shape<Q5, FAST, false>(g, s);
 }
 

@@ -921,6 +921,13 @@ smq_status smq_model_forward(smq_model *m, const uint32_t *tokens, uint32_t n, u
     if (mode < SMQ_LOGITS_NONE || mode > SMQ_LOGITS_ALL) return fail(SMQ_ERR_RANGE, "invalid logits mode %d", mode);
     for (t = 0; t < n; ++t)
         if (tokens[t] >= m->c.vocab) return fail(SMQ_ERR_RANGE, "token %u out of vocabulary", tokens[t]);
+    /* A captured decode step is replayed only over launches made after its capture: a batch
+     * forward (a prefill) drops it and the next smq_model_generate captures afresh. */
+    if (n > 1 && m->step) {
+        TRY(smq_synchronize());
+        smq_graph_destroy(m->step);
+        m->step = NULL;
+    }
     TRY(smq_memcpy_htod(m->tokens, tokens, (size_t)n * 4));
     TRY(enqueue_forward(m, m->tokens, n, pos0, NULL, mode));
     return smq_numeric_check();
@@ -967,6 +974,20 @@ static smq_status enqueue_step(smq_model *m) {
     return smq_argmax_advance(m->logits, m->c.vocab, m->banned, m->token, m->pos, m->count, m->history, m->context);
 }
 
+smq_status smq_model_prepare_decode(smq_model *m) {
+    smq_status st;
+    if (!m) return fail(SMQ_ERR_RANGE, "prepare_decode: model is NULL");
+    if (m->step) return SMQ_OK;
+    /* capture once; replays read pos/token from device memory */
+    TRY(smq_synchronize());
+    TRY(smq_capture_begin());
+    st = enqueue_step(m);
+    m->step = smq_capture_end();
+    if (st != SMQ_OK) return st;
+    if (!m->step) return smq_last_status();
+    return SMQ_OK;
+}
+
 smq_status smq_model_generate(smq_model *m, uint32_t pos, uint32_t ntokens, uint32_t *out) {
     const int32_t start = (int32_t)pos;
     const uint32_t one = 1;
@@ -975,15 +996,7 @@ smq_status smq_model_generate(smq_model *m, uint32_t pos, uint32_t ntokens, uint
     if (!ntokens) return SMQ_OK;
     if (pos > m->context || ntokens - 1 > m->context - pos || ntokens > m->context)
         return fail(SMQ_ERR_RANGE, "prompt + tokens exceeds context");
-    if (!m->step && ntokens > 1) { /* capture once; replays read pos/token from device memory */
-        smq_status st;
-        TRY(smq_synchronize());
-        TRY(smq_capture_begin());
-        st = enqueue_step(m);
-        m->step = smq_capture_end();
-        if (st != SMQ_OK) return st;
-        if (!m->step) return smq_last_status();
-    }
+    if (ntokens > 1) TRY(smq_model_prepare_decode(m));
     /* out[0] from the logits already there (main.c:580-582) */
     TRY(smq_argmax(m->logits, m->c.vocab, m->banned, m->token));
     TRY(smq_memcpy_dtod(m->history, m->token, 4));

@@ -55,6 +55,7 @@ _SIGS = {
     "smq_model_kv_layer": (_vp, [_vp, _u32, ctypes.c_int]),
     "smq_model_set_banned": (ctypes.c_int, [_vp, _vp]),
     "smq_model_generate": (ctypes.c_int, [_vp, _u32, _u32, _vp]),
+    "smq_model_prepare_decode": (ctypes.c_int, [_vp]),
     "smq_synth_checkpoint": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_uint64, ctypes.c_float,
                                             ctypes.c_int, _u32]),
 }
@@ -202,3 +203,7 @@ class Model:
         out = np.zeros(ntokens, np.uint32)
         _check(load_model_lib().smq_model_generate(self._m, pos, ntokens, out.ctypes.data))
         return out
+
+    def prepare_decode(self):
+        """Captures the decode step now (a batch forward drops it), so a timed generate only replays."""
+        _check(load_model_lib().smq_model_prepare_decode(self._m))

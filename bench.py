@@ -401,7 +401,7 @@ def main():
     same_as_sequential = all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(gpu_layer0, seq_layer0))
     log(f"bench: FFN step streamed {ms_per_step * 1e3:.1f} us, {value:.0f} GB/s")
 
-    # dominant kernel: the gate/up group launch (k_gemv_ct: coalesced 16-row x 28-block tiles, 236 MB), eight launches
+    # dominant kernel: the gate/up group launch (k_gemv_ct: coalesced 8-row x 28-block tiles, 236 MB), eight launches
     # per graph (the two copies alternating) so that one graph launch's host overhead is spread over eight
     per_graph = 8
     gu_graphs = [smq.capture(lambda: [gateup_group(copies[i % 2]) for i in range(per_graph)] and None)]
@@ -612,8 +612,9 @@ def main():
                    "parallelism": "none (1 GPU)"},
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
         "decode_tok_s": extra.get("c4_qwen05_forward", {}).get("decode_tok_s"),
-        "roofline": {"kernel": "k_gemv_ct<exact, NB=28, RT=16>: coalesced 16-row x 28-block tiles (48 gate/up GEMVs "
-                               "4864x896, one launch); HIP events, median of 11 graph replays of 8 launches",
+        "roofline": {"kernel": "k_gemv_ct<exact, NB=28, RT=8, D=2>: coalesced 8-row x 28-block tiles, two in flight, "
+                               "3 workgroups per CU (48 gate/up GEMVs 4864x896, one launch); HIP events, median of 11 "
+                               "graph replays of 8 launches",
                      "bound": "hbm",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,

@@ -358,16 +358,17 @@ __global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     }
 }
 
-/* every item a share of the resident workgroups of kernel k in proportion to its tiles of rt rows
- * (at least one, at most one per tile), each a contiguous tile range */
+/* every item a share of the resident workgroups of kernel k (at most max_per_cu per CU) in proportion
+ * to its tiles of rt rows (at least one, at most one per tile), each a contiguous tile range */
 template <class GA>
-hipError_t launch_tiles(const void *k, int &resident, uint32_t rt, GA &g, hipStream_t s) {
+hipError_t launch_tiles(const void *k, int &resident, uint32_t rt, GA &g, hipStream_t s, int max_per_cu = 0) {
     if (!resident) {
         int per_cu = 0, dev = 0, cus = 0;
         hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, CT_NT, 0);
         if (e == hipSuccess) e = hipGetDevice(&dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (e != hipSuccess) return e;
+        if (max_per_cu > 0 && per_cu > max_per_cu) per_cu = max_per_cu;
         resident = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
     }
     uint64_t tiles = 0;
@@ -388,15 +389,16 @@ hipError_t launch_tiles(const void *k, int &resident, uint32_t rt, GA &g, hipStr
 }
 
 /* a launch of few items takes the kernel built for the small argument struct */
-template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT, uint32_t D>
+template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT, uint32_t D, int PER_CU>
 hipError_t launch_ct_shape(GroupArgs &g, hipStream_t s) {
     if (g.nitems <= FEW_GROUP_ITEMS) {
         static int resident = 0;
         GroupArgsFew f = group_args_few(g);
-        return launch_tiles((const void *)k_gemv_ct<FAST, BP, NB, RT, CPT, D, GroupArgsFew>, resident, RT, f, s);
+        return launch_tiles((const void *)k_gemv_ct<FAST, BP, NB, RT, CPT, D, GroupArgsFew>, resident, RT, f, s,
+                            PER_CU);
     }
     static int resident = 0;
-    return launch_tiles((const void *)k_gemv_ct<FAST, BP, NB, RT, CPT, D, GroupArgs>, resident, RT, g, s);
+    return launch_tiles((const void *)k_gemv_ct<FAST, BP, NB, RT, CPT, D, GroupArgs>, resident, RT, g, s, PER_CU);
 }
 
 template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT>
@@ -410,12 +412,14 @@ hipError_t launch_ck_shape(GroupArgs &g, hipStream_t s) {
     return launch_tiles((const void *)k_gemv_ck<FAST, BP, NB, RT, CPT, GroupArgs>, resident, RT, g, s);
 }
 
-/* 16 rows of 28 blocks per step: 1008 pieces in 1024 thread slots; one tile in flight per
- * workgroup while the previous one is reduced (measured on the 48 gate/up GEMVs of Qwen2.5-0.5B:
- * two in flight, or 8- and 12-row tiles, were no faster) */
+/* 8 rows of 28 blocks per step: 504 pieces, one per thread of 512; two tiles in flight per workgroup
+ * while the previous one is reduced, three workgroups per CU (about 12 MB requested chip-wide, where a
+ * plain streaming read peaks). Measured on the 48 gate/up GEMVs of Qwen2.5-0.5B (235 MB): 38.8 us
+ * against 40.8-42.1 us for 16-row tiles with one in flight; two or four workgroups per CU, or three
+ * tiles in flight, were slower; configs[0]'s 48 x 896 x 896 group 11.7 against 12.3 us. */
 template <bool FAST, bool BP>
 hipError_t launch_ct_bp(GroupArgs &g, hipStream_t s) {
-    if (g.nb == 28) return launch_ct_shape<FAST, BP, 28, 16, 2, 1>(g, s);
+    if (g.nb == 28) return launch_ct_shape<FAST, BP, 28, 8, 1, 2, 3>(g, s);
     if (g.nb == 152) return launch_ck_shape<FAST, BP, 152, 14, 2>(g, s); /* 14 rows x 32-block chunks: 1008 pieces */
     return hipErrorInvalidValue;
 }

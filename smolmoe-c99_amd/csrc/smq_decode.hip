@@ -4,8 +4,10 @@
  *
  * Reference steps fused here (src/model.c:334-415, 496-509, 622-643;
  * vecmath.c:61-93; kernels.c:912-935):
- *  PRO_NORM  RMSNorm of x (sum of squares in element order by one lane,
- *            inv = 1/sqrtf(sum/n + eps), (x*inv)*w), then its Q8 blocks;
+ *  PRO_NORM  RMSNorm of x (sum of squares in element order by one wave,
+ *            the running sum moving lane to lane over squares held in
+ *            registers, inv = 1/sqrtf(sum/n + eps), (x*inv)*w), then its Q8
+ *            blocks;
  *  PRO_F32   the Q8 blocks of the f32 row x;
  *  EPI_STORE each item's rows + bias, finiteness, y or y += result;
  *  EPI_GLU   gate and up rows of 32 outputs h = up*act(gate) (SwiGLU or
@@ -176,9 +178,13 @@ __global__ __launch_bounds__(DC_NT) void k_decode_ct(FusedArgs a) {
         if (tid < NQ) *(float4 *)&L.sq[4 * tid] = make_float4(xv[0] * xv[0], xv[1] * xv[1], xv[2] * xv[2], xv[3] * xv[3]);
         __syncthreads(); /* every activation element is in */
         fetch();
-        if (tid < 64) { /* the whole first wave runs the chain (faster than one lane) */
-            const float ss = serial_sum_lds(L.sq, n);
-            if (tid == 0) {
+        if (tid < 64) { /* the first wave runs the chain, NB / 2 squares per lane in registers */
+            constexpr int KT = NB * 32 / 64;
+            float t[KT];
+#pragma unroll
+            for (int k = 0; k < KT; ++k) t[k] = L.sq[KT * tid + k]; /* +0.0 past n */
+            const float ss = wave_chain<KT>(t);
+            if (tid == 63) {
                 const float iv = 1.0f / sqrtf(ss / (float)n + a.eps); /* model.c:338 */
                 L.inv = iv;
                 L.bad = !(fabsf(ss) <= FLT_MAX) || !(fabsf(iv) <= FLT_MAX);

@@ -172,9 +172,9 @@ __global__ __launch_bounds__(WG) void k_gemv_fused(FusedArgs a, uint32_t ntiles)
                 }
             }
             lds_barrier();
-            if (tid < 64) { /* the whole first wave runs the chain (faster than one lane) */
-                const float ss = serial_sum_lds(sq, n);
-                if (tid == 0) {
+            if (tid < 64) { /* the whole first wave runs the chain; lane 63 ends with the total */
+                const float ss = serial_sum_wave(sq, n);
+                if (tid == 63) {
                     const float iv = 1.0f / sqrtf(ss / (float)n + a.eps); /* model.c:338 */
                     s_inv = iv;
                     s_bad = !(fabsf(ss) <= FLT_MAX) || !(fabsf(iv) <= FLT_MAX);

@@ -1301,9 +1301,9 @@ __global__ __launch_bounds__(ATT_WG) void k_attend(const float *q, const float *
     __syncthreads();
 
     /* 3. the total in position order */
-    if (tid < 64) { /* the whole first wave runs the chain */
-        const float tot = serial_sum_lds(sc, np);
-        if (tid == 0) s_inv = 1.0f / tot;
+    if (tid < 64) { /* the whole first wave runs the chain; lane 63 ends with the total */
+        const float tot = serial_sum_wave(sc, np);
+        if (tid == 63) s_inv = 1.0f / tot;
     }
     __syncthreads();
     const float inv = s_inv;
@@ -1486,9 +1486,9 @@ __device__ __forceinline__ void att_tail(float high, float *sc, float *prod, uin
     for (uint32_t p = tid; p < np; p += AR_WG) sc[p] = exp_det_tab(sc[p] - high, etab);
     __syncthreads();
 
-    if (tid < 64) { /* the whole first wave runs the chain */
-        const float tot = serial_sum_lds(sc, np);
-        if (tid == 0) *s_inv = 1.0f / tot;
+    if (tid < 64) { /* the whole first wave runs the chain; lane 63 ends with the total */
+        const float tot = serial_sum_wave(sc, np);
+        if (tid == 63) *s_inv = 1.0f / tot;
     }
     __syncthreads();
     const float inv = *s_inv;

@@ -30,7 +30,7 @@ model_forward on the same checkpoint as CPU rate and bit-exactness gate.
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
        python bench.py --forward-only [--checkpoint PATH] [--decode-steps N] [--runs R]   (configs[4]
                                 alone, for profiling; PATH from python bench.py --write-checkpoint PATH)
-       python bench.py --anchor   (the HBM read/copy anchor alone)
+       python bench.py --anchor   (the HBM read/copy anchor and the hand-off anchor alone)
        python bench.py --q5-only   (configs[2] alone, for profiling)
        python bench.py --prefill-only   (the batched prefill GEMMs alone, for profiling)
 """
@@ -274,10 +274,11 @@ def main():
         print(json.dumps(extra), flush=True)
         return
     if len(sys.argv) > 1 and sys.argv[1] == "--anchor":
-        # the HBM bandwidth anchor alone (the program its rocprofv3 summary profiles)
+        # the HBM bandwidth and hand-off anchors alone (the program their rocprofv3 summary profiles)
         log("bench: init", smq.init(0), smq.kernels_select())
         extra = {}
         hbm_anchor(extra)
+        handoff_anchor(extra)
         print(json.dumps(extra), flush=True)
         return
     if len(sys.argv) > 1 and sys.argv[1] == "--prefill-only":
@@ -559,6 +560,7 @@ def main():
         del rb, rout
         q5_extra(single, extra)
         hbm_anchor(extra)
+        handoff_anchor(extra)
 
     if not args.no_extra:
         model_forward_extra(args, extra)
@@ -829,6 +831,34 @@ def hbm_anchor(extra, gib=2):
         "copy_GBps": copy[best_copy], "copy_shape": best_copy,
         "read_sweep": sweep, "copy_sweep": copy}
     log(f"bench: HBM anchor read {sweep[best_read]} GB/s ({best_read}), copy {copy[best_copy]} GB/s ({best_copy})")
+
+
+def handoff_anchor(extra, episodes=200):
+    """What a hand-off between dependent phases costs: a grid barrier among resident workgroups (one per
+    CU; smq_grid_barrier_probe, kinds 0-2, at 64/128/256 workgroups: (launch with `episodes` barriers -
+    launch with none) / episodes, best of 5 each), against the dependent-launch gap of a graph of 200
+    small kernels (smq_stream_read of 16 KiB at 64/256/1024 workgroups: replay time / 200, best of 5)."""
+    kinds = {0: "one_counter", 1: "per_xcd_counters", 2: "per_workgroup_flags"}
+    cus = {}
+    for kind, kname in kinds.items():
+        for wgs in (64, 128, 256):
+            t0 = min(smq.grid_barrier_probe(wgs, 0, kind) for _ in range(5))
+            t1 = min(smq.grid_barrier_probe(wgs, episodes, kind) for _ in range(5))
+            cus[f"{kname}_{wgs}wg_us"] = round((t1 - t0) * 1e3 / episodes, 3)
+    buf = smq.DeviceBuffer(16384)
+    sink = smq.DeviceBuffer(4)
+    gaps = {}
+    for wgs in (64, 256, 1024):
+        g = [smq.capture(lambda: [smq.stream_read(buf, 16384, wgs, 64, False, sink) for _ in range(200)] and None)]
+        timed_graph(g, 1)
+        gaps[f"{wgs}wg_us"] = round(min(timed_graph(g, 1) for _ in range(5)) * 1e3 / 200, 3)
+    del buf, sink
+    extra["handoff_anchor"] = {
+        "what": "cost of one hand-off between dependent phases: a grid barrier among resident workgroups (one per "
+                "CU, agent-scope release/acquire, bounded waits) against a dependent kernel launch inside a "
+                "HIP graph; best of 5",
+        "grid_barrier": cus, "graph_launch_gap": gaps}
+    log(f"bench: hand-off anchor: barrier {cus}, graph launch gap {gaps}")
 
 
 def prefill_only(extra):

@@ -361,6 +361,20 @@ smq_status smq_timer_start(void);
 /* Records a stop event, waits for it, returns milliseconds since start (<0 on error). */
 double smq_timer_stop(void);
 
+/* ---- cross-workgroup hand-off anchor (no reference counterpart: measurement)
+ * One launch of `workgroups` workgroups (1..the device's CU count; each holds
+ * 96 KB of LDS, so one per CU and all resident) passing `episodes` (<= 100000)
+ * grid barriers, timed on the library stream into *ms (host). kind 0: one
+ * counter, every workgroup adds 1 and waits for the generation's total; kind
+ * 1: eight counters by workgroup index % 8 (the XCD the workgroup is dealt
+ * to), the last arriver of each adds 1 to one release counter; kind 2: no
+ * atomics, every workgroup stores the generation into a word of its own,
+ * workgroup 0 waits for all of them and publishes it. Agent-scope release and
+ * acquire. Every wait is bounded (2^20 polls), a workgroup that gives up ends
+ * every other wait, and the call then returns SMQ_ERR_STATE. Synchronizes;
+ * not for use under capture; allocates a 2.5 KB counter buffer once. */
+smq_status smq_grid_barrier_probe(uint32_t workgroups, uint32_t episodes, uint32_t kind, double *ms);
+
 /* ---- HBM bandwidth anchors (no reference counterpart: measurement) ------
  * Plain kernels that read (smq_stream_read) or copy (smq_stream_copy) `bytes`
  * (a multiple of 16, 16-byte aligned) with coalesced 16-byte loads, so a

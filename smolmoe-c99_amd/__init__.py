@@ -137,6 +137,7 @@ _SIGS = {
     "smq_timer_stop": (ctypes.c_double, []),
     "smq_stream_read": (ctypes.c_int, [_vp, _sz, _u32, _u32, ctypes.c_int, _vp]),
     "smq_stream_copy": (ctypes.c_int, [_vp, _vp, _sz, _u32, _u32, ctypes.c_int]),
+    "smq_grid_barrier_probe": (ctypes.c_int, [_u32, _u32, _u32, ctypes.POINTER(ctypes.c_double)]),
 }
 
 _lib = None
@@ -574,6 +575,14 @@ def timer_stop():
 def stream_read(buf, nbytes, workgroups, threads, nontemporal, sink):
     """smq_stream_read: the HBM read anchor (coalesced 16-byte loads, nothing written)."""
     _check(load().smq_stream_read(_p(buf), nbytes, workgroups, threads, int(bool(nontemporal)), _p(sink)))
+
+
+def grid_barrier_probe(workgroups, episodes, kind):
+    """smq_grid_barrier_probe: milliseconds of one launch of `workgroups` resident workgroups passing
+    `episodes` grid barriers (kind 0 one counter, 1 per-XCD counters, 2 per-workgroup flags)."""
+    ms = ctypes.c_double()
+    _check(load().smq_grid_barrier_probe(workgroups, episodes, kind, ctypes.byref(ms)))
+    return ms.value
 
 
 def stream_copy(dst, src, nbytes, workgroups, threads, nontemporal):

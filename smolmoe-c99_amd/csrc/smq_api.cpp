@@ -1215,6 +1215,36 @@ smq_status smq_stream_copy(void *dst, const void *src, size_t bytes, uint32_t wo
                : t_status;
 }
 
+smq_status smq_grid_barrier_probe(uint32_t workgroups, uint32_t episodes, uint32_t kind, double *ms) {
+    if (!ready()) return t_status;
+    if (t_capturing) return set_status(SMQ_ERR_RANGE, "grid_barrier_probe: not under capture");
+    int cus = 0;
+    if (!hip_ok(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, g.device), "grid_barrier_probe"))
+        return t_status;
+    if (!workgroups || workgroups > (uint32_t)cus || workgroups > 1024 || episodes > 100000 || kind > 2 || !ms)
+        return set_status(SMQ_ERR_RANGE, "grid_barrier_probe: %u workgroups (1..%d), %u episodes, kind %u", workgroups,
+                          cus, episodes, kind);
+    static uint32_t *words[64];
+    if (g.device < 0 || g.device >= 64) return set_status(SMQ_ERR_RANGE, "grid_barrier_probe: device %d", g.device);
+    if (!words[g.device] &&
+        !hip_ok(hipMalloc((void **)&words[g.device], smq::GRID_BARRIER_WORDS * 4), "grid_barrier_probe"))
+        return t_status;
+    uint32_t *w = words[g.device];
+    float t = 0.0f;
+    uint32_t timed_out = 0;
+    if (!hip_ok(hipEventRecord(g.t0, g.cur), "grid_barrier_probe") ||
+        !hip_ok(smq::launch_grid_barrier(w, workgroups, episodes, kind, g.cur), "grid_barrier_probe") ||
+        !hip_ok(hipEventRecord(g.t1, g.cur), "grid_barrier_probe") ||
+        !hip_ok(hipEventSynchronize(g.t1), "grid_barrier_probe") ||
+        !hip_ok(hipEventElapsedTime(&t, g.t0, g.t1), "grid_barrier_probe") ||
+        !hip_ok(hipMemcpy(&timed_out, w + smq::GRID_BARRIER_TIMEOUTS, 4, hipMemcpyDeviceToHost), "grid_barrier_probe"))
+        return t_status;
+    if (timed_out)
+        return set_status(SMQ_ERR_STATE, "grid_barrier_probe: %u workgroups gave up a wait", timed_out);
+    *ms = (double)t;
+    return SMQ_OK;
+}
+
 smq_status smq_timer_start(void) {
     if (!ready()) return t_status;
     return hip_ok(hipEventRecord(g.t0, g.cur), "timer") ? SMQ_OK : t_status;

@@ -226,6 +226,13 @@ hipError_t launch_embed(const unsigned char *w, size_t row_bytes, bool q5, uint3
 hipError_t launch_quantize_q5(const float *x, uint32_t rows, uint32_t cols, unsigned char *out, hipStream_t s);
 hipError_t launch_dequantize_row(const unsigned char *w, uint32_t cols, float *out, bool q5, hipStream_t s);
 
+/* Grid barrier probe (csrc/smq_anchor.hip): clears `words` (GRID_BARRIER_WORDS of them), then one launch
+ * of wgs workgroups (one per CU, wgs <= the CU count) passing `episodes` barriers of the given kind;
+ * words[GRID_BARRIER_TIMEOUTS] counts the workgroups that gave up a wait. */
+constexpr uint32_t GRID_BARRIER_WORDS = 10 * 64;
+constexpr uint32_t GRID_BARRIER_TIMEOUTS = 9 * 64 + 16;
+hipError_t launch_grid_barrier(uint32_t *words, uint32_t wgs, uint32_t episodes, uint32_t kind, hipStream_t s);
+
 /* HBM bandwidth anchors (csrc/smq_anchor.hip): bytes / 16 pieces of 16 bytes over wgs x threads. */
 hipError_t launch_stream_read(const void *p, size_t bytes, uint32_t wgs, uint32_t threads, bool nt, uint32_t *sink,
                               hipStream_t s);

@@ -793,7 +793,8 @@ def hbm_anchor(extra, gib=2):
     """What this device's HBM delivers to plain kernels (smq_stream_read / smq_stream_copy: coalesced
     16-byte pieces, grid-stride, eight in flight per thread) over a `gib` GiB buffer, swept over launch
     shapes; each shape is a graph of 4 launches timed 5 times (median of the samples), the best
-    shape reported with the whole sweep beside it."""
+    shape reported with the whole sweep beside it. Then the best read shape over the byte count of each
+    grouped GEMV launch bench.py reports (one launch per region, the launch's fixed cost included)."""
     nbytes = gib << 30
     src = smq.DeviceBuffer(nbytes)
     src.fill(1)
@@ -819,9 +820,24 @@ def hbm_anchor(extra, gib=2):
             timed_graph(g, 1)
             med, best, _ = timed_samples(g, 1, 5)
             copy[f"copy_{'nt' if nt else 'plain'}_{wgs}x{threads}"] = round(2 * half * 4 / (med * 1e-3) / 1e9, 1)
-    del src, dst
     best_read = max(sweep, key=sweep.get)
     best_copy = max(copy, key=copy.get)
+    # the same read at the byte counts of single grouped launches: one launch per region, eight distinct
+    # regions per graph (no region is read twice in a row), so the launch's fixed cost is in the rate
+    rshape = best_read.split("_")
+    rnt, (rwgs, rthr) = rshape[1] == "nt", map(int, rshape[2].split("x"))
+    sized = {}
+    for name, size in (("c0_group48_896x896", 48 * q8_bytes(DIM, DIM)),
+                       ("down_group24_896x4864", LAYERS * q8_bytes(DIM, HIDDEN)),
+                       ("q5_group16_8960x1536", 16 * q8_bytes(8960, 1536, block=22)),
+                       ("gateup_group48_4864x896", 2 * LAYERS * q8_bytes(HIDDEN, DIM))):
+        size = size // 256 * 256
+        g = [smq.capture(lambda: [smq.stream_read(src.at(k * size), size, rwgs, rthr, rnt, sink) for k in range(8)]
+                         and None)]
+        timed_graph(g, 1)
+        med, best, _ = timed_samples(g, 1, 11)
+        sized[name] = {"bytes": size, "us": round(med * 1e3 / 8, 2), "GBps": round(size * 8 / (med * 1e-3) / 1e9, 1)}
+    del src, dst
     extra["hbm_anchor"] = {
         "what": f"plain coalesced 16-byte streaming kernels over {gib} GiB (read: nothing written; copy: bytes read "
                 "+ bytes written), medians of 5 samples of 4 graph-captured launches, per launch shape "
@@ -829,8 +845,11 @@ def hbm_anchor(extra, gib=2):
         "read_GBps": sweep[best_read], "read_shape": best_read,
         "read_pct_hbm_peak": round(100 * sweep[best_read] / HBM_PEAK_GBS, 1),
         "copy_GBps": copy[best_copy], "copy_shape": best_copy,
+        "read_at_launch_sizes": sized,
         "read_sweep": sweep, "copy_sweep": copy}
-    log(f"bench: HBM anchor read {sweep[best_read]} GB/s ({best_read}), copy {copy[best_copy]} GB/s ({best_copy})")
+    log(f"bench: HBM anchor read {sweep[best_read]} GB/s ({best_read}), copy {copy[best_copy]} GB/s ({best_copy}); "
+        f"one read launch of a grouped GEMV's bytes: " + ", ".join(f"{k} {v['us']} us {v['GBps']} GB/s"
+                                                                for k, v in sized.items()))
 
 
 def handoff_anchor(extra, episodes=200):

@@ -212,9 +212,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
     /* one chunk: each buffer ends in a sink for the product writes of idle task lanes */
     __shared__ __attribute__((aligned(16))) float prod[2][PF + (ONE ? 32 : 0)];
     __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? PF / 8 + 128 + (ONE ? 4 : 0) : 4];
-    /* the staged activation (a hoisting launch reads its words straight into registers) */
-    constexpr uint32_t ACT_NB = HOIST ? 1 : MAXNB;
-    __shared__ __attribute__((aligned(16))) uint32_t act_q[ACT_NB * 8];
+    /* the staged activation (a hoisting launch reads its words straight into registers), piece-major:
+     * the 16-byte piece k of task t's activation (TB blocks, 2 TB pieces) at act_q[(k * ATASKS + t) * 4],
+     * so the lanes of one read instruction (consecutive tasks, one k) read consecutive 16-byte pieces
+     * and meet no bank twice (task-major, 32 or 64 bytes apart, cost 2- and 4-way conflicts) */
+    constexpr uint32_t ACT_NB = HOIST ? 1 : MAXNB, ATASKS = (ACT_NB + TB - 1) / TB;
+    __shared__ __attribute__((aligned(16))) uint32_t act_q[ATASKS * TB * 8];
     __shared__ float act_d[ACT_NB];
 
     const uint32_t tid = threadIdx.x, nb = g.nb, cpr = g.cpr, nch = ONE ? 1u : g.nch, rt = g.rt;
@@ -235,7 +238,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
     /* the activation, once (kernels.c:912-935 layout: nb scales, nb*8 words) */
     const uint32_t *xq32 = (const uint32_t *)I.xq;
     if constexpr (!HOIST) {
-        for (uint32_t i = tid; i < nb * 8; i += NT) act_q[i] = xq32[i];
+        for (uint32_t i = tid; i < nb * 8; i += NT) {
+            const uint32_t b = i / 8, o = (b % TB) * 8 + i % 8; /* word o of task b / TB */
+            act_q[((o / 4) * ATASKS + b / TB) * 4 + o % 4] = xq32[i];
+        }
         for (uint32_t i = tid; i < nb; i += NT) act_d[i] = xd[i];
     }
     if constexpr (ONE && !Q5) {
@@ -335,7 +341,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
 #pragma unroll
                 for (int l = 0; l < 8; ++l) xs[q][l] = hx_q[q][l];
             } else {
-                const u4a xa = *(const u4a *)&act_q[b * 8], xb = *(const u4a *)&act_q[b * 8 + 4];
+                const uint32_t at = (2 * (b % TB) * ATASKS + b / TB) * 4;
+                const u4a xa = *(const u4a *)&act_q[at], xb = *(const u4a *)&act_q[at + ATASKS * 4];
                 xs[q][0] = xa.x; xs[q][1] = xa.y; xs[q][2] = xa.z; xs[q][3] = xa.w;
                 xs[q][4] = xb.x; xs[q][5] = xb.y; xs[q][6] = xb.z; xs[q][7] = xb.w;
             }

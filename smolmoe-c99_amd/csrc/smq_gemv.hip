@@ -281,17 +281,26 @@ __global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) v
         }
     };
 
+    /* the activation's words, all requested first (loads complete in order, so storing them waits
+     * for nothing later; a loop of load-then-store after the first tile's loads waited one memory
+     * round trip per iteration, each also taking the tile's loads) */
+    constexpr uint32_t AW = (NB * 9 + CT_NT - 1) / CT_NT;
+    uint32_t av[AW];
+    {
+        const uint32_t *xq32 = (const uint32_t *)I.xq;
+#pragma unroll
+        for (uint32_t k = 0; k < AW; ++k) {
+            const uint32_t i = tid + k * CT_NT, ic = i < NB * 9 ? i : 0, b = ic / 9, f = ic % 9;
+            av[k] = *(f == 0 ? (const uint32_t *)xd + b : xq32 + 8 * b + f - 1);
+        }
+    }
     float B = 0.0f, Pr = 0.0f;
     load_bp(B, Pr, t0);
     u4a W[CPT];
     load(W, 0);
-    {
-        const uint32_t *xq32 = (const uint32_t *)I.xq;
-        for (uint32_t i = tid; i < NB * 9; i += CT_NT) {
-            const uint32_t b = i / 9, f = i % 9;
-            act[i] = f == 0 ? __float_as_uint(xd[b]) : xq32[8 * b + f - 1];
-        }
-    }
+#pragma unroll
+    for (uint32_t k = 0; k < AW; ++k)
+        if (tid + k * CT_NT < NB * 9) act[tid + k * CT_NT] = av[k];
     __syncthreads();
 
     float acc = 0.0f;

@@ -209,9 +209,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
     constexpr int TB = Q5 ? 2 : 1;
     constexpr bool HOIST = ONE && Q5;
     constexpr uint32_t BYTES = Q5 ? Q5_BYTES : Q8_BYTES;
-    /* one chunk: each buffer ends in a sink for the product writes of idle task lanes */
-    __shared__ __attribute__((aligned(16))) float prod[2][PF + (ONE ? 32 : 0)];
-    __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? PF / 8 + 128 + (ONE ? 4 : 0) : 4];
+    /* each buffer ends in a sink for the product writes of idle task lanes */
+    __shared__ __attribute__((aligned(16))) float prod[2][PF + 32];
+    __shared__ __attribute__((aligned(16))) float dsc[FAST ? 2 : 1][FAST ? PF / 8 + 128 + 4 : 4];
     /* the staged activation (a hoisting launch reads its words straight into registers), piece-major:
      * the 16-byte piece k of task t's activation (TB blocks, 2 TB pieces) at act_q[(k * ATASKS + t) * 4],
      * so the lanes of one read instruction (consecutive tasks, one k) read consecutive 16-byte pieces
@@ -237,12 +237,23 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
 
     /* the activation, once (kernels.c:912-935 layout: nb scales, nb*8 words) */
     const uint32_t *xq32 = (const uint32_t *)I.xq;
+    /* the activation's 16-byte pieces (piece p: words 4(p % 2).. of block p / 2) and scales, all
+     * requested before the first task and stored into LDS after the first tasks are requested (a
+     * loop of load-then-store waited one memory round trip per iteration) */
+    constexpr uint32_t SPT = HOIST ? 1 : (ACT_NB * 2 + NT - 1) / NT, SDT = HOIST ? 1 : (ACT_NB + NT - 1) / NT;
+    u4a pv[SPT];
+    float dv[SDT];
     if constexpr (!HOIST) {
-        for (uint32_t i = tid; i < nb * 8; i += NT) {
-            const uint32_t b = i / 8, o = (b % TB) * 8 + i % 8; /* word o of task b / TB */
-            act_q[((o / 4) * ATASKS + b / TB) * 4 + o % 4] = xq32[i];
+#pragma unroll
+        for (uint32_t k = 0; k < SPT; ++k) {
+            const uint32_t pp = tid + k * NT, pc = pp < nb * 2 ? pp : 0;
+            pv[k] = *(const u4a *)&xq32[4 * pc];
         }
-        for (uint32_t i = tid; i < nb; i += NT) act_d[i] = xd[i];
+#pragma unroll
+        for (uint32_t k = 0; k < SDT; ++k) {
+            const uint32_t i = tid + k * NT;
+            dv[k] = xd[i < nb ? i : 0];
+        }
     }
     if constexpr (ONE && !Q5) {
         /* +0.0 in the slots past the last block, never written after (chain_sum_padded): both
@@ -279,14 +290,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
             const uint32_t rc = rl < rows ? rl : rows - 1, bc = b < nb ? b : 0;
             fetch(wbase + (size_t)rc * row_bytes + (size_t)bc * BYTES);
         } else {
-            /* several chunks per row: idle task lanes issue nothing (measured
-             * faster here than the branch-free form) */
-            if (T.ok) fetch(wbase + (size_t)row * row_bytes + (size_t)b * BYTES);
-            if (tid < chains) {
-                const uint32_t orow = row0 + tid / 8, oc = orow < rows ? orow : 0;
-                T.bias = bias_p ? bias_p[oc] : 0.0f;
-                T.prior = accum ? y[oc] : 0.0f;
-            }
+            /* several chunks per row: the same loads at every step too (an idle task re-reads its
+             * tile's first row or its row's first block, a step past the range the last tile) */
+            const uint32_t tl = real ? tile : t1 - 1, rl = tl * rt + (worker ? tr : 0);
+            const uint32_t rc = rl < rows ? rl : rows - 1, bc = b < nb ? b : 0;
+            fetch(wbase + (size_t)rc * row_bytes + (size_t)bc * BYTES);
         }
     };
     /* one chunk: the chain threads' row, its bias and prior output (the other threads read the
@@ -299,19 +307,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
         T.bias = *(bias_p ? bias_p + oc : xd);
         T.prior = *(accum ? y + oc : xd);
     };
-    PinTask<Q5> T[D];
-    uint32_t lt = t0, lc = 0; /* load cursor */
-#pragma unroll
-    for (int j = 0; j < D; ++j) {
-        load(T[j], lt, lc, (uint32_t)j < my_steps);
-        if constexpr (ONE) load_bp(T[j], lt, (uint32_t)j < my_steps);
-        if (++lc == nch) { lc = 0; ++lt; }
-    }
-    __syncthreads(); /* activation staged */
-    /* Q5, one chunk: a thread's blocks are the same at every step, so their
-     * activation words, scales and offsets c = -16 * (sum of the four int8 of
-     * a lane) live in registers (idle threads read clamped, unused indices) */
-    uint32_t hx_q[HOIST ? TB : 1][8], hx_c[HOIST ? TB : 1][8];
+    /* Q5, one chunk: a thread's blocks are the same at every step, so their activation words and
+     * scales live in registers (idle threads read clamped, unused indices). Requested before the first
+     * tasks: loads complete in order, so no wait for them inside the step loop counts later loads (one
+     * requested after the tasks made every step wait for all loads in flight) */
+    uint32_t hx_q[HOIST ? TB : 1][8];
     float hx_d[HOIST ? TB : 1];
     if constexpr (HOIST) {
 #pragma unroll
@@ -321,9 +321,45 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
             const u4a xa = *(const u4a *)&xq32[b * 8], xb = *(const u4a *)&xq32[b * 8 + 4];
             hx_q[q][0] = xa.x; hx_q[q][1] = xa.y; hx_q[q][2] = xa.z; hx_q[q][3] = xa.w;
             hx_q[q][4] = xb.x; hx_q[q][5] = xb.y; hx_q[q][6] = xb.z; hx_q[q][7] = xb.w;
+        }
+    }
+    PinTask<Q5> T[D];
+    uint32_t lt = t0, lc = 0; /* load cursor */
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+        load(T[j], lt, lc, (uint32_t)j < my_steps);
+        if constexpr (ONE) load_bp(T[j], lt, (uint32_t)j < my_steps);
+        if (++lc == nch) { lc = 0; ++lt; }
+    }
+    /* several chunks per row: the bias and prior output of the chain threads' rows, requested for a
+     * tile right after the store of the previous one (a whole tile of steps ahead of their use) */
+    auto load_tile_bp = [&](float &bias, float &prior, uint32_t tile) __attribute__((always_inline)) {
+        const uint32_t tl = tile < t1 ? tile : t1 - 1;
+        const uint32_t orow = tl * rt + (tid < chains ? tid / 8 : 0), oc = orow < rows ? orow : rows - 1;
+        bias = *(bias_p ? bias_p + oc : xd);
+        prior = *(accum ? y + oc : xd);
+    };
+    float mbias = 0.0f, mprior = 0.0f;
+    if constexpr (!ONE) load_tile_bp(mbias, mprior, t0);
+    if constexpr (!HOIST) {
+#pragma unroll
+        for (uint32_t k = 0; k < SPT; ++k) {
+            const uint32_t pp = tid + k * NT, b = pp / 2, o = (b % TB) * 8 + (pp % 2) * 4; /* word o of task b / TB */
+            if (pp < nb * 2) *(u4a *)&act_q[((o / 4) * ATASKS + b / TB) * 4] = pv[k];
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < SDT; ++k)
+            if (tid + k * NT < nb) act_d[tid + k * NT] = dv[k];
+    }
+    __syncthreads(); /* activation staged */
+    /* Q5, one chunk: the offsets c = -16 * (sum of the four int8 of a lane) of the activation words
+     * requested above, formed once the task loads are on their way */
+    uint32_t hx_c[HOIST ? TB : 1][8];
+    if constexpr (HOIST) {
+#pragma unroll
+        for (int q = 0; q < TB; ++q)
 #pragma unroll
             for (int l = 0; l < 8; ++l) hx_c[q][l] = dot4(hx_q[q][l], 0xf0f0f0f0u, 0);
-        }
     }
     /* one product step of task T: its lane products into pb (an idle task's to the sink) */
     auto products = [&](const PinTask<Q5> &Tk, float *pb, float *db, uint32_t chunk) __attribute__((always_inline)) {
@@ -401,25 +437,22 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
         return;
     }
     uint32_t ct = t0, cc = 0; /* chain cursor */
-    float acc = 0.0f, bias = 0.0f, prior = 0.0f;
+    float acc = 0.0f;
     for (uint32_t k = 0; k < my_steps; k += D) {
 #pragma unroll
-        for (int j = 0; j < D; ++j) {
-            if (k + j >= my_steps) break;
+        for (int j = 0; j < D; ++j) { /* a straight trip of D steps; a step past the range stores nothing */
+            const bool live = k + j < my_steps;
             float *pb = prod[(k + j) & 1];
             float *db = dsc[FAST ? (k + j) & 1 : 0];
-            if (T[j].ok) products(T[j], pb, db, cc);
+            /* every task's products, an idle one's to the sink: a branch around them left the
+             * task's loads unwaited on one path, so reusing its registers waited for every load */
+            products(T[j], pb, db, cc);
             /* this task is consumed: its slot reloads now, a barrier and a chain earlier than
-             * at the end of the step (the chain threads keep its bias and prior output) */
-            const float tbias = T[j].bias, tprior = T[j].prior;
+             * at the end of the step */
             load(T[j], lt, lc, k + j + D < my_steps);
             if (++lc == nch) { lc = 0; ++lt; }
             __syncthreads();
             if (tid < chains) {
-                if (cc == 0) {
-                    bias = tbias;
-                    prior = tprior;
-                }
                 const uint32_t count = nb - cc * cb < cb ? nb - cc * cb : cb;
                 const float4 *pp = (const float4 *)pb + tid, *dp = FAST ? (const float4 *)db + tid / 8 : nullptr;
                 if (!Q5 || cb <= 32) chain_sum<FAST, 8>(acc, pp, gs / 4, dp, ds / 4, count);
@@ -427,16 +460,17 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
                 if (cc + 1 == nch) {
                     const float v = reduce8_to_lane7(acc);
                     const uint32_t r = ct * rt + tid / 8;
-                    if ((tid & 7) == 7 && r < rows) {
+                    if (live && (tid & 7) == 7 && r < rows) {
                         float o = v;
-                        if (bias_p) o = o + bias; /* model.c:259-262 */
+                        if (bias_p) o = o + mbias; /* model.c:259-262 */
                         if (g.flag && !(fabsf(o) <= FLT_MAX)) *g.flag = 1;
-                        if (accum) o = prior + o;
+                        if (accum) o = mprior + o;
                         y[r] = o;
                     }
                     acc = 0.0f;
                 }
             }
+            if (cc + 1 == nch) load_tile_bp(mbias, mprior, ct + 1); /* uniform; the store above used them */
             if (++cc == nch) { cc = 0; ++ct; }
         }
     }

@@ -196,22 +196,31 @@ def cpu_baseline(model, acts_x, acts_h, threads_list, budget_s, gpu_out):
     return kind, name, out, gate
 
 
+def ffn_items(m, ax, ah, gu, yo):
+    """The FFN step's 72 GEMVs (48 gate/up 4864x896, 24 down 896x4864), each with its layer's activation."""
+    return ([(layer.qmat(k), None, gu[l].ptr + (HIDDEN * 4 if k == "up" else 0), False, ax[l].d, ax[l].q)
+             for l, layer in enumerate(m) for k in ("gate", "up")] +
+            [(layer.qmat("down"), None, yo[l], False, ah[l].d, ah[l].q) for l, layer in enumerate(m)])
+
+
 def traffic_probe():
     """Short program for rocprofv3 --pmc runs: 4 launches of the dominant
-    kernel (the grouped gate/up launch: 48 GEMVs 4864x896 Q8, 235 MB) alternating
-    two model copies, then one 256 MiB device-to-device copy whose FETCH_SIZE /
+    kernel (the planned FFN step: 72 GEMVs, 354 MB) alternating two model
+    copies, then one 256 MiB device-to-device copy whose FETCH_SIZE /
     WRITE_SIZE calibrate the counters (expected 262,144 KiB each)."""
     smq.init(0)
     model = [Layer(1000 + 16 * l) for l in range(LAYERS)]
     copies = [model, [layer.copy() for layer in model]]
     ax = [Act(2000 + l, 1, DIM) for l in range(LAYERS)]
+    ah = [Act(3000 + l, 1, HIDDEN) for l in range(LAYERS)]
     gu = [smq.DeviceBuffer(2 * HIDDEN * 4) for _ in range(LAYERS)]
+    yo = [smq.DeviceBuffer(DIM * 4) for _ in range(LAYERS)]
+    plans = [smq.GemvPlan(ffn_items(m, ax, ah, gu, yo)) for m in copies]
     big = [smq.DeviceBuffer(256 << 20) for _ in range(2)]
     big[0].fill(1)
     smq.synchronize()
     for i in range(4):
-        smq.gemv_grouped([(layer.qmat(k), None, gu[l].ptr + (HIDDEN * 4 if k == "up" else 0), False, ax[l].d,
-                           ax[l].q) for l, layer in enumerate(copies[i % 2]) for k in ("gate", "up")])
+        plans[i % 2].launch()
     smq.synchronize()
     big[1].copy_from(big[0])
     smq.synchronize()
@@ -219,7 +228,7 @@ def traffic_probe():
 
 
 def summarize_pmc(fetch_dir, write_dir):
-    """Per-dispatch HBM traffic of the grouped gate/up launch from two
+    """Per-dispatch HBM traffic of the planned FFN-step launch from two
     rocprofv3 --pmc runs of --traffic-probe, scaled by the copy's counter
     reading."""
     import csv
@@ -229,7 +238,7 @@ def summarize_pmc(fetch_dir, write_dir):
         rows = []
         for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
             rows += [r for r in csv.DictReader(open(f)) if r["Counter_Name"] == counter]
-        gemv = [float(r["Counter_Value"]) for r in rows if "k_gemv_ct" in r["Kernel_Name"]]
+        gemv = [float(r["Counter_Value"]) for r in rows if "k_gemv_plan" in r["Kernel_Name"]]
         copy = sum(float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]
                    and float(r["Counter_Value"]) > 1e5)
         return gemv, copy
@@ -242,7 +251,8 @@ def summarize_pmc(fetch_dir, write_dir):
     w_kib = float(np.median(write)) * wscale
     out = {"fetch_kib_raw_median": float(np.median(fetch)), "write_kib_raw_median": float(np.median(write)),
            "copy_fetch_kib_raw": fcopy, "copy_write_kib_raw": wcopy, "fetch_scale": fscale, "write_scale": wscale,
-           "traffic_bytes": int((f_kib + w_kib) * 1024), "algorithmic_bytes": LAYERS * q8_bytes(2 * HIDDEN, DIM),
+           "traffic_bytes": int((f_kib + w_kib) * 1024),
+           "algorithmic_bytes": LAYERS * (q8_bytes(2 * HIDDEN, DIM) + q8_bytes(DIM, HIDDEN)),
            "dispatches": len(fetch)}
     print(json.dumps(out))
     return out
@@ -370,9 +380,15 @@ def main():
     def down_group(m):
         smq.gemv_grouped([(layer.qmat("down"), None, y_out[l], False, ah[l].d, ah[l].q) for l, layer in enumerate(m)])
 
-    def ffn_streamed(m):
+    def ffn_grouped(m):
         gateup_group(m)
         down_group(m)
+
+    # the step's 72 GEMVs as one planned launch per model copy (the split over workgroups made once)
+    plans = [smq.GemvPlan(ffn_items(m, ax, ah, gu_out, y_out)) for m in copies]
+
+    def ffn_streamed(c):
+        plans[c].launch()
 
     # one checked eager pass of each form (bounds checks on), then timing without host checks
     ffn_step(copies[0])
@@ -380,30 +396,36 @@ def main():
     seq_layer0 = [gu_out[0].download(np.float32), y_out[0].download(np.float32)]
     for b in gu_out + y_out:
         b.fill(0)
-    ffn_streamed(copies[0])
+    ffn_streamed(0)
     smq.numeric_check()
     smq.set_checks(False)
     step_bytes = LAYERS * (q8_bytes(2 * HIDDEN, DIM) + q8_bytes(DIM, HIDDEN))
 
-    # headline: the 72 GEMVs of the 24-layer FFN step streamed in two launches; the K timed steps (model
-    # copies alternating) are one captured graph, so no per-step graph launch gap sits between them
+    # headline: the 72 GEMVs of the 24-layer FFN step streamed in one planned launch; the K timed steps
+    # (model copies alternating) are one captured graph, so no per-step graph launch gap sits between them
     if args.warmup:
-        warm = smq.capture(lambda: [ffn_streamed(copies[i % 2]) for i in range(args.warmup)] and None)
+        warm = smq.capture(lambda: [ffn_streamed(i % 2) for i in range(args.warmup)] and None)
         warm.launch()
-    timed = smq.capture(lambda: [ffn_streamed(copies[i % 2]) for i in range(args.steps)] and None)
+    timed = smq.capture(lambda: [ffn_streamed(i % 2) for i in range(args.steps)] and None)
     # ms_per_step: the median of HEAD_SAMPLES replays of the K-step graph (best and all beside it)
     med, best, samples = timed_samples([timed], 1, HEAD_SAMPLES)
     ms_per_step = med / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    step_graphs = [smq.capture(lambda m=m: ffn_streamed(m)) for m in copies]
+    step_graphs = [smq.capture(lambda c=c: ffn_streamed(c)) for c in range(2)]
     per_graph_ms = timed_graph(step_graphs, args.steps)
     smq.numeric_check()
     gpu_layer0 = [gu_out[0].download(np.float32), y_out[0].download(np.float32)]  # for the CPU parity gate
     same_as_sequential = all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(gpu_layer0, seq_layer0))
     log(f"bench: FFN step streamed {ms_per_step * 1e3:.1f} us, {value:.0f} GB/s")
+    # the same step as two grouped launches (48 gate/up, 24 down): the form before the plan
+    two_graphs = [smq.capture(lambda: [ffn_grouped(copies[i % 2]) for i in range(args.steps)] and None)]
+    timed_graph(two_graphs, 1)
+    two_med, two_best, _ = timed_samples(two_graphs, 1, HEAD_SAMPLES)
+    two_ms = two_med / args.steps
+    log(f"bench: FFN step as two grouped launches {two_ms * 1e3:.1f} us")
 
-    # dominant kernel: the gate/up group launch (k_gemv_ct: coalesced 8-row x 28-block tiles, 236 MB), eight launches
-    # per graph (the two copies alternating) so that one graph launch's host overhead is spread over eight
+    # the gate/up group alone (k_gemv_ct: coalesced 8-row x 28-block tiles, 236 MB), eight launches per graph
+    # (the two copies alternating) so that one graph launch's host overhead is spread over eight
     per_graph = 8
     gu_graphs = [smq.capture(lambda: [gateup_group(copies[i % 2]) for i in range(per_graph)] and None)]
     timed_graph(gu_graphs, 2)
@@ -420,9 +442,9 @@ def main():
     seq_ms = timed_graph(seq_graphs, max(20, args.steps))
     one_ms = timed_graph([smq.capture(lambda m=m: gateup_only(m)) for m in copies], max(20, args.steps)) / LAYERS
     extra = {"headline_timing": {
-        "what": "value = the 24-layer FFN step's 72 GEMVs as two grouped launches (cross-layer grouped GEMV "
-                "bandwidth: each GEMV has its own precomputed activation, so no layer waits for another); "
-                "ms_per_step = median of the samples below, each one replay of the K-step graph",
+        "what": "value = the 24-layer FFN step's 72 GEMVs as one planned launch (smq_gemv_plan: cross-layer "
+                "grouped GEMV bandwidth, each GEMV with its own precomputed activation, so no layer waits for "
+                "another); ms_per_step = median of the samples below, each one replay of the K-step graph",
         "samples_us_per_step": [round(t / args.steps * 1e3, 3) for t in samples],
         "median_us_per_step": round(med / args.steps * 1e3, 3), "best_us_per_step": round(best / args.steps * 1e3, 3),
         "best_GBps": round(step_bytes / (best / args.steps * 1e-3) / 1e9, 1)},
@@ -432,6 +454,15 @@ def main():
         "gateup_single_launch_us": round(one_ms * 1e3, 3),
         "gateup_single_launch_GBps": round(q8_bytes(2 * HIDDEN, DIM) / (one_ms * 1e-3) / 1e9, 1),
         "bit_identical_to_streamed": same_as_sequential},
+        "ffn_step_two_grouped_launches": {
+            "what": "the same step as two grouped launches per step (smq_gemv_grouped: 48 gate/up, then 24 down)",
+            "us_per_step": round(two_ms * 1e3, 2), "GBps": round(step_bytes / (two_ms * 1e-3) / 1e9, 1),
+            "best_us_per_step": round(two_best / args.steps * 1e3, 2)},
+        "gateup_group48": {
+            "what": "the 48 gate/up GEMVs alone as one grouped launch (k_gemv_ct), eight launches per graph, "
+                    "median of 11 replays",
+            "us_per_launch": round(gu_ms * 1e3, 3), "GBps": round(gu_gbs, 1), "bytes_per_launch": gu_bytes,
+            "pct_hbm_peak": round(100 * gu_gbs / HBM_PEAK_GBS, 1)},
         "ffn_step_streamed_graph_per_step": {
             "what": "the headline step, one graph launch per step (includes the gap between graph launches)",
             "us_per_step": round(per_graph_ms * 1e3, 2), "GBps": round(step_bytes / (per_graph_ms * 1e-3) / 1e9, 1)}}
@@ -504,6 +535,20 @@ def main():
         smq.matmul([(smq.QMat(c0_bufs[(n0 // g0 - 1) * g0 + 5], DIM, Q_DIM), None, one)], ax[5].d, ax[5].q, 1)
         extra["c0_gemv_896x896_grouped48"]["bit_identical_to_single"] = bool(np.array_equal(
             c0_out[5].download(np.float32).view(np.uint32), one.download(np.float32).view(np.uint32)))
+        # the same matrices as planned launches of 192 GEMVs (smq_gemv_plan: more items than a grouped
+        # launch takes, so a launch's fixed cost is spread over 173 MB); three plans in turn
+        p0 = 192
+        c0_pout = [smq.DeviceBuffer(DIM * 4) for _ in range(p0)]
+        c0_plans = [smq.GemvPlan([(smq.QMat(c0_bufs[k * p0 + j], DIM, Q_DIM), None, c0_pout[j], False,
+                                   ax[j % LAYERS].d, ax[j % LAYERS].q) for j in range(p0)]) for k in range(n0 // p0)]
+        single("c0_gemv_896x896_plan192", lambda i: c0_plans[i % len(c0_plans)].launch(), p0 * q8_bytes(DIM, Q_DIM),
+               n0 // p0 * 2, note="one planned launch of 192 distinct 896x896 GEMVs, 576 matrices (520 MB) in turn")
+        smq.synchronize()
+        smq.matmul([(smq.QMat(c0_bufs[(n0 // p0 - 1) * p0 + 7], DIM, Q_DIM), None, one)], ax[7].d, ax[7].q, 1)
+        extra["c0_gemv_896x896_plan192"]["bit_identical_to_single"] = bool(np.array_equal(
+            c0_pout[7].download(np.float32).view(np.uint32), one.download(np.float32).view(np.uint32)))
+        for pl in c0_plans:
+            pl.destroy()
         del c0_bufs
         # configs[1] down projection at batch 128 (exact GEMM; int8 MFMA)
         hx128 = Act(4200, 128, HIDDEN)
@@ -589,7 +634,7 @@ def main():
             log(f"bench: cpu baseline failed: {ex!r}")
 
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", "gemv_ct_q8_gateup_group_traffic.json")
+    tfile = os.path.join(ROOT, "profiles", "gemv_plan_q8_ffn_step_traffic.json")
     if os.path.exists(tfile):  # measured by two rocprofv3 --pmc runs of --traffic-probe (see that file)
         with open(tfile) as f:
             traffic = json.load(f).get("traffic_bytes")
@@ -609,18 +654,19 @@ def main():
         "data": "synthetic: seeded N(0,0.02) weights packed by the q8pack rule, N(0,1) activations quantized on GPU",
         "config": {"workload": "configs[1]: Qwen2.5-0.5B Q8 FFN matmuls, batch 1 (decode GEMV), all 24 layers "
                                "(gate 4864x896, up 4864x896, down 896x4864 per layer, each with its layer's "
-                               "activation), 353 MB/step streamed as two grouped launches (48 gate/up, 24 down), "
+                               "activation), 354 MB/step streamed as one planned launch of the 72 GEMVs, "
                                "2 model copies alternated", "bytes_per_step": step_bytes,
                    "parallelism": "none (1 GPU)"},
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
         "decode_tok_s": extra.get("c4_qwen05_forward", {}).get("decode_tok_s"),
-        "roofline": {"kernel": "k_gemv_ct<exact, NB=28, RT=8, D=2>: coalesced 8-row x 28-block tiles, two in flight, "
-                               "3 workgroups per CU (48 gate/up GEMVs 4864x896, one launch); HIP events, median of 11 "
-                               "graph replays of 8 launches",
+        "roofline": {"kernel": "k_gemv_plan<exact>: the FFN step's 72 GEMVs in one launch, 768 workgroups (3 per "
+                               "CU) split by bytes; 4864x896 items on coalesced 8-row x 28-block tiles (two in "
+                               "flight), 896x4864 items on 14-row x 32-block K chunks; HIP events over the K-step "
+                               "graph on the launch stream, median of 11 replays",
                      "bound": "hbm",
-                     "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "bytes_per_launch": gu_bytes, "us_per_launch": round(gu_ms * 1e3, 3)},
+                     "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "bytes_per_launch": step_bytes, "us_per_launch": round(ms_per_step * 1e3, 3)},
         "cpu_baseline": cpu,
         "extra": extra,
         "wall_s": round(time.time() - t_start, 1),
@@ -822,21 +868,26 @@ def hbm_anchor(extra, gib=2):
             copy[f"copy_{'nt' if nt else 'plain'}_{wgs}x{threads}"] = round(2 * half * 4 / (med * 1e-3) / 1e9, 1)
     best_read = max(sweep, key=sweep.get)
     best_copy = max(copy, key=copy.get)
-    # the same read at the byte counts of single grouped launches: one launch per region, eight distinct
-    # regions per graph (no region is read twice in a row), so the launch's fixed cost is in the rate
+    # the same read at the byte counts of single grouped launches: one launch per region, up to eight
+    # distinct regions of the buffer per graph (no region is read twice in a row), so the launch's fixed
+    # cost is in the rate
     rshape = best_read.split("_")
     rnt, (rwgs, rthr) = rshape[1] == "nt", map(int, rshape[2].split("x"))
     sized = {}
     for name, size in (("c0_group48_896x896", 48 * q8_bytes(DIM, DIM)),
+                       ("c0_plan192_896x896", 192 * q8_bytes(DIM, DIM)),
                        ("down_group24_896x4864", LAYERS * q8_bytes(DIM, HIDDEN)),
                        ("q5_group16_8960x1536", 16 * q8_bytes(8960, 1536, block=22)),
-                       ("gateup_group48_4864x896", 2 * LAYERS * q8_bytes(HIDDEN, DIM))):
+                       ("gateup_group48_4864x896", 2 * LAYERS * q8_bytes(HIDDEN, DIM)),
+                       ("ffn_step_plan72", LAYERS * (q8_bytes(2 * HIDDEN, DIM) + q8_bytes(DIM, HIDDEN)))):
         size = size // 256 * 256
-        g = [smq.capture(lambda: [smq.stream_read(src.at(k * size), size, rwgs, rthr, rnt, sink) for k in range(8)]
-                         and None)]
+        nreg = min(8, nbytes // size)  # distinct regions inside the buffer
+        g = [smq.capture(lambda: [smq.stream_read(src.at(k * size), size, rwgs, rthr, rnt, sink)
+                                  for k in range(nreg)] and None)]
         timed_graph(g, 1)
         med, best, _ = timed_samples(g, 1, 11)
-        sized[name] = {"bytes": size, "us": round(med * 1e3 / 8, 2), "GBps": round(size * 8 / (med * 1e-3) / 1e9, 1)}
+        sized[name] = {"bytes": size, "us": round(med * 1e3 / nreg, 2),
+                       "GBps": round(size * nreg / (med * 1e-3) / 1e9, 1), "regions": nreg}
     del src, dst
     extra["hbm_anchor"] = {
         "what": f"plain coalesced 16-byte streaming kernels over {gib} GiB (read: nothing written; copy: bytes read "

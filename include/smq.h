@@ -203,6 +203,23 @@ typedef struct smq_group_item {
     const int8_t *xq;   /* device: nb*32 values */
 } smq_group_item;
 smq_status smq_gemv_grouped(const smq_group_item *items, uint32_t n);
+/* A plan of independent one-token Q8 GEMVs streamed by one launch (no
+ * reference counterpart: the reference runs them one after another), for
+ * more items than SMQ_MAX_GROUP and for 28- and 152-block rows together (the
+ * 896- and 4864-wide projections of Qwen2.5-0.5B: a whole FFN step's 72
+ * GEMVs in one launch). Every item: packed Q8 rows (row_bytes = nb*36) of
+ * nb = 28 or 152 blocks, 16-byte aligned, 4-byte aligned activations; every
+ * output bit-identical to smq_matmul's. smq_gemv_plan_create validates the
+ * items, splits them over workgroups in proportion to their bytes and copies
+ * the split to device memory the plan owns (synchronously; not under
+ * capture). smq_gemv_plan_launch is one asynchronous launch that may be
+ * captured; the numeric flag as smq_matmul. The items' buffers must outlive
+ * the plan; destroy a plan after every graph that launches it. */
+#define SMQ_MAX_PLAN_ITEMS 4096
+typedef struct smq_gemv_plan smq_gemv_plan;
+smq_status smq_gemv_plan_create(const smq_group_item *items, uint32_t n, smq_gemv_plan **plan);
+smq_status smq_gemv_plan_launch(const smq_gemv_plan *plan);
+void smq_gemv_plan_destroy(smq_gemv_plan *plan);
 /* Synchronizes, then returns SMQ_ERR_NUMERIC (and clears the flag) if any
  * quantize or matmul since the last check saw a non-finite value. */
 /* ---- fused decode matmuls (one token) --------------------------------------

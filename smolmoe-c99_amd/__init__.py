@@ -110,6 +110,9 @@ _SIGS = {
     "smq_matmul_glu_q8": (ctypes.c_int, [ctypes.POINTER(_QMat), ctypes.POINTER(_QMat), ctypes.POINTER(_Act),
                                          ctypes.c_int, _vp, _vp, _vp, _vp]),
     "smq_gemv_grouped": (ctypes.c_int, [ctypes.POINTER(_GroupItem), _u32]),
+    "smq_gemv_plan_create": (ctypes.c_int, [ctypes.POINTER(_GroupItem), _u32, ctypes.POINTER(ctypes.c_void_p)]),
+    "smq_gemv_plan_launch": (ctypes.c_int, [_vp]),
+    "smq_gemv_plan_destroy": (None, [_vp]),
     "smq_rope_kv": (ctypes.c_int, [_vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _vp, _vp, _vp, _vp, _u32, _vp]),
     "smq_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _u32, _vp]),
     "smq_attention_q8": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, ctypes.POINTER(_AttnShape), _u32, _vp, _vp, _vp]),
@@ -438,9 +441,7 @@ def matmul_glu_q8(gate, up, activation, glu, h, hd, hq, gate_scratch=None):
                                     _p(hq), _p(gate_scratch)))
 
 
-def gemv_grouped(items):
-    """items: sequence of (QMat, bias or None, y, accumulate, xd, xq): independent
-    one-token GEMVs with their own activations, one launch."""
+def _group_items(items):
     cm = [it[0]._c() for it in items]
     arr = (_GroupItem * len(items))()
     for i, it in enumerate(items):
@@ -450,7 +451,40 @@ def gemv_grouped(items):
         arr[i].accumulate = int(bool(it[3]))
         arr[i].xd = _p(it[4])
         arr[i].xq = _p(it[5])
+    return arr, cm
+
+
+def gemv_grouped(items):
+    """items: sequence of (QMat, bias or None, y, accumulate, xd, xq): independent
+    one-token GEMVs with their own activations, one launch."""
+    arr, _keep = _group_items(items)
     _check(load().smq_gemv_grouped(arr, len(items)))
+
+
+class GemvPlan:
+    """smq_gemv_plan: items as for gemv_grouped (Q8 rows of 28 or 152 blocks, any number up to
+    4096), split over workgroups once; launch() is one launch (capturable)."""
+
+    def __init__(self, items):
+        arr, _keep = _group_items(items)
+        self._items = items  # the buffers the plan points at live as long as the plan
+        h = ctypes.c_void_p()
+        _check(load().smq_gemv_plan_create(arr, len(items), ctypes.byref(h)))
+        self.handle = h.value
+
+    def launch(self):
+        _check(load().smq_gemv_plan_launch(self.handle))
+
+    def destroy(self):
+        if self.handle:
+            load().smq_gemv_plan_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
 
 
 # ---- decoder pieces (src/model.c:425-542, 669-677; src/sampler.c:57-63)

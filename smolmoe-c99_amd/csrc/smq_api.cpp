@@ -13,6 +13,8 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <new>
+#include <vector>
 #include <mutex>
 
 #include "smq.h"
@@ -558,6 +560,130 @@ smq_status smq_gemv_grouped(const smq_group_item *items, uint32_t n) {
         return SMQ_OK;
     }
     return hip_ok(smq::launch_gemv_grouped(ga, q5, g.fast != 0, g.cur), "gemv_grouped") ? SMQ_OK : t_status;
+}
+
+struct smq_gemv_plan {
+    smq::PlanWg *dev; /* one descriptor per workgroup, device memory owned by the plan */
+    uint32_t wgs;
+    int bp, device;
+};
+
+smq_status smq_gemv_plan_create(const smq_group_item *items, uint32_t n, smq_gemv_plan **plan) {
+    if (!ready()) return t_status;
+    if (!plan) return set_status(SMQ_ERR_RANGE, "gemv_plan_create: plan is NULL");
+    *plan = nullptr;
+    if (t_capturing) return set_status(SMQ_ERR_STATE, "gemv_plan_create: not under capture");
+    if (!items || n < 1 || n > SMQ_MAX_PLAN_ITEMS)
+        return set_status(SMQ_ERR_RANGE, "gemv_plan_create: %u items (1..%u)", n, (unsigned)SMQ_MAX_PLAN_ITEMS);
+    std::vector<smq::GroupItem> its(n);
+    std::vector<uint32_t> kind(n), tiles(n);
+    std::vector<double> bytes(n);
+    double total = 0.0;
+    int bp = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        const smq_qmat *w = items[i].w;
+        if (!w) return set_status(SMQ_ERR_RANGE, "gemv_plan_create: item %u has no matrix", i);
+        if (w->dtype != 1 || (w->nb != 28 && w->nb != 152) || w->nb != (w->cols + smq::QK - 1) / smq::QK ||
+            w->row_bytes != (size_t)w->nb * smq::Q8_BYTES || ((uintptr_t)w->data & 15u) || !w->rows ||
+            (((uintptr_t)items[i].xd | (uintptr_t)items[i].xq) & 3u))
+            return set_status(SMQ_ERR_RANGE,
+                              "gemv_plan_create: item %u: a plan takes packed, 16-byte aligned Q8 rows of 28 or 152 "
+                              "blocks with 4-byte aligned activations",
+                              i);
+        if (!check_operands(w->data, w->row_bytes, w->rows, w->nb, false, items[i].xd, items[i].xq, 1, w->nb,
+                            items[i].y, w->rows, "gemv_plan_create") ||
+            !extent_ok(items[i].bias, items[i].bias ? (size_t)w->rows * 4 : 0, "bias"))
+            return t_status;
+        smq::GroupItem &it = its[i];
+        memset(&it, 0, sizeof(it));
+        it.w = w->data;
+        it.row_bytes = w->row_bytes;
+        it.bias = items[i].bias;
+        it.y = items[i].y;
+        it.xd = items[i].xd;
+        it.xq = items[i].xq;
+        it.rows = w->rows;
+        it.accumulate = items[i].accumulate != 0;
+        bp |= items[i].bias || items[i].accumulate;
+        kind[i] = w->nb == 152;
+        const uint32_t rt = smq::plan_rows_per_tile(kind[i] != 0);
+        tiles[i] = (w->rows + rt - 1) / rt;
+        bytes[i] = (double)w->rows * (double)w->row_bytes;
+        total += bytes[i];
+    }
+    int per_cu = 0, cus = 0;
+    if (!hip_ok(smq::plan_resident(per_cu), "gemv_plan_create") ||
+        !hip_ok(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, g.device), "gemv_plan_create"))
+        return t_status;
+    /* every item a share of the resident workgroups in proportion to its bytes (at least one, at most
+     * one per tile; largest remainders first, so the shares add up to the resident workgroups and
+     * none waits for a second wave), each workgroup a contiguous tile range */
+    const uint32_t resident = (uint32_t)per_cu * (uint32_t)(cus > 0 ? cus : 1);
+    std::vector<uint32_t> share(n);
+    std::vector<double> frac(n);
+    uint64_t given = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        const double q = (double)resident * bytes[i] / total;
+        uint32_t k = (uint32_t)q;
+        k = k < 1 ? 1 : (k > tiles[i] ? tiles[i] : k);
+        share[i] = k;
+        frac[i] = q - (double)(uint32_t)q;
+        given += k;
+    }
+    while (given < resident) {
+        uint32_t best = n;
+        for (uint32_t i = 0; i < n; ++i)
+            if (share[i] < tiles[i] && (best == n || frac[i] > frac[best])) best = i;
+        if (best == n) break; /* every tile has its own workgroup */
+        ++share[best];
+        frac[best] = -1.0;
+        ++given;
+    }
+    std::vector<smq::PlanWg> host;
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t k = share[i];
+        for (uint32_t j = 0; j < k; ++j) {
+            smq::PlanWg d;
+            memset(&d, 0, sizeof(d));
+            d.item = its[i];
+            d.t0 = (uint32_t)((uint64_t)tiles[i] * j / k);
+            d.t1 = (uint32_t)((uint64_t)tiles[i] * (j + 1) / k);
+            d.kind = kind[i];
+            host.push_back(d);
+        }
+    }
+    smq_gemv_plan *p = new (std::nothrow) smq_gemv_plan;
+    if (!p) return set_status(SMQ_ERR_NOMEM, "gemv_plan_create: out of host memory");
+    p->wgs = (uint32_t)host.size();
+    p->bp = bp;
+    p->device = g.device;
+    p->dev = nullptr;
+    const size_t nbytes = host.size() * sizeof(smq::PlanWg);
+    if (!hip_ok(hipMalloc((void **)&p->dev, nbytes), "gemv_plan_create") ||
+        !hip_ok(hipMemcpy(p->dev, host.data(), nbytes, hipMemcpyHostToDevice), "gemv_plan_create")) {
+        if (p->dev) (void)hipFree(p->dev);
+        delete p;
+        return t_status;
+    }
+    *plan = p;
+    return SMQ_OK;
+}
+
+smq_status smq_gemv_plan_launch(const smq_gemv_plan *plan) {
+    if (!ready()) return t_status;
+    if (!plan || !plan->dev) return set_status(SMQ_ERR_RANGE, "gemv_plan_launch: plan is NULL");
+    if (plan->device != g.device)
+        return set_status(SMQ_ERR_STATE, "gemv_plan_launch: plan made on device %d", plan->device);
+    return hip_ok(smq::launch_gemv_plan(plan->dev, plan->wgs, g.fast != 0, plan->bp != 0, g.flag, g.cur),
+                  "gemv_plan_launch")
+               ? SMQ_OK
+               : t_status;
+}
+
+void smq_gemv_plan_destroy(smq_gemv_plan *plan) {
+    if (!plan) return;
+    if (plan->dev) (void)hipFree(plan->dev);
+    delete plan;
 }
 
 /* Validates a fused-call activation for matrices of `cols` columns. */

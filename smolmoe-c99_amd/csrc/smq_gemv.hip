@@ -57,26 +57,28 @@ struct CtBuf {
     float sink[64];
 };
 
-template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT, uint32_t D, class GA>
-__global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gemv_ct(GA g) {
+/* LDS pitch of a tile's rows: a multiple of four floats (16-byte chain reads) that is 4 mod 32, so
+ * the lane sums of one block's eight lanes (stored 8 pitches apart by one write) fall in distinct
+ * banks, and the eight chain lanes of a row read distinct 16-byte bank groups (measured: a pitch of
+ * 32 floats, where those writes collide, cost 7 %) */
+template <uint32_t NB>
+constexpr uint32_t ct_pitch() { return (NB + 3) / 4 * 4 + (36 - (NB + 3) / 4 * 4 % 32) % 32; }
+
+/* Tiles t0..t1-1 (t1 > t0) of item I, RT rows each, through the two LDS buffers `buf`. */
+template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT, uint32_t D>
+__device__ __forceinline__ void ct_tiles(const GroupItem &I, uint32_t t0, uint32_t t1, int *flag,
+                                         CtBuf<RT, ct_pitch<NB>()> (&buf)[2]) {
     static_assert(NB % 4 == 0, "rows of whole 16-byte pieces");
     constexpr uint32_t C16 = 9 * NB / 4;       /* 16-byte pieces per row */
     constexpr uint32_t TCH = RT * C16;         /* pieces per tile */
-    /* LDS pitch: a multiple of four floats (16-byte chain reads) that is 4 mod 32, so the lane
-     * sums of one block's eight lanes (stored 8 pitches apart by one write) fall in distinct
-     * banks, and the eight chain lanes of a row read distinct 16-byte bank groups (measured: a
-     * pitch of 32 floats, where those writes collide, cost 7 %) */
-    constexpr uint32_t SP = (NB + 3) / 4 * 4 + (36 - (NB + 3) / 4 * 4 % 32) % 32;
+    constexpr uint32_t SP = ct_pitch<NB>();
     static_assert(SP % 32 == 4 && SP >= NB, "pitch 4 mod 32");
     constexpr uint32_t NQ = NB / 4;
     static_assert(TCH <= CPT * CT_NT, "each piece of a tile has a thread slot");
     using Buf = CtBuf<RT, SP>;
-    __shared__ __attribute__((aligned(16))) Buf buf[2];
 
     const uint32_t tid = threadIdx.x;
-    const GroupItem &I = g.item[find_ct_item(g, blockIdx.x)];
-    const uint32_t rows = I.rows, tiles = (rows + RT - 1) / RT, wg = blockIdx.x - I.wg_begin;
-    const uint32_t t0 = (uint32_t)((uint64_t)tiles * wg / I.nwg), t1 = (uint32_t)((uint64_t)tiles * (wg + 1) / I.nwg);
+    const uint32_t rows = I.rows;
     const uint32_t my_steps = t1 - t0;
     const unsigned char *wbase = I.w;
     const size_t row_bytes = I.row_bytes;
@@ -191,7 +193,7 @@ __global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) v
                 if (live && cl == 7 && row < rows) {
                     float o = v;
                     if (bias_p) o = o + B[j]; /* model.c:259-262 */
-                    if (g.flag && !(fabsf(o) <= FLT_MAX)) *g.flag = 1;
+                    if (flag && !(fabsf(o) <= FLT_MAX)) *flag = 1;
                     if (accum) o = P[j] + o;
                     y[row] = o;
                 }
@@ -204,6 +206,15 @@ __global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     trip(k, std::false_type{}); /* my_steps >= 1: the last trip */
 }
 
+template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT, uint32_t D, class GA>
+__global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gemv_ct(GA g) {
+    __shared__ __attribute__((aligned(16))) CtBuf<RT, ct_pitch<NB>()> buf[2];
+    const GroupItem &I = g.item[find_ct_item(g, blockIdx.x)];
+    const uint32_t tiles = (I.rows + RT - 1) / RT, wg = blockIdx.x - I.wg_begin;
+    const uint32_t t0 = (uint32_t)((uint64_t)tiles * wg / I.nwg), t1 = (uint32_t)((uint64_t)tiles * (wg + 1) / I.nwg);
+    ct_tiles<FAST, BP, NB, RT, CPT, D>(I, t0, t1, g.flag, buf);
+}
+
 /* Wide rows (nb > CK_KC, 152 blocks = the 4864-wide down projection): the same coalesced pieces
  * over K chunks of CK_KC blocks. A step is RT rows x one chunk (RT*9*CK_KC/4 contiguous-per-row
  * pieces); the chain thread (row, lane) keeps its sum in a register across the chunks of a tile,
@@ -213,25 +224,26 @@ __global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) v
  * activation words of one 16-byte LDS read. */
 constexpr uint32_t CK_KC = 32;
 
-template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT, class GA>
-__global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gemv_ck(GA g) {
+constexpr uint32_t CK_SP = CK_KC + (36 - CK_KC % 32) % 32; /* LDS pitch of a chunk's rows */
+
+/* Tiles t0..t1-1 (t1 > t0) of item I, RT rows each, K chunk by K chunk, through the two LDS buffers
+ * `buf`; `act` holds the item's activation in the rows' layout. */
+template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT>
+__device__ __forceinline__ void ck_tiles(const GroupItem &I, uint32_t t0, uint32_t t1, int *flag,
+                                         CtBuf<RT, CK_SP> (&buf)[2], uint32_t (&act)[NB * 9]) {
     constexpr uint32_t KC = CK_KC;
     constexpr uint32_t NCH = (NB + KC - 1) / KC;    /* chunks per row */
     constexpr uint32_t KL = NB - (NCH - 1) * KC;    /* blocks of the last chunk */
     static_assert(NB % 4 == 0 && NB > KC && KL % 4 == 0, "whole 16-byte pieces in every chunk");
     constexpr uint32_t P = 9 * KC / 4, PL = 9 * KL / 4; /* pieces per row of a chunk, of the last */
     constexpr uint32_t TCH = RT * P;
-    constexpr uint32_t SP = KC + (36 - KC % 32) % 32;
+    constexpr uint32_t SP = CK_SP;
     static_assert(SP % 32 == 4 && SP >= KC, "pitch 4 mod 32");
     static_assert(TCH <= CPT * CT_NT, "each piece of a step has a thread slot");
     using Buf = CtBuf<RT, SP>;
-    __shared__ __attribute__((aligned(16))) Buf buf[2];
-    __shared__ __attribute__((aligned(16))) uint32_t act[NB * 9];
 
     const uint32_t tid = threadIdx.x;
-    const GroupItem &I = g.item[find_ct_item(g, blockIdx.x)];
-    const uint32_t rows = I.rows, tiles = (rows + RT - 1) / RT, wg = blockIdx.x - I.wg_begin;
-    const uint32_t t0 = (uint32_t)((uint64_t)tiles * wg / I.nwg), t1 = (uint32_t)((uint64_t)tiles * (wg + 1) / I.nwg);
+    const uint32_t rows = I.rows;
     const uint32_t my_steps = (t1 - t0) * NCH;
     const unsigned char *wbase = I.w;
     const size_t row_bytes = I.row_bytes;
@@ -355,7 +367,7 @@ __global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) v
                 if (cl == 7 && row < rows) {
                     float o = v;
                     if (bias_p) o = o + B; /* model.c:259-262 */
-                    if (g.flag && !(fabsf(o) <= FLT_MAX)) *g.flag = 1;
+                    if (flag && !(fabsf(o) <= FLT_MAX)) *flag = 1;
                     if (accum) o = Pr + o;
                     y[row] = o;
                 }
@@ -365,6 +377,39 @@ __global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) v
         B = Bn;
         Pr = Pn;
     }
+}
+
+template <bool FAST, bool BP, uint32_t NB, uint32_t RT, uint32_t CPT, class GA>
+__global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gemv_ck(GA g) {
+    __shared__ __attribute__((aligned(16))) CtBuf<RT, CK_SP> buf[2];
+    __shared__ __attribute__((aligned(16))) uint32_t act[NB * 9];
+    const GroupItem &I = g.item[find_ct_item(g, blockIdx.x)];
+    const uint32_t tiles = (I.rows + RT - 1) / RT, wg = blockIdx.x - I.wg_begin;
+    const uint32_t t0 = (uint32_t)((uint64_t)tiles * wg / I.nwg), t1 = (uint32_t)((uint64_t)tiles * (wg + 1) / I.nwg);
+    ck_tiles<FAST, BP, NB, RT, CPT>(I, t0, t1, g.flag, buf, act);
+}
+
+/* A planned launch (smq_gemv_plan): one workgroup per descriptor, each a contiguous tile range of
+ * one item, 28-block items on the coalesced tiles and 152-block items on the K chunks, in one
+ * launch. The descriptor is read at a uniform address (scalar loads, one round trip); the two
+ * forms share the LDS. */
+constexpr uint32_t PLAN_CT_RT = 8, PLAN_CK_RT = 14;
+union PlanLds {
+    CtBuf<PLAN_CT_RT, ct_pitch<28>()> ct[2];
+    struct {
+        CtBuf<PLAN_CK_RT, CK_SP> buf[2];
+        uint32_t act[152 * 9];
+    } ck;
+};
+
+template <bool FAST, bool BP>
+__global__ __launch_bounds__(CT_NT) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gemv_plan(const PlanWg *wgs,
+                                                                                                int *flag) {
+    __shared__ __attribute__((aligned(16))) PlanLds lds;
+    const PlanWg &d = wgs[blockIdx.x];
+    const GroupItem I = d.item;
+    if (d.kind == 0) ct_tiles<FAST, BP, 28, PLAN_CT_RT, 1, 2>(I, d.t0, d.t1, flag, lds.ct);
+    else ck_tiles<FAST, BP, 152, PLAN_CK_RT, 2>(I, d.t0, d.t1, flag, lds.ck.buf, lds.ck.act);
 }
 
 /* every item a share of the resident workgroups of kernel k (at most max_per_cu per CU) in proportion
@@ -441,6 +486,33 @@ hipError_t launch_ct_fast(GroupArgs &g, hipStream_t s) {
 }
 
 }  // namespace
+
+uint32_t plan_rows_per_tile(bool wide) { return wide ? PLAN_CK_RT : PLAN_CT_RT; }
+
+hipError_t plan_resident(int &per_cu) {
+    static int resident = 0;
+    if (!resident) {
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, (const void *)k_gemv_plan<false, false>,
+                                                                          CT_NT, 0);
+        if (e != hipSuccess) return e;
+        if (resident > 3) resident = 3; /* as the grouped launches: about 12 MB in flight chip-wide */
+        if (resident < 1) resident = 1;
+    }
+    per_cu = resident;
+    return hipSuccess;
+}
+
+hipError_t launch_gemv_plan(const PlanWg *wgs, uint32_t n, bool fast, bool bp, int *flag, hipStream_t s) {
+    if (!n) return hipSuccess;
+    if (fast) {
+        if (bp) hipLaunchKernelGGL((k_gemv_plan<true, true>), dim3(n), dim3(CT_NT), 0, s, wgs, flag);
+        else hipLaunchKernelGGL((k_gemv_plan<true, false>), dim3(n), dim3(CT_NT), 0, s, wgs, flag);
+    } else {
+        if (bp) hipLaunchKernelGGL((k_gemv_plan<false, true>), dim3(n), dim3(CT_NT), 0, s, wgs, flag);
+        else hipLaunchKernelGGL((k_gemv_plan<false, false>), dim3(n), dim3(CT_NT), 0, s, wgs, flag);
+    }
+    return hipGetLastError();
+}
 
 bool gemv_ct_ok(const GroupArgs &g, bool q5) {
     if (q5 || (g.nb != 28 && g.nb != 152)) return false;

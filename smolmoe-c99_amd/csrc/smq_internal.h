@@ -83,6 +83,16 @@ inline GroupArgsFew group_args_few(const GroupArgs &g) {
  * packed at 36*nb bytes, 16-byte aligned, 4-byte aligned activations. */
 bool gemv_ct_ok(const GroupArgs &g, bool q5);
 hipError_t launch_gemv_ct(GroupArgs &g, bool fast, hipStream_t s);
+/* A planned grouped launch (csrc/smq_gemv.hip): one descriptor per workgroup, a contiguous tile range
+ * [t0, t1), t1 > t0, of one item; kind 0 = Q8 rows of 28 blocks (tiles of plan_rows_per_tile(false)
+ * rows), 1 = Q8 rows of 152 blocks (plan_rows_per_tile(true) rows); both as gemv_ct_ok requires. */
+struct PlanWg {
+    GroupItem item;
+    uint32_t t0, t1, kind, pad;
+};
+uint32_t plan_rows_per_tile(bool wide);
+hipError_t plan_resident(int &per_cu);
+hipError_t launch_gemv_plan(const PlanWg *wgs, uint32_t n, bool fast, bool bp, int *flag, hipStream_t s);
 /* Layout the streaming kernel needs: 4-byte aligned rows, Q5 nb even. */
 bool group_layout_ok(const GroupArgs &g, bool q5);
 hipError_t launch_gemv_grouped(GroupArgs &g, bool q5, bool fast, hipStream_t s);

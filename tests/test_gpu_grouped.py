@@ -118,3 +118,80 @@ def test_lm_head_streams(orc, fast):
     assert ok
     assert_same_f32(y.download(np.float32), want, "lm head")
     smq.kernels_set_fast(False)
+
+
+def plan_items(orc, shapes, fast, plain=False, seed=500):
+    """(items, wanted outputs) for Q8 matrices of the given (rows, cols) shapes, each with its own
+    activation; odd items carry a bias, every third adds into its output (unless plain)."""
+    items, want = [], []
+    for i, (r, cols) in enumerate(shapes):
+        nb = cols // 32
+        w = synth.q8_weights(seed + i, r, cols)
+        bias = synth.normal(seed + 1000 + i, r, 0.02) if i % 2 == 1 and not plain else None
+        acc = i % 3 == 2 and not plain
+        y0 = synth.normal(seed + 2000 + i, r) if acc else np.zeros(r, np.float32)
+        d, q, hd, hq = quantized(seed + 3000 + i, cols)
+        ok, prod = orc.mat_item(w, nb * 36, r, bias, hd, hq, 1, nb, fast=fast)
+        assert ok
+        want.append(y0 + prod if acc else prod)
+        items.append((smq.QMat(dev(w), r, cols), dev(bias) if bias is not None else None, dev(y0), acc, d, q))
+    return items, want
+
+
+PLAN_CASES = [
+    # (rows, cols) of the items, fast, plain
+    ([(4864, 896), (896, 4864)] * 3, False, False),            # the FFN step's two widths in one launch
+    ([(4864, 896), (896, 4864)] * 3, True, False),             # fast contract
+    ([(896, 896)] * 60 + [(7, 896), (13, 4864)], False, True),  # more items than a grouped launch takes
+    ([(5, 4864), (1, 896), (15, 4864), (9, 896)], False, False),  # items smaller than a tile
+    ([(100000, 896), (30, 4864)], False, True),                # one item of many workgroups
+]
+
+
+@pytest.mark.parametrize("shapes,fast,plain", PLAN_CASES)
+def test_gemv_plan(orc, shapes, fast, plain):
+    """smq_gemv_plan: 28- and 152-block Q8 items in one launch, every output equal to the oracle's
+    mat_item (bias, residual add) bit for bit."""
+    say("gemv plan", len(shapes), shapes[:2], fast, plain)
+    smq.kernels_set_fast(fast)
+    items, want = plan_items(orc, shapes, fast, plain)
+    plan = smq.GemvPlan(items)
+    plan.launch()
+    smq.numeric_check()
+    for i, (it, wnt) in enumerate(zip(items, want)):
+        assert_same_f32(it[2].download(np.float32), wnt, f"item {i}")
+    plan.destroy()
+    smq.kernels_set_fast(False)
+
+
+def test_gemv_plan_in_a_graph(orc):
+    """A plan launch captured once and replayed: each replay equals the oracle (items without a
+    residual add, so every replay writes the same outputs)."""
+    items, want = plan_items(orc, [(4864, 896), (896, 4864), (896, 896)] * 4, False, plain=True, seed=700)
+    plan = smq.GemvPlan(items)
+    g = smq.capture(plan.launch)
+    for rep in range(3):
+        say("gemv plan graph replay", rep)
+        for it in items:
+            it[2].fill(0)
+        g.launch()
+        smq.synchronize()
+        smq.numeric_check()
+        for i, (it, wnt) in enumerate(zip(items, want)):
+            assert_same_f32(it[2].download(np.float32), wnt, f"replay {rep} item {i}")
+    g.destroy()
+    plan.destroy()
+
+
+def test_gemv_plan_rejects_other_rows():
+    d, q, _, _ = quantized(3, 1536)
+    y = smq.DeviceBuffer(64 * 4)
+    q8_48 = smq.QMat(dev(synth.q8_weights(1, 64, 1536)), 64, 1536)
+    q5 = smq.QMat(dev(synth.q5_weights(2, 64, 896)), 64, 896, smq.DTYPE_Q5)
+    d28, q28, _, _ = quantized(4, 896)
+    for item in ((q8_48, None, y, False, d, q), (q5, None, y, False, d28, q28)):
+        with pytest.raises(smq.SmqError) as e:
+            smq.GemvPlan([item])
+        assert e.value.status == smq.SM_ERR_RANGE
+    with pytest.raises(smq.SmqError):
+        smq.GemvPlan([])

@@ -255,9 +255,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
             dv[k] = xd[i < nb ? i : 0];
         }
     }
-    if constexpr (ONE && !Q5) {
-        /* +0.0 in the slots past the last block, never written after (chain_sum_padded): both
-         * buffers whole, sinks included (the launcher keeps every chain read below PF) */
+    if constexpr (ONE) {
+        /* +0.0 in the slots past the last block, never written after (chain_sum_padded: a one-chunk
+         * row's blocks fill the same slots at every step): both buffers whole, sinks included (the
+         * launcher keeps every chain read below PF) */
         constexpr uint32_t PROD_FLOATS = sizeof(prod) / sizeof(float), DSC_FLOATS = sizeof(dsc) / sizeof(float);
         for (uint32_t i = tid; i < PROD_FLOATS; i += NT) (&prod[0][0])[i] = 0.0f;
         if constexpr (FAST)
@@ -419,6 +420,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
                     float acc = 0.0f;
                     const float4 *pp = (const float4 *)pb + tid, *dp = FAST ? (const float4 *)db + tid / 8 : nullptr;
                     if constexpr (!Q5) chain_sum_padded<FAST, 8>(acc, pp, gs / 4, dp, ds / 4, (nb + 3) / 4);
+                    else if (!FAST && nb <= 48) /* every group read at once, plain adds (the 1536-wide rows: 37.2-38.7
+                                                 * against 43.8-44.3 us with a count select per slot, same box) */
+                        chain_sum_padded<FAST, 12>(acc, pp, gs / 4, dp, ds / 4, (nb + 3) / 4);
                     else if (nb <= 32) chain_sum<FAST, 8>(acc, pp, gs / 4, dp, ds / 4, nb);
                     else chain_sum<FAST, 32>(acc, pp, gs / 4, dp, ds / 4, nb);
                     const float v = reduce8_to_lane7(acc);

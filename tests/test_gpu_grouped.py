@@ -52,6 +52,10 @@ GROUP_CASES = [
     (False, 20, [600, 3], False),                     # nb = 1: most threads of a tile idle
     (True, 2048, [700, 3], True),                     # Q5, 64 blocks (the widest pinned pair row), fast
     (True, 64, [100, 1], False),                      # Q5, one pair per row
+    (True, 1472, [900, 5], False),                    # Q5, 46 blocks: one chunk, the last group of the chain half used
+    (True, 4288, [700, 3], False),                    # Q5, 134 blocks: chunks of 68 and 66 (the last chunk's last
+                                                      # group half used, its other slots written by the first chunk)
+    (True, 4480, [500, 7], False),                    # Q5, 140 blocks: two chunks of 70
     # nb = 17: 30-row tiles whose last lane group's padded slots sit at the end of the product
     # buffer; enough rows for several tiles per workgroup, so both product buffers are used
     (False, 544, [100000], False),

@@ -340,6 +340,15 @@ smq_status smq_decode_advance(int32_t *pos, uint32_t *count, const uint32_t *tok
  * streams race. */
 smq_status smq_argmax_advance(const float *logits, uint32_t vocab, const unsigned char *banned, uint32_t *token,
                               int32_t *pos, uint32_t *count, uint32_t *history, uint32_t capacity);
+/* smq_argmax_advance, then the chosen token's embedding row into x
+ * (embed->cols floats): the next decode step's input (model.c:669-677), so a
+ * captured step needs no embedding launch of its own. No reference
+ * counterpart: it fuses the greedy pick (sampler.c:57-63) with the next
+ * step's smq_embed. An id past the vocabulary (every id banned) raises the
+ * numeric flag instead of writing x, as smq_embed does. */
+smq_status smq_argmax_advance_embed(const float *logits, uint32_t vocab, const unsigned char *banned, uint32_t *token,
+                                    int32_t *pos, uint32_t *count, uint32_t *history, uint32_t capacity,
+                                    const smq_qmat *embed, float *x);
 
 /* ---- Q5 weight conversion (src/kernels.h:205, kernels.c:1064-1117) -------
  * quantize_q5_row: cols floats x -> ceil(cols/32) Q5 blocks (22 B each) at

@@ -122,6 +122,8 @@ _SIGS = {
     "smq_decode_advance": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32]),
     "smq_attention_rope_q8": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp]),
     "smq_argmax_advance": (ctypes.c_int, [_vp, _u32, _vp, _vp, _vp, _vp, _vp, _u32]),
+    "smq_argmax_advance_embed": (ctypes.c_int, [_vp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, ctypes.POINTER(_QMat),
+                                                _vp]),
     "smq_quantize_q5_row": (None, [_vp, _u32, _vp]),
     "smq_quantize_q5_rows": (ctypes.c_int, [_vp, _u32, _u32, _vp]),
     "smq_dequantize_q8_row": (None, [_vp, _u32, _vp]),
@@ -532,6 +534,13 @@ def decode_advance(pos, count, token, history, capacity):
 def argmax_advance(logits, vocab, banned, token, pos, count, history, capacity):
     _check(load().smq_argmax_advance(_p(logits), vocab, _p(banned), _p(token), _p(pos), _p(count), _p(history),
                                      capacity))
+
+
+def argmax_advance_embed(logits, vocab, banned, token, pos, count, history, capacity, embed, x):
+    """smq_argmax_advance, then x = the embedding row (QMat `embed`) of the chosen token."""
+    e = embed._c()
+    _check(load().smq_argmax_advance_embed(_p(logits), vocab, _p(banned), _p(token), _p(pos), _p(count),
+                                           _p(history), capacity, ctypes.byref(e), _p(x)))
 
 
 def numeric_check():

@@ -1171,6 +1171,30 @@ smq_status smq_argmax_advance(const float *logits, uint32_t vocab, const unsigne
                : t_status;
 }
 
+smq_status smq_argmax_advance_embed(const float *logits, uint32_t vocab, const unsigned char *banned, uint32_t *token,
+                                    int32_t *pos, uint32_t *count, uint32_t *history, uint32_t capacity,
+                                    const smq_qmat *embed, float *x) {
+    if (!ready()) return t_status;
+    if (!vocab) return set_status(SMQ_ERR_RANGE, "argmax: empty vocabulary");
+    if (!embed || (embed->dtype != 1 && embed->dtype != 2) || embed->nb != (embed->cols + smq::QK - 1) / smq::QK ||
+        embed->row_bytes < (size_t)embed->nb * block_bytes(embed->dtype == 2))
+        return set_status(SMQ_ERR_FORMAT, "argmax_advance_embed: invalid matrix descriptor");
+    if (!extent_ok(logits, (size_t)vocab * 4, "logits") || !extent_ok(banned, banned ? vocab : 0, "banned") ||
+        !extent_ok(token, 4, "token") || !extent_ok(pos, 4, "pos") || !extent_ok(count, 4, "count") ||
+        !extent_ok(history, (size_t)capacity * 4, "history") ||
+        !extent_ok(embed->data, (size_t)embed->rows * embed->row_bytes, "embed") ||
+        !extent_ok(x, (size_t)embed->cols * 4, "x"))
+        return t_status;
+    if (!pos || !count || !x || (capacity && !history))
+        return set_status(SMQ_ERR_RANGE, "argmax_advance_embed: NULL argument");
+    const smq::EmbedArgs e = {embed->data, embed->row_bytes, embed->rows, embed->cols, embed->dtype == 2, x, g.flag};
+    return hip_ok(smq::launch_argmax(logits, vocab, banned, token, g.argmax_parts, pos, count, history, capacity, g.cur,
+                                     &e),
+                  "argmax_advance_embed")
+               ? SMQ_OK
+               : t_status;
+}
+
 smq_status smq_embed(const smq_qmat *embed, const uint32_t *tokens, uint32_t ntok, float *x) {
     if (!ready()) return t_status;
     if (!embed || (embed->dtype != 1 && embed->dtype != 2) || embed->nb != (embed->cols + smq::QK - 1) / smq::QK ||

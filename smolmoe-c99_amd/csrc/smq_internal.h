@@ -211,11 +211,21 @@ hipError_t launch_decode_advance(int32_t *pos, uint32_t *count, const uint32_t *
                                  uint32_t capacity, hipStream_t s);
 /* Greedy argmax in two launches through `parts` (ARGMAX_PART_BYTES *
  * MAX_ARGMAX_PARTS bytes of device workspace); with count != NULL also the
- * bookkeeping of one decode step (as launch_decode_advance). */
+ * bookkeeping of one decode step (as launch_decode_advance); with embed also
+ * the chosen token's embedding row into embed->out (as launch_embed). */
 constexpr uint32_t MAX_ARGMAX_PARTS = 1024;
 constexpr uint32_t ARGMAX_PART_BYTES = 12;
+struct EmbedArgs {
+    const unsigned char *w;
+    size_t row_bytes;
+    uint32_t vocab, cols;
+    bool q5;
+    float *out;
+    int *flag;
+};
 hipError_t launch_argmax(const float *logits, uint32_t n, const unsigned char *banned, uint32_t *out, void *parts,
-                         int32_t *pos, uint32_t *count, uint32_t *history, uint32_t capacity, hipStream_t s);
+                         int32_t *pos, uint32_t *count, uint32_t *history, uint32_t capacity, hipStream_t s,
+                         const EmbedArgs *embed = nullptr);
 /* The allocation-free argmax's partials: a static device array of
  * MAX_ARGMAX_PARTS partials. bind_noalloc_scratch (with `device` current)
  * records its device address; noalloc_scratch returns it (NULL if unbound).

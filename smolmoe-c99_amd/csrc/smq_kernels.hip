@@ -2004,6 +2004,26 @@ __global__ __launch_bounds__(AG_WG) void k_attend_group(const float *q, const fl
     }
 }
 
+/* Element j of a dequantized embedding row (kernels.c:1044-1062): scale * float(q). */
+template <bool Q5>
+__device__ __forceinline__ float embed_value(const unsigned char *row, uint32_t j) {
+    const uint32_t b = j / QK, kk = j % QK;
+    float scale;
+    int v;
+    if (Q5) {
+        const unsigned char *blk = row + (size_t)b * Q5_BYTES;
+        scale = half_to_float((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+        const uint32_t high = ld_u32_bytes(blk + 2);
+        const uint32_t lo = kk < 16 ? (blk[6 + kk] & 15u) : (uint32_t)(blk[6 + kk - 16] >> 4);
+        v = (int)(lo | (((high >> kk) & 1u) << 4)) - 16;
+    } else {
+        const unsigned char *blk = row + (size_t)b * Q8_BYTES;
+        scale = __uint_as_float(ld_u32_bytes(blk));
+        v = (int)(int8_t)blk[4 + kk];
+    }
+    return scale * (float)v;
+}
+
 /* Greedy choice (sampler.c:57-63): the first non-banned id, replaced by any
  * later id with a strictly greater logit. Equivalently: the lowest id of the
  * largest non-NaN logit, unless the first candidate itself is NaN (then that
@@ -2075,11 +2095,22 @@ __global__ __launch_bounds__(AM_WG) void k_argmax_part(const float *logits, uint
 }
 
 /* Stage 2: merge the partials; optionally the decode bookkeeping of one
- * step (history[*count] = token, ++*count, ++*pos). */
+ * step (history[*count] = token, ++*count, ++*pos) and the chosen token's
+ * embedding row into emb.out (the next step's input, model.c:669-677; a token
+ * past the vocabulary, when every id is banned, raises the flag instead). */
+struct ArgEmbed {
+    const unsigned char *w;
+    size_t row_bytes;
+    uint32_t vocab, cols, q5;
+    float *out; /* NULL: no embedding */
+    int *flag;
+};
+
 __global__ __launch_bounds__(AM_FINAL_WG) void k_argmax_final(const float *logits, const ArgBest *part, uint32_t np,
                                                               uint32_t *out, int32_t *pos, uint32_t *count,
-                                                              uint32_t *history, uint32_t capacity) {
+                                                              uint32_t *history, uint32_t capacity, ArgEmbed emb) {
     __shared__ ArgBest red[AM_FINAL_WG / 64];
+    __shared__ uint32_t s_tok;
     const uint32_t tid = threadIdx.x;
     ArgBest a = {0.0f, UINT32_MAX, UINT32_MAX};
     for (uint32_t p = tid; p < np; p += AM_FINAL_WG) am_merge(a, part[p].v, part[p].i, part[p].first);
@@ -2088,6 +2119,7 @@ __global__ __launch_bounds__(AM_FINAL_WG) void k_argmax_final(const float *logit
         const uint32_t f = a.first;
         const uint32_t tok = (f != UINT32_MAX && logits[f] != logits[f]) ? f : a.i;
         *out = tok;
+        s_tok = tok;
         if (count) {
             const uint32_t c = *count;
             if (c < capacity) history[c] = tok;
@@ -2095,6 +2127,16 @@ __global__ __launch_bounds__(AM_FINAL_WG) void k_argmax_final(const float *logit
             *pos = *pos + 1;
         }
     }
+    if (!emb.out) return; /* uniform */
+    __syncthreads();
+    const uint32_t tok = s_tok;
+    if (tok >= emb.vocab) {
+        if (tid == 0 && emb.flag) *emb.flag = 1;
+        return;
+    }
+    const unsigned char *row = emb.w + (size_t)tok * emb.row_bytes;
+    for (uint32_t j = tid; j < emb.cols; j += AM_FINAL_WG)
+        emb.out[j] = emb.q5 ? embed_value<true>(row, j) : embed_value<false>(row, j);
 }
 
 /* Bookkeeping after one replayed decode step: history[*count] = *token
@@ -2119,23 +2161,7 @@ __global__ __launch_bounds__(256) void k_embed(const unsigned char *w, size_t ro
         return;
     }
     const unsigned char *row = w + (size_t)tok * row_bytes;
-    for (uint32_t j = threadIdx.x; j < cols; j += 256) {
-        const uint32_t b = j / QK, kk = j % QK;
-        float scale;
-        int v;
-        if (Q5) {
-            const unsigned char *blk = row + (size_t)b * Q5_BYTES;
-            scale = half_to_float((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-            const uint32_t high = ld_u32_bytes(blk + 2);
-            const uint32_t lo = kk < 16 ? (blk[6 + kk] & 15u) : (uint32_t)(blk[6 + kk - 16] >> 4);
-            v = (int)(lo | (((high >> kk) & 1u) << 4)) - 16;
-        } else {
-            const unsigned char *blk = row + (size_t)b * Q8_BYTES;
-            scale = __uint_as_float(ld_u32_bytes(blk));
-            v = (int)(int8_t)blk[4 + kk];
-        }
-        out[(size_t)t * cols + j] = scale * (float)v;
-    }
+    for (uint32_t j = threadIdx.x; j < cols; j += 256) out[(size_t)t * cols + j] = embed_value<Q5>(row, j);
 }
 
 /* Row dequantization (reference: src/kernels.c:1044-1062): scale * float(q). */
@@ -2598,13 +2624,16 @@ void *noalloc_scratch(int device) {
 }
 
 hipError_t launch_argmax(const float *logits, uint32_t n, const unsigned char *banned, uint32_t *out, void *parts,
-                         int32_t *pos, uint32_t *count, uint32_t *history, uint32_t capacity, hipStream_t s) {
+                         int32_t *pos, uint32_t *count, uint32_t *history, uint32_t capacity, hipStream_t s,
+                         const EmbedArgs *embed) {
     /* span: a multiple of AM_SPAN, large enough for at most MAX_ARGMAX_PARTS workgroups */
     const uint32_t span = ((n + MAX_ARGMAX_PARTS - 1) / MAX_ARGMAX_PARTS + AM_SPAN - 1) / AM_SPAN * AM_SPAN;
     const uint32_t np = (n + span - 1) / span;
+    ArgEmbed emb = {nullptr, 0, 0, 0, 0, nullptr, nullptr};
+    if (embed) emb = {embed->w, embed->row_bytes, embed->vocab, embed->cols, embed->q5 ? 1u : 0u, embed->out, embed->flag};
     hipLaunchKernelGGL(k_argmax_part, dim3(np), dim3(AM_WG), 0, s, logits, n, span, banned, (ArgBest *)parts);
     hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(AM_FINAL_WG), 0, s, logits, (const ArgBest *)parts, np, out, pos,
-                       count, history, capacity);
+                       count, history, capacity, emb);
     return hipGetLastError();
 }
 

@@ -893,11 +893,12 @@ static smq_status ffn_block(smq_model *m, uint32_t l, uint32_t n) {
     return smq_matmul(it, 1, m->hd, m->hq, n);
 }
 
-/* model_forward_body (model.c:660-686) on device ids; asynchronous. */
+/* model_forward_body (model.c:660-686) on device ids; asynchronous. With tokens_dev NULL, x already holds
+ * the embedding of the one token (written by the previous decode step's argmax). */
 static smq_status enqueue_forward(smq_model *m, const uint32_t *tokens_dev, uint32_t n, uint32_t pos0,
                                   const int32_t *pos_dev, int mode) {
     uint32_t l;
-    TRY(smq_embed(&m->embed, tokens_dev, n, m->x));
+    if (tokens_dev) TRY(smq_embed(&m->embed, tokens_dev, n, m->x));
     for (l = 0; l < m->c.layers; ++l) {
         TRY(attention_block(m, l, n, pos0, pos_dev));
         TRY(ffn_block(m, l, n));
@@ -967,11 +968,13 @@ smq_status smq_model_set_banned(smq_model *m, const unsigned char *banned) {
     return smq_memcpy_htod(m->banned, banned, m->c.vocab);
 }
 
-/* One decode step on device state: embed(*token) at *pos, logits, argmax
- * into *token, then history[*count++] = *token and ++*pos. */
+/* One decode step on device state: the layers over x (the embedding of *token) at *pos, logits, argmax
+ * into *token, history[*count++] = *token and ++*pos, and x = the embedding of the new *token, the next
+ * step's input (one launch fewer per token than embedding at the step's start). */
 static smq_status enqueue_step(smq_model *m) {
-    TRY(enqueue_forward(m, m->token, 1, 0, m->pos, SMQ_LOGITS_LAST));
-    return smq_argmax_advance(m->logits, m->c.vocab, m->banned, m->token, m->pos, m->count, m->history, m->context);
+    TRY(enqueue_forward(m, NULL, 1, 0, m->pos, SMQ_LOGITS_LAST));
+    return smq_argmax_advance_embed(m->logits, m->c.vocab, m->banned, m->token, m->pos, m->count, m->history,
+                                    m->context, &m->embed, m->x);
 }
 
 smq_status smq_model_prepare_decode(smq_model *m) {
@@ -997,8 +1000,9 @@ smq_status smq_model_generate(smq_model *m, uint32_t pos, uint32_t ntokens, uint
     if (pos > m->context || ntokens - 1 > m->context - pos || ntokens > m->context)
         return fail(SMQ_ERR_RANGE, "prompt + tokens exceeds context");
     if (ntokens > 1) TRY(smq_model_prepare_decode(m));
-    /* out[0] from the logits already there (main.c:580-582) */
+    /* out[0] from the logits already there (main.c:580-582); its embedding is the first step's input */
     TRY(smq_argmax(m->logits, m->c.vocab, m->banned, m->token));
+    if (ntokens > 1) TRY(smq_embed(&m->embed, m->token, 1, m->x));
     TRY(smq_memcpy_dtod(m->history, m->token, 4));
     TRY(smq_memcpy_htod(m->count, &one, 4));
     TRY(smq_memcpy_htod(m->pos, &start, 4));

@@ -287,6 +287,40 @@ def test_argmax_advance(orc):
 
 
 @pytest.mark.parametrize("q5", [False, True])
+def test_argmax_advance_embed(orc, q5):
+    """The pick, the bookkeeping and the chosen token's embedding row in one call."""
+    vocab, cols = 300, 200  # partial last block
+    say("argmax_advance_embed q5" if q5 else "argmax_advance_embed q8")
+    w = synth.q5_weights(52, vocab, cols) if q5 else synth.q8_weights(52, vocab, cols)
+    mat = smq.QMat(dev(w), vocab, cols, smq.DTYPE_Q5 if q5 else smq.DTYPE_Q8)
+    pos = dev(np.array([10], np.int32))
+    count = dev(np.array([0], np.uint32))
+    hist = dev(np.zeros(8, np.uint32))
+    tok, x = smq.DeviceBuffer(4), smq.DeviceBuffer(cols * 4)
+    want = []
+    for i in range(4):
+        logits = synth.normal(90 + i, vocab)
+        banned = np.zeros(vocab, np.uint8)
+        banned[int(np.argmax(logits))] = i & 1  # every other call bans the plain maximum
+        smq.argmax_advance_embed(dev(logits), vocab, dev(banned), tok, pos, count, hist, 8, mat, x)
+        smq.numeric_check()
+        want.append(orc.argmax(logits, banned))
+        assert int(tok.download(np.uint32)[0]) == want[-1]
+        assert_same_f32(x.download(np.float32), orc.dequantize_row(w[want[-1]], cols, q5=q5), "embedded row")
+    assert int(pos.download(np.int32)[0]) == 14
+    assert hist.download(np.uint32).tolist()[:4] == want
+    # a token past the embedding's rows is no row: the numeric flag is raised and x keeps its contents
+    logits = np.full(vocab + 10, -1.0, np.float32)
+    logits[vocab + 5] = 1.0
+    before = x.download(np.float32)
+    smq.argmax_advance_embed(dev(logits), vocab + 10, None, tok, pos, count, hist, 8, mat, x)
+    with pytest.raises(smq.SmqError):
+        smq.numeric_check()
+    assert int(tok.download(np.uint32)[0]) == vocab + 5
+    assert np.array_equal(x.download(np.float32), before)
+
+
+@pytest.mark.parametrize("q5", [False, True])
 def test_embed(orc, q5):
     vocab, cols = 300, 200  # partial last block
     say("embed q5" if q5 else "embed q8")

@@ -63,7 +63,18 @@ struct Q5Fields {
     float scale;
     uint32_t high;   /* bit j = bit 4 of element j */
     uint32_t nib[4]; /* byte j: element j low nibble, element j+16 high nibble */
+    uint32_t even, odd; /* (high << 4) & 0xf0f0f0f0 and high & 0xf0f0f0f0 (q5_codes) */
 };
+
+/* The two words whose bytes feed q5_codes' multiplies, formed once per block and
+ * hidden from the optimiser by an empty asm: each lane's byte then reaches its
+ * v_mul_u32_u24 as an operand byte select (SDWA src0_sel) instead of a shift
+ * and a mask per lane (folded together, the two masks left no byte pattern). */
+__device__ __forceinline__ void q5_spread_words(Q5Fields &b) {
+    b.even = (b.high << 4) & 0xf0f0f0f0u;
+    b.odd = b.high & 0xf0f0f0f0u;
+    asm("" : "+v"(b.even), "+v"(b.odd));
+}
 
 /* A pair of Q5 blocks is 44 bytes = 11 dwords: the first block's fields sit
  * at 2-byte offsets inside the dwords, the second block's are dword aligned. */
@@ -76,6 +87,8 @@ __device__ __forceinline__ void q5_parse_pair(const uint32_t d[11], Q5Fields &b0
     b1.high = d[6];
 #pragma unroll
     for (int k = 0; k < 4; ++k) b1.nib[k] = d[7 + k];
+    q5_spread_words(b0);
+    q5_spread_words(b1);
 }
 
 /* Lane l's four 5-bit codes q in [0, 31] as bytes: low nibble | high bit << 4.
@@ -85,7 +98,7 @@ __device__ __forceinline__ void q5_parse_pair(const uint32_t d[11], Q5Fields &b0
  * 0x204081 puts bit i at 8i + 4: the sixteen partial products land on
  * distinct bits (no carries) and the mask keeps the four wanted ones. */
 __device__ __forceinline__ uint32_t q5_codes(const Q5Fields &b, int l) {
-    const uint32_t src = (l & 1) ? (b.high & 0xf0f0f0f0u) : ((b.high << 4) & 0xf0f0f0f0u);
+    const uint32_t src = (l & 1) ? b.odd : b.even;
     /* byte l/2, already shifted: the multiply needs no constant wider than 24
      * bits, so it stays one v_mul_u32_u24 */
     const uint32_t spread = __umul24((src >> (8 * (l >> 1))) & 0xffu, 0x204081u);

@@ -160,11 +160,13 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
  * per-lane order, the fixed lane tree.
  *
  * The tile is shaped to the row at launch: a row of ppr tasks is cut into
- * nch chunks of cpr tasks (pin_cpr at most), and a tile is rt rows (NT / cpr,
- * within PIN_RT and the product buffer), so rt * cpr of the NT threads hold
- * a task (row tid / cpr, task tid % cpr): 28-block Q8 rows run 18 rows of 28
- * threads of 512, 24-pair Q5 rows 20 rows of 24 of 512. ONE: a single chunk
- * per row.
+ * nch chunks of cpr tasks (pin_cpr at most; for Q5 rows of several chunks the
+ * count whose slowest workgroup takes the fewest steps), and a tile is rt rows
+ * (NT / cpr, within PIN_RT and the product buffer), so rt * cpr of the NT
+ * threads hold a task (row tid / cpr, task tid % cpr): 28-block Q8 rows run
+ * 18 rows of 28 threads of 512, 24-pair Q5 rows 32 rows of 24 of 768, 140-pair
+ * Q5 rows (16 items) 7 chunks of 20 pairs, 24 rows of 20 of 512. ONE: a single
+ * chunk per row.
  * ---------------------------------------------------------------------- */
 /* Tasks per chunk at most: a Q8 chunk stays within 32 blocks (the chain
  * threads' short path), a Q5 chunk within 64 pairs (measured: the 280-block
@@ -2260,50 +2262,87 @@ uint32_t pin_split(GA &g, uint32_t rt, uint64_t resident) {
     return wgs;
 }
 
+/* Steps of the slowest workgroup for tiles of rt rows in nch chunks, under the split pin_split
+ * would make (an item's workgroups take floor or ceil of its tiles / workgroups each). */
+inline uint64_t pin_max_steps(const GroupArgs &g, uint32_t rt, uint32_t nch, uint64_t resident) {
+    uint64_t tiles = 0, worst = 0;
+    for (uint32_t i = 0; i < g.nitems; ++i) tiles += (g.item[i].rows + rt - 1) / rt;
+    if (!tiles) return 0;
+    for (uint32_t i = 0; i < g.nitems; ++i) {
+        const uint64_t t = (g.item[i].rows + rt - 1) / rt;
+        uint64_t n = (resident * t + tiles / 2) / tiles;
+        n = n < 1 ? 1 : (n > t ? t : n);
+        const uint64_t per = (t + n - 1) / n;
+        worst = per > worst ? per : worst;
+    }
+    return worst * nch;
+}
+
 /* The pinned launch: the tile shape for the row width (see k_gemv_pin), then
  * each item's share of the resident workgroups in proportion to its tiles.
  * LDS per workgroup (product buffers, the staged activation) is sized for
- * three resident workgroups per CU (Q8, fast Q5: four for one-chunk rows) or
- * two (exact Q5). A launch of few items passes the small argument struct. */
+ * three resident workgroups per CU (Q8, fast Q5: four for one-chunk rows), two
+ * (exact Q5) or one (exact one-chunk Q5, 768 threads). A launch of few items
+ * passes the small argument struct. */
 template <bool Q5, bool FAST, bool ONE>
 hipError_t launch_gemv_pin_shape(GroupArgs &g, hipStream_t s) {
     /* exact Q5: 512 threads, two workgroups per CU (measured 10-16 % faster than
-     * four of 256 threads: larger tiles, fewer barriers per byte); fast Q5
-     * keeps 256 (its registers allow three waves per SIMD) */
-    constexpr int NT = Q5 && FAST ? 256 : 512, D = 2;
+     * four of 256 threads: larger tiles, fewer barriers per byte); one-chunk exact
+     * Q5 rows 768 threads, one workgroup per CU: three waves per SIMD within its
+     * 168 registers, 32-row tiles (16 x 8960x1536: 30.3-30.5 against 33.0-33.3 us
+     * best at 512); fast Q5 keeps 256 (its registers allow three waves per SIMD) */
+    constexpr int NT = Q5 && FAST ? 256 : (Q5 && ONE ? 768 : 512), D = 2;
     constexpr uint32_t TB = Q5 ? 2 : 1, CPR = pin_cpr<Q5, FAST>();
     constexpr uint32_t MAXNB = ONE ? CPR * TB : MAX_FAST_NB;
     /* floats of one product buffer; LDS is allocated in 512-byte units */
-    constexpr uint32_t PF = Q5 ? (FAST ? (ONE ? 4480 : 4400) : 7776) : (ONE ? 4832 : 4400);
+    constexpr uint32_t PF = Q5 ? (FAST ? (ONE ? 4480 : 4400) : (ONE ? 12336 : 7776)) : (ONE ? 4832 : 4400);
+    const auto kf = k_gemv_pin<Q5, FAST, ONE, NT, D, MAXNB, PF, GroupArgsFew>;
+    const auto km = k_gemv_pin<Q5, FAST, ONE, NT, D, MAXNB, PF, GroupArgs>;
+    const bool few = g.nitems <= FEW_GROUP_ITEMS;
+    static int res_few = 0, res_many = 0;
+    const hipError_t e = few ? resident_wgs((const void *)kf, NT, res_few) : resident_wgs((const void *)km, NT, res_many);
+    if (e != hipSuccess) return e;
+    const uint64_t resident = (uint64_t)(few ? res_few : res_many);
+    /* a chunk's tiles fit the product buffer (every chain read, groups of four blocks of a chunk, rt rows
+     * each, lies below PF, clear of the sinks that idle tasks write past PF; in fast mode the scale
+     * products, groups of rt * 4 + 4, below the scale buffer's sink at PF / 8 + 128) */
+    auto fits = [&](uint32_t cpr, uint32_t rt) {
+        const uint64_t groups = (cpr * TB + 3) / 4;
+        return rt != 0 && groups * (rt * 32 + 4) <= PF && (!FAST || groups * (rt * 4 + 4) <= PF / 8 + 128);
+    };
     const uint32_t ppr = (g.nb + TB - 1) / TB;
     g.nch = (ppr + CPR - 1) / CPR;
+    if constexpr (Q5 && !ONE) {
+        /* several chunks per row: the chunk count whose slowest workgroup takes the fewest steps, at a
+         * tie the shorter chunks (shorter chains per step). 16 x 1536x8960 (140 pairs a row): 3 chunks of
+         * 47 (10-row tiles, 5 tiles for the slowest workgroup) 44.8-46.7 us; 7 of 20 (24-row tiles, two
+         * each) 37.8-39.0 us; 5 of 28 41.1, 6 of 24 42.9, 10 of 14 47.6 us, same box */
+        uint32_t best_nch = g.nch;
+        uint64_t best = ~0ull;
+        for (uint32_t n = g.nch; n <= g.nch + 8 && n <= ppr; ++n) {
+            const uint32_t c = (ppr + n - 1) / n, r = pin_rows(NT, TB, c, PF);
+            if (!fits(c, r)) continue;
+            const uint64_t st = pin_max_steps(g, r, n, resident);
+            if (st <= best) {
+                best = st;
+                best_nch = n;
+            }
+        }
+        g.nch = best_nch;
+    }
     g.cpr = (ppr + g.nch - 1) / g.nch;
     g.rt = pin_rows(NT, TB, g.cpr, PF);
-    if (g.nb > MAXNB || (ONE && g.nch != 1) || g.rt == 0) return hipErrorInvalidValue; /* launcher precondition */
-    /* every chain read (groups of four blocks of a chunk, rt rows each) lies below PF, clear of the
-     * sinks that idle tasks write past PF; in fast mode the scale products (groups of rt * 4 + 4)
-     * below the scale buffer's sink at PF / 8 + 128 */
-    const uint64_t groups = (g.cpr * TB + 3) / 4;
-    if (groups * (g.rt * 32 + 4) > PF) return hipErrorInvalidValue;
-    if (FAST && groups * (g.rt * 4 + 4) > PF / 8 + 128) return hipErrorInvalidValue;
-    if (g.nitems <= FEW_GROUP_ITEMS) {
-        static int resident = 0;
-        const auto k = k_gemv_pin<Q5, FAST, ONE, NT, D, MAXNB, PF, GroupArgsFew>;
-        const hipError_t e = resident_wgs((const void *)k, NT, resident);
-        if (e != hipSuccess) return e;
+    if (g.nb > MAXNB || (ONE && g.nch != 1) || !fits(g.cpr, g.rt)) return hipErrorInvalidValue; /* launcher precondition */
+    if (few) {
         GroupArgsFew f = group_args_few(g);
-        const uint32_t wgs = pin_split(f, g.rt, (uint64_t)resident);
+        const uint32_t wgs = pin_split(f, g.rt, resident);
         if (!wgs) return hipSuccess;
-        hipLaunchKernelGGL(k, dim3(wgs), dim3(NT), 0, s, f);
+        hipLaunchKernelGGL(kf, dim3(wgs), dim3(NT), 0, s, f);
         return hipGetLastError();
     }
-    static int resident = 0;
-    const auto k = k_gemv_pin<Q5, FAST, ONE, NT, D, MAXNB, PF, GroupArgs>;
-    const hipError_t e = resident_wgs((const void *)k, NT, resident);
-    if (e != hipSuccess) return e;
-    const uint32_t wgs = pin_split(g, g.rt, (uint64_t)resident);
+    const uint32_t wgs = pin_split(g, g.rt, resident);
     if (!wgs) return hipSuccess;
-    hipLaunchKernelGGL(k, dim3(wgs), dim3(NT), 0, s, g);
+    hipLaunchKernelGGL(km, dim3(wgs), dim3(NT), 0, s, g);
     return hipGetLastError();
 }
 

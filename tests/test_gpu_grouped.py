@@ -97,6 +97,46 @@ def test_grouped_gemv(orc, q5, cols, rows, fast, plain):
     smq.kernels_set_fast(False)
 
 
+def q5_random(seed, rows, cols):
+    """Q5 rows of random high-bit planes and nibbles under random finite f16 scales (every code and
+    both signs of the scale; the kernels decode any bytes, so the 21-candidate rule is not needed)."""
+    nb = (cols + 31) // 32
+    rng = np.random.default_rng(seed)
+    w = rng.integers(0, 256, (rows, nb, 22), dtype=np.uint8)
+    scale = rng.uniform(-2e-3, 2e-3, (rows, nb)).astype(np.float16)
+    w[:, :, 0:2] = scale.view(np.uint8).reshape(rows, nb, 2)
+    return w.reshape(rows, nb * 22)
+
+
+@pytest.mark.parametrize("fast", [False, True])
+def test_grouped_q5_configs2_down(orc, fast):
+    """configs[2]'s 16 x 1536 x 8960 group as benched: 140 pairs a row, which the launcher cuts into
+    7 chunks of 20 pairs (24-row tiles, two per workgroup); every item its own activation, some with
+    a bias or a residual add."""
+    say("grouped q5 configs2 down", fast)
+    smq.kernels_set_fast(fast)
+    rows, cols, n = 1536, 8960, 16
+    nb = (cols + 31) // 32
+    w = q5_random(77, rows, cols)
+    wb = dev(w)  # one weight buffer shared by the items: the kernels read it as 16 matrices
+    items, want = [], []
+    for i in range(n):
+        bias = synth.normal(500 + i, rows, 0.02) if i % 2 == 0 else None
+        acc = i % 3 == 1
+        y0 = synth.normal(600 + i, rows) if acc else np.zeros(rows, np.float32)
+        d, q, hd, hq = quantized(700 + i, cols)
+        ok, prod = orc.mat_item(w, nb * 22, rows, bias, hd, hq, 1, nb, q5=True, fast=fast)
+        assert ok
+        want.append(y0 + prod if acc else prod)
+        items.append((smq.QMat(wb, rows, cols, smq.DTYPE_Q5), dev(bias) if bias is not None else None, dev(y0),
+                      acc, d, q))
+    smq.gemv_grouped(items)
+    smq.numeric_check()
+    for i, (it, wnt) in enumerate(zip(items, want)):
+        assert_same_f32(it[2].download(np.float32), wnt, f"item {i}")
+    smq.kernels_set_fast(False)
+
+
 def test_grouped_rejects_mixed_widths():
     a = smq.QMat(dev(synth.q8_weights(1, 8, 64)), 8, 64)
     b = smq.QMat(dev(synth.q8_weights(2, 8, 96)), 8, 96)

@@ -294,9 +294,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
             fetch(wbase + (size_t)rc * row_bytes + (size_t)bc * BYTES);
         } else {
             /* several chunks per row: the same loads at every step too (an idle task re-reads its
-             * tile's first row or its row's first block, a step past the range the last tile) */
+             * tile's first row or its row's first block; a step past the range re-reads the last
+             * step's chunk, bytes read at most D steps before and still in L2: re-reading the last
+             * tile's first chunks, 7 chunks of 20 pairs, fetched 1.167x the algorithmic bytes) */
             const uint32_t tl = real ? tile : t1 - 1, rl = tl * rt + (worker ? tr : 0);
-            const uint32_t rc = rl < rows ? rl : rows - 1, bc = b < nb ? b : 0;
+            const uint32_t bl = real ? b : (nch - 1) * cb + ti * TB;
+            const uint32_t rc = rl < rows ? rl : rows - 1, bc = bl < nb ? bl : 0;
             fetch(wbase + (size_t)rc * row_bytes + (size_t)bc * BYTES);
         }
     };

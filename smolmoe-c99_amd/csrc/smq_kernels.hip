@@ -17,6 +17,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "smq_device.h"
 #include "smq_internal.h"
 
@@ -203,10 +205,11 @@ __device__ __forceinline__ uint32_t find_pin_item(const GA &g, uint32_t wg) {
     return lo;
 }
 
-/* occupancy floor: exact Q8 6 waves per SIMD (three 512-thread workgroups per CU);
+/* occupancy floor: exact Q8 6 waves per SIMD (three 512-thread workgroups per CU), exact Q5 of several
+ * chunks 4 (two per CU);
  * PF: floats of one product buffer (the launcher keeps rt within it) */
 template <bool Q5, bool FAST, bool ONE, int NT, int D, uint32_t MAXNB, uint32_t PF, class GA>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FAST ? 4 : 6), 8))) void k_gemv_pin(
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? (ONE || FAST ? 3 : 4) : (FAST ? 4 : 6), 8))) void k_gemv_pin(
     GA g) {
     constexpr int TB = Q5 ? 2 : 1;
     constexpr bool HOIST = ONE && Q5;
@@ -294,12 +297,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
             fetch(wbase + (size_t)rc * row_bytes + (size_t)bc * BYTES);
         } else {
             /* several chunks per row: the same loads at every step too (an idle task re-reads its
-             * tile's first row or its row's first block; a step past the range re-reads the last
-             * step's chunk, bytes read at most D steps before and still in L2: re-reading the last
-             * tile's first chunks, 7 chunks of 20 pairs, fetched 1.167x the algorithmic bytes) */
+             * tile's first row or its row's first block, a step past the range the last tile) */
             const uint32_t tl = real ? tile : t1 - 1, rl = tl * rt + (worker ? tr : 0);
-            const uint32_t bl = real ? b : (nch - 1) * cb + ti * TB;
-            const uint32_t rc = rl < rows ? rl : rows - 1, bc = bl < nb ? bl : 0;
+            const uint32_t rc = rl < rows ? rl : rows - 1, bc = b < nb ? b : 0;
             fetch(wbase + (size_t)rc * row_bytes + (size_t)bc * BYTES);
         }
     };
@@ -447,9 +447,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
     }
     uint32_t ct = t0, cc = 0; /* chain cursor */
     float acc = 0.0f;
-    for (uint32_t k = 0; k < my_steps; k += D) {
+    /* a straight trip of D steps; a step past the range stores nothing. Every trip but the last
+     * requests the next tasks, the last nothing (as for one chunk) */
+    auto trip = [&](uint32_t k, auto next) __attribute__((always_inline)) {
+        constexpr bool NEXT = decltype(next)::value;
 #pragma unroll
-        for (int j = 0; j < D; ++j) { /* a straight trip of D steps; a step past the range stores nothing */
+        for (int j = 0; j < D; ++j) {
             const bool live = k + j < my_steps;
             float *pb = prod[(k + j) & 1];
             float *db = dsc[FAST ? (k + j) & 1 : 0];
@@ -458,8 +461,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
             products(T[j], pb, db, cc);
             /* this task is consumed: its slot reloads now, a barrier and a chain earlier than
              * at the end of the step */
-            load(T[j], lt, lc, k + j + D < my_steps);
-            if (++lc == nch) { lc = 0; ++lt; }
+            if constexpr (NEXT) {
+                load(T[j], lt, lc, k + j + D < my_steps);
+                if (++lc == nch) { lc = 0; ++lt; }
+            }
             __syncthreads();
             if (tid < chains) {
                 const uint32_t count = nb - cc * cb < cb ? nb - cc * cb : cb;
@@ -482,7 +487,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? 3 : (FA
             if (cc + 1 == nch) load_tile_bp(mbias, mprior, ct + 1); /* uniform; the store above used them */
             if (++cc == nch) { cc = 0; ++ct; }
         }
-    }
+    };
+    uint32_t k = 0;
+    for (; k + D < my_steps; k += D) trip(k, std::true_type{});
+    trip(k, std::false_type{}); /* my_steps >= 1: the last trip */
 }
 
 /* ------------------------------------------------------------------------

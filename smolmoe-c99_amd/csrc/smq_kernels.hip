@@ -177,6 +177,7 @@ __global__ __launch_bounds__(WG) void k_gemv(MatArgs a) {
 template <bool Q5, bool FAST>
 constexpr uint32_t pin_cpr() { return Q5 ? 64u : 32u; }
 constexpr uint32_t PIN_RT = 32; /* rows per tile at most */
+constexpr uint32_t PIN_OOB = 0x80000000u; /* a buffer offset past every tile's records: reads zeros */
 
 /* Rows per tile for chunks of c tasks: as many as the threads allow, at most
  * PIN_RT, and within a product buffer of pf floats (ceil(tb*c/4) groups of
@@ -270,37 +271,33 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? (ONE ||
             for (uint32_t i = tid; i < DSC_FLOATS; i += NT) (&dsc[0][0])[i] = 0.0f;
     }
 
-    /* step s: tile t0 + s / nch, chunk s % nch (counters, no division per step) */
+    /* step s: tile t0 + s / nch, chunk s % nch (counters, no division per step). A step's tile is one
+     * buffer resource formed by scalar arithmetic: its first row, and records covering its rows within
+     * the matrix (none for a step past this workgroup's range). A lane's offset into it is fixed (its
+     * row of the tile, its task's blocks; the chunk is a scalar offset), and a row past the matrix, a
+     * step past the range or an idle task (an out-of-range offset) reads zeros without touching memory.
+     * Every thread issues the same loads at every step, outside any branch, so the compiler's in-order
+     * wait counts stay exact and the next task stays in flight across the step. (Before, 64-bit
+     * addresses with clamps took 13 VALU instructions a task, and a step past the range re-read the
+     * range's last tile.) */
+    const uint32_t rb32 = (uint32_t)row_bytes;
+    const uint32_t lane_off = worker ? tr * rb32 + ti * TB * BYTES : PIN_OOB;
     auto load = [&](PinTask<Q5> &T, uint32_t tile, uint32_t chunk, bool real) __attribute__((always_inline)) {
-        const uint32_t row0 = tile * rt, row = row0 + tr, b = chunk * cb + ti * TB;
-        T.ok = real && worker && row < rows && b < nb;
-        auto fetch = [&](const unsigned char *p) __attribute__((always_inline)) {
-            const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
-            T.w[0] = v0.x; T.w[1] = v0.y; T.w[2] = v0.z; T.w[3] = v0.w;
-            T.w[4] = v1.x; T.w[5] = v1.y; T.w[6] = v1.z; T.w[7] = v1.w;
-            if constexpr (Q5) { /* a pair: 44 bytes */
-                const u3a v2 = *(const u3a *)(p + 32);
-                T.w[8] = v2.x; T.w[9] = v2.y; T.w[10] = v2.z;
-            } else {
-                T.w[8] = *(const uint32_t *)(p + 32);
-            }
-        };
-        if constexpr (ONE) {
-            /* every thread issues the same loads at every step, outside any
-             * branch, so the compiler's in-order wait counts stay exact and the
-             * next task stays in flight across the step. An idle task re-reads
-             * bytes this workgroup reads anyway (past its range: its last tile;
-             * a spare thread: the tile's first row; past the row: its block 0;
-             * past the matrix: the last row), so no extra HBM traffic. */
-            const uint32_t tl = real ? tile : t1 - 1, rl = tl * rt + (worker ? tr : 0);
-            const uint32_t rc = rl < rows ? rl : rows - 1, bc = b < nb ? b : 0;
-            fetch(wbase + (size_t)rc * row_bytes + (size_t)bc * BYTES);
+        const uint32_t row0 = tile * rt, b = chunk * cb + ti * TB;
+        T.ok = real && worker && row0 + tr < rows && b < nb;
+        const uint32_t in_rows = real ? (rows - row0 < rt ? rows - row0 : rt) : 0u;
+        const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(wbase + (size_t)row0 * row_bytes), (short)0, (int)(in_rows * rb32), 0x00020000);
+        const uint32_t voff = b < nb ? lane_off : PIN_OOB, soff = chunk * cb * BYTES;
+        const u4a v0 = __builtin_bit_cast(u4a, __builtin_amdgcn_raw_buffer_load_b128(src, voff, soff, 0));
+        const u4a v1 = __builtin_bit_cast(u4a, __builtin_amdgcn_raw_buffer_load_b128(src, voff + 16, soff, 0));
+        T.w[0] = v0.x; T.w[1] = v0.y; T.w[2] = v0.z; T.w[3] = v0.w;
+        T.w[4] = v1.x; T.w[5] = v1.y; T.w[6] = v1.z; T.w[7] = v1.w;
+        if constexpr (Q5) { /* a pair: 44 bytes */
+            const auto v2 = __builtin_amdgcn_raw_buffer_load_b96(src, voff + 32, soff, 0);
+            T.w[8] = v2[0]; T.w[9] = v2[1]; T.w[10] = v2[2];
         } else {
-            /* several chunks per row: the same loads at every step too (an idle task re-reads its
-             * tile's first row or its row's first block, a step past the range the last tile) */
-            const uint32_t tl = real ? tile : t1 - 1, rl = tl * rt + (worker ? tr : 0);
-            const uint32_t rc = rl < rows ? rl : rows - 1, bc = b < nb ? b : 0;
-            fetch(wbase + (size_t)rc * row_bytes + (size_t)bc * BYTES);
+            T.w[8] = __builtin_amdgcn_raw_buffer_load_b32(src, voff + 32, soff, 0);
         }
     };
     /* one chunk: the chain threads' row, its bias and prior output (the other threads read the

@@ -178,6 +178,9 @@ template <bool Q5, bool FAST>
 constexpr uint32_t pin_cpr() { return Q5 ? 64u : 32u; }
 constexpr uint32_t PIN_RT = 32; /* rows per tile at most */
 constexpr uint32_t PIN_OOB = 0x80000000u; /* a buffer offset past every tile's records: reads zeros */
+/* row strides the pinned kernel's 32-bit tile offsets hold: PIN_RT rows of this many bytes stay below
+ * PIN_OOB (wider strides take the per-tile kernels) */
+constexpr size_t PIN_MAX_ROW_BYTES = (size_t)1 << 25;
 
 /* Rows per tile for chunks of c tasks: as many as the threads allow, at most
  * PIN_RT, and within a product buffer of pf floats (ceil(tb*c/4) groups of
@@ -2371,7 +2374,9 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
     if (fast_layout(a, Q5)) {
         if (a.ntok == 1) {
             const int rt = gemv_rows_per_tile(a.nb, Q5, total_rows);
-            if (!g_forced_rt && gemv_persistent(total_rows, rt)) {
+            bool pin_ok = true;
+            for (uint32_t i = 0; i < a.nitems; ++i) pin_ok = pin_ok && a.item[i].row_bytes <= PIN_MAX_ROW_BYTES;
+            if (!g_forced_rt && pin_ok && gemv_persistent(total_rows, rt)) {
                 /* many tiles: the pinned persistent kernel streams them (same products and order) */
                 GroupArgs g;
                 memset(&g, 0, sizeof(g));
@@ -2540,7 +2545,9 @@ hipError_t launch_row_quantize(const float *src, const float *norm, float eps, c
 bool group_layout_ok(const GroupArgs &g, bool q5) {
     if (!g.nb || g.nb > MAX_FAST_NB || (q5 && (g.nb & 1u))) return false;
     for (uint32_t i = 0; i < g.nitems; ++i)
-        if ((((uintptr_t)g.item[i].w) | g.item[i].row_bytes | (uintptr_t)g.item[i].xq) & 3u) return false;
+        if ((((uintptr_t)g.item[i].w) | g.item[i].row_bytes | (uintptr_t)g.item[i].xq) & 3u ||
+            g.item[i].row_bytes > PIN_MAX_ROW_BYTES)
+            return false;
     return true;
 }
 

@@ -497,21 +497,25 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? (ONE ||
  * Exact prefill GEMM (ntok > 1). Workgroup tile = 32 rows x 16 tokens; K in
  * chunks of 16 blocks staged in LDS (weights decoded once per block: Q5
  * becomes signed int8 words, so the inner loop is the same for both formats).
- * Thread (lane l, row group, token group) owns 4 rows x 4 tokens of lane l:
- * sixteen serial chains, each step one dot4, one convert, one multiply for d,
- * one multiply and one add. The next chunk's global loads are issued before
- * the current chunk is computed.
+ * Thread (row pair, token) owns all eight lanes of two (row, token) outputs:
+ * sixteen serial chains, each block one d = wscale * xscale per output and per
+ * lane one dot4, one convert, one multiply and one add; the lane tree runs in
+ * the thread. A block's eight words of a row or token are two 16-byte LDS
+ * reads. (Thread per lane of 4 rows x 4 tokens, before: d formed in all eight
+ * lanes, one LDS read per product, 88 VALU per 16 lane sums against 66.) The
+ * next chunk's global loads are issued before the current chunk is computed.
  * ---------------------------------------------------------------------- */
 constexpr int GT_R = 32, GT_T = 16, GT_CB = 16;
-constexpr int WQ_PITCH = GT_CB * 8 + 2; /* dwords; rows of a wave hit distinct banks */
+constexpr int WQ_PITCH = GT_CB * 8 + 4; /* dwords, 16-byte rows; 4 mod 64: the 16 tokens of a wave's
+                                          * 16-byte reads start 4 banks apart */
 constexpr int SC_PITCH = GT_CB + 1;
 
 template <bool Q5, bool FAST>
 __global__ __launch_bounds__(WG) void k_gemm_exact(MatArgs a, uint32_t tok_tiles) {
     __shared__ float wsl[GT_R][SC_PITCH];
-    __shared__ __attribute__((aligned(8))) uint32_t wql[GT_R][WQ_PITCH];
+    __shared__ __attribute__((aligned(16))) uint32_t wql[GT_R][WQ_PITCH];
     __shared__ float xdl[GT_T][SC_PITCH];
-    __shared__ __attribute__((aligned(8))) uint32_t xql[GT_T][WQ_PITCH];
+    __shared__ __attribute__((aligned(16))) uint32_t xql[GT_T][WQ_PITCH];
 
     const uint32_t tid = threadIdx.x, nb = a.nb;
     /* XCD-aware order: workgroup i runs on XCD i % 8; give each XCD a
@@ -603,12 +607,13 @@ __global__ __launch_bounds__(WG) void k_gemm_exact(MatArgs a, uint32_t tok_tiles
         xdl[stok][spiece] = (stok_ok && bx < nb) ? xs : 0.0f;
     };
 
-    const uint32_t l = tid % 8, rg = (tid / 8) % 8, tg = tid / 64;
-    float acc[4][4];
+    const uint32_t tg = tid % GT_T, rg = tid / GT_T; /* token tg, rows 2 rg and 2 rg + 1 */
+    static_assert(GT_T * GT_R / 2 == WG, "one thread per (row pair, token)");
+    float acc[2][8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+        for (int l = 0; l < 8; ++l) acc[i][l] = 0.0f;
 
     const uint32_t nchunks = (nb + GT_CB - 1) / GT_CB;
     fetch(0);
@@ -618,37 +623,28 @@ __global__ __launch_bounds__(WG) void k_gemm_exact(MatArgs a, uint32_t tok_tiles
         if (c + 1 < nchunks) fetch(c + 1);
         const uint32_t count = nb - c * GT_CB < (uint32_t)GT_CB ? nb - c * GT_CB : (uint32_t)GT_CB;
         for (uint32_t bb = 0; bb < count; ++bb) {
-            float ws[4], xsc[4];
-            uint32_t w[4], x[4];
+            const u4a x0 = *(const u4a *)&xql[tg][bb * 8], x1 = *(const u4a *)&xql[tg][bb * 8 + 4];
+            const uint32_t x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            const float xsc = xdl[tg][bb];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                ws[i] = wsl[rg * 4 + i][bb];
-                w[i] = wql[rg * 4 + i][bb * 8 + l];
-                xsc[i] = xdl[tg * 4 + i][bb];
-                x[i] = xql[tg * 4 + i][bb * 8 + l];
+            for (int i = 0; i < 2; ++i) {
+                const u4a w0 = *(const u4a *)&wql[2 * rg + i][bb * 8], w1 = *(const u4a *)&wql[2 * rg + i][bb * 8 + 4];
+                const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                const float d = wsl[2 * rg + i][bb] * xsc;
+#pragma unroll
+                for (int l = 0; l < 8; ++l) acc[i][l] = lane_step<FAST>(acc[i][l], d, dot4(w[l], x[l], 0));
             }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float d = ws[i] * xsc[j];
-                    acc[i][j] = lane_step<FAST>(acc[i][j], d, dot4(w[i], x[j], 0));
-                }
         }
         __syncthreads();
     }
 
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float v = reduce8(acc[i][j]);
-            const int idx = i * 4 + j;
-            if (idx == (int)l || idx == (int)l + 8) {
-                const uint32_t r = r0 + rg * 4 + i, t = t0 + tg * 4 + j;
-                if (r < I.rows && t < a.ntok) store_out(I, a.flag, t, r, v);
-            }
-        }
+    for (int i = 0; i < 2; ++i) {
+        const float *a8 = acc[i]; /* the lane tree of reduce8: ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) */
+        const float v = ((a8[0] + a8[4]) + (a8[2] + a8[6])) + ((a8[1] + a8[5]) + (a8[3] + a8[7]));
+        const uint32_t r = r0 + 2 * rg + i, t = t0 + tg;
+        if (r < I.rows && t < a.ntok) store_out(I, a.flag, t, r, v);
+    }
 }
 
 /* ------------------------------------------------------------------------

@@ -494,10 +494,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? (ONE ||
 }
 
 /* ------------------------------------------------------------------------
- * Exact prefill GEMM (ntok > 1). Workgroup tile = 32 rows x 16 tokens; K in
- * chunks of 16 blocks staged in LDS (weights decoded once per block: Q5
- * becomes signed int8 words, so the inner loop is the same for both formats).
- * Thread (row pair, token) owns all eight lanes of two (row, token) outputs:
+ * Exact prefill GEMM (ntok > 1). Workgroup tile = 32 rows x 16 tokens (x 8
+ * tokens where 16-token tiles leave CUs idle); K in chunks of 16 blocks staged
+ * in LDS (weights decoded once per block: Q5 becomes signed int8 words, so the
+ * inner loop is the same for both formats). Thread (row pair, token), or
+ * (row, token) in 8-token tiles, owns all eight lanes of its (row, token) outputs:
  * sixteen serial chains, each block one d = wscale * xscale per output and per
  * lane one dot4, one convert, one multiply and one add; the lane tree runs in
  * the thread. A block's eight words of a row or token are two 16-byte LDS
@@ -505,17 +506,22 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q5 ? (ONE ||
  * lanes, one LDS read per product, 88 VALU per 16 lane sums against 66.) The
  * next chunk's global loads are issued before the current chunk is computed.
  * ---------------------------------------------------------------------- */
-constexpr int GT_R = 32, GT_T = 16, GT_CB = 16;
+constexpr int GT_R = 32, GT_CB = 16;
 constexpr int WQ_PITCH = GT_CB * 8 + 4; /* dwords, 16-byte rows; 4 mod 64: the 16 tokens of a wave's
                                           * 16-byte reads start 4 banks apart */
 constexpr int SC_PITCH = GT_CB + 1;
 
-template <bool Q5, bool FAST>
+/* TT tokens per tile: 16, or 8 where 16-token tiles would leave CUs idle (a thread then owns one row) */
+template <bool Q5, bool FAST, int TT>
 __global__ __launch_bounds__(WG) void k_gemm_exact(MatArgs a, uint32_t tok_tiles) {
+    static_assert(TT == 16 || TT == 8, "token tile");
+    constexpr uint32_t TPT = WG / TT;          /* staging threads per token */
+    constexpr uint32_t NP = 32 / TPT;          /* 16-byte activation pieces per staging thread */
+    constexpr int RPT = GT_R * TT / WG;        /* rows per thread */
     __shared__ float wsl[GT_R][SC_PITCH];
     __shared__ __attribute__((aligned(16))) uint32_t wql[GT_R][WQ_PITCH];
-    __shared__ float xdl[GT_T][SC_PITCH];
-    __shared__ __attribute__((aligned(16))) uint32_t xql[GT_T][WQ_PITCH];
+    __shared__ float xdl[TT][SC_PITCH];
+    __shared__ __attribute__((aligned(16))) uint32_t xql[TT][WQ_PITCH];
 
     const uint32_t tid = threadIdx.x, nb = a.nb;
     /* XCD-aware order: workgroup i runs on XCD i % 8; give each XCD a
@@ -526,18 +532,18 @@ __global__ __launch_bounds__(WG) void k_gemm_exact(MatArgs a, uint32_t tok_tiles
     const uint32_t row_tile = L / tok_tiles, tok_tile = L % tok_tiles;
 
     const Item &I = a.item[find_item(a, row_tile)];
-    const uint32_t r0 = (row_tile - I.tile_begin) * GT_R, t0 = tok_tile * GT_T;
+    const uint32_t r0 = (row_tile - I.tile_begin) * GT_R, t0 = tok_tile * TT;
 
     /* staging roles */
     const uint32_t srow = tid / 8, spart = tid % 8; /* weights: row, pair of blocks */
     const bool srow_ok = r0 + srow < I.rows;
     const unsigned char *wrow = I.w + (size_t)(srow_ok ? r0 + srow : 0) * I.row_bytes;
-    const uint32_t stok = tid / 16, spiece = tid % 16; /* activations */
+    const uint32_t stok = tid / TPT, spiece = tid % TPT; /* activations */
     const bool stok_ok = t0 + stok < a.ntok;
     const size_t tok_base = (size_t)(stok_ok ? t0 + stok : 0) * a.xstride;
 
     uint32_t wr[Q5 ? 11 : 18] = {};
-    u4a xr[2] = {};
+    u4a xr[NP] = {};
     float xs = 0.0f;
     auto fetch = [&](uint32_t c) {
         const uint32_t b = c * GT_CB + spart * 2;
@@ -562,14 +568,14 @@ __global__ __launch_bounds__(WG) void k_gemm_exact(MatArgs a, uint32_t tok_tiles
                 }
             }
         }
-        /* token stok, 16-byte pieces spiece and spiece+16 of the chunk's 512 bytes */
+        /* token stok, 16-byte pieces spiece + TPT h of the chunk's 512 bytes */
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t piece = spiece + 16 * h, b = c * GT_CB + piece / 2;
+        for (uint32_t h = 0; h < NP; ++h) {
+            const uint32_t piece = spiece + TPT * h, b = c * GT_CB + piece / 2;
             if (stok_ok && b < nb) xr[h] = *(const u4a *)(a.xq + (tok_base + c * GT_CB) * QK + piece * 16);
         }
         const uint32_t bx = c * GT_CB + spiece;
-        if (stok_ok && bx < nb) xs = a.xd[tok_base + bx];
+        if (stok_ok && spiece < (uint32_t)GT_CB && bx < nb) xs = a.xd[tok_base + bx];
     };
     auto stage = [&](uint32_t c) {
         const uint32_t b = c * GT_CB + spart * 2;
@@ -596,22 +602,22 @@ __global__ __launch_bounds__(WG) void k_gemm_exact(MatArgs a, uint32_t tok_tiles
             for (int l = 0; l < 4; ++l) dst[l] = make_uint2(words[2 * l], words[2 * l + 1]);
         }
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t piece = spiece + 16 * h, b = c * GT_CB + piece / 2;
+        for (uint32_t h = 0; h < NP; ++h) {
+            const uint32_t piece = spiece + TPT * h, b = c * GT_CB + piece / 2;
             const bool ok = stok_ok && b < nb;
             uint2 *dst = (uint2 *)&xql[stok][piece * 4];
             dst[0] = ok ? make_uint2(xr[h].x, xr[h].y) : make_uint2(0u, 0u);
             dst[1] = ok ? make_uint2(xr[h].z, xr[h].w) : make_uint2(0u, 0u);
         }
         const uint32_t bx = c * GT_CB + spiece;
-        xdl[stok][spiece] = (stok_ok && bx < nb) ? xs : 0.0f;
+        if (spiece < (uint32_t)GT_CB) xdl[stok][spiece] = (stok_ok && bx < nb) ? xs : 0.0f;
     };
 
-    const uint32_t tg = tid % GT_T, rg = tid / GT_T; /* token tg, rows 2 rg and 2 rg + 1 */
-    static_assert(GT_T * GT_R / 2 == WG, "one thread per (row pair, token)");
-    float acc[2][8];
+    const uint32_t tg = tid % TT, rg = tid / TT; /* token tg, rows RPT rg .. RPT rg + RPT - 1 */
+    static_assert(TT * GT_R / RPT == WG, "one thread per (RPT rows, token)");
+    float acc[RPT][8];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < RPT; ++i)
 #pragma unroll
         for (int l = 0; l < 8; ++l) acc[i][l] = 0.0f;
 
@@ -627,10 +633,10 @@ __global__ __launch_bounds__(WG) void k_gemm_exact(MatArgs a, uint32_t tok_tiles
             const uint32_t x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
             const float xsc = xdl[tg][bb];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const u4a w0 = *(const u4a *)&wql[2 * rg + i][bb * 8], w1 = *(const u4a *)&wql[2 * rg + i][bb * 8 + 4];
+            for (int i = 0; i < RPT; ++i) {
+                const u4a w0 = *(const u4a *)&wql[RPT * rg + i][bb * 8], w1 = *(const u4a *)&wql[RPT * rg + i][bb * 8 + 4];
                 const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-                const float d = wsl[2 * rg + i][bb] * xsc;
+                const float d = wsl[RPT * rg + i][bb] * xsc;
 #pragma unroll
                 for (int l = 0; l < 8; ++l) acc[i][l] = lane_step<FAST>(acc[i][l], d, dot4(w[l], x[l], 0));
             }
@@ -646,10 +652,10 @@ __global__ __launch_bounds__(WG) void k_gemm_exact(MatArgs a, uint32_t tok_tiles
     }
 
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < RPT; ++i) {
         const float *a8 = acc[i]; /* the lane tree of reduce8: ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) */
         const float v = ((a8[0] + a8[4]) + (a8[2] + a8[6])) + ((a8[1] + a8[5]) + (a8[3] + a8[7]));
-        const uint32_t r = r0 + 2 * rg + i, t = t0 + tg;
+        const uint32_t r = r0 + RPT * rg + i, t = t0 + tg;
         if (r < I.rows && t < a.ntok) store_out(I, a.flag, t, r, v);
     }
 }
@@ -2405,8 +2411,23 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
             a.item[i].tile_begin = tiles;
             tiles += (a.item[i].rows + GT_R - 1) / GT_R;
         }
-        const uint32_t tok_tiles = (a.ntok + GT_T - 1) / GT_T;
-        hipLaunchKernelGGL((k_gemm_exact<Q5, FAST>), dim3(tiles * tok_tiles), dim3(WG), 0, s, a, tok_tiles);
+        /* 8-token tiles where 16-token ones would give fewer than two workgroups per CU (c1 down at 128
+         * tokens: 224 workgroups) */
+        static int cus = 0;
+        if (!cus) {
+            int dev = 0, v = 0;
+            if (hipGetDevice(&dev) != hipSuccess ||
+                hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+                v = 256;
+            cus = v;
+        }
+        if ((uint64_t)tiles * ((a.ntok + 15) / 16) < 2ull * (uint64_t)cus) {
+            const uint32_t tok_tiles = (a.ntok + 7) / 8;
+            hipLaunchKernelGGL((k_gemm_exact<Q5, FAST, 8>), dim3(tiles * tok_tiles), dim3(WG), 0, s, a, tok_tiles);
+        } else {
+            const uint32_t tok_tiles = (a.ntok + 15) / 16;
+            hipLaunchKernelGGL((k_gemm_exact<Q5, FAST, 16>), dim3(tiles * tok_tiles), dim3(WG), 0, s, a, tok_tiles);
+        }
         return hipGetLastError();
     }
     uint32_t begin = 0;

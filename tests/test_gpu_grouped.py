@@ -5,7 +5,7 @@ CPU oracle, bit for bit, in the exact and the fast (FMA) contract."""
 import numpy as np
 import pytest
 
-from checks import assert_same_f32, say
+from checks import assert_same_f32, q5_random, say
 from smq_pkg import smq, synth
 
 pytestmark = pytest.mark.gpu
@@ -95,17 +95,6 @@ def test_grouped_gemv(orc, q5, cols, rows, fast, plain):
     for i, (it, wnt) in enumerate(zip(items, want)):
         assert_same_f32(it[2].download(np.float32), wnt, f"item {i}")
     smq.kernels_set_fast(False)
-
-
-def q5_random(seed, rows, cols):
-    """Q5 rows of random high-bit planes and nibbles under random finite f16 scales (every code and
-    both signs of the scale; the kernels decode any bytes, so the 21-candidate rule is not needed)."""
-    nb = (cols + 31) // 32
-    rng = np.random.default_rng(seed)
-    w = rng.integers(0, 256, (rows, nb, 22), dtype=np.uint8)
-    scale = rng.uniform(-2e-3, 2e-3, (rows, nb)).astype(np.float16)
-    w[:, :, 0:2] = scale.view(np.uint8).reshape(rows, nb, 2)
-    return w.reshape(rows, nb * 22)
 
 
 @pytest.mark.parametrize("fast", [False, True])

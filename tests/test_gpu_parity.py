@@ -6,6 +6,7 @@ import sys
 import numpy as np
 import pytest
 
+from checks import q5_random
 from patterns import LcgUniform
 from smq_pkg import smq, synth
 
@@ -157,6 +158,24 @@ def test_lm_head_bit_exact(orc, ntok):
     wsub = w.reshape(rows, nb * Q8B)[pick].reshape(-1)
     want = orc.gemm(wsub, nb * Q8B, xd, xq, len(pick), ntok, nb).reshape(ntok, len(pick))
     assert_same_f32(got[:, pick], want, "lm head")
+
+
+@pytest.mark.parametrize("q5,fast", [(False, False), (True, False), (False, True)])
+def test_exact_gemm_16_token_tiles_ragged(orc, q5, fast):
+    """Enough row tiles for the exact GEMM's 16-token tiles (304 row tiles x 3 token tiles; shapes with
+    fewer workgroups take 8-token tiles): a ragged last row tile and token tile, an output stride wider
+    than the rows, 30 blocks (a partial second K chunk), the fast contract."""
+    rows, cols, ntok = 9723, 960, 37
+    nb, stride = cols // 32, 9723 + 3
+    say("exact 16-token tiles", q5, fast)
+    w = (q5_random(91, rows, cols) if q5 else synth.q8_weights(91, rows, cols)).reshape(-1)
+    x = synth.activations(92, ntok, cols)
+    got, xd, xq = run_gemm(w, nb * (Q5B if q5 else Q8B), x, rows, ntok, nb, q5, stride, fast)
+    want = orc.gemm(w, nb * (Q5B if q5 else Q8B), xd, xq, rows, ntok, nb, stride=stride, q5=q5, fast=fast)
+    m = np.zeros(ntok * stride, bool)
+    m.reshape(ntok, stride)[:, :rows] = True
+    assert_same_f32(got[m], want[m], "16-token tiles")
+    assert np.all(bits(got[~m]) == 0xFFFFFFFF), "wrote outside the output rows"
 
 
 def test_random_shapes_and_strides(orc):

@@ -100,6 +100,7 @@ _SIGS = {
     "smq_block_sums": (None, [ctypes.c_int, _vp, _sz, _vp, _u32, _u32, _u32, _vp]),
     "smq_set_prefill_mfma": (None, [ctypes.c_int]),
     "smq_set_gemv_rows": (ctypes.c_int, [ctypes.c_int]),
+    "smq_set_exact_gemm": (ctypes.c_int, [ctypes.c_int]),
     "smq_matmul": (ctypes.c_int, [ctypes.POINTER(_MatItem), _u32, _vp, _vp, _u32]),
     "smq_numeric_check": (ctypes.c_int, []),
     "smq_matmul_act": (ctypes.c_int, [ctypes.POINTER(_MatItem), _u32, ctypes.POINTER(_Act)]),
@@ -365,6 +366,15 @@ def set_prefill_mfma(on):
 def set_gemv_rows(rows):
     """Rows per workgroup of the one-launch decode GEMV (1, 2, 4, 8, 16), or 0 for the default choice."""
     _check(load().smq_set_gemv_rows(int(rows)))
+
+
+EXACT_BY_SHAPE, EXACT_MFMA, EXACT_VALU = 0, 1, 2
+
+
+def set_exact_gemm(mode):
+    """Kernel of the exact prefill GEMM: EXACT_BY_SHAPE (default), EXACT_MFMA (lane sums on the matrix
+    cores) or EXACT_VALU (lane sums as v_dot4); the outputs are the same bit for bit."""
+    _check(load().smq_set_exact_gemm(int(mode)))
 
 
 # ---- src/model.c:236-310

@@ -465,6 +465,11 @@ smq_status smq_set_gemv_rows(int rows) {
     return SMQ_OK;
 }
 
+smq_status smq_set_exact_gemm(int mode) {
+    if (!smq::set_exact_gemm(mode)) return set_status(SMQ_ERR_RANGE, "set_exact_gemm: %d is not 0, 1 or 2", mode);
+    return SMQ_OK;
+}
+
 smq_status smq_matmul(const smq_mat_item *items, uint32_t n, const float *xd, const int8_t *xq, uint32_t ntok) {
     if (!ready()) return t_status;
     if (!items || n < 1 || n > SMQ_MAX_ITEMS) return set_status(SMQ_ERR_RANGE, "matmul: %u items", n);

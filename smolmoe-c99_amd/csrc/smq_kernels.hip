@@ -2250,6 +2250,8 @@ bool gemv_persistent(uint32_t total_rows, int rt) { return (total_rows + rt - 1)
 int g_forced_rt = 0;
 /* set_att_grouped(false) sends prefill attention to k_attend_rows instead (tuning, tests) */
 bool g_att_grouped = true;
+/* set_exact_gemm: 0 = the exact prefill GEMM chosen by shape, 1 = always k_gemm_xm, 2 = never */
+int g_exact_mode = 0;
 
 /* Workgroups of kernel k resident on the device (computed once per kernel by the caller's static). */
 inline hipError_t resident_wgs(const void *k, int nt, int &resident) {
@@ -2406,13 +2408,12 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
             }
             return launch_gemv_tile<Q5, FAST>(a, rt, s);
         }
-        uint32_t tiles = 0;
+        uint32_t tiles = 0, tiles32 = 0;
         for (uint32_t i = 0; i < a.nitems; ++i) {
             a.item[i].tile_begin = tiles;
             tiles += (a.item[i].rows + GT_R - 1) / GT_R;
+            tiles32 += (a.item[i].rows + 31) / 32;
         }
-        /* 8-token tiles where 16-token ones would give fewer than two workgroups per CU (c1 down at 128
-         * tokens: 224 workgroups) */
         static int cus = 0;
         if (!cus) {
             int dev = 0, v = 0;
@@ -2421,6 +2422,14 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
                 v = 256;
             cus = v;
         }
+        /* the lane sums on MFMA from about 7/8 of a workgroup of 32 x 32 per CU (measured on MI355X:
+         * 896x4864 at 256 tokens, 224 workgroups, 51.5 against 53.4 us; at 192 tokens, 168 workgroups,
+         * 50.1 against 43.9 us; 9728x896 at 128 tokens 29.6 against 42.3 us) */
+        if (g_exact_mode == 1 ||
+            (g_exact_mode == 0 && 8ull * tiles32 * ((a.ntok + 31) / 32) >= 7ull * (uint64_t)cus))
+            return launch_gemm_xm(a, Q5, FAST, s);
+        /* 8-token tiles where 16-token ones would give fewer than two workgroups per CU (c1 down at 128
+         * tokens: 224 workgroups) */
         if ((uint64_t)tiles * ((a.ntok + 15) / 16) < 2ull * (uint64_t)cus) {
             const uint32_t tok_tiles = (a.ntok + 7) / 8;
             hipLaunchKernelGGL((k_gemm_exact<Q5, FAST, 8>), dim3(tiles * tok_tiles), dim3(WG), 0, s, a, tok_tiles);
@@ -2502,6 +2511,12 @@ int gemv_rows_per_tile(uint32_t nb, bool q5, uint32_t total_rows) {
 bool set_gemv_rows(int rt) {
     if (rt != 0 && rt != 1 && rt != 2 && rt != 4 && rt != 8 && rt != 16) return false;
     g_forced_rt = rt;
+    return true;
+}
+
+bool set_exact_gemm(int mode) {
+    if (mode < 0 || mode > 2) return false;
+    g_exact_mode = mode;
     return true;
 }
 

@@ -558,7 +558,211 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_mh(MhArgs q) {
     if (a.flag && __ballot(bad) && l == 0) *a.flag = 1;
 }
 
+/* ------------------------------------------------------------------------
+ * Exact prefill GEMM with the lane sums on f16 MFMA (k_gemm_xm): the results
+ * of k_gemm_exact, bit for bit, with the eight lane sums of each (row, token,
+ * block) formed by the matrix cores instead of v_dot4.
+ * v_mfma_f32_16x16x4_4b_f16 computes four independent 16 x 16 products of
+ * K = 4. Instruction h (0, 1) gives its block m lane 4h + m of a Q8 block:
+ * A = weight word 4h + m of 16 rows, B = activation word 4h + m of 16
+ * tokens, so it returns four of the eight lane sums s_l (kernels.c:36-50) of
+ * a 16 x 16 tile. They are exact: int8 values (and Q5 codes - 16) are exact
+ * in f16, their products exact in f32, and a sum of four is an integer below
+ * 2^24; with C = +0 a zero sum is +0, as v_dot4's convert gives. The VALU
+ * keeps the contract's own arithmetic: per lane sum acc_l = acc_l + d * s_l
+ * (FAST: fmaf), per output and block one d = wscale * xscale, blocks in
+ * order, then the fixed lane tree.
+ * Operand layout (checked on MI355X): lane L supplies A[m = L/16][i = L%16][0..3]
+ * and B[m][0..3][j = L%16] and receives D[m][4 (L/16) + v][L%16] in register
+ * 4m + v, so a lane ends with rows 4 (L/16) + v (v = 0..3) of token L%16 and
+ * all eight lane sums of each.
+ * Workgroup tile 32 rows x 32 tokens; wave w takes rows 16 (w%2) .. and tokens
+ * 16 (w/2) ... K advances in chunks of XM_CB blocks: each thread loads one
+ * block of a row (Q5: the pair holding it) and one block of a token, turns
+ * their eight words into f16 and writes them in MFMA operand order (a wave's
+ * operand read is one contiguous 512-byte run); the next chunk's loads are
+ * issued before the current chunk is computed.
+ * ---------------------------------------------------------------------- */
+constexpr uint32_t XM_CB = 8;          /* blocks per K chunk */
+constexpr uint32_t XM_PS = 4 * 64 + 4; /* uint2 per block: [group][half][lane] and 32 bytes, so that a staging write
+                                        * (8 blocks x 4 rows per 32 lanes) meets 64 distinct banks */
+constexpr uint32_t XM_SP = 36;         /* scale plane pitch: 16-byte reads, the 8 x 4 staging writes conflict-free */
+static_assert(XM_PS % 32 == 4 && XM_SP % 4 == 0 && XM_SP % 64 == 36, "bank spread of the staging writes");
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+typedef float f16x __attribute__((ext_vector_type(16)));
+
+/* Four bytes of 5-bit codes q as the four exact f16 q - 16: the half 0x6400 | q is 1024 + q. */
+__device__ __forceinline__ uint2 q5x4_f16(uint32_t codes) {
+    const h2v m = {(_Float16)1040.0f, (_Float16)1040.0f};
+    const h2v lo = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, codes, 0x04010400u)) - m;
+    const h2v hi = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, codes, 0x04030402u)) - m;
+    return make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+}
+
+template <bool FAST>
+__device__ __forceinline__ float lane_step_f(float acc, float d, float s) {
+    if (FAST) return __builtin_fmaf(d, s, acc);
+    const float p = d * s;
+    return acc + p;
+}
+
+template <bool Q5, bool FAST>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gemm_xm(MatArgs a,
+                                                                                           uint32_t tok_tiles) {
+    __shared__ __attribute__((aligned(16))) uint2 opa[XM_CB * XM_PS];
+    __shared__ __attribute__((aligned(16))) uint2 opb[XM_CB * XM_PS];
+    __shared__ __attribute__((aligned(16))) float wsc[XM_CB][XM_SP];
+    __shared__ __attribute__((aligned(16))) float xsc[XM_CB][XM_SP];
+
+    const uint32_t tid = threadIdx.x, nb = a.nb;
+    /* XCD-aware order: workgroup i runs on XCD i % 8; each XCD takes a contiguous range of tiles, so
+     * the token tiles of one row tile share an L2 */
+    const uint32_t G = gridDim.x, xcd = blockIdx.x % 8u, k = blockIdx.x / 8u;
+    const uint32_t per = G / 8u, extra = G % 8u;
+    const uint32_t L = xcd * per + (xcd < extra ? xcd : extra) + k;
+    const uint32_t row_tile = L / tok_tiles, tok_tile = L % tok_tiles;
+    const Item I = pick_item(a, row_tile);
+    const uint32_t r0 = (row_tile - I.tile_begin) * 32, t0 = tok_tile * 32;
+
+    /* staging: thread (row or token tid/8, block tid%8 of the chunk) */
+    const uint32_t srow = tid / 8, sblk = tid % 8;
+    const bool srow_ok = r0 + srow < I.rows, stok_ok = t0 + srow < a.ntok;
+    const unsigned char *wrow = I.w + (size_t)(srow_ok ? r0 + srow : 0) * I.row_bytes;
+    const size_t tok_base = (size_t)(stok_ok ? t0 + srow : 0) * a.xstride;
+    uint32_t wr[Q5 ? 11 : 9] = {};
+    uint32_t xr[8] = {};
+    float xs = 0.0f;
+    auto fetch = [&](uint32_t c) __attribute__((always_inline)) {
+        if (Q5) {
+            const uint32_t b = c * XM_CB + (sblk & ~1u); /* the pair holding the block (nb even) */
+            if (srow_ok && b < nb) {
+                const unsigned char *p = wrow + (size_t)b * Q5_BYTES;
+                const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
+                const u3a v2 = *(const u3a *)(p + 32);
+                wr[0] = v0.x; wr[1] = v0.y; wr[2] = v0.z; wr[3] = v0.w;
+                wr[4] = v1.x; wr[5] = v1.y; wr[6] = v1.z; wr[7] = v1.w;
+                wr[8] = v2.x; wr[9] = v2.y; wr[10] = v2.z;
+            }
+        } else {
+            const uint32_t b = c * XM_CB + sblk;
+            if (srow_ok && b < nb) {
+                const unsigned char *p = wrow + (size_t)b * Q8_BYTES;
+                const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
+                wr[0] = v0.x; wr[1] = v0.y; wr[2] = v0.z; wr[3] = v0.w;
+                wr[4] = v1.x; wr[5] = v1.y; wr[6] = v1.z; wr[7] = v1.w;
+                wr[8] = *(const uint32_t *)(p + 32);
+            }
+        }
+        const uint32_t bx = c * XM_CB + sblk;
+        if (stok_ok && bx < nb) {
+            const int8_t *p = a.xq + (tok_base + bx) * QK;
+            const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
+            xr[0] = v0.x; xr[1] = v0.y; xr[2] = v0.z; xr[3] = v0.w;
+            xr[4] = v1.x; xr[5] = v1.y; xr[6] = v1.z; xr[7] = v1.w;
+            xs = a.xd[tok_base + bx];
+        }
+    };
+    auto stage = [&](uint32_t c) __attribute__((always_inline)) {
+        const uint32_t b = c * XM_CB + sblk;
+        const bool ok = srow_ok && b < nb, xok = stok_ok && b < nb;
+        /* lane word l = 4h + m of row (token) s goes to [block][s / 16][h][s % 16 + 16 m] */
+        uint2 *wd = opa + sblk * XM_PS + (srow / 16) * 128 + srow % 16;
+        uint2 *xd = opb + sblk * XM_PS + (srow / 16) * 128 + srow % 16;
+        float sc;
+        if (Q5) {
+            Q5Fields f[2];
+            q5_parse_pair(wr, f[0], f[1]);
+            const bool second = sblk & 1u;
+            Q5Fields q;
+            q.scale = second ? f[1].scale : f[0].scale;
+            q.high = second ? f[1].high : f[0].high;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) q.nib[j] = second ? f[1].nib[j] : f[0].nib[j];
+            q.even = second ? f[1].even : f[0].even;
+            q.odd = second ? f[1].odd : f[0].odd;
+#pragma unroll
+            for (int l = 0; l < 8; ++l) wd[(l / 4) * 64 + (l % 4) * 16] = ok ? q5x4_f16(q5_codes(q, l)) : make_uint2(0u, 0u);
+            sc = ok ? q.scale : 0.0f;
+        } else {
+#pragma unroll
+            for (int l = 0; l < 8; ++l) wd[(l / 4) * 64 + (l % 4) * 16] = ok ? i8x4_f16(wr[1 + l]) : make_uint2(0u, 0u);
+            sc = ok ? __uint_as_float(wr[0]) : 0.0f;
+        }
+        wsc[sblk][srow] = sc;
+#pragma unroll
+        for (int l = 0; l < 8; ++l) xd[(l / 4) * 64 + (l % 4) * 16] = xok ? i8x4_f16(xr[l]) : make_uint2(0u, 0u);
+        xsc[sblk][srow] = xok ? xs : 0.0f;
+    };
+
+    const uint32_t lane = tid & 63u, w = tid >> 6, rg = w & 1u, tg = w >> 1;
+    float acc[8][4];
+#pragma unroll
+    for (int l = 0; l < 8; ++l)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[l][v] = 0.0f;
+
+    const uint32_t nchunks = (nb + XM_CB - 1) / XM_CB;
+    fetch(0);
+    for (uint32_t c = 0; c < nchunks; ++c) {
+        stage(c);
+        __syncthreads();
+        if (c + 1 < nchunks) fetch(c + 1);
+        const uint32_t count = nb - c * XM_CB < XM_CB ? nb - c * XM_CB : XM_CB;
+        auto block = [&](uint32_t bb) __attribute__((always_inline)) {
+            const uint2 *pa = opa + bb * XM_PS + rg * 128 + lane, *pb = opb + bb * XM_PS + tg * 128 + lane;
+            const h4v a0 = __builtin_bit_cast(h4v, pa[0]), a1 = __builtin_bit_cast(h4v, pa[64]);
+            const h4v b0 = __builtin_bit_cast(h4v, pb[0]), b1 = __builtin_bit_cast(h4v, pb[64]);
+            const f16x z = {};
+            const f16x s0 = __builtin_amdgcn_mfma_f32_16x16x4f16(a0, b0, z, 0, 0, 0); /* lanes 0-3 */
+            const f16x s1 = __builtin_amdgcn_mfma_f32_16x16x4f16(a1, b1, z, 0, 0, 0); /* lanes 4-7 */
+            const float4 dw = *(const float4 *)&wsc[bb][rg * 16 + 4 * (lane >> 4)];
+            const float dx = xsc[bb][tg * 16 + (lane & 15u)];
+            const float d[4] = {dw.x * dx, dw.y * dx, dw.z * dx, dw.w * dx};
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[m][v] = lane_step_f<FAST>(acc[m][v], d[v], s0[4 * m + v]);
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[4 + m][v] = lane_step_f<FAST>(acc[4 + m][v], d[v], s1[4 * m + v]);
+        };
+        /* unrolled with uniform guards: fixed LDS offsets per block, 103-106 registers (four waves per SIMD) */
+#pragma unroll
+        for (uint32_t bb = 0; bb < XM_CB; ++bb)
+            if (bb < count) block(bb);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int v = 0; v < 4; ++v) { /* the lane tree of reduce8: ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) */
+        const float o = ((acc[0][v] + acc[4][v]) + (acc[2][v] + acc[6][v])) +
+                        ((acc[1][v] + acc[5][v]) + (acc[3][v] + acc[7][v]));
+        const uint32_t r = r0 + rg * 16 + 4 * (lane >> 4) + v, t = t0 + tg * 16 + (lane & 15u);
+        if (r < I.rows && t < a.ntok) store_out(I, a.flag, t, r, o);
+    }
+}
+
 }  // namespace
+
+hipError_t launch_gemm_xm(MatArgs a, bool q5, bool fast, hipStream_t s) {
+    uint32_t tiles = 0;
+    for (uint32_t i = 0; i < a.nitems; ++i) {
+        a.item[i].tile_begin = tiles;
+        tiles += (a.item[i].rows + 31) / 32;
+    }
+    const uint32_t tok_tiles = (a.ntok + 31) / 32;
+    if (!tiles || !tok_tiles || !a.nb) return hipSuccess;
+    const dim3 grid(tiles * tok_tiles), block(256);
+    if (q5) {
+        if (fast) hipLaunchKernelGGL((k_gemm_xm<true, true>), grid, block, 0, s, a, tok_tiles);
+        else hipLaunchKernelGGL((k_gemm_xm<true, false>), grid, block, 0, s, a, tok_tiles);
+    } else {
+        if (fast) hipLaunchKernelGGL((k_gemm_xm<false, true>), grid, block, 0, s, a, tok_tiles);
+        else hipLaunchKernelGGL((k_gemm_xm<false, false>), grid, block, 0, s, a, tok_tiles);
+    }
+    return hipGetLastError();
+}
 
 namespace {
 bool g_mh_on = true;

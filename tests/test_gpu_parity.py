@@ -160,17 +160,36 @@ def test_lm_head_bit_exact(orc, ntok):
     assert_same_f32(got[:, pick], want, "lm head")
 
 
-@pytest.mark.parametrize("q5,fast", [(False, False), (True, False), (False, True)])
-def test_exact_gemm_16_token_tiles_ragged(orc, q5, fast):
-    """Enough row tiles for the exact GEMM's 16-token tiles (304 row tiles x 3 token tiles; shapes with
-    fewer workgroups take 8-token tiles): a ragged last row tile and token tile, an output stride wider
-    than the rows, 30 blocks (a partial second K chunk), the fast contract."""
+class exact_kernel:
+    """Which kernel the exact prefill GEMM takes inside the block (smq_set_exact_gemm), back to the
+    choice by shape afterwards."""
+
+    def __init__(self, mode):
+        self.mode = mode
+
+    def __enter__(self):
+        smq.set_exact_gemm(self.mode)
+
+    def __exit__(self, *exc):
+        smq.set_exact_gemm(smq.EXACT_BY_SHAPE)
+
+
+EXACT_MODES = [smq.EXACT_MFMA, smq.EXACT_VALU]
+
+
+@pytest.mark.parametrize("mode", EXACT_MODES)
+@pytest.mark.parametrize("q5,fast", [(False, False), (True, False), (False, True), (True, True)])
+def test_exact_gemm_16_token_tiles_ragged(orc, q5, fast, mode):
+    """Both exact kernels on a shape with enough row tiles for 16-token (and 32-token) tiles: a ragged
+    last row tile and token tile, an output stride wider than the rows, 30 blocks (a partial last K
+    chunk), the fast contract."""
     rows, cols, ntok = 9723, 960, 37
     nb, stride = cols // 32, 9723 + 3
-    say("exact 16-token tiles", q5, fast)
+    say("exact 16-token tiles", q5, fast, mode)
     w = (q5_random(91, rows, cols) if q5 else synth.q8_weights(91, rows, cols)).reshape(-1)
     x = synth.activations(92, ntok, cols)
-    got, xd, xq = run_gemm(w, nb * (Q5B if q5 else Q8B), x, rows, ntok, nb, q5, stride, fast)
+    with exact_kernel(mode):
+        got, xd, xq = run_gemm(w, nb * (Q5B if q5 else Q8B), x, rows, ntok, nb, q5, stride, fast)
     want = orc.gemm(w, nb * (Q5B if q5 else Q8B), xd, xq, rows, ntok, nb, stride=stride, q5=q5, fast=fast)
     m = np.zeros(ntok * stride, bool)
     m.reshape(ntok, stride)[:, :rows] = True
@@ -178,9 +197,11 @@ def test_exact_gemm_16_token_tiles_ragged(orc, q5, fast):
     assert np.all(bits(got[~m]) == 0xFFFFFFFF), "wrote outside the output rows"
 
 
-def test_random_shapes_and_strides(orc):
+@pytest.mark.parametrize("mode", [smq.EXACT_BY_SHAPE, smq.EXACT_MFMA])
+def test_random_shapes_and_strides(orc, mode):
     """Ragged rows and tokens, odd widths (including odd Q5 widths, which take
-    the generic kernel), output strides wider than the row count."""
+    the generic kernel), output strides wider than the row count; then the
+    same with every prefill shape on the MFMA lane-sum kernel."""
     g = LcgUniform(77)
     for trial in range(40):
         q5 = trial % 2 == 1
@@ -192,8 +213,9 @@ def test_random_shapes_and_strides(orc):
         fast = trial % 5 == 4
         w = weights(q5, trial, rows, cols, 0.5)
         x = g.uniform(-30, 30, ntok * cols).reshape(ntok, cols)
-        say("random", trial, q5, nb, rows, ntok, stride, fast)
-        got, xd, xq = run_gemm(w, nb * (Q5B if q5 else Q8B), x, rows, ntok, nb, q5, stride, fast)
+        say("random", trial, q5, nb, rows, ntok, stride, fast, mode)
+        with exact_kernel(mode):
+            got, xd, xq = run_gemm(w, nb * (Q5B if q5 else Q8B), x, rows, ntok, nb, q5, stride, fast)
         want = orc.gemm(w, nb * (Q5B if q5 else Q8B), xd, xq, rows, ntok, nb, stride=stride, q5=q5, fast=fast)
         m = np.zeros(ntok * stride, bool)
         m.reshape(ntok, stride)[:, :rows] = True
@@ -307,13 +329,22 @@ def test_empty_and_bad_arguments():
 
 # ------------------------------------------------------------------ matmul glue
 
-def test_matmul_fused_items_bias_and_fault(orc):
+@pytest.mark.parametrize("mode", EXACT_MODES)
+def test_matmul_fused_items_bias_and_fault(orc, mode):
     """model.c:291-310: q/k/v share one input (896+128+128 rows), bias added,
-    outputs checked finite."""
+    outputs checked finite; the prefill case on each exact kernel."""
+    smq.set_exact_gemm(mode)
+    try:
+        matmul_fused_items_bias_and_fault(orc)
+    finally:
+        smq.set_exact_gemm(smq.EXACT_BY_SHAPE)
+
+
+def matmul_fused_items_bias_and_fault(orc):
     g = LcgUniform(44)
     cols, nb = 896, 28
     shapes = [896, 128, 128]
-    for ntok in (1, 5):
+    for ntok in (1, 5, 40):
         x = synth.activations(9 + ntok, ntok, cols)
         dbuf, qbuf, xd, xq = gpu_quantize(x)
         items, wants = [], []
@@ -345,6 +376,51 @@ def test_matmul_fused_items_bias_and_fault(orc):
     with pytest.raises(smq.SmqError) as e:
         smq.matmul([(smq.QMat(wb, 4, cols), None, yb), (smq.QMat(w2, 4, 64), None, yb)], dbuf, qbuf, 1)
     assert e.value.status == 7
+
+
+@pytest.mark.parametrize("q5", [False, True])
+def test_exact_mfma_items_bias_accumulate_nonfinite(orc, q5):
+    """The MFMA lane-sum kernel through smq_matmul: four items of ragged row counts (item edges inside
+    and between 32-row tiles), bias on some, residual add on others, 70 tokens (a ragged 32-token tile);
+    then an infinite weight scale flags SM_ERR_NUMERIC."""
+    g = LcgUniform(45)
+    cols, ntok = 1024, 70
+    nb, bb = cols // 32, Q5B if q5 else Q8B
+    x = synth.activations(46, ntok, cols)
+    dbuf, qbuf, xd, xq = gpu_quantize(x)
+    items, wants = [], []
+    for i, rows in enumerate([33, 100, 7, 64]):
+        w = (q5_random(60 + i, rows, cols) if q5 else synth.q8_weights(60 + i, rows, cols)).reshape(-1)
+        bias = g.uniform(-0.1, 0.1, rows) if i % 2 == 0 else None
+        acc = i % 3 == 1
+        y0 = g.uniform(-1, 1, ntok * rows).astype(np.float32) if acc else np.zeros(ntok * rows, np.float32)
+        ok, y = orc.mat_item(w, nb * bb, rows, bias, xd, xq, ntok, nb, q5=q5)
+        assert ok
+        wants.append(y0 + y if acc else y)
+        items.append((smq.QMat(smq.DeviceBuffer.from_array(w), rows, cols, smq.DTYPE_Q5 if q5 else smq.DTYPE_Q8),
+                      smq.DeviceBuffer.from_array(bias) if bias is not None else None,
+                      smq.DeviceBuffer.from_array(y0), acc))
+    say("exact mfma items", q5)
+    with exact_kernel(smq.EXACT_MFMA):
+        smq.matmul(items, dbuf, qbuf, ntok)
+        smq.numeric_check()
+        for i, (it, want) in enumerate(zip(items, wants)):
+            assert_same_f32(it[2].download(np.float32), want, f"item {i}")
+        w = synth.q8_weights(7, 40, cols).reshape(-1)
+        w[36 * nb * 3:36 * nb * 3 + 4] = np.array([np.inf], np.float32).view(np.uint8)  # row 3, block 0
+        yb = smq.DeviceBuffer(ntok * 40 * 4)
+        smq.matmul([(smq.QMat(smq.DeviceBuffer.from_array(w), 40, cols), None, yb)], dbuf, qbuf, ntok)
+        with pytest.raises(smq.SmqError) as e:
+            smq.numeric_check()
+        assert e.value.status == smq.SM_ERR_NUMERIC
+
+
+def test_exact_gemm_mode_refuses_other_values():
+    for bad in (-1, 3, 7):
+        with pytest.raises(smq.SmqError) as e:
+            smq.set_exact_gemm(bad)
+        assert e.value.status == smq.SM_ERR_RANGE
+    smq.set_exact_gemm(smq.EXACT_BY_SHAPE)
 
 
 def test_dequantize_rows(orc):

@@ -1009,9 +1009,9 @@ __global__ __launch_bounds__(RW_WG) void k_row_quantize(const float *src, const 
             if (i < n) sq_lds[i] = v[k] * v[k];
         }
         __syncthreads();
-        if (tid < 64) { /* the whole first wave runs the chain (faster than one lane) */
-            const float sq = serial_sum_lds(sq_lds, n);
-            if (tid == 0) {
+        if (tid < 64) { /* the whole first wave runs the chain; lane 63 ends with the sum */
+            const float sq = serial_sum_wave(sq_lds, n);
+            if (tid == 63) {
                 const float inv = 1.0f / sqrtf(sq / (float)n + eps); /* model.c:338 */
                 s_inv = inv;
                 s_bad = !(fabsf(sq) <= FLT_MAX) || !(fabsf(inv) <= FLT_MAX);
@@ -1886,22 +1886,26 @@ __global__ __launch_bounds__(AR_WG) __attribute__((amdgpu_waves_per_eu(1, 2))) v
  * 1. scores: eight threads per position, lane l accumulating q[8e+l]*k[8e+l]
  *    over e in order (the 8-lane dot_f32), the fixed lane tree, times 1/8;
  * 2. the maximum (order-free; NaN never wins), exp_det(s - max) in parallel;
- * 3. each head's total in position order by one lane;
- * 4. thread (head, j) sums (s_p * inv) * v_p[j] in position order, v rows
- *    read a batch ahead;
+ * 3. each head's total in position order by one wave (a register chain),
+ *    then w_p = s_p * inv for every position in parallel;
+ * 4. thread (head, j) sums w_p * v_p[j] in position order, the V rows
+ *    staged in LDS in chunks of 64 by all waves, two chunks ahead;
  * 5. the 64 outputs of a head, and with xd their two Q8 blocks. */
-constexpr uint32_t AG_WG = 512, AG_MAXG = 8, AG_MAXP = 1024, AG_VB = 16;
+constexpr uint32_t AG_WG = 512, AG_MAXG = 8, AG_MAXP = 1024, AG_VC = 64;
 
 __global__ __launch_bounds__(AG_WG) void k_attend_group(const float *q, const float *kcache, const float *vcache,
                                                         float *att, AttnShape sh, uint32_t pos0,
                                                         const int32_t *pos_dev, int *flag, float *xd, int8_t *xq) {
     __shared__ __attribute__((aligned(16))) float sc[AG_MAXG * AG_MAXP];
+    __shared__ __attribute__((aligned(16))) float vs[2][AG_VC * AR_HD]; /* V rows of two chunks */
     __shared__ float qs[AG_MAXG * AR_HD];
     __shared__ float hmax[AG_MAXG][AG_WG / 8];
     __shared__ float hinv[AG_MAXG];
     __shared__ uint64_t etab[32];
     const uint32_t tid = threadIdx.x, grp = sh.heads / sh.kv_heads, kvd = sh.kv_dim;
-    const uint32_t t = blockIdx.x / sh.kv_heads, kh = blockIdx.x % sh.kv_heads;
+    /* the last token first: workgroups start in index order, so the longest rows start in the first wave of
+     * workgroups and the short ones fill in behind them */
+    const uint32_t t = gridDim.x / sh.kv_heads - 1 - blockIdx.x / sh.kv_heads, kh = blockIdx.x % sh.kv_heads;
     const uint32_t pos = (pos_dev ? (uint32_t)*pos_dev : pos0) + t;
     if (pos >= sh.context) { /* the scores row holds at most context positions */
         if (tid == 0 && flag) *flag = 1;
@@ -1925,11 +1929,17 @@ __global__ __launch_bounds__(AG_WG) void k_attend_group(const float *q, const fl
         for (uint32_t e = 0; e < 8; ++e) qr[hh][e] = hh < grp ? qs[hh * AR_HD + 8 * e + l] : 0.0f;
     }
     const float factor = 1.0f / sqrtf((float)AR_HD);
-    for (uint32_t p = gi; p < np; p += AG_WG / 8) { /* all eight threads of a group take the same positions */
-        const float *kr = kbase + (size_t)p * kvd + l;
-        float kv[8];
+    /* the next position's K row is requested before this one's products (a position past the context reads
+     * row 0: in bounds, unused) */
+    auto kload = [&](float (&k)[8], uint32_t pp) __attribute__((always_inline)) {
+        const float *kr = kbase + (size_t)(pp < np ? pp : 0) * kvd + l;
 #pragma unroll
-        for (uint32_t e = 0; e < 8; ++e) kv[e] = kr[8 * e];
+        for (uint32_t e = 0; e < 8; ++e) k[e] = kr[8 * e];
+    };
+    float kv[8], kn[8];
+    kload(kv, gi);
+    for (uint32_t p = gi; p < np; p += AG_WG / 8) { /* all eight threads of a group take the same positions */
+        kload(kn, p + AG_WG / 8);
 #pragma unroll
         for (uint32_t hh = 0; hh < AG_MAXG; ++hh) {
             if (hh < grp) { /* uniform */
@@ -1946,7 +1956,26 @@ __global__ __launch_bounds__(AG_WG) void k_attend_group(const float *q, const fl
                 }
             }
         }
+#pragma unroll
+        for (uint32_t e = 0; e < 8; ++e) kv[e] = kn[e];
     }
+    /* the first two chunks of V rows requested now (thread: float4 tid%16 of rows tid/16 and tid/16 + 32 of a
+     * chunk; a row past the context re-reads the last one: in bounds, unused) */
+    const uint32_t nch = (np + AG_VC - 1) / AG_VC;
+    float4 vr[2][2];
+    auto vfetch = [&](float4 (&r)[2], uint32_t c) __attribute__((always_inline)) {
+#pragma unroll
+        for (uint32_t i = 0; i < 2; ++i) {
+            const uint32_t p = c * AG_VC + tid / 16 + 32 * i;
+            r[i] = *(const float4 *)(vbase + (size_t)(p < np ? p : np - 1) * kvd + 4 * (tid % 16));
+        }
+    };
+    auto vstore = [&](const float4 (&r)[2], uint32_t buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (uint32_t i = 0; i < 2; ++i) *(float4 *)&vs[buf][(tid / 16 + 32 * i) * AR_HD + 4 * (tid % 16)] = r[i];
+    };
+    vfetch(vr[0], 0);
+    if (nch > 1) vfetch(vr[1], 1);
     if (l == 7)
 #pragma unroll
         for (uint32_t hh = 0; hh < AG_MAXG; ++hh) hmax[hh][gi] = mx[hh];
@@ -1966,43 +1995,55 @@ __global__ __launch_bounds__(AG_WG) void k_attend_group(const float *q, const fl
     __syncthreads();
 
     /* 3. totals in position order */
-    if (tid < 64) { /* the whole first wave: lane h < grp sums head h's row, the others re-run row 0 */
-        const float tot = serial_sum_lds(sc + (tid < grp ? tid : 0) * AG_MAXP, np);
-        if (tid < grp) hinv[tid] = 1.0f / tot;
+    {   /* wave h < grp sums head h's row in a register chain; lane 63 ends with the total */
+        const uint32_t w = tid / 64;
+        if (w < grp) {
+            const float tot = serial_sum_wave(sc + w * AG_MAXP, np);
+            if ((tid & 63u) == 63u) hinv[w] = 1.0f / tot;
+        }
     }
     __syncthreads();
-
-    /* 4. values: wave hh (64 threads) is head kh*grp + hh, thread j its column */
-    const uint32_t hh = tid / AR_HD, j = tid % AR_HD;
-    if (hh >= grp) return; /* whole waves */
-    const float inv = hinv[hh];
-    const float *srow = sc + hh * AG_MAXP, *vcol = vbase + j;
-    float vb[2][AG_VB];
-    auto vload = [&](float (&v)[AG_VB], uint32_t p0) __attribute__((always_inline)) {
-#pragma unroll
-        for (uint32_t u = 0; u < AG_VB; ++u) {
-            const uint32_t p = p0 + u < np ? p0 + u : np - 1; /* in bounds; unused past np */
-            v[u] = vcol[(size_t)p * kvd];
-        }
-    };
-    float acc = 0.0f;
-    vload(vb[0], 0);
-    uint32_t p0 = 0;
-    auto vadd = [&](const float (&v)[AG_VB], uint32_t b0) __attribute__((always_inline)) {
-#pragma unroll
-        for (uint32_t u = 0; u < AG_VB; ++u) {
-            const float w = srow[b0 + u < np ? b0 + u : np - 1] * inv; /* kernels.c:1165: w = scores[p] * inv */
-            const float pr = w * v[u];
-            acc = acc + (b0 + u < np ? pr : 0.0f); /* past np: +0.0, which leaves acc unchanged */
-        }
-    };
-    for (; p0 + AG_VB < np; p0 += 2 * AG_VB) {
-        vload(vb[1], p0 + AG_VB);
-        vadd(vb[0], p0);
-        if (p0 + 2 * AG_VB < np) vload(vb[0], p0 + 2 * AG_VB);
-        vadd(vb[1], p0 + AG_VB);
+    /* kernels.c:1165: w = scores[p] * inv, formed for every position before the ordered sums */
+    for (uint32_t hq = 0; hq < grp; ++hq) {
+        const float inv = hinv[hq];
+        for (uint32_t p = tid; p < np; p += AG_WG) sc[hq * AG_MAXP + p] = sc[hq * AG_MAXP + p] * inv;
     }
-    if (p0 < np) vadd(vb[0], p0);
+    vstore(vr[0], 0);
+    if (nch > 2) vfetch(vr[0], 2);
+    __syncthreads();
+
+    /* 4. values: wave hh (64 threads) is head kh*grp + hh, thread j its column, adding w_p * v_p[j] in position
+     * order from the chunk in LDS; every wave stages the chunks (chunk c+1 stored while c is summed, c+3
+     * requested), one barrier per chunk */
+    const uint32_t hh = tid / AR_HD, j = tid % AR_HD;
+    const float *srow = sc + hh * AG_MAXP;
+    float acc = 0.0f;
+    auto vstep = [&](uint32_t c, float4 (&nxt)[2]) __attribute__((always_inline)) {
+        if (hh < grp) { /* whole waves */
+            const float *vc = vs[c & 1u] + j, *wc = srow + c * AG_VC;
+            const uint32_t cnt = np - c * AG_VC < AG_VC ? np - c * AG_VC : AG_VC;
+            if (cnt == AG_VC) {
+#pragma unroll 16
+                for (uint32_t u = 0; u < AG_VC; ++u) {
+                    const float pr = wc[u] * vc[u * AR_HD];
+                    acc = acc + pr;
+                }
+            } else {
+                for (uint32_t u = 0; u < cnt; ++u) {
+                    const float pr = wc[u] * vc[u * AR_HD];
+                    acc = acc + pr;
+                }
+            }
+        }
+        if (c + 1 < nch) vstore(nxt, (c + 1) & 1u);
+        if (c + 3 < nch) vfetch(nxt, c + 3);
+        __syncthreads();
+    };
+    for (uint32_t c = 0; c < nch; c += 2) { /* register sets alternate: vr[1] holds chunk c+1, vr[0] chunk c+2 */
+        vstep(c, vr[1]);
+        if (c + 1 < nch) vstep(c + 1, vr[0]);
+    }
+    if (hh >= grp) return; /* whole waves */
 
     /* 5. the outputs and their Q8 blocks (lanes 0-31 and 32-63: one block each) */
     const uint32_t head = kh * grp + hh;

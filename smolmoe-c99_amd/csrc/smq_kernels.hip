@@ -978,17 +978,20 @@ __global__ __launch_bounds__(WG) void k_quantize_q8(const float *x, uint32_t row
 
 /* ------------------------------------------------------------------------
  * Activation producers (reference: src/model.c:334-415, src/vecmath.c:61-93).
- * One workgroup of 1024 threads per token row: optional RMSNorm (sequential
- * f32 sum of squares, model.c:337 — the squares are formed in parallel, one
- * lane adds them in element order), optional SwiGLU / GeGLU with the binary64
- * exp below, then the Q8 block quantization of kernels.c:912-935, written
- * straight to d/q. Element i lives in thread i % 1024, register i / 1024.
+ * One workgroup of NT threads per token row (256 for rows up to 4096
+ * elements, so that many rows run at once; 1024 for longer ones; 512 for
+ * rows up to 8192 measured no faster on the 4864-wide SwiGLU rows): optional
+ * RMSNorm (sequential f32 sum of squares, model.c:337 — the squares are formed
+ * in parallel, one wave adds them in element order), optional SwiGLU / GeGLU
+ * with the binary64 exp below, then the Q8 block quantization of
+ * kernels.c:912-935, written straight to d/q. Element i lives in thread
+ * i % NT, register i / NT.
  * ---------------------------------------------------------------------- */
-constexpr int RW_WG = 1024;
-constexpr int RW_EPT = 16; /* elements per thread: rows up to 16384 */
+constexpr int RW_WG = 1024, RW_NARROW = 256;
+constexpr int RW_EPT = 16; /* elements per thread: rows up to 16384 (4096 at 256 threads) */
 
-template <bool NORM, int ACT>
-__global__ __launch_bounds__(RW_WG) void k_row_quantize(const float *src, const float *norm, float eps,
+template <bool NORM, int ACT, int NT>
+__global__ __launch_bounds__(NT) void k_row_quantize(const float *src, const float *norm, float eps,
                                                        const float *gate, uint32_t n, float *yout, float *d,
                                                        int8_t *q, int *flag) {
     extern __shared__ __attribute__((aligned(16))) float sq_lds[]; /* NORM: the n squares (4*ceil(n/4) floats) */
@@ -999,13 +1002,13 @@ __global__ __launch_bounds__(RW_WG) void k_row_quantize(const float *src, const 
     float v[RW_EPT];
 #pragma unroll
     for (int k = 0; k < RW_EPT; ++k) {
-        const uint32_t i = tid + k * RW_WG;
+        const uint32_t i = tid + k * NT;
         v[k] = i < n ? x[i] : 0.0f;
     }
     if (NORM) {
 #pragma unroll
         for (int k = 0; k < RW_EPT; ++k) {
-            const uint32_t i = tid + k * RW_WG;
+            const uint32_t i = tid + k * NT;
             if (i < n) sq_lds[i] = v[k] * v[k];
         }
         __syncthreads();
@@ -1022,7 +1025,7 @@ __global__ __launch_bounds__(RW_WG) void k_row_quantize(const float *src, const 
         if (s_bad && tid == 0 && flag) *flag = 1;
 #pragma unroll
         for (int k = 0; k < RW_EPT; ++k) {
-            const uint32_t i = tid + k * RW_WG;
+            const uint32_t i = tid + k * NT;
             if (i < n) {
                 const float t = v[k] * inv;
                 v[k] = t * norm[i]; /* model.c:340 */
@@ -1033,7 +1036,7 @@ __global__ __launch_bounds__(RW_WG) void k_row_quantize(const float *src, const 
         const float *g = gate + (size_t)row * n;
 #pragma unroll
         for (int k = 0; k < RW_EPT; ++k) {
-            const uint32_t i = tid + k * RW_WG;
+            const uint32_t i = tid + k * NT;
             if (i < n) {
                 const float gv = g[i];
                 float e;
@@ -1053,15 +1056,15 @@ __global__ __launch_bounds__(RW_WG) void k_row_quantize(const float *src, const 
     if (yout) {
 #pragma unroll
         for (int k = 0; k < RW_EPT; ++k) {
-            const uint32_t i = tid + k * RW_WG;
+            const uint32_t i = tid + k * NT;
             if (i < n) yout[(size_t)row * n + i] = v[k];
         }
     }
     /* Q8 blocks: 32 consecutive elements = 32 consecutive threads of one k */
 #pragma unroll
     for (int k = 0; k < RW_EPT; ++k) {
-        const uint32_t i = tid + k * RW_WG;
-        if (k * RW_WG >= np) break; /* uniform */
+        const uint32_t i = tid + k * NT;
+        if (k * NT >= np) break; /* uniform */
         const bool valid = i < n;
         const float av = fabsf(v[k]);
         int bad = valid && !(av <= FLT_MAX);
@@ -2606,9 +2609,17 @@ hipError_t launch_row_quantize(const float *src, const float *norm, float eps, c
     if (!rows || !n) return hipSuccess;
     if (n > (uint32_t)(RW_WG * RW_EPT)) return hipErrorInvalidValue;
     const size_t lds = norm ? (size_t)((n + 3) & ~3u) * sizeof(float) : 0; /* the squares' whole float4s */
-    const dim3 grid(rows), block(RW_WG);
-#define SMQ_RQ(NORM, ACT) \
-    hipLaunchKernelGGL((k_row_quantize<NORM, ACT>), grid, block, lds, s, src, norm, eps, gate, n, y, d, q, flag)
+    const dim3 grid(rows);
+    const int nt = n <= (uint32_t)(RW_NARROW * RW_EPT) ? RW_NARROW : RW_WG;
+#define SMQ_RQ(NORM, ACT)                                                                                      \
+    do {                                                                                                       \
+        if (nt == RW_NARROW)                                                                                   \
+            hipLaunchKernelGGL((k_row_quantize<NORM, ACT, RW_NARROW>), grid, dim3(RW_NARROW), lds, s, src, norm, \
+                               eps, gate, n, y, d, q, flag);                                                   \
+        else                                                                                                   \
+            hipLaunchKernelGGL((k_row_quantize<NORM, ACT, RW_WG>), grid, dim3(RW_WG), lds, s, src, norm, eps,    \
+                               gate, n, y, d, q, flag);                                                        \
+    } while (0)
     if (norm) {
         if (act == 1) SMQ_RQ(true, 1);
         else if (act == 2) SMQ_RQ(true, 2);

@@ -723,9 +723,10 @@ def test_matmul_prefill_switch(orc):
 
 # ------------------------------------------------------------------ activation producers
 
-@pytest.mark.parametrize("n", [896, 4864, 8960, 100, 1])
+@pytest.mark.parametrize("n", [896, 4864, 8960, 100, 1, 4096, 4097])
 def test_norm_quantize_bit_exact(orc, n):
-    """RMSNorm (sequential f32 sum) then Q8, against the oracle's row_work."""
+    """RMSNorm (sequential f32 sum) then Q8, against the oracle's row_work; 4096 and 4097 are the last row
+    of the 256-thread workgroups and the first of the 1024-thread ones."""
     g = LcgUniform(300 + n)
     rows = 5
     x = g.uniform(-3, 3, rows * n)
@@ -742,12 +743,12 @@ def test_norm_quantize_bit_exact(orc, n):
     assert np.array_equal(q.download(np.int8), wq)
 
 
-@pytest.mark.parametrize("gelu", [False, True])
-def test_silu_quantize_bit_exact(orc, gelu):
+@pytest.mark.parametrize("gelu,n", [(False, 4864), (True, 4864), (False, 4096)])
+def test_silu_quantize_bit_exact(orc, gelu, n):
     """SwiGLU / GeGLU with the binary64 exp, in place, then Q8; gate values
-    cover the exp clamps, infinities and NaN-free extremes."""
+    cover the exp clamps, infinities and NaN-free extremes; 1024- and 256-thread rows."""
     g = LcgUniform(400 + gelu)
-    rows, n = 3, 4864
+    rows = 3
     nb = n // 32
     up = g.uniform(-4, 4, rows * n)
     gate = g.uniform(-30, 30, rows * n)

@@ -368,12 +368,13 @@ def set_gemv_rows(rows):
     _check(load().smq_set_gemv_rows(int(rows)))
 
 
-EXACT_BY_SHAPE, EXACT_MFMA, EXACT_VALU = 0, 1, 2
+EXACT_BY_SHAPE, EXACT_MFMA, EXACT_VALU, EXACT_MFMA_SPLIT = 0, 1, 2, 3
 
 
 def set_exact_gemm(mode):
     """Kernel of the exact prefill GEMM: EXACT_BY_SHAPE (default), EXACT_MFMA (lane sums on the matrix
-    cores) or EXACT_VALU (lane sums as v_dot4); the outputs are the same bit for bit."""
+    cores), EXACT_VALU (lane sums as v_dot4) or EXACT_MFMA_SPLIT (matrix cores, each tile's lane sums over
+    two waves); the outputs are the same bit for bit."""
     _check(load().smq_set_exact_gemm(int(mode)))
 
 

@@ -606,10 +606,15 @@ __device__ __forceinline__ float lane_step_f(float acc, float d, float s) {
     return acc + p;
 }
 
-template <bool Q5, bool FAST>
+template <bool Q5, bool FAST, bool SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gemm_xm(MatArgs a,
                                                                                            uint32_t tok_tiles) {
-    __shared__ __attribute__((aligned(16))) uint2 opa[XM_CB * XM_PS];
+    /* SPLIT: 16-row x 32-token tiles, wave w takes tokens 16 (w/2) .. and lane sums 4 (w%2) .. 4 (w%2) + 3,
+     * the two halves joined in the lane tree at the end (twice the workgroups of a shape, half the chain
+     * per wave) */
+    constexpr uint32_t TR = SPLIT ? 16 : 32, APS = SPLIT ? 2 * 64 + 4 : XM_PS;
+    static_assert(APS % 32 == 4, "bank spread of the staging writes");
+    __shared__ __attribute__((aligned(16))) uint2 opa[XM_CB * APS];
     __shared__ __attribute__((aligned(16))) uint2 opb[XM_CB * XM_PS];
     __shared__ __attribute__((aligned(16))) float wsc[XM_CB][XM_SP];
     __shared__ __attribute__((aligned(16))) float xsc[XM_CB][XM_SP];
@@ -622,11 +627,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const uint32_t L = xcd * per + (xcd < extra ? xcd : extra) + k;
     const uint32_t row_tile = L / tok_tiles, tok_tile = L % tok_tiles;
     const Item I = pick_item(a, row_tile);
-    const uint32_t r0 = (row_tile - I.tile_begin) * 32, t0 = tok_tile * 32;
+    const uint32_t r0 = (row_tile - I.tile_begin) * TR, t0 = tok_tile * 32;
 
-    /* staging: thread (row or token tid/8, block tid%8 of the chunk) */
+    /* staging: thread (row or token tid/8, block tid%8 of the chunk); SPLIT: rows for threads below 128 */
     const uint32_t srow = tid / 8, sblk = tid % 8;
-    const bool srow_ok = r0 + srow < I.rows, stok_ok = t0 + srow < a.ntok;
+    const bool wstage = srow < TR;
+    const bool srow_ok = wstage && r0 + srow < I.rows, stok_ok = t0 + srow < a.ntok;
     const unsigned char *wrow = I.w + (size_t)(srow_ok ? r0 + srow : 0) * I.row_bytes;
     const size_t tok_base = (size_t)(stok_ok ? t0 + srow : 0) * a.xstride;
     uint32_t wr[Q5 ? 11 : 9] = {};
@@ -666,10 +672,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const uint32_t b = c * XM_CB + sblk;
         const bool ok = srow_ok && b < nb, xok = stok_ok && b < nb;
         /* lane word l = 4h + m of row (token) s goes to [block][s / 16][h][s % 16 + 16 m] */
-        uint2 *wd = opa + sblk * XM_PS + (srow / 16) * 128 + srow % 16;
+        uint2 *wd = opa + sblk * APS + (srow / 16) * 128 + srow % 16;
         uint2 *xd = opb + sblk * XM_PS + (srow / 16) * 128 + srow % 16;
-        float sc;
-        if (Q5) {
+        float sc = 0.0f;
+        if (!wstage) {
+        } else if (Q5) {
             Q5Fields f[2];
             q5_parse_pair(wr, f[0], f[1]);
             const bool second = sblk & 1u;
@@ -688,16 +695,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             for (int l = 0; l < 8; ++l) wd[(l / 4) * 64 + (l % 4) * 16] = ok ? i8x4_f16(wr[1 + l]) : make_uint2(0u, 0u);
             sc = ok ? __uint_as_float(wr[0]) : 0.0f;
         }
-        wsc[sblk][srow] = sc;
+        if (wstage) wsc[sblk][srow] = sc;
 #pragma unroll
         for (int l = 0; l < 8; ++l) xd[(l / 4) * 64 + (l % 4) * 16] = xok ? i8x4_f16(xr[l]) : make_uint2(0u, 0u);
         xsc[sblk][srow] = xok ? xs : 0.0f;
     };
 
-    const uint32_t lane = tid & 63u, w = tid >> 6, rg = w & 1u, tg = w >> 1;
-    float acc[8][4];
+    const uint32_t lane = tid & 63u, w = tid >> 6, rg = SPLIT ? 0u : w & 1u, tg = w >> 1, hs = SPLIT ? w & 1u : 0u;
+    constexpr int NL = SPLIT ? 4 : 8; /* lane sums per output held by this wave */
+    float acc[NL][4];
 #pragma unroll
-    for (int l = 0; l < 8; ++l)
+    for (int l = 0; l < NL; ++l)
 #pragma unroll
         for (int v = 0; v < 4; ++v) acc[l][v] = 0.0f;
 
@@ -709,6 +717,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         if (c + 1 < nchunks) fetch(c + 1);
         const uint32_t count = nb - c * XM_CB < XM_CB ? nb - c * XM_CB : XM_CB;
         auto block = [&](uint32_t bb) __attribute__((always_inline)) {
+            if constexpr (SPLIT) {
+                const uint2 *pa = opa + bb * APS + hs * 64 + lane, *pb = opb + bb * XM_PS + tg * 128 + hs * 64 + lane;
+                const h4v a0 = __builtin_bit_cast(h4v, pa[0]), b0 = __builtin_bit_cast(h4v, pb[0]);
+                const f16x z = {};
+                const f16x s0 = __builtin_amdgcn_mfma_f32_16x16x4f16(a0, b0, z, 0, 0, 0); /* lanes 4hs .. 4hs+3 */
+                const float4 dw = *(const float4 *)&wsc[bb][4 * (lane >> 4)];
+                const float dx = xsc[bb][tg * 16 + (lane & 15u)];
+                const float d[4] = {dw.x * dx, dw.y * dx, dw.z * dx, dw.w * dx};
+#pragma unroll
+                for (int m = 0; m < NL; ++m)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[m][v] = lane_step_f<FAST>(acc[m][v], d[v], s0[4 * m + v]);
+                return;
+            }
             const uint2 *pa = opa + bb * XM_PS + rg * 128 + lane, *pb = opb + bb * XM_PS + tg * 128 + lane;
             const h4v a0 = __builtin_bit_cast(h4v, pa[0]), a1 = __builtin_bit_cast(h4v, pa[64]);
             const h4v b0 = __builtin_bit_cast(h4v, pb[0]), b1 = __builtin_bit_cast(h4v, pb[64]);
@@ -725,7 +747,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 #pragma unroll
             for (int m = 0; m < 4; ++m)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) acc[4 + m][v] = lane_step_f<FAST>(acc[4 + m][v], d[v], s1[4 * m + v]);
+                for (int v = 0; v < 4; ++v) acc[(4 + m) % NL][v] = lane_step_f<FAST>(acc[(4 + m) % NL][v], d[v], s1[4 * m + v]);
         };
         /* unrolled with uniform guards: fixed LDS offsets per block, 103-106 registers (four waves per SIMD) */
 #pragma unroll
@@ -734,10 +756,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         __syncthreads();
     }
 
+    float hi[4][4]; /* lane sums 4-7 of each output */
+    if constexpr (SPLIT) { /* from the partner wave, through LDS (opa: every read of it ended at the last barrier) */
+        float *xch = (float *)opa;
+        static_assert(16 * 128 * sizeof(float) <= sizeof(opa), "exchange buffer");
+        if (hs == 1) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) xch[(4 * m + v) * 128 + tg * 64 + lane] = acc[m][v];
+        }
+        __syncthreads();
+        if (hs == 1) return; /* whole waves */
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) hi[m][v] = xch[(4 * m + v) * 128 + tg * 64 + lane];
+    } else {
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) hi[m][v] = acc[(4 + m) % NL][v];
+    }
 #pragma unroll
     for (int v = 0; v < 4; ++v) { /* the lane tree of reduce8: ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) */
-        const float o = ((acc[0][v] + acc[4][v]) + (acc[2][v] + acc[6][v])) +
-                        ((acc[1][v] + acc[5][v]) + (acc[3][v] + acc[7][v]));
+        const float o = ((acc[0][v] + hi[0][v]) + (acc[2][v] + hi[2][v])) + ((acc[1][v] + hi[1][v]) + (acc[3][v] + hi[3][v]));
         const uint32_t r = r0 + rg * 16 + 4 * (lane >> 4) + v, t = t0 + tg * 16 + (lane & 15u);
         if (r < I.rows && t < a.ntok) store_out(I, a.flag, t, r, o);
     }
@@ -745,22 +788,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 
 }  // namespace
 
-hipError_t launch_gemm_xm(MatArgs a, bool q5, bool fast, hipStream_t s) {
+hipError_t launch_gemm_xm(MatArgs a, bool q5, bool fast, bool split, hipStream_t s) {
+    const uint32_t tr = split ? 16 : 32;
     uint32_t tiles = 0;
     for (uint32_t i = 0; i < a.nitems; ++i) {
         a.item[i].tile_begin = tiles;
-        tiles += (a.item[i].rows + 31) / 32;
+        tiles += (a.item[i].rows + tr - 1) / tr;
     }
     const uint32_t tok_tiles = (a.ntok + 31) / 32;
     if (!tiles || !tok_tiles || !a.nb) return hipSuccess;
     const dim3 grid(tiles * tok_tiles), block(256);
+#define SMQ_XM(Q5, FAST)                                                                               \
+    do {                                                                                               \
+        if (split) hipLaunchKernelGGL((k_gemm_xm<Q5, FAST, true>), grid, block, 0, s, a, tok_tiles);  \
+        else hipLaunchKernelGGL((k_gemm_xm<Q5, FAST, false>), grid, block, 0, s, a, tok_tiles);       \
+    } while (0)
     if (q5) {
-        if (fast) hipLaunchKernelGGL((k_gemm_xm<true, true>), grid, block, 0, s, a, tok_tiles);
-        else hipLaunchKernelGGL((k_gemm_xm<true, false>), grid, block, 0, s, a, tok_tiles);
+        if (fast) SMQ_XM(true, true);
+        else SMQ_XM(true, false);
     } else {
-        if (fast) hipLaunchKernelGGL((k_gemm_xm<false, true>), grid, block, 0, s, a, tok_tiles);
-        else hipLaunchKernelGGL((k_gemm_xm<false, false>), grid, block, 0, s, a, tok_tiles);
+        if (fast) SMQ_XM(false, true);
+        else SMQ_XM(false, false);
     }
+#undef SMQ_XM
     return hipGetLastError();
 }
 

@@ -174,7 +174,7 @@ class exact_kernel:
         smq.set_exact_gemm(smq.EXACT_BY_SHAPE)
 
 
-EXACT_MODES = [smq.EXACT_MFMA, smq.EXACT_VALU]
+EXACT_MODES = [smq.EXACT_MFMA, smq.EXACT_VALU, smq.EXACT_MFMA_SPLIT]
 
 
 @pytest.mark.parametrize("mode", EXACT_MODES)
@@ -197,7 +197,7 @@ def test_exact_gemm_16_token_tiles_ragged(orc, q5, fast, mode):
     assert np.all(bits(got[~m]) == 0xFFFFFFFF), "wrote outside the output rows"
 
 
-@pytest.mark.parametrize("mode", [smq.EXACT_BY_SHAPE, smq.EXACT_MFMA])
+@pytest.mark.parametrize("mode", [smq.EXACT_BY_SHAPE, smq.EXACT_MFMA, smq.EXACT_MFMA_SPLIT])
 def test_random_shapes_and_strides(orc, mode):
     """Ragged rows and tokens, odd widths (including odd Q5 widths, which take
     the generic kernel), output strides wider than the row count; then the
@@ -378,8 +378,9 @@ def matmul_fused_items_bias_and_fault(orc):
     assert e.value.status == 7
 
 
+@pytest.mark.parametrize("mode", [smq.EXACT_MFMA, smq.EXACT_MFMA_SPLIT])
 @pytest.mark.parametrize("q5", [False, True])
-def test_exact_mfma_items_bias_accumulate_nonfinite(orc, q5):
+def test_exact_mfma_items_bias_accumulate_nonfinite(orc, q5, mode):
     """The MFMA lane-sum kernel through smq_matmul: four items of ragged row counts (item edges inside
     and between 32-row tiles), bias on some, residual add on others, 70 tokens (a ragged 32-token tile);
     then an infinite weight scale flags SM_ERR_NUMERIC."""
@@ -400,8 +401,8 @@ def test_exact_mfma_items_bias_accumulate_nonfinite(orc, q5):
         items.append((smq.QMat(smq.DeviceBuffer.from_array(w), rows, cols, smq.DTYPE_Q5 if q5 else smq.DTYPE_Q8),
                       smq.DeviceBuffer.from_array(bias) if bias is not None else None,
                       smq.DeviceBuffer.from_array(y0), acc))
-    say("exact mfma items", q5)
-    with exact_kernel(smq.EXACT_MFMA):
+    say("exact mfma items", q5, mode)
+    with exact_kernel(mode):
         smq.matmul(items, dbuf, qbuf, ntok)
         smq.numeric_check()
         for i, (it, want) in enumerate(zip(items, wants)):
@@ -416,7 +417,7 @@ def test_exact_mfma_items_bias_accumulate_nonfinite(orc, q5):
 
 
 def test_exact_gemm_mode_refuses_other_values():
-    for bad in (-1, 3, 7):
+    for bad in (-1, 4, 7):
         with pytest.raises(smq.SmqError) as e:
             smq.set_exact_gemm(bad)
         assert e.value.status == smq.SM_ERR_RANGE

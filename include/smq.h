@@ -164,9 +164,9 @@ smq_status smq_set_gemv_rows(int rows);
 /* Tuning (no reference counterpart): which kernel the exact prefill GEMM
  * (smq_gemm_q8 / smq_gemm_q5 / smq_matmul with ntok > 1) takes: 0 = chosen by
  * shape (the default), 1 = the one whose lane sums run on the matrix cores,
- * 2 = the one whose lane sums run as v_dot4, 3 = the matrix-core one with each
- * tile's eight lane sums split over two waves. Every output is the same, bit
- * for bit. Any other value is refused with SMQ_ERR_RANGE. */
+ * 2 = the one whose lane sums run as v_dot4, 3 (4) = the matrix-core one with
+ * each tile's eight lane sums split over two (four) waves. Every output is the
+ * same, bit for bit. Any other value is refused with SMQ_ERR_RANGE. */
 smq_status smq_set_exact_gemm(int mode);
 
 /* ---- fused matmul with bias and finiteness (src/model.c:236-310) -------- */

@@ -368,13 +368,13 @@ def set_gemv_rows(rows):
     _check(load().smq_set_gemv_rows(int(rows)))
 
 
-EXACT_BY_SHAPE, EXACT_MFMA, EXACT_VALU, EXACT_MFMA_SPLIT = 0, 1, 2, 3
+EXACT_BY_SHAPE, EXACT_MFMA, EXACT_VALU, EXACT_MFMA_SPLIT, EXACT_MFMA_SPLIT4 = 0, 1, 2, 3, 4
 
 
 def set_exact_gemm(mode):
     """Kernel of the exact prefill GEMM: EXACT_BY_SHAPE (default), EXACT_MFMA (lane sums on the matrix
-    cores), EXACT_VALU (lane sums as v_dot4) or EXACT_MFMA_SPLIT (matrix cores, each tile's lane sums over
-    two waves); the outputs are the same bit for bit."""
+    cores), EXACT_VALU (lane sums as v_dot4), EXACT_MFMA_SPLIT or EXACT_MFMA_SPLIT4 (matrix cores, each tile's
+    lane sums over two or four waves); the outputs are the same bit for bit."""
     _check(load().smq_set_exact_gemm(int(mode)))
 
 

@@ -466,7 +466,7 @@ smq_status smq_set_gemv_rows(int rows) {
 }
 
 smq_status smq_set_exact_gemm(int mode) {
-    if (!smq::set_exact_gemm(mode)) return set_status(SMQ_ERR_RANGE, "set_exact_gemm: %d is not 0, 1, 2 or 3", mode);
+    if (!smq::set_exact_gemm(mode)) return set_status(SMQ_ERR_RANGE, "set_exact_gemm: %d is not 0, 1, 2, 3 or 4", mode);
     return SMQ_OK;
 }
 

@@ -143,12 +143,13 @@ int gemv_rows_per_tile(uint32_t nb, bool q5, uint32_t total_rows);
 bool set_gemv_rows(int rt);
 void set_att_grouped(bool on);
 /* Which kernel the exact prefill GEMM (ntok > 1) takes: 0 = chosen by shape, 1 = the MFMA lane-sum
- * kernel, 2 = the VALU kernel, 3 = the MFMA lane-sum kernel with each tile's lane sums split over two
- * waves (false for any other value); every output is the same. */
+ * kernel, 2 = the VALU kernel, 3 (4) = the MFMA lane-sum kernel with each tile's lane sums split over two
+ * (four) waves (false for any other value); every output is the same. */
 bool set_exact_gemm(int mode);
-/* The exact prefill GEMM with its lane sums on f16 MFMA (csrc/smq_mfma.hip): fast_layout shapes,
- * 32 x 32 tiles of rows and tokens, or (split) 16 x 32 tiles whose lane sums 0-3 and 4-7 run in two waves. */
-hipError_t launch_gemm_xm(MatArgs a, bool q5, bool fast, bool split, hipStream_t s);
+/* The exact prefill GEMM with its lane sums on f16 MFMA (csrc/smq_mfma.hip): fast_layout shapes; split 1:
+ * 32 x 32 tiles of rows and tokens; 2: 16 x 32 tiles whose lane sums 0-3 and 4-7 run in two waves; 4: 16 x 16
+ * tiles, two lane sums per wave. */
+hipError_t launch_gemm_xm(MatArgs a, bool q5, bool fast, int split, hipStream_t s);
 hipError_t launch_matmul_fused(const FusedArgs &a, bool q5, int pro, bool glu, hipStream_t s);
 /* h = h * act(gate) elementwise (act 1 SwiGLU, 2 GeGLU). */
 hipError_t launch_glu(float *h, const float *gate, uint32_t n, int act, hipStream_t s);

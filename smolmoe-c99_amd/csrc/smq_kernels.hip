@@ -2294,8 +2294,8 @@ bool gemv_persistent(uint32_t total_rows, int rt) { return (total_rows + rt - 1)
 int g_forced_rt = 0;
 /* set_att_grouped(false) sends prefill attention to k_attend_rows instead (tuning, tests) */
 bool g_att_grouped = true;
-/* set_exact_gemm: 0 = the exact prefill GEMM chosen by shape, 1 = always k_gemm_xm, 2 = never, 3 = always
- * k_gemm_xm with split tiles */
+/* set_exact_gemm: 0 = the exact prefill GEMM chosen by shape, 1 = always k_gemm_xm, 2 = never, 3 (4) = always
+ * k_gemm_xm with each tile's lane sums split over two (four) waves */
 int g_exact_mode = 0;
 
 /* Workgroups of kernel k resident on the device (computed once per kernel by the caller's static). */
@@ -2453,12 +2453,11 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
             }
             return launch_gemv_tile<Q5, FAST>(a, rt, s);
         }
-        uint32_t tiles = 0, tiles32 = 0, tiles16 = 0;
+        uint32_t tiles = 0, tiles32 = 0;
         for (uint32_t i = 0; i < a.nitems; ++i) {
             a.item[i].tile_begin = tiles;
             tiles += (a.item[i].rows + GT_R - 1) / GT_R;
             tiles32 += (a.item[i].rows + 31) / 32;
-            tiles16 += (a.item[i].rows + 15) / 16;
         }
         static int cus = 0;
         if (!cus) {
@@ -2468,16 +2467,17 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
                 v = 256;
             cus = v;
         }
-        /* The lane sums on MFMA: 32 x 32 tiles from 7/4 workgroups per CU, tiles of 16 rows with their lane
-         * sums split over two waves from 21/16 of those workgroups per CU, else the v_dot4 kernel. Measured on
-         * MI355X (32 x 32 / split / v_dot4): 9728x896 at 128 tokens 29.2 / 30.8 / 42.3 us; 896x4864 at 512
-         * tokens 56.5 / 56.9 / 82.2; at 256 tokens 50.5 / 41.0 / 53.5; at 192 tokens 50.3 / 40.9 / 43.5; at
-         * 128 tokens 50.5 / 36.8 / 34.7; Q5 1536x8960 at 128 tokens 94.3 / 73.9 / 78.9 */
-        const uint64_t tokt32 = (a.ntok + 31) / 32;
-        if (g_exact_mode == 1 || (g_exact_mode == 0 && 4ull * tiles32 * tokt32 >= 7ull * (uint64_t)cus))
-            return launch_gemm_xm(a, Q5, FAST, false, s);
-        if (g_exact_mode == 3 || (g_exact_mode == 0 && 16ull * tiles16 * tokt32 >= 21ull * (uint64_t)cus))
-            return launch_gemm_xm(a, Q5, FAST, true, s);
+        /* The lane sums on MFMA, by the count W of 32 x 32 tiles (rows x tokens) per CU: from 7/4, 32 x 32
+         * workgroups; from 7/8, 16-row tiles with each tile's lane sums over two waves; from 1/2, 16 x 16 tiles
+         * over four waves; below, the v_dot4 kernel. Measured on MI355X (32 x 32 / two / four waves / v_dot4):
+         * 9728x896 at 128 tokens 28.9 / 30.2 / 35.4 / 41.8 us; 896x4864 at 512 tokens 56.1 / 57.1 / 63.3 /
+         * 82.7; at 256 tokens 50.0 / 41.4 / 43.5 / 53.2; at 192 tokens 49.7 / 41.1 / 38.0 / 44.1; at 128
+         * tokens 49.7 / 37.7 / 35.1 / 35.2; Q5 1536x8960 at 128 tokens 90.9 / 74.1 / 69.9 / 79.8; at 64
+         * tokens 91.6 / 67.7 / 62.9 / 62.4 */
+        const uint64_t w32 = (uint64_t)tiles32 * ((a.ntok + 31) / 32), cu = (uint64_t)cus;
+        if (g_exact_mode == 1 || (g_exact_mode == 0 && 4 * w32 >= 7 * cu)) return launch_gemm_xm(a, Q5, FAST, 1, s);
+        if (g_exact_mode == 3 || (g_exact_mode == 0 && 8 * w32 >= 7 * cu)) return launch_gemm_xm(a, Q5, FAST, 2, s);
+        if (g_exact_mode == 4 || (g_exact_mode == 0 && 2 * w32 >= cu)) return launch_gemm_xm(a, Q5, FAST, 4, s);
         /* 8-token tiles where 16-token ones would give fewer than two workgroups per CU (c1 down at 128
          * tokens: 224 workgroups) */
         if ((uint64_t)tiles * ((a.ntok + 15) / 16) < 2ull * (uint64_t)cus) {
@@ -2565,7 +2565,7 @@ bool set_gemv_rows(int rt) {
 }
 
 bool set_exact_gemm(int mode) {
-    if (mode < 0 || mode > 3) return false;
+    if (mode < 0 || mode > 4) return false;
     g_exact_mode = mode;
     return true;
 }

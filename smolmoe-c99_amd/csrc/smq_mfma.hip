@@ -606,16 +606,19 @@ __device__ __forceinline__ float lane_step_f(float acc, float d, float s) {
     return acc + p;
 }
 
-template <bool Q5, bool FAST, bool SPLIT>
+template <bool Q5, bool FAST, int S>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gemm_xm(MatArgs a,
                                                                                            uint32_t tok_tiles) {
-    /* SPLIT: 16-row x 32-token tiles, wave w takes tokens 16 (w/2) .. and lane sums 4 (w%2) .. 4 (w%2) + 3,
-     * the two halves joined in the lane tree at the end (twice the workgroups of a shape, half the chain
-     * per wave) */
-    constexpr uint32_t TR = SPLIT ? 16 : 32, APS = SPLIT ? 2 * 64 + 4 : XM_PS;
-    static_assert(APS % 32 == 4, "bank spread of the staging writes");
+    /* S waves share each 16 x 16 tile's eight lane sums: S = 1, 32 x 32 workgroup tiles, a wave all eight
+     * lane sums of its tile; S = 2, 16-row x 32-token tiles, wave w tokens 16 (w/2) .. and lane sums
+     * 4 (w%2) .. 4 (w%2) + 3; S = 4, one 16 x 16 tile, wave w lane sums 2w, 2w + 1. The parts are joined
+     * in the lane tree at the end (S times the workgroups of a shape, 1/S of the chain per wave). */
+    static_assert(S == 1 || S == 2 || S == 4, "lane-sum split");
+    constexpr uint32_t TR = S == 1 ? 32 : 16, TT = S == 4 ? 16 : 32;
+    constexpr uint32_t APS = S == 1 ? XM_PS : 2 * 64 + 4, BPS = S == 4 ? 2 * 64 + 4 : XM_PS;
+    static_assert(APS % 32 == 4 && BPS % 32 == 4, "bank spread of the staging writes");
     __shared__ __attribute__((aligned(16))) uint2 opa[XM_CB * APS];
-    __shared__ __attribute__((aligned(16))) uint2 opb[XM_CB * XM_PS];
+    __shared__ __attribute__((aligned(16))) uint2 opb[XM_CB * BPS];
     __shared__ __attribute__((aligned(16))) float wsc[XM_CB][XM_SP];
     __shared__ __attribute__((aligned(16))) float xsc[XM_CB][XM_SP];
 
@@ -627,12 +630,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const uint32_t L = xcd * per + (xcd < extra ? xcd : extra) + k;
     const uint32_t row_tile = L / tok_tiles, tok_tile = L % tok_tiles;
     const Item I = pick_item(a, row_tile);
-    const uint32_t r0 = (row_tile - I.tile_begin) * TR, t0 = tok_tile * 32;
+    const uint32_t r0 = (row_tile - I.tile_begin) * TR, t0 = tok_tile * TT;
 
-    /* staging: thread (row or token tid/8, block tid%8 of the chunk); SPLIT: rows for threads below 128 */
+    /* staging: thread (row or token tid/8, block tid%8 of the chunk); 16-row (16-token) tiles: threads below 128 */
     const uint32_t srow = tid / 8, sblk = tid % 8;
-    const bool wstage = srow < TR;
-    const bool srow_ok = wstage && r0 + srow < I.rows, stok_ok = t0 + srow < a.ntok;
+    const bool wstage = srow < TR, xstage = srow < TT;
+    const bool srow_ok = wstage && r0 + srow < I.rows, stok_ok = xstage && t0 + srow < a.ntok;
     const unsigned char *wrow = I.w + (size_t)(srow_ok ? r0 + srow : 0) * I.row_bytes;
     const size_t tok_base = (size_t)(stok_ok ? t0 + srow : 0) * a.xstride;
     uint32_t wr[Q5 ? 11 : 9] = {};
@@ -673,7 +676,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const bool ok = srow_ok && b < nb, xok = stok_ok && b < nb;
         /* lane word l = 4h + m of row (token) s goes to [block][s / 16][h][s % 16 + 16 m] */
         uint2 *wd = opa + sblk * APS + (srow / 16) * 128 + srow % 16;
-        uint2 *xd = opb + sblk * XM_PS + (srow / 16) * 128 + srow % 16;
+        uint2 *xd = opb + sblk * BPS + (srow / 16) * 128 + srow % 16;
         float sc = 0.0f;
         if (!wstage) {
         } else if (Q5) {
@@ -696,13 +699,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             sc = ok ? __uint_as_float(wr[0]) : 0.0f;
         }
         if (wstage) wsc[sblk][srow] = sc;
+        if (xstage) {
 #pragma unroll
-        for (int l = 0; l < 8; ++l) xd[(l / 4) * 64 + (l % 4) * 16] = xok ? i8x4_f16(xr[l]) : make_uint2(0u, 0u);
-        xsc[sblk][srow] = xok ? xs : 0.0f;
+            for (int l = 0; l < 8; ++l) xd[(l / 4) * 64 + (l % 4) * 16] = xok ? i8x4_f16(xr[l]) : make_uint2(0u, 0u);
+            xsc[sblk][srow] = xok ? xs : 0.0f;
+        }
     };
 
-    const uint32_t lane = tid & 63u, w = tid >> 6, rg = SPLIT ? 0u : w & 1u, tg = w >> 1, hs = SPLIT ? w & 1u : 0u;
-    constexpr int NL = SPLIT ? 4 : 8; /* lane sums per output held by this wave */
+    /* this wave's row group rg, token group tg, and (S > 1) the MFMA instruction hs (lane sums 4hs .. 4hs+3)
+     * and its first MFMA block mb */
+    const uint32_t lane = tid & 63u, w = tid >> 6;
+    const uint32_t rg = S == 1 ? w & 1u : 0u, tg = S == 4 ? 0u : w >> 1;
+    const uint32_t hs = S == 2 ? w & 1u : (S == 4 ? w >> 1 : 0u), mb = S == 4 ? 2 * (w & 1u) : 0u;
+    constexpr int NL = 8 / S; /* lane sums per output held by this wave */
     float acc[NL][4];
 #pragma unroll
     for (int l = 0; l < NL; ++l)
@@ -717,11 +726,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         if (c + 1 < nchunks) fetch(c + 1);
         const uint32_t count = nb - c * XM_CB < XM_CB ? nb - c * XM_CB : XM_CB;
         auto block = [&](uint32_t bb) __attribute__((always_inline)) {
-            if constexpr (SPLIT) {
-                const uint2 *pa = opa + bb * APS + hs * 64 + lane, *pb = opb + bb * XM_PS + tg * 128 + hs * 64 + lane;
+            if constexpr (S > 1) {
+                /* S = 4: a wave whose lane sums are the instruction's blocks 2 and 3 reads the operands of lane
+                 * L ^ 32, so that they arrive in blocks 0 and 1 (the result registers are then indexed by
+                 * constants; indexing them by the wave's half made the compiler select every element) */
+                const uint32_t ol = S == 4 ? lane ^ (mb * 16u) : lane;
+                const uint2 *pa = opa + bb * APS + hs * 64 + ol, *pb = opb + bb * BPS + tg * 128 + hs * 64 + ol;
                 const h4v a0 = __builtin_bit_cast(h4v, pa[0]), b0 = __builtin_bit_cast(h4v, pb[0]);
                 const f16x z = {};
-                const f16x s0 = __builtin_amdgcn_mfma_f32_16x16x4f16(a0, b0, z, 0, 0, 0); /* lanes 4hs .. 4hs+3 */
+                const f16x s0 = __builtin_amdgcn_mfma_f32_16x16x4f16(a0, b0, z, 0, 0, 0); /* lanes 4hs + mb .. */
                 const float4 dw = *(const float4 *)&wsc[bb][4 * (lane >> 4)];
                 const float dx = xsc[bb][tg * 16 + (lane & 15u)];
                 const float d[4] = {dw.x * dx, dw.y * dx, dw.z * dx, dw.w * dx};
@@ -756,31 +769,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         __syncthreads();
     }
 
-    float hi[4][4]; /* lane sums 4-7 of each output */
-    if constexpr (SPLIT) { /* from the partner wave, through LDS (opa: every read of it ended at the last barrier) */
+    float a8[8][4]; /* the eight lane sums of each of this lane's four outputs */
+    if constexpr (S == 1) {
+#pragma unroll
+        for (int l = 0; l < 8; ++l)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) a8[l][v] = acc[l][v];
+    } else { /* the other waves' lane sums through LDS (opa: every read of it ended at the last barrier);
+              * the wave holding lane sum 0 of a tile forms the tree */
+        constexpr uint32_t XS = S == 2 ? 128 : 64; /* exchange row: a slot per (token group, lane) */
         float *xch = (float *)opa;
-        static_assert(16 * 128 * sizeof(float) <= sizeof(opa), "exchange buffer");
-        if (hs == 1) {
+        static_assert((8 - NL) * 4 * XS * sizeof(float) <= sizeof(opa), "exchange buffer");
+        const uint32_t part = S == 2 ? hs : w, slot = S == 2 ? tg * 64 + lane : lane; /* part: lane sums NL*part.. */
+        if (part != 0) {
 #pragma unroll
-            for (int m = 0; m < 4; ++m)
+            for (int m = 0; m < NL; ++m)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) xch[(4 * m + v) * 128 + tg * 64 + lane] = acc[m][v];
+                for (int v = 0; v < 4; ++v) xch[((part - 1) * NL * 4 + 4 * m + v) * XS + slot] = acc[m][v];
         }
         __syncthreads();
-        if (hs == 1) return; /* whole waves */
+        if (part != 0) return; /* whole waves */
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+        for (int l = 0; l < 8; ++l)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) hi[m][v] = xch[(4 * m + v) * 128 + tg * 64 + lane];
-    } else {
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) hi[m][v] = acc[(4 + m) % NL][v];
+            for (int v = 0; v < 4; ++v)
+                a8[l][v] = l < NL ? acc[l % NL][v] : xch[((l / NL - 1) * NL * 4 + 4 * (l % NL) + v) * XS + slot];
     }
 #pragma unroll
     for (int v = 0; v < 4; ++v) { /* the lane tree of reduce8: ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) */
-        const float o = ((acc[0][v] + hi[0][v]) + (acc[2][v] + hi[2][v])) + ((acc[1][v] + hi[1][v]) + (acc[3][v] + hi[3][v]));
+        const float o = ((a8[0][v] + a8[4][v]) + (a8[2][v] + a8[6][v])) + ((a8[1][v] + a8[5][v]) + (a8[3][v] + a8[7][v]));
         const uint32_t r = r0 + rg * 16 + 4 * (lane >> 4) + v, t = t0 + tg * 16 + (lane & 15u);
         if (r < I.rows && t < a.ntok) store_out(I, a.flag, t, r, o);
     }
@@ -788,20 +805,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 
 }  // namespace
 
-hipError_t launch_gemm_xm(MatArgs a, bool q5, bool fast, bool split, hipStream_t s) {
-    const uint32_t tr = split ? 16 : 32;
+hipError_t launch_gemm_xm(MatArgs a, bool q5, bool fast, int split, hipStream_t s) {
+    if (split != 1 && split != 2 && split != 4) return hipErrorInvalidValue;
+    const uint32_t tr = split == 1 ? 32 : 16, tt = split == 4 ? 16 : 32;
     uint32_t tiles = 0;
     for (uint32_t i = 0; i < a.nitems; ++i) {
         a.item[i].tile_begin = tiles;
         tiles += (a.item[i].rows + tr - 1) / tr;
     }
-    const uint32_t tok_tiles = (a.ntok + 31) / 32;
+    const uint32_t tok_tiles = (a.ntok + tt - 1) / tt;
     if (!tiles || !tok_tiles || !a.nb) return hipSuccess;
     const dim3 grid(tiles * tok_tiles), block(256);
-#define SMQ_XM(Q5, FAST)                                                                               \
-    do {                                                                                               \
-        if (split) hipLaunchKernelGGL((k_gemm_xm<Q5, FAST, true>), grid, block, 0, s, a, tok_tiles);  \
-        else hipLaunchKernelGGL((k_gemm_xm<Q5, FAST, false>), grid, block, 0, s, a, tok_tiles);       \
+#define SMQ_XM(Q5, FAST)                                                                                \
+    do {                                                                                                \
+        if (split == 4) hipLaunchKernelGGL((k_gemm_xm<Q5, FAST, 4>), grid, block, 0, s, a, tok_tiles);  \
+        else if (split == 2) hipLaunchKernelGGL((k_gemm_xm<Q5, FAST, 2>), grid, block, 0, s, a, tok_tiles); \
+        else hipLaunchKernelGGL((k_gemm_xm<Q5, FAST, 1>), grid, block, 0, s, a, tok_tiles);            \
     } while (0)
     if (q5) {
         if (fast) SMQ_XM(true, true);

@@ -174,7 +174,7 @@ class exact_kernel:
         smq.set_exact_gemm(smq.EXACT_BY_SHAPE)
 
 
-EXACT_MODES = [smq.EXACT_MFMA, smq.EXACT_VALU, smq.EXACT_MFMA_SPLIT]
+EXACT_MODES = [smq.EXACT_MFMA, smq.EXACT_VALU, smq.EXACT_MFMA_SPLIT, smq.EXACT_MFMA_SPLIT4]
 
 
 @pytest.mark.parametrize("mode", EXACT_MODES)
@@ -197,7 +197,7 @@ def test_exact_gemm_16_token_tiles_ragged(orc, q5, fast, mode):
     assert np.all(bits(got[~m]) == 0xFFFFFFFF), "wrote outside the output rows"
 
 
-@pytest.mark.parametrize("mode", [smq.EXACT_BY_SHAPE, smq.EXACT_MFMA, smq.EXACT_MFMA_SPLIT])
+@pytest.mark.parametrize("mode", [smq.EXACT_BY_SHAPE, smq.EXACT_MFMA, smq.EXACT_MFMA_SPLIT, smq.EXACT_MFMA_SPLIT4])
 def test_random_shapes_and_strides(orc, mode):
     """Ragged rows and tokens, odd widths (including odd Q5 widths, which take
     the generic kernel), output strides wider than the row count; then the
@@ -378,7 +378,7 @@ def matmul_fused_items_bias_and_fault(orc):
     assert e.value.status == 7
 
 
-@pytest.mark.parametrize("mode", [smq.EXACT_MFMA, smq.EXACT_MFMA_SPLIT])
+@pytest.mark.parametrize("mode", [smq.EXACT_MFMA, smq.EXACT_MFMA_SPLIT, smq.EXACT_MFMA_SPLIT4])
 @pytest.mark.parametrize("q5", [False, True])
 def test_exact_mfma_items_bias_accumulate_nonfinite(orc, q5, mode):
     """The MFMA lane-sum kernel through smq_matmul: four items of ragged row counts (item edges inside
@@ -417,7 +417,7 @@ def test_exact_mfma_items_bias_accumulate_nonfinite(orc, q5, mode):
 
 
 def test_exact_gemm_mode_refuses_other_values():
-    for bad in (-1, 4, 7):
+    for bad in (-1, 5, 7):
         with pytest.raises(smq.SmqError) as e:
             smq.set_exact_gemm(bad)
         assert e.value.status == smq.SM_ERR_RANGE

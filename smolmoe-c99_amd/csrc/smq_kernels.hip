@@ -2468,16 +2468,16 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
             cus = v;
         }
         /* The lane sums on MFMA, by the count W of 32 x 32 tiles (rows x tokens) per CU: from 7/4, 32 x 32
-         * workgroups; from 7/8, 16-row tiles with each tile's lane sums over two waves; from 1/2, 16 x 16 tiles
-         * over four waves; below, the v_dot4 kernel. Measured on MI355X (32 x 32 / two / four waves / v_dot4):
-         * 9728x896 at 128 tokens 28.9 / 30.2 / 35.4 / 41.8 us; 896x4864 at 512 tokens 56.1 / 57.1 / 63.3 /
-         * 82.7; at 256 tokens 50.0 / 41.4 / 43.5 / 53.2; at 192 tokens 49.7 / 41.1 / 38.0 / 44.1; at 128
-         * tokens 49.7 / 37.7 / 35.1 / 35.2; Q5 1536x8960 at 128 tokens 90.9 / 74.1 / 69.9 / 79.8; at 64
-         * tokens 91.6 / 67.7 / 62.9 / 62.4 */
+         * workgroups; from 7/8, 16-row tiles with each tile's lane sums over two waves; from 1/4, 16 x 16 tiles
+         * over four waves (16-block K chunks); below, the v_dot4 kernel. Measured on MI355X (32 x 32 / two /
+         * four waves / v_dot4): 9728x896 at 128 tokens 28.9 / 30.2 / 35.4 / 41.8 us; 896x4864 at 512 tokens
+         * 56.1 / 57.1 / 63.3 / 82.7; at 256 tokens 49.6 / 41.0 / 45.7 / 52.5; at 192 tokens 49.6 / 41.0 / 37.3
+         * / 43.9; at 128 tokens 50.1 / 37.6 / 30.9 / 35.0; Q5 1536x8960 at 128 tokens 90.4 / 73.9 / 65.9 /
+         * 79.3; at 64 tokens 90.7 / 67.5 / 52.3 / 62.0 */
         const uint64_t w32 = (uint64_t)tiles32 * ((a.ntok + 31) / 32), cu = (uint64_t)cus;
         if (g_exact_mode == 1 || (g_exact_mode == 0 && 4 * w32 >= 7 * cu)) return launch_gemm_xm(a, Q5, FAST, 1, s);
         if (g_exact_mode == 3 || (g_exact_mode == 0 && 8 * w32 >= 7 * cu)) return launch_gemm_xm(a, Q5, FAST, 2, s);
-        if (g_exact_mode == 4 || (g_exact_mode == 0 && 2 * w32 >= cu)) return launch_gemm_xm(a, Q5, FAST, 4, s);
+        if (g_exact_mode == 4 || (g_exact_mode == 0 && 4 * w32 >= cu)) return launch_gemm_xm(a, Q5, FAST, 4, s);
         /* 8-token tiles where 16-token ones would give fewer than two workgroups per CU (c1 down at 128
          * tokens: 224 workgroups) */
         if ((uint64_t)tiles * ((a.ntok + 15) / 16) < 2ull * (uint64_t)cus) {

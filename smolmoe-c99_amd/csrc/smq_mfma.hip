@@ -577,7 +577,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_mh(MhArgs q) {
  * 4m + v, so a lane ends with rows 4 (L/16) + v (v = 0..3) of token L%16 and
  * all eight lane sums of each.
  * Workgroup tile 32 rows x 32 tokens; wave w takes rows 16 (w%2) .. and tokens
- * 16 (w/2) ... K advances in chunks of XM_CB blocks: each thread loads one
+ * 16 (w/2) ... K advances in chunks of XM_CB blocks (2 XM_CB for the 16 x 16
+ * tiles of the four-wave split, 38 KB of LDS: half the barriers per block,
+ * 896x4864 at 128 tokens 35.1 -> 30.9 us): each thread loads one
  * block of a row (Q5: the pair holding it) and one block of a token, turns
  * their eight words into f16 and writes them in MFMA operand order (a wave's
  * operand read is one contiguous 512-byte run); the next chunk's loads are
@@ -616,11 +618,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     static_assert(S == 1 || S == 2 || S == 4, "lane-sum split");
     constexpr uint32_t TR = S == 1 ? 32 : 16, TT = S == 4 ? 16 : 32;
     constexpr uint32_t APS = S == 1 ? XM_PS : 2 * 64 + 4, BPS = S == 4 ? 2 * 64 + 4 : XM_PS;
+    constexpr uint32_t CB = S == 4 ? 2 * XM_CB : XM_CB; /* blocks per K chunk: S = 4 stages 16 rows and 16
+                                                         * tokens, so a thread per (row, block) takes 16 */
     static_assert(APS % 32 == 4 && BPS % 32 == 4, "bank spread of the staging writes");
-    __shared__ __attribute__((aligned(16))) uint2 opa[XM_CB * APS];
-    __shared__ __attribute__((aligned(16))) uint2 opb[XM_CB * BPS];
-    __shared__ __attribute__((aligned(16))) float wsc[XM_CB][XM_SP];
-    __shared__ __attribute__((aligned(16))) float xsc[XM_CB][XM_SP];
+    __shared__ __attribute__((aligned(16))) uint2 opa[CB * APS];
+    __shared__ __attribute__((aligned(16))) uint2 opb[CB * BPS];
+    __shared__ __attribute__((aligned(16))) float wsc[CB][XM_SP];
+    __shared__ __attribute__((aligned(16))) float xsc[CB][XM_SP];
 
     const uint32_t tid = threadIdx.x, nb = a.nb;
     /* XCD-aware order: workgroup i runs on XCD i % 8; each XCD takes a contiguous range of tiles, so
@@ -632,8 +636,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const Item I = pick_item(a, row_tile);
     const uint32_t r0 = (row_tile - I.tile_begin) * TR, t0 = tok_tile * TT;
 
-    /* staging: thread (row or token tid/8, block tid%8 of the chunk); 16-row (16-token) tiles: threads below 128 */
-    const uint32_t srow = tid / 8, sblk = tid % 8;
+    /* staging: thread (row or token tid/CB, block tid%CB of the chunk); 16-row (16-token) tiles of 8-block
+     * chunks: threads below 128 */
+    const uint32_t srow = tid / CB, sblk = tid % CB;
     const bool wstage = srow < TR, xstage = srow < TT;
     const bool srow_ok = wstage && r0 + srow < I.rows, stok_ok = xstage && t0 + srow < a.ntok;
     const unsigned char *wrow = I.w + (size_t)(srow_ok ? r0 + srow : 0) * I.row_bytes;
@@ -643,7 +648,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     float xs = 0.0f;
     auto fetch = [&](uint32_t c) __attribute__((always_inline)) {
         if (Q5) {
-            const uint32_t b = c * XM_CB + (sblk & ~1u); /* the pair holding the block (nb even) */
+            const uint32_t b = c * CB + (sblk & ~1u); /* the pair holding the block (nb even) */
             if (srow_ok && b < nb) {
                 const unsigned char *p = wrow + (size_t)b * Q5_BYTES;
                 const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
@@ -653,7 +658,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                 wr[8] = v2.x; wr[9] = v2.y; wr[10] = v2.z;
             }
         } else {
-            const uint32_t b = c * XM_CB + sblk;
+            const uint32_t b = c * CB + sblk;
             if (srow_ok && b < nb) {
                 const unsigned char *p = wrow + (size_t)b * Q8_BYTES;
                 const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
@@ -662,7 +667,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                 wr[8] = *(const uint32_t *)(p + 32);
             }
         }
-        const uint32_t bx = c * XM_CB + sblk;
+        const uint32_t bx = c * CB + sblk;
         if (stok_ok && bx < nb) {
             const int8_t *p = a.xq + (tok_base + bx) * QK;
             const u4a v0 = *(const u4a *)p, v1 = *(const u4a *)(p + 16);
@@ -672,7 +677,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         }
     };
     auto stage = [&](uint32_t c) __attribute__((always_inline)) {
-        const uint32_t b = c * XM_CB + sblk;
+        const uint32_t b = c * CB + sblk;
         const bool ok = srow_ok && b < nb, xok = stok_ok && b < nb;
         /* lane word l = 4h + m of row (token) s goes to [block][s / 16][h][s % 16 + 16 m] */
         uint2 *wd = opa + sblk * APS + (srow / 16) * 128 + srow % 16;
@@ -718,13 +723,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 #pragma unroll
         for (int v = 0; v < 4; ++v) acc[l][v] = 0.0f;
 
-    const uint32_t nchunks = (nb + XM_CB - 1) / XM_CB;
+    const uint32_t nchunks = (nb + CB - 1) / CB;
     fetch(0);
     for (uint32_t c = 0; c < nchunks; ++c) {
         stage(c);
         __syncthreads();
         if (c + 1 < nchunks) fetch(c + 1);
-        const uint32_t count = nb - c * XM_CB < XM_CB ? nb - c * XM_CB : XM_CB;
+        const uint32_t count = nb - c * CB < CB ? nb - c * CB : CB;
         auto block = [&](uint32_t bb) __attribute__((always_inline)) {
             if constexpr (S > 1) {
                 /* S = 4: a wave whose lane sums are the instruction's blocks 2 and 3 reads the operands of lane
@@ -764,7 +769,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         };
         /* unrolled with uniform guards: fixed LDS offsets per block, 103-106 registers (four waves per SIMD) */
 #pragma unroll
-        for (uint32_t bb = 0; bb < XM_CB; ++bb)
+        for (uint32_t bb = 0; bb < CB; ++bb)
             if (bb < count) block(bb);
         __syncthreads();
     }

@@ -676,9 +676,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             xs = a.xd[tok_base + bx];
         }
     };
-    auto stage = [&](uint32_t c) __attribute__((always_inline)) {
-        const uint32_t b = c * CB + sblk;
-        const bool ok = srow_ok && b < nb, xok = stok_ok && b < nb;
+    /* no select on the staged words: a row past the matrix or a token past the batch stages whatever its
+     * registers hold (zeros, or an earlier chunk's words) and is never stored, since each output takes only
+     * its own row's and token's operands; a block past the row is skipped by the block loop (34 fewer VALU
+     * per thread and chunk) */
+    auto stage = [&]() __attribute__((always_inline)) {
         /* lane word l = 4h + m of row (token) s goes to [block][s / 16][h][s % 16 + 16 m] */
         uint2 *wd = opa + sblk * APS + (srow / 16) * 128 + srow % 16;
         uint2 *xd = opb + sblk * BPS + (srow / 16) * 128 + srow % 16;
@@ -696,18 +698,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             q.even = second ? f[1].even : f[0].even;
             q.odd = second ? f[1].odd : f[0].odd;
 #pragma unroll
-            for (int l = 0; l < 8; ++l) wd[(l / 4) * 64 + (l % 4) * 16] = ok ? q5x4_f16(q5_codes(q, l)) : make_uint2(0u, 0u);
-            sc = ok ? q.scale : 0.0f;
+            for (int l = 0; l < 8; ++l) wd[(l / 4) * 64 + (l % 4) * 16] = q5x4_f16(q5_codes(q, l));
+            sc = q.scale;
         } else {
 #pragma unroll
-            for (int l = 0; l < 8; ++l) wd[(l / 4) * 64 + (l % 4) * 16] = ok ? i8x4_f16(wr[1 + l]) : make_uint2(0u, 0u);
-            sc = ok ? __uint_as_float(wr[0]) : 0.0f;
+            for (int l = 0; l < 8; ++l) wd[(l / 4) * 64 + (l % 4) * 16] = i8x4_f16(wr[1 + l]);
+            sc = __uint_as_float(wr[0]);
         }
         if (wstage) wsc[sblk][srow] = sc;
         if (xstage) {
 #pragma unroll
-            for (int l = 0; l < 8; ++l) xd[(l / 4) * 64 + (l % 4) * 16] = xok ? i8x4_f16(xr[l]) : make_uint2(0u, 0u);
-            xsc[sblk][srow] = xok ? xs : 0.0f;
+            for (int l = 0; l < 8; ++l) xd[(l / 4) * 64 + (l % 4) * 16] = i8x4_f16(xr[l]);
+            xsc[sblk][srow] = xs;
         }
     };
 
@@ -726,7 +728,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const uint32_t nchunks = (nb + CB - 1) / CB;
     fetch(0);
     for (uint32_t c = 0; c < nchunks; ++c) {
-        stage(c);
+        stage();
         __syncthreads();
         if (c + 1 < nchunks) fetch(c + 1);
         const uint32_t count = nb - c * CB < CB ? nb - c * CB : CB;

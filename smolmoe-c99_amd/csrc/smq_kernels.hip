@@ -2468,14 +2468,18 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
             cus = v;
         }
         /* The lane sums on MFMA, by the count W of 32 x 32 tiles (rows x tokens) per CU: from 7/4, 32 x 32
-         * workgroups; from 7/8, 16-row tiles with each tile's lane sums over two waves; from 1/4, 16 x 16 tiles
-         * over four waves (16-block K chunks); below, the v_dot4 kernel. Measured on MI355X (32 x 32 / two /
-         * four waves / v_dot4): 9728x896 at 128 tokens 28.9 / 30.2 / 35.4 / 41.8 us; 896x4864 at 512 tokens
-         * 56.1 / 57.1 / 63.3 / 82.7; at 256 tokens 49.6 / 41.0 / 45.7 / 52.5; at 192 tokens 49.6 / 41.0 / 37.3
-         * / 43.9; at 128 tokens 50.1 / 37.6 / 30.9 / 35.0; Q5 1536x8960 at 128 tokens 90.4 / 73.9 / 65.9 /
-         * 79.3; at 64 tokens 90.7 / 67.5 / 52.3 / 62.0 */
+         * workgroups, except from 2 to 3; from 7/8 (and from 2 to 3), 16-row tiles with each tile's lane sums
+         * over two waves; from 1/4, 16 x 16 tiles over four waves (16-block K chunks); below, the v_dot4
+         * kernel. Measured on MI355X (32 x 32 / two / four waves / v_dot4, us): 9728x896 at 128 tokens (W 4.75)
+         * 26.4-27.0 / 27.7-28.5; at 96 (3.56) 21.0-21.3 / 23.3-23.5; at 64 (2.38) 17.4-17.6 / 16.6-17.1;
+         * 1152x896 at 512 (2.25) 17.4-17.7 / 16.6-17.1; Q5 8960x1536 at 64 (2.19) 26.4-26.8 / 24.3-25.1;
+         * 896x896 at 512 (1.75) 14.0 / 14.8; 896x4864 at 512 (1.75) 50.7-51.1 / 52.3-52.4; at 256 (0.88) 44.9 /
+         * 35.8-36.1 / 45.1 / 53.0; at 128 (0.44) 44.6 / 32.3-32.5 / 30.4-30.8 / 34.6; Q5 1536x8960 at 64
+         * (0.38) 83.1 / 60.5 / 52.2 / 62.5 */
         const uint64_t w32 = (uint64_t)tiles32 * ((a.ntok + 31) / 32), cu = (uint64_t)cus;
-        if (g_exact_mode == 1 || (g_exact_mode == 0 && 4 * w32 >= 7 * cu)) return launch_gemm_xm(a, Q5, FAST, 1, s);
+        const bool two_ahead = w32 >= 2 * cu && w32 < 3 * cu;
+        if (g_exact_mode == 1 || (g_exact_mode == 0 && 4 * w32 >= 7 * cu && !two_ahead))
+            return launch_gemm_xm(a, Q5, FAST, 1, s);
         if (g_exact_mode == 3 || (g_exact_mode == 0 && 8 * w32 >= 7 * cu)) return launch_gemm_xm(a, Q5, FAST, 2, s);
         if (g_exact_mode == 4 || (g_exact_mode == 0 && 4 * w32 >= cu)) return launch_gemm_xm(a, Q5, FAST, 4, s);
         /* 8-token tiles where 16-token ones would give fewer than two workgroups per CU (c1 down at 128

@@ -223,6 +223,26 @@ def test_random_shapes_and_strides(orc, mode):
         assert np.all(bits(got[~m]) == 0xFFFFFFFF), "wrote outside the output rows"
 
 
+@pytest.mark.parametrize("q5", [False, True])
+@pytest.mark.parametrize("ntok", [20, 60, 150, 220, 300, 410])
+def test_by_shape_bands(orc, q5, ntok):
+    """The by-shape choice at every band of the exact GEMM: 2043 ragged rows (64 tiles of 32) at 20-410
+    tokens give 32, 128, 320, 448, 640 and 832 tiles of 32 x 32, i.e. on 256 CUs the v_dot4 kernel, the
+    four-wave split, the two-wave split, 32 x 32 workgroups, the two-wave split again (2 to 3 tiles per
+    CU) and 32 x 32 workgroups; ragged widths and one FAST case."""
+    rows, nb = 2043, 4
+    cols = nb * 32 - 3
+    fast = ntok == 300
+    g = LcgUniform(300 + ntok)
+    w = weights(q5, ntok, rows, cols, 0.5)
+    x = g.uniform(-30, 30, ntok * cols).reshape(ntok, cols)
+    say("bands", q5, rows, ntok, nb, fast)
+    with exact_kernel(smq.EXACT_BY_SHAPE):
+        got, xd, xq = run_gemm(w, nb * (Q5B if q5 else Q8B), x, rows, ntok, nb, q5, rows, fast)
+    want = orc.gemm(w, nb * (Q5B if q5 else Q8B), xd, xq, rows, ntok, nb, stride=rows, q5=q5, fast=fast)
+    assert_same_f32(got, want, f"bands q5={q5} ntok={ntok}")
+
+
 def test_fma_probe_exact_and_fast():
     """tests/test_kernels.c:223-249: 0.0 with two roundings, 2^-12 with FMA."""
     w = np.zeros(2 * Q8B, np.uint8)

@@ -2472,7 +2472,7 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
             cus = v;
         }
         /* The lane sums on MFMA, by the count W of 32 x 32 tiles (rows x tokens) per CU: from 7/4, 32 x 32
-         * workgroups, except from 2 to 3; from 7/8 (and from 2 to 3), 16-row tiles with each tile's lane sums
+         * workgroups, except from 2 to 3; from 7/8 (Q8 5/8; and from 2 to 3), 16-row tiles with each tile's lane sums
          * over two waves; from 1/4, 16 x 16 tiles over four waves (16-block K chunks); below, the v_dot4
          * kernel. Measured on MI355X (32 x 32 / two / four waves / v_dot4, us): 9728x896 at 128 tokens (W 4.75)
          * 26.4-27.0 / 27.7-28.5; at 96 (3.56) 21.0-21.3 / 23.3-23.5; at 64 (2.38) 17.4-17.6 / 16.6-17.1;
@@ -2484,7 +2484,10 @@ hipError_t launch_typed(MatArgs a, hipStream_t s) {
         const bool two_ahead = w32 >= 2 * cu && w32 < 3 * cu;
         if (g_exact_mode == 1 || (g_exact_mode == 0 && 4 * w32 >= 7 * cu && !two_ahead))
             return launch_gemm_xm(a, Q5, FAST, 1, s);
-        if (g_exact_mode == 3 || (g_exact_mode == 0 && 8 * w32 >= 7 * cu)) return launch_gemm_xm(a, Q5, FAST, 2, s);
+        /* Q8 takes the two-wave split from 5/8 (896x4864 at 192 tokens, W 0.66: 35.4-35.8 / 36.8-37.2 on four
+         * waves), Q5 from 7/8 (1536x8960 at 128 tokens, W 0.75: 66.0-66.5 / 64.1-65.3) */
+        if (g_exact_mode == 3 || (g_exact_mode == 0 && 8 * w32 >= (Q5 ? 7 : 5) * cu))
+            return launch_gemm_xm(a, Q5, FAST, 2, s);
         if (g_exact_mode == 4 || (g_exact_mode == 0 && 4 * w32 >= cu)) return launch_gemm_xm(a, Q5, FAST, 4, s);
         /* 8-token tiles where 16-token ones would give fewer than two workgroups per CU (c1 down at 128
          * tokens: 224 workgroups) */

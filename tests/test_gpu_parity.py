@@ -224,12 +224,13 @@ def test_random_shapes_and_strides(orc, mode):
 
 
 @pytest.mark.parametrize("q5", [False, True])
-@pytest.mark.parametrize("ntok", [20, 60, 150, 220, 300, 410])
+@pytest.mark.parametrize("ntok", [20, 60, 90, 150, 220, 300, 410])
 def test_by_shape_bands(orc, q5, ntok):
     """The by-shape choice at every band of the exact GEMM: 2043 ragged rows (64 tiles of 32) at 20-410
-    tokens give 32, 128, 320, 448, 640 and 832 tiles of 32 x 32, i.e. on 256 CUs the v_dot4 kernel, the
-    four-wave split, the two-wave split, 32 x 32 workgroups, the two-wave split again (2 to 3 tiles per
-    CU) and 32 x 32 workgroups; ragged widths and one FAST case."""
+    tokens give 32, 128, 192, 320, 448, 640 and 832 tiles of 32 x 32, i.e. on 256 CUs the v_dot4 kernel,
+    the four-wave split, the two-wave split for Q8 and the four-wave one for Q5, the two-wave split,
+    32 x 32 workgroups, the two-wave split again (2 to 3 tiles per CU) and 32 x 32 workgroups; ragged
+    widths and one FAST case."""
     rows, nb = 2043, 4
     cols = nb * 32 - 3
     fast = ntok == 300
